@@ -1,0 +1,125 @@
+/*
+ * rfx_prox.h -- C ABI of the MI355X (gfx950) proximity library librfxprox.so.
+ *
+ * Plain pointers and sizes only: no C++ or torch types cross this boundary,
+ * and no exception escapes it.  Every function returns RFXP_OK or an error
+ * code; the message of the last error on a context is read with
+ * rfxp_last_error().  Device pointers are HIP device allocations on the
+ * context's device unless a function says "host".
+ *
+ * The reference's C++ entry points for this path (include/rf_proximity.hpp,
+ * rf_finishprox.hpp, rf_proximity_upper_triangle.hpp,
+ * rf_quantization_kernels.hpp, rf_proximity_lowrank.hpp,
+ * rf_lowrank_helpers.hpp) are re-implemented on top of this ABI with their
+ * original signatures in the same library; each function below names the
+ * reference interface it serves.
+ *
+ * Layout conventions
+ *   leaf (i, t)   int32 leaf[i*stride_i + t*stride_t]; the reference keeps
+ *                 tree-major [t*N + i] (include/rf_random_forest.hpp:496-501,
+ *                 stride_i = 1, stride_t = N) and sample-major [i*T + t] for
+ *                 new queries (src/rf_random_forest.cpp:4789-4852,
+ *                 stride_i = T, stride_t = 1).  Labels outside [0, nleaf)
+ *                 mean "no valid terminal node" (src/rf_proximity.cpp:126-135).
+ *   oob (i, t)    bit (i & 31) of oob_words[t*oob_ld + (i >> 5)]: 1 when
+ *                 sample i is out-of-bag in tree t (nin == 0,
+ *                 src/rf_bootstrap.cpp:67-82).
+ *   triangle      row-wise packed upper triangle with the diagonal,
+ *                 idx(i,j) = i*N - i*(i+1)/2 + j for i <= j, 64-bit
+ *                 (cuda/rf_proximity_upper_triangle.cu:34-39).
+ */
+#ifndef RFX_PROX_H
+#define RFX_PROX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define RFXP_OK 0
+#define RFXP_ERR_INVALID 1     /* bad argument, size or pointer */
+#define RFXP_ERR_HIP 2         /* a HIP runtime call failed */
+#define RFXP_ERR_NOMEM 3       /* device allocation failed */
+#define RFXP_ERR_STATE 4       /* call out of order (e.g. no forest set) */
+#define RFXP_ERR_UNSUPPORTED 5 /* size or mode outside what the kernels handle */
+
+/* Triangle output formats.  The numbering extends the reference's
+ * QuantizationLevel (FP32=0, FP16=1, INT8=2, NF4=3;
+ * include/rf_quantization_kernels.hpp:13-18). */
+#define RFXP_FMT_F32 0 /* (float)P                                        */
+#define RFXP_FMT_F16 1 /* IEEE half of (float)P, RN-even                  */
+#define RFXP_FMT_I8 2  /* fp32_to_int8((float)P, scale, zp)               */
+#define RFXP_FMT_NF4 3 /* fp32_to_nf4((float)P), 2 entries per byte,
+                          entry e in byte e/2 at bit (e%2)*4              */
+#define RFXP_FMT_U8 4  /* trunc(clamp((float)P / scale + zp, 0, 255))     */
+#define RFXP_FMT_U16 5 /* raw co-occurrence count U                       */
+
+typedef struct rfxp_ctx rfxp_ctx;
+
+/* ---- context --------------------------------------------------------- */
+
+/* Creates a context on HIP device `device` with its own stream.
+ * Replaces the reference's implicit device-0/stream-0 state
+ * (cuda/rf_growtree.cu:5209, cuda/rf_config_cuda.cu:37). */
+int rfxp_ctx_create(int device, rfxp_ctx** out);
+int rfxp_ctx_destroy(rfxp_ctx* ctx);
+/* Work is queued on `hip_stream` (a hipStream_t) from now on; NULL is the
+ * null (legacy default) stream.  A new context uses a non-blocking stream of
+ * its own, which rfxp_ctx_own_stream returns.  Streams must be of default
+ * priority. */
+int rfxp_ctx_set_stream(rfxp_ctx* ctx, void* hip_stream);
+void* rfxp_ctx_stream(rfxp_ctx* ctx);
+void* rfxp_ctx_own_stream(rfxp_ctx* ctx);
+int rfxp_sync(rfxp_ctx* ctx);
+/* Copies the last error message (NUL-terminated, truncated to n); ctx may
+ * be NULL for errors of rfxp_ctx_create.  Returns the last status code. */
+int rfxp_last_error(rfxp_ctx* ctx, char* buf, size_t n);
+/* Per-kernel timing with HIP events on the context stream (off by
+ * default).  rfxp_kernel_time returns the summed milliseconds and launch
+ * count of kernel `name` since the last reset. */
+int rfxp_set_timing(rfxp_ctx* ctx, int on);
+int rfxp_kernel_time(rfxp_ctx* ctx, const char* name, double* ms, int64_t* launches);
+int rfxp_reset_timing(rfxp_ctx* ctx);
+
+/* ---- forest leaves (input of the batched paths) ------------------------ */
+
+/* Loads the N x T leaf matrix and OOB bitmask (device pointers, read during
+ * this call only) and builds the device-resident bucket index used by the
+ * triangle: per tree, samples grouped by (leaf, OOB bit).  nout (device
+ * int32[N]) may be NULL, in which case nout_i = number of trees where i is
+ * OOB (src/rf_bootstrap.cpp:67-70).  Serves the per-tree accumulation done
+ * through rf::cpu_proximity (include/rf_proximity.hpp:10-14) and
+ * rf::cuda::gpu_proximity_upper_triangle* (include/rf_proximity_upper_triangle.hpp:42-156)
+ * as one batched call over all trees. */
+int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t,
+                    const uint32_t* oob_words, int64_t oob_ld, int64_t N, int32_t T,
+                    int32_t nleaf, const int32_t* nout);
+
+/* Computes rows [row_begin, row_end) of the packed upper triangle over all
+ * trees of the current forest and writes them, in format fmt, to the device
+ * buffer `out`, whose first entry is idx(row_begin, row_begin).  For NF4,
+ * `out` points at the byte holding that entry; nibbles of boundary bytes
+ * that belong to entries outside the range are left untouched.
+ * The entries are, for i < j (src/rf_proximity.cpp:179-230 with
+ * src/rf_finishprox.cpp:12-74):
+ *   U_ij = #{t : leaf_i(t) == leaf_j(t) valid, oob_i(t) != oob_j(t)}
+ *   P_ij = 0.5 * ((U/2)*r_i + (U/2)*r_j),  r = nout > 0 ? 1/nout : 1
+ * and P_ii = 1 (U_ii = 0).  scale/zp are the affine parameters of I8 and U8
+ * (finite, scale != 0).  Replaces the N x N double accumulation of
+ * rf::cpu_proximity + rf::cpu_finishprox for the large-N case. */
+int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t row_begin, int64_t row_end,
+               void* out);
+
+/* Size in bytes of the output of rfxp_upper for rows [row_begin, row_end). */
+int64_t rfxp_upper_nbytes(int fmt, int64_t N, int64_t row_begin, int64_t row_end);
+
+/* The per-sample nout actually used (device int32[N] copy into `nout`). */
+int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,531 @@
+/*
+ * rfx_oracle.c -- CPU restatement of RFX-Fuse's proximity path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product): loaded by
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+ * Written from the reference's algorithm, not from its code; each function
+ * names the reference lines it restates.  Built with -ffp-contract=off and
+ * without fast-math so that every double/float operation is the IEEE
+ * operation the reference performs.
+ */
+#include "rfx_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define UNUSED_LABEL (-1)
+
+static inline int64_t tri_idx(int64_t N, int64_t i, int64_t j) {
+    return i * N - i * (i + 1) / 2 + j;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a1: src/rf_proximity.cpp:99-231                                           */
+/* ------------------------------------------------------------------------ */
+void orc_cpu_proximity(const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin,
+                       int32_t nsample, int32_t nnode, int use_casewise, double* prox) {
+    const int64_t N = nsample;
+    int32_t* nod = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nnode > 0 ? nnode : 1));
+    int32_t* term = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+    int32_t nterm = 0;
+    /* terminal nodes get ordinals (src/rf_proximity.cpp:110-119) */
+    for (int32_t k = 0; k < nnode; ++k) nod[k] = (nodestatus[k] == -1) ? nterm++ : -1;
+    /* sample -> terminal ordinal or -1 (src/rf_proximity.cpp:126-135) */
+    for (int64_t n = 0; n < N; ++n) {
+        int32_t node = nodextr[n];
+        term[n] = (node >= 0 && node < nnode) ? nod[node] : -1;
+    }
+    /* CSR of members per terminal ordinal, in sample order (:138-171) */
+    int32_t* start = (int32_t*)calloc((size_t)nterm + 1, sizeof(int32_t));
+    int32_t* members = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+    int32_t* fill = (int32_t*)calloc((size_t)nterm + 1, sizeof(int32_t));
+    for (int64_t n = 0; n < N; ++n)
+        if (term[n] >= 0) start[term[n] + 1]++;
+    for (int32_t k = 0; k < nterm; ++k) start[k + 1] += start[k];
+    for (int64_t n = 0; n < N; ++n)
+        if (term[n] >= 0) members[start[term[n]] + fill[term[n]]++] = (int32_t)n;
+    /* OOB n x in-bag kk of the same terminal node (:179-230) */
+    for (int64_t n = 0; n < N; ++n) {
+        if (nin[n] != 0) continue;
+        int32_t k = term[n];
+        if (k < 0) continue;
+        int32_t nodesize = 0;
+        for (int32_t p = start[k]; p < start[k + 1]; ++p)
+            if (nin[members[p]] > 0) nodesize += nin[members[p]];
+        if (!(nodesize > 0 || !use_casewise)) continue;
+        for (int32_t p = start[k]; p < start[k + 1]; ++p) {
+            int32_t kk = members[p];
+            if (nin[kk] <= 0) continue;
+            double w = (use_casewise && nodesize > 0) ? (double)nin[kk] / (double)nodesize : 1.0;
+            prox[n + (int64_t)kk * N] += w;
+        }
+    }
+    free(nod);
+    free(term);
+    free(start);
+    free(members);
+    free(fill);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a2: src/rf_finishprox.cpp:12-74                                           */
+/* ------------------------------------------------------------------------ */
+void orc_finishprox(int32_t nsample, const int32_t* nout, const double* prox, double* proxsym) {
+    const int64_t N = nsample;
+    for (int64_t e = 0; e < N * N; ++e) proxsym[e] = prox[e];               /* :19-21 */
+    for (int64_t i = 0; i < N; ++i) proxsym[i + i * N] = (double)nout[i];   /* :26-28 */
+    for (int64_t i = 0; i < N; ++i)                                         /* :33-42 */
+        for (int64_t j = i + 1; j < N; ++j) {
+            double avg = (prox[i + j * N] + prox[j + i * N]) / 2.0;
+            proxsym[i + j * N] = avg;
+            proxsym[j + i * N] = avg;
+        }
+    for (int64_t i = 0; i < N; ++i) {                                       /* :47-55 */
+        if (nout[i] <= 0) continue;
+        double inv = 1.0 / (double)nout[i];
+        for (int64_t j = 0; j < N; ++j) proxsym[i + j * N] *= inv;
+    }
+    for (int64_t i = 0; i < N; ++i) {                                       /* :61-73 */
+        proxsym[i + i * N] = 1.0;
+        for (int64_t j = i + 1; j < N; ++j) {
+            double avg = 0.5 * (proxsym[i + j * N] + proxsym[j + i * N]);
+            proxsym[i + j * N] = avg;
+            proxsym[j + i * N] = avg;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a10: src/rf_proximity.cpp:238-397 (RF-GAP)                                */
+/* ------------------------------------------------------------------------ */
+void orc_rfgap(int32_t ntree, int32_t nsample, const int32_t* nin_flat,
+               const int32_t* nodextr_flat, double* prox) {
+    const int64_t N = nsample;
+    memset(prox, 0, sizeof(double) * (size_t)(N * N));
+    for (int64_t i = 0; i < N; ++i) {
+        int32_t n_oob = 0;
+        for (int32_t t = 0; t < ntree; ++t)
+            if (nin_flat[(int64_t)t * N + i] == 0) n_oob++;
+        if (n_oob == 0) {                       /* :314-318 */
+            prox[i + i * N] = 1.0;
+            continue;
+        }
+        for (int32_t t = 0; t < ntree; ++t) {   /* trees in ascending order (:321) */
+            const int32_t* nin = nin_flat + (int64_t)t * N;
+            const int32_t* ndx = nodextr_flat + (int64_t)t * N;
+            if (nin[i] != 0) continue;
+            int32_t node = ndx[i];
+            if (node < 0) continue;
+            int32_t mult = 0;
+            for (int64_t j = 0; j < N; ++j)
+                if (nin[j] > 0 && ndx[j] == node) mult += nin[j];
+            if (mult == 0) continue;
+            double inv = 1.0 / (double)mult;
+            for (int64_t j = 0; j < N; ++j)
+                if (nin[j] > 0 && ndx[j] == node) prox[i + j * N] += (double)nin[j] * inv;
+        }
+        double norm = 1.0 / (double)n_oob;       /* :370-375 */
+        for (int64_t j = 0; j < N; ++j) prox[i + j * N] *= norm;
+    }
+    for (int64_t i = 0; i < N; ++i)              /* :383-396 */
+        for (int64_t j = i + 1; j < N; ++j) {
+            double avg = (prox[i + j * N] + prox[j + i * N]) / 2.0;
+            prox[i + j * N] = avg;
+            prox[j + i * N] = avg;
+        }
+}
+
+void orc_terminal_leaf(const int32_t* nodestatus, int32_t nnode, const int32_t* nodextr,
+                       int32_t nsample, int32_t* leaf_out) {
+    int32_t* nod = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nnode > 0 ? nnode : 1));
+    int32_t nterm = 0;
+    for (int32_t k = 0; k < nnode; ++k) nod[k] = (nodestatus[k] == -1) ? nterm++ : -1;
+    for (int32_t n = 0; n < nsample; ++n) {
+        int32_t node = nodextr[n];
+        leaf_out[n] = (node >= 0 && node < nnode) ? nod[node] : UNUSED_LABEL;
+    }
+    free(nod);
+}
+
+/* ------------------------------------------------------------------------ */
+/* normalisation + quantizers                                                */
+/* ------------------------------------------------------------------------ */
+
+/* For i != j with integer counts c_ij, c_ji (U = c_ij + c_ji) the finishprox
+ * steps reduce to this sequence of IEEE double operations
+ * (src/rf_finishprox.cpp:38, :49-52, :69). */
+double orc_p(uint32_t U, int32_t n_i, int32_t n_j) {
+    double s = (double)U / 2.0;
+    double a = (n_i > 0) ? s * (1.0 / (double)n_i) : s;
+    double b = (n_j > 0) ? s * (1.0 / (double)n_j) : s;
+    return 0.5 * (a + b);
+}
+
+/* IEEE-754 binary32 -> binary16, round to nearest even. */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ex = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (ex == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    int32_t e = (int32_t)ex - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t h = man >> shift;
+        uint32_t rem = man & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+int8_t orc_q_i8(float v, float scale, float zp) {
+    float r = v / scale + zp;
+    r = fmaxf(-128.0f, fminf(127.0f, r));
+    return (int8_t)r;
+}
+
+uint8_t orc_q_nf4(float v) {
+    if (v >= 0.0f) return (uint8_t)fminf(7.0f, roundf(v * 7.0f));
+    return (uint8_t)fmaxf(8.0f, roundf(8.0f - v * 7.0f));
+}
+
+uint8_t orc_q_u8(float v, float scale, float zp) {
+    float r = v / scale + zp;
+    r = fmaxf(0.0f, fminf(255.0f, r));
+    return (uint8_t)r;
+}
+
+void orc_u8_scale_from_minmax(float vmin, float vmax, float* scale, float* zp) {
+    float s = (vmax - vmin) / 255.0f;
+    *scale = s;
+    *zp = -vmin / s;
+}
+
+/* Writes the entry for (U, n_i, n_j) -- or the diagonal when diag -- into
+ * a packed output at element e. NF4 entries are OR-ed into a zeroed byte. */
+static inline void put_entry(int fmt, void* out, int64_t e, int diag, uint32_t U, int32_t ni,
+                             int32_t nj, float scale, float zp) {
+    double P = diag ? 1.0 : orc_p(U, ni, nj);
+    float pf = (float)P;
+    switch (fmt) {
+        case 0: ((float*)out)[e] = pf; break;
+        case 1: ((uint16_t*)out)[e] = orc_f32_to_f16(pf); break;
+        case 2: ((int8_t*)out)[e] = orc_q_i8(pf, scale, zp); break;
+        case 3: ((uint8_t*)out)[e >> 1] |= (uint8_t)((orc_q_nf4(pf) & 0xfu) << ((e & 1) * 4)); break;
+        case 4: ((uint8_t*)out)[e] = orc_q_u8(pf, scale, zp); break;
+        case 5: ((uint16_t*)out)[e] = diag ? 0 : (uint16_t)U; break;
+        default: break;
+    }
+}
+
+void orc_nout(const uint8_t* oob, int64_t N, int32_t T, int32_t* nout) {
+    for (int64_t i = 0; i < N; ++i) nout[i] = 0;
+    for (int32_t t = 0; t < T; ++t)
+        for (int64_t i = 0; i < N; ++i) nout[i] += oob[(int64_t)t * N + i] ? 1 : 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* counts, reference-shaped                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* CSR of one tree's members grouped by label, in ascending sample order. */
+typedef struct {
+    int32_t* start; /* nleaf + 1 */
+    int32_t* mem;   /* N */
+} tree_csr;
+
+static void csr_build(const int32_t* lab, int64_t N, int32_t nleaf, tree_csr* c) {
+    c->start = (int32_t*)calloc((size_t)nleaf + 1, sizeof(int32_t));
+    c->mem = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+    int32_t* fill = (int32_t*)calloc((size_t)nleaf + 1, sizeof(int32_t));
+    for (int64_t n = 0; n < N; ++n)
+        if (lab[n] >= 0 && lab[n] < nleaf) c->start[lab[n] + 1]++;
+    for (int32_t l = 0; l < nleaf; ++l) c->start[l + 1] += c->start[l];
+    for (int64_t n = 0; n < N; ++n)
+        if (lab[n] >= 0 && lab[n] < nleaf) c->mem[c->start[lab[n]] + fill[lab[n]]++] = (int32_t)n;
+    free(fill);
+}
+
+static void csr_free(tree_csr* c) {
+    free(c->start);
+    free(c->mem);
+}
+
+void orc_upper_counts_scatter(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T,
+                              int32_t nleaf, uint16_t* U) {
+    memset(U, 0, sizeof(uint16_t) * (size_t)(N * (N + 1) / 2));
+    for (int32_t t = 0; t < T; ++t) {
+        const int32_t* lab = leaf + (int64_t)t * N;
+        const uint8_t* ob = oob + (int64_t)t * N;
+        tree_csr c;
+        csr_build(lab, N, nleaf, &c);
+        for (int64_t n = 0; n < N; ++n) {
+            if (!ob[n]) continue;                       /* OOB sample n */
+            int32_t l = lab[n];
+            if (l < 0 || l >= nleaf) continue;
+            for (int32_t p = c.start[l]; p < c.start[l + 1]; ++p) {
+                int32_t kk = c.mem[p];
+                if (ob[kk]) continue;                   /* in-bag partner only */
+                int64_t i = n < kk ? n : kk, j = n < kk ? kk : n;
+                U[tri_idx(N, i, j)]++;
+            }
+        }
+        csr_free(&c);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* counts, row-oriented (same count, used for row ranges and the baseline)   */
+/* ------------------------------------------------------------------------ */
+struct orc_index {
+    const int32_t* leaf;
+    const uint8_t* oob;
+    int64_t N;
+    int32_t T;
+    int32_t nleaf;
+    int32_t* nout;
+    tree_csr* csr;
+};
+
+orc_index* orc_index_build(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T,
+                           int32_t nleaf, const int32_t* nout_in, int threads) {
+    orc_index* x = (orc_index*)calloc(1, sizeof(orc_index));
+    x->leaf = leaf;
+    x->oob = oob;
+    x->N = N;
+    x->T = T;
+    x->nleaf = nleaf;
+    x->csr = (tree_csr*)malloc(sizeof(tree_csr) * (size_t)(T > 0 ? T : 1));
+    x->nout = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+    if (nout_in) memcpy(x->nout, nout_in, sizeof(int32_t) * (size_t)N);
+    else orc_nout(oob, N, T, x->nout);
+#ifdef _OPENMP
+    int nth = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nth)
+#endif
+    for (int32_t t = 0; t < T; ++t) csr_build(leaf + (int64_t)t * N, N, nleaf, &x->csr[t]);
+    return x;
+}
+
+void orc_index_free(orc_index* x) {
+    if (!x) return;
+    for (int32_t t = 0; t < x->T; ++t) csr_free(&x->csr[t]);
+    free(x->csr);
+    free(x->nout);
+    free(x);
+}
+
+int orc_index_rows(const orc_index* x, int fmt, float scale, float zp, int64_t r0, int64_t r1,
+                   void* out, int threads) {
+    const int64_t N = x->N;
+    const int32_t T = x->T;
+    const int32_t nleaf = x->nleaf;
+    const int32_t* leaf = x->leaf;
+    const uint8_t* oob = x->oob;
+    const int32_t* nout = x->nout;
+    const tree_csr* csr = x->csr;
+    if (r0 < 0 || r1 > N || r0 > r1) return -1;
+#ifdef _OPENMP
+    int nth = threads > 0 ? threads : omp_get_max_threads();
+#endif
+    const int64_t base = tri_idx(N, r0, r0);
+    if (fmt == 3) { /* NF4: zero the bytes we own before OR-ing nibbles in */
+        int64_t e0 = base, e1 = tri_idx(N, r1, r1);
+        if (e1 > e0) memset((uint8_t*)out, 0, (size_t)(((e1 - 1) >> 1) - (e0 >> 1) + 1));
+    }
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nth)
+#endif
+    {
+        uint16_t* cnt = (uint16_t*)calloc((size_t)(N > 0 ? N : 1), sizeof(uint16_t));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 8)
+#endif
+        for (int64_t i = r0; i < r1; ++i) {
+            for (int32_t t = 0; t < T; ++t) {
+                int32_t l = leaf[(int64_t)t * N + i];
+                if (l < 0 || l >= nleaf) continue;
+                const uint8_t* ob = oob + (int64_t)t * N;
+                uint8_t oi = ob[i] ? 1 : 0;
+                const tree_csr* c = &csr[t];
+                for (int32_t p = c->start[l + 1] - 1; p >= c->start[l]; --p) {
+                    int32_t j = c->mem[p];
+                    if (j <= i) break;                   /* members ascend */
+                    if ((ob[j] ? 1 : 0) != oi) cnt[j]++;
+                }
+            }
+            int64_t rowe = tri_idx(N, i, i) - base;
+            for (int64_t j = i; j < N; ++j) {
+                int64_t e = rowe + (j - i);
+                if (fmt == 3) {
+                    /* NF4 bytes straddling two rows are shared between
+                     * threads: compose atomically */
+                    double P = (j == i) ? 1.0 : orc_p(cnt[j], nout[i], nout[j]);
+                    uint8_t v = (uint8_t)((orc_q_nf4((float)P) & 0xfu) << (((e + base) & 1) * 4));
+                    if (v) {
+#ifdef _OPENMP
+#pragma omp atomic
+#endif
+                        ((uint8_t*)out)[((e + base) >> 1) - (base >> 1)] |= v;
+                    }
+                } else {
+                    put_entry(fmt, out, e, j == i, cnt[j], nout[i], nout[j], scale, zp);
+                }
+                cnt[j] = 0;
+            }
+        }
+        free(cnt);
+    }
+    return 0;
+}
+
+int orc_upper_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf,
+                   const int32_t* nout_in, int fmt, float scale, float zp, int64_t r0, int64_t r1,
+                   void* out, int threads) {
+    if (r0 < 0 || r1 > N || r0 > r1) return -1;
+    orc_index* x = orc_index_build(leaf, oob, N, T, nleaf, nout_in, threads);
+    int rc = orc_index_rows(x, fmt, scale, zp, r0, r1, out, threads);
+    orc_index_free(x);
+    return rc;
+}
+
+void orc_upper_from_counts(const uint16_t* U, const int32_t* nout, int64_t N, int fmt, float scale,
+                           float zp, void* out) {
+    if (fmt == 3) memset(out, 0, (size_t)((N * (N + 1) / 2 + 1) / 2));
+    for (int64_t i = 0; i < N; ++i)
+        for (int64_t j = i; j < N; ++j) {
+            int64_t e = tri_idx(N, i, j);
+            put_entry(fmt, out, e, i == j, U[e], nout[i], nout[j], scale, zp);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* top-K                                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Keep the K best (count desc, index asc) in a sorted array. */
+static inline void topk_insert(int32_t K, int32_t* n_have, int32_t* bi, uint16_t* bc, int32_t j,
+                               uint16_t c) {
+    int32_t n = *n_have;
+    if (n == K) {
+        uint16_t lc = bc[K - 1];
+        int32_t li = bi[K - 1];
+        if (c < lc || (c == lc && j > li)) return;
+        n = K - 1;
+    }
+    int32_t p = n;
+    while (p > 0 && (bc[p - 1] < c || (bc[p - 1] == c && bi[p - 1] > j))) {
+        bc[p] = bc[p - 1];
+        bi[p] = bi[p - 1];
+        --p;
+    }
+    bc[p] = c;
+    bi[p] = j;
+    *n_have = n + 1;
+}
+
+void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* qleaf, int64_t Q,
+                  int32_t K, const int32_t* exclude, int32_t* idx_out, uint16_t* cnt_out,
+                  int threads) {
+#ifdef _OPENMP
+    int nth = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel num_threads(nth)
+#endif
+    {
+        uint16_t* cnt = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(N > 0 ? N : 1));
+        int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)(K > 0 ? K : 1));
+        uint16_t* bc = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(K > 0 ? K : 1));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+        for (int64_t q = 0; q < Q; ++q) {
+            memset(cnt, 0, sizeof(uint16_t) * (size_t)N);
+            for (int32_t t = 0; t < T; ++t) {
+                int32_t ql = qleaf[q * T + t];
+                const int32_t* rl = ref_leaf + (int64_t)t * N;
+                for (int64_t j = 0; j < N; ++j) cnt[j] += (rl[j] == ql);
+            }
+            int32_t have = 0;
+            int32_t ex = exclude ? exclude[q] : -1;
+            for (int64_t j = 0; j < N; ++j)
+                if (j != ex) topk_insert(K, &have, bi, bc, (int32_t)j, cnt[j]);
+            for (int32_t k = 0; k < K; ++k) {
+                idx_out[q * K + k] = k < have ? bi[k] : -1;
+                cnt_out[q * K + k] = k < have ? bc[k] : 0;
+            }
+        }
+        free(cnt);
+        free(bi);
+        free(bc);
+    }
+}
+
+int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int64_t q,
+                     int32_t K, int exclude_self, int32_t* idx_out, uint16_t* cnt_out,
+                     float* score_out) {
+    uint16_t* cnt = (uint16_t*)calloc((size_t)(N > 0 ? N : 1), sizeof(uint16_t));
+    int32_t n_oob = 0;
+    for (int32_t t = 0; t < T; ++t) {
+        if (!oob[(int64_t)t * N + q]) continue;
+        n_oob++;
+        int32_t ql = leaf[(int64_t)t * N + q];
+        const int32_t* rl = leaf + (int64_t)t * N;
+        for (int64_t j = 0; j < N; ++j)
+            if (rl[j] == ql && !(exclude_self && j == q)) cnt[j]++;
+    }
+    int32_t have = 0;
+    if (n_oob > 0) {
+        int32_t* bi = (int32_t*)malloc(sizeof(int32_t) * (size_t)(K > 0 ? K : 1));
+        uint16_t* bc = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(K > 0 ? K : 1));
+        for (int64_t j = 0; j < N; ++j)
+            if (cnt[j] > 0 && !(exclude_self && j == q)) topk_insert(K, &have, bi, bc, (int32_t)j, cnt[j]);
+        float norm = 1.0f / (float)n_oob;   /* src/rf_random_forest.cpp:4744 */
+        for (int32_t k = 0; k < have; ++k) {
+            idx_out[k] = bi[k];
+            cnt_out[k] = bc[k];
+            score_out[k] = (float)bc[k] * norm;
+        }
+        free(bi);
+        free(bc);
+    }
+    free(cnt);
+    return have;
+}
+
+/* ------------------------------------------------------------------------ */
+/* low rank: P V with P = A A^T / T                                          */
+/* ------------------------------------------------------------------------ */
+void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, const double* V,
+                    int32_t r, double* Y) {
+    double* W = (double*)malloc(sizeof(double) * (size_t)nleaf * (size_t)r);
+    memset(Y, 0, sizeof(double) * (size_t)(N * r));
+    for (int32_t t = 0; t < T; ++t) {
+        const int32_t* lab = leaf + (int64_t)t * N;
+        memset(W, 0, sizeof(double) * (size_t)nleaf * (size_t)r);
+        for (int64_t j = 0; j < N; ++j) {
+            int32_t l = lab[j];
+            if (l < 0 || l >= nleaf) continue;
+            for (int32_t c = 0; c < r; ++c) W[(int64_t)l * r + c] += V[j * r + c];
+        }
+        for (int64_t i = 0; i < N; ++i) {
+            int32_t l = lab[i];
+            if (l < 0 || l >= nleaf) continue;
+            for (int32_t c = 0; c < r; ++c) Y[i * r + c] += W[(int64_t)l * r + c];
+        }
+    }
+    for (int64_t e = 0; e < N * r; ++e) Y[e] /= (double)T;
+    free(W);
+}

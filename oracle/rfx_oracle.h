@@ -1,0 +1,133 @@
+/*
+ * rfx_oracle.h -- CPU restatement of RFX-Fuse's Breiman-Cutler proximity path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP product
+ * path: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it.  The product library never links or calls it.
+ *
+ * Every function cites the reference file:line it restates.  Layout
+ * conventions (shared with the HIP path):
+ *   leaf[t*N + i]   int32 terminal-leaf label of sample i in tree t
+ *                   (tree-major, as leaf_assignments_ in
+ *                   include/rf_random_forest.hpp:496-501); a label outside
+ *                   [0, nleaf) means "no valid terminal node" and the sample
+ *                   takes no part in tree t (src/rf_proximity.cpp:126-135,184-186).
+ *   oob[t*N + i]    uint8, 1 when sample i is out-of-bag in tree t (nin == 0,
+ *                   src/rf_bootstrap.cpp:67-82).
+ *   packed upper triangle, row-wise with the diagonal:
+ *                   idx(i,j) = i*N - i*(i+1)/2 + j  for i <= j
+ *                   (cuda/rf_proximity_upper_triangle.cu:34-39, 64-bit here).
+ *
+ * Output formats of the triangle (enum values of RFXP_FMT_* in
+ * include/rfx_prox.h):
+ *   0 F32   (float)P                              4 B/entry
+ *   1 F16   IEEE half, RN-even, of (float)P         2 B/entry
+ *   2 I8    reference fp32_to_int8((float)P, scale, zp)
+ *                                  (include/rf_quantization_kernels.hpp:24-29)
+ *   3 NF4   reference fp32_to_nf4((float)P), 2 entries per byte, entry e in
+ *           byte e/2 at bit (e%2)*4 (cuda/rf_proximity_upper_triangle.cu:486-519)
+ *   4 U8    trunc(clamp((float)P/scale + zp, 0, 255))
+ *   5 U16   raw co-occurrence count U (no normalisation)
+ */
+#ifndef RFX_ORACLE_H
+#define RFX_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference-shaped restatements (column-major N x N double) ---------- */
+
+/* src/rf_proximity.cpp:99-231 (dense branch): one tree, accumulates
+ * prox[n + kk*N] += w for OOB n and in-bag kk in the same terminal node. */
+void orc_cpu_proximity(const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin,
+                       int32_t nsample, int32_t nnode, int use_casewise, double* prox);
+
+/* src/rf_finishprox.cpp:12-74 */
+void orc_finishprox(int32_t nsample, const int32_t* nout, const double* prox, double* proxsym);
+
+/* src/rf_proximity.cpp:238-397; nin/nodextr tree-major [t*nsample + i]. */
+void orc_rfgap(int32_t ntree, int32_t nsample, const int32_t* nin_flat,
+               const int32_t* nodextr_flat, double* prox);
+
+/* src/rf_proximity.cpp:110-135: node index -> terminal ordinal, -1 if the
+ * node is not terminal or out of range. */
+void orc_terminal_leaf(const int32_t* nodestatus, int32_t nnode, const int32_t* nodextr,
+                       int32_t nsample, int32_t* leaf_out);
+
+/* ---- normalisation and quantizers ---------------------------------------- */
+
+/* src/rf_finishprox.cpp:33-73 for one off-diagonal pair with count U. */
+double orc_p(uint32_t U, int32_t n_i, int32_t n_j);
+uint16_t orc_f32_to_f16(float f);
+int8_t orc_q_i8(float v, float scale, float zp);   /* rf_quantization_kernels.hpp:24-29 */
+uint8_t orc_q_nf4(float v);                        /* rf_quantization_kernels.hpp:37-50 */
+uint8_t orc_q_u8(float v, float scale, float zp);
+/* reference host min/max rule (cuda/rf_quantization_kernels.cu:107-119) */
+void orc_u8_scale_from_minmax(float vmin, float vmax, float* scale, float* zp);
+
+/* ---- packed upper triangle ---------------------------------------------- */
+
+/* Sum over trees of oob bits. */
+void orc_nout(const uint8_t* oob, int64_t N, int32_t T, int32_t* nout);
+
+/* Reference-shaped count: per tree bucket the samples by leaf, then for every
+ * OOB n and in-bag kk of the bucket add 1 at (min(n,kk), max(n,kk))
+ * (src/rf_proximity.cpp:110-230 folded as cuda/rf_proximity_upper_triangle.cu:229-237).
+ * U has N(N+1)/2 entries, zeroed here. */
+void orc_upper_counts_scatter(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T,
+                              int32_t nleaf, uint16_t* U);
+
+/* Row-oriented restatement of the same count for rows [r0, r1): for row i
+ * and tree t, the members j > i of i's bucket whose OOB bit differs from
+ * i's.  Writes the rows' packed entries (diagonal included) starting at
+ * idx(r0, r0), in format fmt (see above).  nout may be NULL (computed).
+ * threads <= 0 uses the OpenMP default.  Returns 0 on success. */
+int orc_upper_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf,
+                   const int32_t* nout, int fmt, float scale, float zp, int64_t r0, int64_t r1,
+                   void* out, int threads);
+
+/* The same, split so the per-tree buckets are built once and rows are
+ * produced in several calls (the CPU baseline times them separately).
+ * leaf/oob must outlive the index. */
+typedef struct orc_index orc_index;
+orc_index* orc_index_build(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T,
+                           int32_t nleaf, const int32_t* nout, int threads);
+int orc_index_rows(const orc_index* x, int fmt, float scale, float zp, int64_t r0, int64_t r1,
+                   void* out, int threads);
+void orc_index_free(orc_index* x);
+
+/* Convert a full packed count triangle to format fmt. */
+void orc_upper_from_counts(const uint16_t* U, const int32_t* nout, int64_t N, int fmt, float scale,
+                           float zp, void* out);
+
+/* ---- top-K --------------------------------------------------------------- */
+
+/* All-trees semantics (python/randomforest_py.cpp:2496-2568, :624-672):
+ * count(q,j) = #{t : qleaf[q*T+t] == ref_leaf[t*N+j]}; the K best j by
+ * (count desc, j asc), zero counts included; exclude[q] >= 0 removes that j.
+ * exclude may be NULL.  idx_out/cnt_out are Q x K. */
+void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* qleaf, int64_t Q,
+                  int32_t K, const int32_t* exclude, int32_t* idx_out, uint16_t* cnt_out, int threads);
+
+/* OOB-query semantics (src/rf_random_forest.cpp:4677-4782): trees where q is
+ * OOB, j != q when exclude_self, counts > 0 only, ordered (count desc, j asc).
+ * Returns the number of results (<= K). */
+int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int64_t q,
+                     int32_t K, int exclude_self, int32_t* idx_out, uint16_t* cnt_out,
+                     float* score_out);
+
+/* ---- low rank ------------------------------------------------------------ */
+
+/* Y = P V with P = A A^T / T, A the one-hot leaf matrix (all trees):
+ * Y[i] = (1/T) sum_t W_t[leaf_i(t)], W_t[l] = sum_{j: leaf_j(t)=l} V[j].
+ * V and Y are N x r row-major double; labels outside [0,nleaf) take no part. */
+void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, const double* V,
+                    int32_t r, double* Y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,99 @@
+// Host-side internals of librfxprox: the context object behind the C ABI,
+// device buffers, error plumbing and launch timing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "rfx_prox.h"
+
+template <class T>
+struct DevBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    // Grows (never shrinks) to hold `count` elements; contents are not kept.
+    hipError_t ensure(size_t count) {
+        if (count == 0) count = 1;
+        if (count <= n) return hipSuccess;
+        release();
+        hipError_t e = hipMalloc((void**)&p, count * sizeof(T));
+        if (e != hipSuccess) {
+            p = nullptr;
+            n = 0;
+            (void)hipGetLastError();
+            return e;
+        }
+        n = count;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+struct KernelTiming {
+    double ms = 0.0;
+    int64_t launches = 0;
+};
+
+struct rfxp_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int last_status = RFXP_OK;
+    std::string last_error;
+    int max_lds = 65536;  // dynamic LDS bytes a workgroup may use
+    int n_cu = 0;
+
+    // forest state (rfxp_set_forest)
+    bool forest_ready = false;
+    int64_t N = 0;
+    int32_t T = 0;
+    int32_t L = 0;
+    DevBuf<int32_t> bkt_off;   // T x (2L+1): bucket b = 2*leaf + oob
+    DevBuf<int32_t> bkt_mem;   // T x N: sample ids grouped by bucket
+    DevBuf<uint32_t> bkt_cnt;  // T x 2L scratch for the global-memory bucketing path
+    DevBuf<uint2> rec;         // N x T: (start, length) of the opposite-OOB bucket
+    DevBuf<int32_t> nout;      // N
+    DevBuf<double> rinv;       // N: nout > 0 ? 1/nout : 1
+    DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits
+    DevBuf<int2> items;        // work list of the triangle kernel
+    int64_t items_key[4] = {-1, -1, -1, -1};
+    int64_t n_items = 0;
+    DevBuf<int32_t> flags;     // device status words
+
+    // timing
+    bool timing = false;
+    std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, KernelTiming> times;
+};
+
+namespace rfxp {
+
+int set_error(rfxp_ctx* ctx, int status, const std::string& msg);
+int hip_error(rfxp_ctx* ctx, hipError_t e, const char* what);
+// Brackets one launch with events when timing is on.
+struct LaunchTimer {
+    rfxp_ctx* ctx;
+    const char* name;
+    hipEvent_t a = nullptr, b = nullptr;
+    LaunchTimer(rfxp_ctx* c, const char* n);
+    ~LaunchTimer();
+};
+int check_launch(rfxp_ctx* ctx, const char* what);
+bool is_device_pointer(const void* p);
+
+}  // namespace rfxp
+
+#define RFXP_HIP(ctx, call)                                            \
+    do {                                                               \
+        hipError_t _e = (call);                                        \
+        if (_e != hipSuccess) return rfxp::hip_error((ctx), _e, #call); \
+    } while (0)

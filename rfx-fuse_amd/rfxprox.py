@@ -1,0 +1,190 @@
+"""Python front end of librfxprox.so (the MI355X proximity library).
+
+A thin ctypes layer over the C ABI declared in include/rfx_prox.h.  Device
+buffers are torch tensors on a HIP device; torch is only the allocator and
+stream provider here, every kernel comes from librfxprox.so.  There is no
+CPU fallback: if the library is missing or no GPU is visible, calls raise.
+
+The reference exposes this path through C++ (rf::cpu_proximity /
+rf::cpu_finishprox, include/rf_proximity.hpp:10-14, include/rf_finishprox.hpp:9;
+rf::cuda::gpu_proximity_upper_triangle*, include/rf_proximity_upper_triangle.hpp:42-156),
+which the same library implements with those signatures; this module is the
+batched interface used by the tests and the benchmark.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "librfxprox.so")
+REPO = os.path.dirname(HERE)
+HEADER = os.path.join(REPO, "include", "rfx_prox.h")
+
+FMT_F32, FMT_F16, FMT_I8, FMT_NF4, FMT_U8, FMT_U16 = range(6)
+FMT_NAMES = {"f32": FMT_F32, "f16": FMT_F16, "i8": FMT_I8, "nf4": FMT_NF4, "u8": FMT_U8,
+             "u16": FMT_U16}
+
+_lib = None
+
+
+class RfxpError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"rfxp error {code}: {msg}")
+        self.code = code
+
+
+def header_functions(path: str = HEADER):
+    """Names of the functions declared in the C header."""
+    src = open(path).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(rfxp_\w+)\s*\(", src, flags=re.M)
+
+
+def load(path: str = LIB_PATH):
+    """Loads librfxprox.so; raises when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"librfxprox.so not built at {path}: run `make -C rfx-fuse_amd`")
+    L = C.CDLL(path)
+    vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
+    L.rfxp_ctx_create.argtypes = [C.c_int, C.POINTER(vp)]
+    L.rfxp_ctx_destroy.argtypes = [vp]
+    L.rfxp_ctx_set_stream.argtypes = [vp, vp]
+    L.rfxp_ctx_stream.argtypes = [vp]
+    L.rfxp_ctx_stream.restype = vp
+    L.rfxp_ctx_own_stream.argtypes = [vp]
+    L.rfxp_ctx_own_stream.restype = vp
+    L.rfxp_sync.argtypes = [vp]
+    L.rfxp_last_error.argtypes = [vp, C.c_char_p, C.c_size_t]
+    L.rfxp_set_timing.argtypes = [vp, C.c_int]
+    L.rfxp_kernel_time.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i64)]
+    L.rfxp_reset_timing.argtypes = [vp]
+    L.rfxp_set_forest.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp]
+    L.rfxp_upper.argtypes = [vp, C.c_int, C.c_float, C.c_float, i64, i64, vp]
+    L.rfxp_upper_nbytes.argtypes = [C.c_int, i64, i64, i64]
+    L.rfxp_upper_nbytes.restype = i64
+    L.rfxp_get_nout.argtypes = [vp, vp]
+    _lib = L
+    return L
+
+
+def upper_nbytes(fmt: int, n: int, r0: int = 0, r1: int | None = None) -> int:
+    r1 = n if r1 is None else r1
+    v = load().rfxp_upper_nbytes(fmt, n, r0, r1)
+    if v < 0:
+        raise ValueError("bad format or row range")
+    return v
+
+
+def pack_oob_bits(oob_tn):
+    """(T, N) bool/uint8 torch tensor -> (T, ceil(N/32)) int32 words, bit i%32
+    of word i//32 set when sample i is OOB."""
+    import torch
+
+    t, n = oob_tn.shape
+    w = (n + 31) // 32
+    pad = torch.zeros((t, w * 32), dtype=torch.int64, device=oob_tn.device)
+    pad[:, :n] = oob_tn.to(torch.int64)
+    weights = (torch.ones(32, dtype=torch.int64, device=oob_tn.device) << torch.arange(
+        32, device=oob_tn.device))
+    words = (pad.view(t, w, 32) * weights).sum(dim=2)
+    words = torch.where(words >= 2 ** 31, words - 2 ** 32, words)
+    return words.to(torch.int32).contiguous()
+
+
+class Context:
+    """One librfxprox context (device, stream, resident forest index)."""
+
+    def __init__(self, device: int = 0):
+        self._L = load()
+        h = C.c_void_p()
+        rc = self._L.rfxp_ctx_create(device, C.byref(h))
+        if rc != 0:
+            buf = C.create_string_buffer(512)
+            self._L.rfxp_last_error(None, buf, 512)
+            raise RfxpError(rc, buf.value.decode())
+        self.h = h
+        self.device = device
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._L.rfxp_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != 0:
+            buf = C.create_string_buffer(1024)
+            self._L.rfxp_last_error(self.h, buf, 1024)
+            raise RfxpError(rc, buf.value.decode())
+
+    def set_stream(self, stream_handle: int | None):
+        self._check(self._L.rfxp_ctx_set_stream(self.h, stream_handle))
+
+    def use_torch_stream(self):
+        import torch
+
+        self.set_stream(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def sync(self):
+        self._check(self._L.rfxp_sync(self.h))
+
+    def set_timing(self, on: bool):
+        self._check(self._L.rfxp_set_timing(self.h, int(on)))
+
+    def kernel_time(self, name: str):
+        ms, n = C.c_double(), C.c_int64()
+        self._check(self._L.rfxp_kernel_time(self.h, name.encode(), C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
+    def reset_timing(self):
+        self._check(self._L.rfxp_reset_timing(self.h))
+
+    def set_forest(self, leaf, oob_words, n: int, t: int, nleaf: int, layout: str = "tree",
+                   nout=None):
+        """leaf: int32 device tensor, (T, N) for layout 'tree' or (N, T) for
+        'sample'; oob_words: int32 device tensor (T, ceil(N/32))."""
+        import torch
+
+        assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
+        assert oob_words.dtype == torch.int32 and oob_words.is_cuda and oob_words.is_contiguous()
+        if layout == "tree":
+            si, st = 1, n
+        elif layout == "sample":
+            si, st = t, 1
+        else:
+            raise ValueError(layout)
+        nptr = None
+        if nout is not None:
+            assert nout.dtype == torch.int32 and nout.is_cuda
+            nptr = nout.data_ptr()
+        self._check(self._L.rfxp_set_forest(self.h, leaf.data_ptr(), si, st, oob_words.data_ptr(),
+                                            oob_words.shape[1], n, t, nleaf, nptr))
+        self.n = n
+        self.t = t
+
+    def upper(self, fmt: int, out, r0: int = 0, r1: int | None = None, scale: float = 1.0,
+              zp: float = 0.0):
+        r1 = self.n if r1 is None else r1
+        need = upper_nbytes(fmt, self.n, r0, r1)
+        have = out.numel() * out.element_size()
+        if have < need:
+            raise ValueError(f"output buffer has {have} bytes, rows need {need}")
+        self._check(self._L.rfxp_upper(self.h, fmt, scale, zp, r0, r1, out.data_ptr()))
+        return out
+
+    def nout(self):
+        import torch
+
+        out = torch.empty(self.n, dtype=torch.int32, device=f"cuda:{self.device}")
+        self._check(self._L.rfxp_get_nout(self.h, out.data_ptr()))
+        return out

@@ -1,0 +1,242 @@
+"""GPU parity of the batched upper-triangle path (rfxp_set_forest + rfxp_upper)
+against the CPU oracle, which is itself pinned to the compiled reference
+(tests/test_oracle.py).  Bar: bit-exact for every format (counts, codes,
+and the float formats, whose values are the same IEEE operations)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import rfxprox as R
+
+pytestmark = pytest.mark.gpu
+
+
+def make_forest(seed, n, t, nleaf, p_oob=0.368, p_invalid=0.0):
+    rng = np.random.default_rng(seed)
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int64).astype(np.int32)
+    if p_invalid > 0:
+        bad = rng.random((t, n)) < p_invalid
+        leaf[bad] = rng.choice(np.array([-1, nleaf, nleaf + 7, -5], dtype=np.int32), size=int(bad.sum()))
+    oob = (rng.random((t, n)) < p_oob).astype(np.uint8)
+    return leaf, oob
+
+
+def upload(ctx, leaf, oob, nleaf, layout="tree", nout=None):
+    import torch
+
+    t, n = leaf.shape
+    dev = torch.device("cuda:0")
+    lt = torch.from_numpy(np.ascontiguousarray(leaf if layout == "tree" else leaf.T)).to(dev)
+    ow = R.pack_oob_bits(torch.from_numpy(oob).to(dev))
+    nt = None if nout is None else torch.from_numpy(np.ascontiguousarray(nout, dtype=np.int32)).to(dev)
+    ctx.set_forest(lt, ow, n, t, nleaf, layout=layout, nout=nt)
+    return lt, ow, nt
+
+
+def gpu_rows(ctx, fmt, r0, r1, scale=1.0, zp=0.0, fill=0xA5, offset=0):
+    """Runs rfxp_upper into a buffer pre-filled with `fill` and returns the
+    bytes (as the oracle's dtype) plus the untouched guard bytes."""
+    import torch
+
+    nb = R.upper_nbytes(fmt, ctx.n, r0, r1)
+    buf = torch.full((nb + 64 + offset,), fill, dtype=torch.uint8, device="cuda:0")
+    view = buf[offset:offset + nb]
+    ctx.upper(fmt, view, r0, r1, scale=scale, zp=zp)
+    torch.cuda.synchronize()
+    host = buf.cpu().numpy()
+    out = host[offset:offset + nb]
+    guard = np.concatenate([host[:offset], host[offset + nb:]])
+    return out.view(O.FMT_DTYPE[fmt]), guard
+
+
+def check_equal(got, want, what):
+    if not np.array_equal(got, want):
+        bad = np.nonzero(got != want)[0]
+        raise AssertionError(f"{what}: {len(bad)} mismatches, first at {bad[:5]}: "
+                             f"got {got[bad[:5]]} want {want[bad[:5]]}")
+
+
+@pytest.mark.parametrize("n,t,nleaf", [(1, 1, 1), (2, 3, 2), (37, 5, 3), (300, 64, 17),
+                                       (2000, 100, 64), (4099, 257, 300)])
+def test_counts_u16_match_oracle(gpu_ctx, n, t, nleaf):
+    leaf, oob = make_forest(n * 31 + t, n, t, nleaf)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    got, guard = gpu_rows(gpu_ctx, O.FMT_U16, 0, n)
+    want = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    check_equal(got, want, f"U16 N={n} T={t}")
+    assert (guard == 0xA5).all(), "write outside the output range"
+    del keep
+
+
+FMT_CASES = [
+    (O.FMT_F32, 1.0, 0.0),
+    (O.FMT_F16, 1.0, 0.0),
+    (O.FMT_U16, 1.0, 0.0),
+    (O.FMT_NF4, 1.0, 0.0),
+    (O.FMT_U8, 1.0 / 255.0, -0.0),       # data-derived rule for min 0, max 1
+    (O.FMT_U8, 1.0 / 4000.0, 3.0),       # codes depend on the column: exact path
+    (O.FMT_U8, 1.0 / 60.0, 0.5),
+    (O.FMT_I8, 1.0 / 127.0, 0.0),        # reference default int8 rule
+    (O.FMT_I8, 1.0 / 2000.0, -100.0),
+]
+
+
+@pytest.mark.parametrize("fmt,scale,zp", FMT_CASES)
+def test_formats_match_oracle(gpu_ctx, fmt, scale, zp):
+    n, t, nleaf = 1531, 120, 23
+    leaf, oob = make_forest(7, n, t, nleaf, p_invalid=0.02)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    got, guard = gpu_rows(gpu_ctx, fmt, 0, n, scale=np.float32(scale), zp=np.float32(zp))
+    want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(scale), zp=np.float32(zp))
+    check_equal(got, want, f"fmt {fmt} scale {scale} zp {zp}")
+    assert (guard == 0xA5).all()
+    del keep
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_U8, O.FMT_NF4, O.FMT_F32, O.FMT_F16])
+@pytest.mark.parametrize("r0,r1,offset", [(0, 1, 0), (3, 4, 1), (5, 400, 3), (101, 150, 0),
+                                          (999, 1000, 2), (0, 1000, 5)])
+def test_row_ranges(gpu_ctx, fmt, r0, r1, offset):
+    n, t, nleaf = 1000, 50, 9
+    leaf, oob = make_forest(11, n, t, nleaf)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    esz = {O.FMT_F32: 4, O.FMT_F16: 2}.get(fmt, 1)
+    got, guard = gpu_rows(gpu_ctx, fmt, r0, r1, scale=np.float32(1 / 255.0), offset=offset * esz)
+    want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(1 / 255.0), r0=r0, r1=r1)
+    if fmt == O.FMT_NF4:
+        # boundary nibbles outside the range keep the buffer's fill value
+        e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
+        want = want.copy()
+        if e0 & 1:
+            want[0] = (want[0] & 0xF0) | (0xA5 & 0x0F)
+        if e1 & 1:
+            want[-1] = (want[-1] & 0x0F) | (0xA5 & 0xF0)
+    check_equal(got, want, f"fmt {fmt} rows {r0}:{r1}")
+    assert (guard == 0xA5).all()
+    del keep
+
+
+def test_sample_major_layout_and_given_nout(gpu_ctx):
+    n, t, nleaf = 777, 33, 5
+    leaf, oob = make_forest(5, n, t, nleaf, p_invalid=0.05)
+    nout = np.random.default_rng(3).integers(0, 4, size=n).astype(np.int32)  # includes zeros
+    keep = upload(gpu_ctx, leaf, oob, nleaf, layout="sample", nout=nout)
+    got, _ = gpu_rows(gpu_ctx, O.FMT_F32, 0, n)
+    want = O.upper_rows(leaf, oob, nleaf, O.FMT_F32, nout_arr=nout)
+    check_equal(got.view(np.uint32), want.view(np.uint32), "sample-major f32 with given nout")
+    del keep
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_U16, O.FMT_U8, O.FMT_F32, O.FMT_NF4])
+def test_counts_beyond_255_use_wide_counters(gpu_ctx, fmt):
+    # one leaf and T=700: every pair co-occurs, U ~ Bin(700, 0.5) > 255
+    n, t, nleaf = 300, 700, 1
+    leaf, oob = make_forest(9, n, t, nleaf, p_oob=0.5)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    want_u = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    assert want_u.max() > 255
+    got, _ = gpu_rows(gpu_ctx, fmt, 0, n, scale=np.float32(1 / 255.0))
+    want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(1 / 255.0))
+    check_equal(got, want, f"wide counters fmt {fmt}")
+    del keep
+
+
+def test_all_oob_and_all_inbag_trees(gpu_ctx):
+    n, t, nleaf = 500, 40, 4
+    leaf, oob = make_forest(13, n, t, nleaf)
+    oob[:10] = 1   # all OOB: no pairs
+    oob[10:20] = 0  # all in-bag: no pairs
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    got, _ = gpu_rows(gpu_ctx, O.FMT_U16, 0, n)
+    check_equal(got, O.upper_rows(leaf, oob, nleaf, O.FMT_U16), "degenerate trees")
+    del keep
+
+
+def test_deterministic(gpu_ctx):
+    n, t, nleaf = 3000, 200, 50
+    leaf, oob = make_forest(17, n, t, nleaf)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    a, _ = gpu_rows(gpu_ctx, O.FMT_U8, 0, n, scale=np.float32(1 / 255.0))
+    b, _ = gpu_rows(gpu_ctx, O.FMT_U8, 0, n, scale=np.float32(1 / 255.0))
+    assert np.array_equal(a, b)
+    del keep
+
+
+def test_rejects_bad_arguments(gpu_ctx):
+    import torch
+
+    n, t, nleaf = 100, 4, 3
+    leaf, oob = make_forest(1, n, t, nleaf)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    out = torch.empty(R.upper_nbytes(O.FMT_U8, n), dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(R.RfxpError):
+        gpu_ctx.upper(O.FMT_U8, out, 0, n, scale=0.0)
+    raw = gpu_ctx._L.rfxp_upper
+    with pytest.raises(R.RfxpError):
+        gpu_ctx._check(raw(gpu_ctx.h, O.FMT_U8, 1.0, 0.0, 5, 3, out.data_ptr()))
+    with pytest.raises(R.RfxpError):
+        gpu_ctx._check(raw(gpu_ctx.h, 9, 1.0, 0.0, 0, n, out.data_ptr()))
+    with pytest.raises(R.RfxpError):
+        gpu_ctx._check(raw(gpu_ctx.h, O.FMT_U8, 1.0, float("nan"), 0, n, out.data_ptr()))
+    host = np.zeros(16, dtype=np.uint8)
+    with pytest.raises(R.RfxpError):
+        gpu_ctx._check(gpu_ctx._L.rfxp_upper(gpu_ctx.h, O.FMT_U8, 1.0, 0.0, 0, 1, host.ctypes.data))
+    del keep
+
+
+def test_c1_forest_matches_reference_digests(gpu_ctx):
+    """BASELINE config 1 leaf matrix (CART forest, N=2000, T=100): the GPU
+    triangle hashes to the digests of the reference's own cpu_proximity +
+    cpu_finishprox output (tests/golden/make_golden.py)."""
+    import hashlib
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "c1_forest.npz"))
+    lab = g["label"].astype(np.int32)
+    oob = (g["nin"] == 0).astype(np.uint8)
+    nleaf = int(g["nleaf"])
+    n = lab.shape[1]
+    keep = upload(gpu_ctx, lab, oob, nleaf, nout=g["nout"])
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    u16, _ = gpu_rows(gpu_ctx, O.FMT_U16, 0, n)
+    assert sha(u16) == str(g["sha_u16"])
+    p32, _ = gpu_rows(gpu_ctx, O.FMT_F32, 0, n)
+    assert sha(p32) == str(g["sha_p32"])
+    u8, _ = gpu_rows(gpu_ctx, O.FMT_U8, 0, n, scale=np.float32(1) / np.float32(255))
+    assert sha(u8) == str(g["sha_u8"])
+    del keep
+
+
+def test_c3_shape_sampled_rows(gpu_ctx):
+    """Full north-star shape (N=100k, T=500, 2048 uniform leaves, uint8):
+    rows spread over the triangle equal the oracle's; all codes are in the
+    range the normalisation allows."""
+    import torch
+
+    n, t, nleaf = 100_000, 500, 2048
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(20261204)
+    leaf = torch.randint(0, nleaf, (t, n), generator=g, device="cuda:0", dtype=torch.int32)
+    oob = torch.rand((t, n), generator=g, device="cuda:0") < 0.368
+    words = R.pack_oob_bits(oob)
+    gpu_ctx.set_forest(leaf, words, n, t, nleaf)
+    scale = float(np.float32(1) / np.float32(255))
+    out = torch.empty(R.upper_nbytes(O.FMT_U8, n), dtype=torch.uint8, device="cuda:0")
+    gpu_ctx.upper(O.FMT_U8, out, 0, n, scale=scale, zp=0.0)
+    torch.cuda.synchronize()
+    leaf_np = leaf.cpu().numpy()
+    oob_np = oob.to(torch.uint8).cpu().numpy()
+    idx = O.RowIndex(leaf_np, oob_np, nleaf)
+    for r0 in (0, 1, 777, 31_313, 50_000, 77_777, 99_990):
+        r1 = min(n, r0 + 10)
+        want = idx.rows(O.FMT_U8, r0, r1, scale, 0.0)
+        e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
+        got = out[e0:e1].cpu().numpy()
+        check_equal(got, want, f"C3 rows {r0}:{r1}")
+    # diagonal entries are code(1.0): the reference quantizer truncates
+    # 1/fl(1/255) = 254.99998 to 254
+    dcode = O.q_u8(1.0, scale, 0.0)
+    assert dcode == 254
+    diag = torch.tensor([O.tri_idx(n, i, i) for i in range(0, n, 997)], device="cuda:0")
+    assert bool((out[diag] == dcode).all())
+    idx.close()

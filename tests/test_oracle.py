@@ -1,0 +1,302 @@
+"""Pins the CPU oracle (oracle/rfx_oracle.c) before it is trusted as the
+checker of the HIP path:
+  * against golden fixtures written by the reference's own CPU code
+    (tests/golden/make_golden.py, oracle/_ref),
+  * against the compiled reference directly when oracle/_ref is built here,
+  * against brute force and closed forms for what the reference leaves open
+    (quantizers, top-K ordering, low rank)."""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def replay(nodestatus, nodextr, nin, casewise):
+    t, n = nodextr.shape
+    prox = np.zeros((n, n), order="F")
+    for k in range(t):
+        O.cpu_proximity(nodestatus[k].astype(np.int32), nodextr[k].astype(np.int32),
+                        nin[k].astype(np.int32), nodestatus.shape[1], prox, casewise)
+    return prox
+
+
+# ---- reference fixtures -------------------------------------------------------
+
+@pytest.mark.parametrize("cw", [0, 1])
+def test_cpu_proximity_and_finishprox_match_reference_fixture(cw):
+    g = np.load(os.path.join(GOLD, "cpu_prox_small.npz"))
+    prox = replay(g["nodestatus"], g["nodextr"], g["nin"], cw)
+    assert np.array_equal(prox, g[f"prox_cw{cw}"])
+    sym = O.finishprox(g["nout"], prox)
+    assert np.array_equal(sym, g[f"proxsym_cw{cw}"])
+
+
+def test_rfgap_matches_reference_fixture():
+    g = np.load(os.path.join(GOLD, "rfgap_small.npz"))
+    got = O.rfgap(g["nin"].astype(np.int32), g["nodextr"].astype(np.int32))
+    assert np.array_equal(got, g["prox"])
+
+
+def test_c1_forest_triangle_matches_reference_digests():
+    """BASELINE config 1 (N=2000, T=100 CART forest): the oracle's packed
+    counts, (float)P and uint8 codes hash to the reference's."""
+    g = np.load(os.path.join(GOLD, "c1_forest.npz"))
+    lab = g["label"].astype(np.int32)
+    oob = (g["nin"] == 0).astype(np.uint8)
+    nleaf = int(g["nleaf"])
+    U = O.upper_counts_scatter(lab, oob, nleaf)
+    assert sha(U) == str(g["sha_u16"])
+    assert np.array_equal(U[g["samp_idx"]], g["samp_u"])
+    p32 = O.upper_rows(lab, oob, nleaf, O.FMT_F32)
+    assert sha(p32) == str(g["sha_p32"])
+    u8 = O.upper_rows(lab, oob, nleaf, O.FMT_U8, scale=np.float32(1) / np.float32(255))
+    assert sha(u8) == str(g["sha_u8"])
+    assert int((U == 0).sum()) - lab.shape[1] == int(g["zero_pairs"])
+
+
+def test_terminal_leaf_adapter_matches_fixture_labels():
+    g = np.load(os.path.join(GOLD, "c1_forest.npz"))
+    ns, node, nn = g["nodestatus"].astype(np.int32), g["node"].astype(np.int32), g["nnodes"]
+    for k in range(0, node.shape[0], 17):
+        lab = O.terminal_leaf(ns[k, :nn[k]], node[k])
+        assert np.array_equal(lab, g["label"][k].astype(np.int32))
+
+
+@pytest.mark.skipif(O.ref() is None, reason="compiled reference (oracle/_ref) not built here")
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_oracle_equals_compiled_reference_random_trees(seed):
+    R = O.ref()
+    rng = np.random.default_rng(seed)
+    n, t, nnode = 211, 25, 19
+    for cw in (0, 1):
+        R.ref_set_config(cw, 0, 2)
+        pr = np.zeros((n, n), order="F")
+        po = np.zeros((n, n), order="F")
+        nout = np.zeros(n, np.int32)
+        for _ in range(t):
+            ns = np.where(rng.random(nnode) < 0.75, -1, rng.integers(1, 3, nnode)).astype(np.int32)
+            nx = rng.integers(-2, nnode + 2, n).astype(np.int32)
+            nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+            nout += nin == 0
+            R.ref_cpu_proximity(ns, nx, nin, n, nnode, pr.reshape(-1, order="F"))
+            O.cpu_proximity(ns, nx, nin, nnode, po, cw)
+        assert np.array_equal(pr, po)
+        ps = np.zeros((n, n), order="F")
+        R.ref_cpu_finishprox(n, nout, pr.reshape(-1, order="F"), ps.reshape(-1, order="F"))
+        assert np.array_equal(ps, O.finishprox(nout, po))
+
+
+@pytest.mark.skipif(O.ref() is None, reason="compiled reference (oracle/_ref) not built here")
+def test_triangle_formats_equal_reference_finishprox():
+    """Every triangle format derives from the reference's (float)P: the float
+    formats equal it, the integer codes equal numpy's independent
+    evaluation of the quantizer formula on it."""
+    R = O.ref()
+    rng = np.random.default_rng(7)
+    n, t, nleaf = 173, 60, 6
+    leaf = rng.integers(-1, nleaf + 1, (t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    oob[:, 5] = 0  # sample 5 never OOB (nout = 0 is left raw)
+    R.ref_set_config(0, 0, 2)
+    pr = np.zeros((n, n), order="F")
+    for k in range(t):
+        ns = -np.ones(nleaf, np.int32)
+        R.ref_cpu_proximity(ns, leaf[k], (1 - oob[k]).astype(np.int32), n, nleaf, pr.reshape(-1, order="F"))
+    nout = O.nout(oob)
+    ps = np.zeros((n, n), order="F")
+    R.ref_cpu_finishprox(n, nout, pr.reshape(-1, order="F"), ps.reshape(-1, order="F"))
+    iu = np.triu_indices(n)
+    P32 = ps[iu].astype(np.float32)
+    assert np.array_equal(O.upper_rows(leaf, oob, nleaf, O.FMT_F32), P32)
+    assert np.array_equal(O.upper_rows(leaf, oob, nleaf, O.FMT_F16), P32.astype(np.float16).view(np.uint16))
+    for scale, zp in ((np.float32(1 / 255.0), np.float32(0)), (np.float32(0.003), np.float32(2.5))):
+        want = np.clip(P32 / scale + zp, np.float32(0), np.float32(255)).astype(np.uint8)
+        assert np.array_equal(O.upper_rows(leaf, oob, nleaf, O.FMT_U8, scale=scale, zp=zp), want)
+        want8 = np.clip(P32 / scale + zp, np.float32(-128), np.float32(127)).astype(np.int8)
+        assert np.array_equal(O.upper_rows(leaf, oob, nleaf, O.FMT_I8, scale=scale, zp=zp), want8)
+
+
+# ---- brute force and invariants ----------------------------------------------
+
+def brute_counts(leaf, oob, nleaf):
+    t, n = leaf.shape
+    valid = (leaf >= 0) & (leaf < nleaf)
+    U = np.zeros((n, n), dtype=np.int64)
+    for k in range(t):
+        same = (leaf[k][:, None] == leaf[k][None, :]) & valid[k][:, None] & valid[k][None, :]
+        xor = oob[k][:, None] != oob[k][None, :]
+        U += same & xor
+    return U[np.triu_indices(n)]
+
+
+@pytest.mark.parametrize("n,t,nleaf,pinv", [(1, 3, 2, 0.0), (7, 9, 2, 0.2), (64, 30, 5, 0.1),
+                                            (130, 17, 1, 0.0)])
+def test_counts_equal_brute_force(n, t, nleaf, pinv):
+    rng = np.random.default_rng(n + t)
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    leaf[rng.random((t, n)) < pinv] = -1
+    oob = (rng.random((t, n)) < 0.37).astype(np.uint8)
+    want = brute_counts(leaf, oob, nleaf)
+    assert np.array_equal(O.upper_counts_scatter(leaf, oob, nleaf), want)
+    assert np.array_equal(O.upper_rows(leaf, oob, nleaf, O.FMT_U16), want)
+
+
+def test_count_invariants():
+    rng = np.random.default_rng(3)
+    n, t, nleaf = 300, 80, 7
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.37).astype(np.uint8)
+    U = O.upper_rows(leaf, oob, nleaf, O.FMT_U16).astype(np.int64)
+    iu = np.triu_indices(n)
+    assert (U[iu[0] == iu[1]] == 0).all()
+    assert U.max() <= t
+    # row sums of the full symmetric matrix: sum_j U_ij = sum_t |opposite bucket of i|
+    full = np.zeros((n, n), np.int64)
+    full[iu] = U
+    full = full + full.T
+    want = np.zeros(n, np.int64)
+    for k in range(t):
+        for i in range(n):
+            want[i] += np.sum((leaf[k] == leaf[k][i]) & (oob[k] != oob[k][i]))
+    assert np.array_equal(full.sum(axis=1), want)
+
+
+def test_row_ranges_tile_the_triangle():
+    rng = np.random.default_rng(4)
+    n, t, nleaf = 97, 20, 4
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.37).astype(np.uint8)
+    full = O.upper_rows(leaf, oob, nleaf, O.FMT_F32)
+    parts = [O.upper_rows(leaf, oob, nleaf, O.FMT_F32, r0=a, r1=b)
+             for a, b in ((0, 10), (10, 11), (11, 60), (60, 97))]
+    assert np.array_equal(np.concatenate(parts), full)
+
+
+def test_p_special_cases():
+    # equal nout: 0.5 * (a + a) == a exactly, so P = (U/2) * (1/n)
+    for u in (1, 2, 7, 500):
+        for nn in (1, 3, 184, 499):
+            assert O.p_value(u, nn, nn) == (u / 2.0) * (1.0 / nn)
+    # nout == 0 rows are not scaled (src/rf_finishprox.cpp:48)
+    assert O.p_value(4, 0, 0) == 2.0
+    assert O.p_value(0, 5, 9) == 0.0
+
+
+# ---- quantizers ---------------------------------------------------------------
+
+def test_f16_conversion_matches_numpy_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-8, 6, 20000),
+        np.array([0.0, -0.0, 1.0, 65504.0, 65520.0, 70000.0, 5.96e-8, 2.98e-8, 1e-9, np.inf, -np.inf],
+                 dtype=np.float32),
+        # exact ties between two halves
+        (np.arange(1, 2000, dtype=np.float32) * np.float32(2.0 ** -11) + np.float32(2.0 ** -12)),
+    ]).astype(np.float32)
+    got = np.array([O.f32_to_f16(v) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, vals.astype(np.float16).view(np.uint16))
+
+
+def np_roundf(x):
+    x = np.asarray(x, dtype=np.float64)
+    return np.sign(x) * np.floor(np.abs(x) + 0.5)
+
+
+def test_integer_quantizers_match_independent_numpy_evaluation():
+    rng = np.random.default_rng(1)
+    v = np.concatenate([rng.random(5000), rng.random(2000) * 3, np.linspace(0, 1, 1021),
+                        -rng.random(500)]).astype(np.float32)
+    for scale, zp in ((np.float32(1) / np.float32(255), np.float32(0)),
+                      (np.float32(1) / np.float32(127), np.float32(0)),
+                      (np.float32(0.0037), np.float32(-3.25))):
+        r = v / scale + zp
+        want_u8 = np.clip(r, np.float32(0), np.float32(255)).astype(np.uint8)
+        want_i8 = np.clip(r, np.float32(-128), np.float32(127)).astype(np.int8)
+        assert np.array_equal(np.array([O.q_u8(x, scale, zp) for x in v], np.uint8), want_u8)
+        assert np.array_equal(np.array([O.q_i8(x, scale, zp) for x in v], np.int8), want_i8)
+    x7 = (v * np.float32(7.0)).astype(np.float32)
+    want_nf4 = np.where(v >= 0, np.minimum(7, np_roundf(x7)),
+                        np.maximum(8, np_roundf((np.float32(8.0) - x7).astype(np.float32))))
+    assert np.array_equal(np.array([O.q_nf4(x) for x in v]), want_nf4.astype(np.uint8))
+    # round-half-away-from-zero at the nibble boundaries
+    assert O.q_nf4(np.float32(0.5) / np.float32(7.0)) in (0, 1)
+    assert O.q_nf4(1.0) == 7 and O.q_nf4(0.0) == 0 and O.q_nf4(-1.0) == 15
+
+
+def test_u8_scale_rule_matches_reference_minmax_formula():
+    s, z = O.u8_scale_from_minmax(0.0, 1.0)
+    assert s == np.float32(1) / np.float32(255) and z == 0.0
+    s, z = O.u8_scale_from_minmax(0.25, 0.75)
+    assert s == (np.float32(0.75) - np.float32(0.25)) / np.float32(255)
+    assert z == np.float32(-np.float32(0.25) / np.float32(s))
+
+
+# ---- top-K ----------------------------------------------------------------------
+
+def brute_topk(ref_leaf, qleaf, K, exclude=None):
+    t, n = ref_leaf.shape
+    out_i, out_c = [], []
+    for q in range(qleaf.shape[0]):
+        cnt = (ref_leaf == qleaf[q][:, None]).sum(axis=0)
+        order = np.lexsort((np.arange(n), -cnt))
+        if exclude is not None:
+            order = order[order != exclude[q]]
+        out_i.append(order[:K])
+        out_c.append(cnt[order[:K]])
+    return np.array(out_i), np.array(out_c)
+
+
+def test_topk_all_trees_matches_brute_force_with_ties():
+    rng = np.random.default_rng(2)
+    n, t, q, nleaf, K = 400, 30, 25, 3, 20   # few leaves: many ties
+    ref = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    ql = rng.integers(0, nleaf, (q, t)).astype(np.int32)
+    idx, cnt = O.topk_all(ref, ql, K)
+    bi, bc = brute_topk(ref, ql, K)
+    assert np.array_equal(idx, bi) and np.array_equal(cnt, bc)
+    ex = rng.integers(0, n, q).astype(np.int32)
+    idx, cnt = O.topk_all(ref, ql, K, exclude=ex)
+    bi, bc = brute_topk(ref, ql, K, exclude=ex)
+    assert np.array_equal(idx, bi) and np.array_equal(cnt, bc)
+
+
+def test_topk_oob_semantics():
+    rng = np.random.default_rng(5)
+    n, t, nleaf, K = 150, 40, 4, 10
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.37).astype(np.uint8)
+    for q in (0, 17, 149):
+        idx, cnt, sc = O.topk_oob(leaf, oob, q, K)
+        trees = np.nonzero(oob[:, q])[0]
+        c = (leaf[trees] == leaf[trees, q][:, None]).sum(axis=0)
+        c[q] = 0
+        order = np.lexsort((np.arange(n), -c))
+        order = order[c[order] > 0][:K]
+        assert np.array_equal(idx, order) and np.array_equal(cnt, c[order])
+        assert np.array_equal(sc, c[order].astype(np.float32) * (np.float32(1) / np.float32(len(trees))))
+
+
+# ---- low rank -------------------------------------------------------------------
+
+def test_lowrank_pv_equals_dense_one_hot_product():
+    rng = np.random.default_rng(6)
+    n, t, nleaf, r = 300, 20, 9, 5
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    leaf[0, :4] = -1
+    V = rng.standard_normal((n, r))
+    A = np.zeros((n, t * nleaf))
+    for k in range(t):
+        ok = leaf[k] >= 0
+        A[np.nonzero(ok)[0], k * nleaf + leaf[k][ok]] = 1.0
+    want = (A @ (A.T @ V)) / t
+    got = O.lowrank_pv(leaf, nleaf, V)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
