@@ -147,7 +147,9 @@ def main():
     wall = time.perf_counter() - wall0
     ms_step = ev0.elapsed_time(ev1) / args.steps
     tri_ms, tri_n = ctx.kernel_time("tri")
-    pack_ms = sum(ctx.kernel_time(k)[0] for k in ("bucket", "records", "nout", "rr_init"))
+    pack_names = ("rr_init", "pack_hist", "rec_transpose", "pack_scatter", "nout", "nout_final")
+    pack_each = {k: ctx.kernel_time(k)[0] / args.steps for k in pack_names}
+    pack_ms = sum(pack_each.values()) * args.steps
     tri_avg = tri_ms / max(tri_n, 1)
     pairs = n * (n - 1) // 2
     value = pairs * t / (ms_step / 1e3)
@@ -171,7 +173,8 @@ def main():
         "config": {"workload": cfg["workload"], "N": n, "T": t, "leaves_per_tree": cfg["nleaf"],
                    "output_bytes": nbytes, "format": "u8", "scale": scale, "zp": zp},
         "output_GBps": nbytes / (ms_step / 1e3) / 1e9,
-        "kernels_ms": {"tri_avg": tri_avg, "pack_per_step": pack_ms / args.steps},
+        "kernels_ms": {"tri_avg": tri_avg, "pack_per_step": pack_ms / args.steps,
+                       **{f"{k}_per_step": v for k, v in pack_each.items()}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None},
         "wall_s": wall,

@@ -1,0 +1,62 @@
+// Device-resident forest index shared by the proximity kernels.
+//
+// Built once per forest by rfxp_set_forest (rfxp_pack.hip) from the N x T
+// leaf matrix and OOB bitmask, then read by the triangle, top-K and
+// low-rank kernels.  Layout in HBM:
+//   mem  [T][N]   uint32  sample ids + 1 grouped, per tree, by bucket
+//                         b = 2*leaf + oob (buckets hold the samples of one
+//                         leaf with one OOB bit, in no particular order); the
+//                         +1 keeps 0 free as "no member" for masked loads;
+//                         in buckets of 255 or more members bit 31 marks the
+//                         last member
+//   off  [T][2L+1] int32  per-tree bucket offsets into mem[t]
+//   roff [N][ldr] uint32  for sample i and tree t, the byte offset in mem
+//                         (4*(t*N + start)) of the bucket of i's leaf with the
+//                         other OOB bit -- exactly the samples that pair with
+//                         i in tree t (src/rf_proximity.cpp:179-230)
+//   rlen [N][ldr] uint8   that bucket's length, 255 meaning "255 or more,
+//                         read up to the bit-31 mark"; 0 when i has no valid
+//                         leaf in t.  Rows are ldr = T rounded up to 16 long
+//                         (padding trees have empty records),
+//                         and both arrays have REC_PAD entries of slack
+//                         (whole-group record loads).
+//   nout [N] int32, rinv [N] double (nout > 0 ? 1/nout : 1), and the min and
+//   max of rinv as IEEE bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rfxp_internal.hpp"
+
+namespace rfxp {
+
+constexpr uint32_t MEM_LAST = 0x80000000u;
+constexpr uint32_t MEM_ID = 0x7fffffffu;
+constexpr uint32_t REC_LONG = 255u;
+constexpr int64_t MAX_FOREST_N = 0x7ffffffe;
+constexpr int REC_PAD = 64;
+constexpr int MEM_PAD = 64;                   // readable slack after mem
+
+struct LeafView {
+    const int32_t* leaf;
+    int64_t si, st;
+    const uint32_t* oob;
+    int64_t old;
+    int64_t N;
+    int32_t T;
+    int32_t L;
+};
+
+// Bucket id of sample i in tree t, -1 when its label is not a valid leaf.
+__device__ __forceinline__ int32_t bucket_of(const LeafView& v, int64_t i, int32_t t) {
+    int32_t l = v.leaf[i * v.si + (int64_t)t * v.st];
+    if (l < 0 || l >= v.L) return -1;
+    uint32_t w = v.oob[(int64_t)t * v.old + (i >> 5)];
+    return 2 * l + (int32_t)((w >> (i & 31)) & 1u);
+}
+
+// Builds mem/off/rec/nout/rinv/rr on ctx->stream (rfxp_pack.hip).
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in);
+
+}  // namespace rfxp

@@ -57,9 +57,15 @@ struct rfxp_ctx {
     int32_t T = 0;
     int32_t L = 0;
     DevBuf<int32_t> bkt_off;   // T x (2L+1): bucket b = 2*leaf + oob
-    DevBuf<int32_t> bkt_mem;   // T x N: sample ids grouped by bucket
-    DevBuf<uint32_t> bkt_cnt;  // T x 2L scratch for the global-memory bucketing path
-    DevBuf<uint2> rec;         // N x T: (start, length) of the opposite-OOB bucket
+    DevBuf<uint32_t> bkt_mem;  // T x N (+ padding): sample ids grouped by bucket
+    int64_t ldr = 0;           // record row stride: T rounded up to 16
+    DevBuf<uint32_t> roff;     // N x ldr (+pad): offset of the opposite-OOB bucket of (i, t)
+    DevBuf<uint8_t> rlen;      // N x ldr (+pad): its length (255 = long)
+    DevBuf<uint32_t> roffT;    // T x N: the same, tree-major (packing)
+    DevBuf<uint8_t> rlenT;
+    DevBuf<uint32_t> scratch;  // packing scratch (large leaf counts)
+    DevBuf<uint32_t> scratch2; // per-sample OOB counts
+    DevBuf<uint16_t> key16;    // T x ceil8(N) bucket ids (packing pass B)
     DevBuf<int32_t> nout;      // N
     DevBuf<double> rinv;       // N: nout > 0 ? 1/nout : 1
     DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits

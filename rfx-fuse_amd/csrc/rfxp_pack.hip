@@ -1,0 +1,419 @@
+// Forest index construction (see rfxp_forest.hpp for the layout).
+//
+// k_pack_hist (one workgroup per tree): bucket histogram, offsets, and the
+// sample-major records.  k_pack_scatter (one workgroup per tree and window
+// of ~16k members): member lists built in LDS and written out coalesced --
+// scattering 4-byte ids straight to HBM costs a partial-line write each.
+// Trees are mapped to workgroups so that related work lands on one XCD:
+// 16 consecutive trees per XCD in the first kernel (they complete the same
+// record lines in L2), all windows of a tree in the second (they re-read
+// the tree's keys from L2).
+//
+// k_nout_part / k_nout_final: nout_i = sum over trees of OOB bits
+// (src/rf_bootstrap.cpp:67-70), its reciprocal, and the reciprocal's range.
+#include <algorithm>
+
+#include "rfxp_device.hpp"
+#include "rfxp_forest.hpp"
+
+namespace rfxp {
+
+constexpr int PACK_THREADS = 1024;
+constexpr int PACK_KR = 8;  // keys per thread per round
+
+// Exclusive scan of cnt[0..nb) (one workgroup) into off0[0..nb] and the
+// global offsets table; cnt becomes the running cursor.
+template <class P>
+__device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t* goff) {
+    const int tid = threadIdx.x;
+    const int32_t chunk = (nb + PACK_THREADS - 1) / PACK_THREADS;
+    const int32_t b0 = tid * chunk;
+    const int32_t b1 = min(nb, b0 + chunk);
+    uint32_t s = 0;
+    for (int32_t b = b0; b < b1; ++b) s += cnt[b];
+    part[tid] = s;
+    __syncthreads();
+    for (int d = 1; d < PACK_THREADS; d <<= 1) {
+        uint32_t v = tid >= d ? part[tid - d] : 0u;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    uint32_t run = part[tid] - s;
+    for (int32_t b = b0; b < b1; ++b) {
+        uint32_t c = cnt[b];
+        cnt[b] = run;
+        off0[b] = run;
+        goff[b] = (int32_t)run;
+        run += c;
+    }
+    if (tid == PACK_THREADS - 1) {
+        off0[nb] = part[tid];
+        goff[nb] = (int32_t)part[tid];
+    }
+    __syncthreads();
+}
+
+// Pass A, one 1024-thread workgroup per tree: bucket histogram (LDS when
+// 2L+1 counters fit, else the zeroed global scratch `gscr`), exclusive scan
+// into the global offsets, the tree's bucket ids as uint16 (`key16`, rows
+// of ldk entries, pads 0xffff; written only when 2L < 0xffff, else NULL),
+// then the records of every sample.  Keys are held in registers, PACK_KR per
+// thread per round, all loads of a round issued before the first atomic.
+template <bool LDS_PATH>
+__global__ __launch_bounds__(PACK_THREADS) void k_pack_hist(LeafView v, int32_t* goff_all, uint32_t* roffT,
+                                                           uint8_t* rlenT, uint32_t* gscr, uint16_t* key16,
+                                                           int64_t ldk) {
+    extern __shared__ uint32_t sh[];
+    __shared__ uint32_t part[PACK_THREADS];
+    const uint32_t bid = blockIdx.x;
+    const int32_t t = (int32_t)((((bid >> 3) >> 4) << 3) + (bid & 7)) * 16 + (int32_t)((bid >> 3) & 15);
+    if (t >= v.T) return;
+    const int32_t nb = 2 * v.L;
+    uint32_t* cnt;
+    if constexpr (LDS_PATH) cnt = sh;
+    else cnt = gscr + (int64_t)t * 2 * (nb + 1);
+    uint32_t* off0 = cnt + (nb + 1);
+    if constexpr (LDS_PATH) {
+        for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) cnt[b] = 0u;
+        __syncthreads();
+    }
+    const int64_t N = v.N;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    uint16_t* kt = key16 ? key16 + (int64_t)t * ldk : nullptr;
+    for (int64_t base = 0; base < N; base += round) {
+        int32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < N ? bucket_of(v, i, t) : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            if (key[k] >= 0) atomicAdd(&cnt[key[k]], 1u);
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            if (kt && i < ldk) kt[i] = key[k] >= 0 ? (uint16_t)key[k] : (uint16_t)0xffffu;
+        }
+    }
+    __syncthreads();
+    int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    if constexpr (LDS_PATH) {
+        scan_offsets(cnt, off0, nb, part, goff);
+    } else {
+        __threadfence_block();
+        scan_offsets((volatile uint32_t*)cnt, (volatile uint32_t*)off0, nb, part, goff);
+        __threadfence_block();
+    }
+    auto rd = [&](int32_t k) -> uint32_t {
+        if constexpr (LDS_PATH) return off0[k];
+        else return ((const volatile uint32_t*)off0)[k];
+    };
+    // Records, tree-major (coalesced); k_rec_transpose makes them sample-major.
+    uint32_t* ro = roffT + (int64_t)t * N;
+    uint8_t* rl = rlenT + (int64_t)t * N;
+    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    for (int64_t base = 0; base < N; base += round) {
+        int32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < N ? bucket_of(v, i, t) : -2;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            const int32_t b = key[k];
+            if (b == -2) continue;
+            uint32_t o = 0u, len = 0u;
+            if (b >= 0) {
+                const int32_t ob = b ^ 1;
+                const uint32_t s = rd(ob);
+                o = (tbase + s) * 4u;
+                len = min(rd(ob + 1) - s, REC_LONG);
+            }
+            ro[i] = o;
+            rl[i] = (uint8_t)len;
+        }
+    }
+}
+
+// [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint8_t* rlenT, int64_t N,
+                                                      int32_t T, int64_t ldr, uint32_t* roff, uint8_t* rlen) {
+    __shared__ uint32_t to[64][65];
+    __shared__ uint8_t tl[64][68];
+    const int64_t i0 = (int64_t)blockIdx.x * 64;
+    const int32_t t0 = blockIdx.y * 64;
+    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+        const int r = k >> 6, c = k & 63;  // r: tree, c: sample
+        const int64_t i = i0 + c;
+        const int32_t t = t0 + r;
+        uint32_t o = 0u;
+        uint8_t l = 0;
+        if (i < N && t < T) {
+            o = roffT[(int64_t)t * N + i];
+            l = rlenT[(int64_t)t * N + i];
+        }
+        to[r][c] = o;
+        tl[r][c] = l;
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+        const int r = k >> 6, c = k & 63;  // r: sample, c: tree
+        const int64_t i = i0 + r;
+        const int32_t t = t0 + c;
+        // padding trees T..ldr-1 get empty records
+        if (i < N && t < ldr) {
+            roff[i * ldr + t] = t < T ? to[c][r] : 0u;
+            rlen[i * ldr + t] = t < T ? tl[c][r] : (uint8_t)0;
+        }
+    }
+}
+
+// Pass B: workgroup (tree t, window w) owns the buckets whose offsets start
+// in [w*PACK_WIN, (w+1)*PACK_WIN) (bucket pairs kept together).  It reads
+// the tree's bucket ids again -- from key16, eight per 16-byte load, when
+// pass A wrote it, else from the leaves -- places its members in an LDS
+// copy of its slice of mem[t] through LDS cursors, and writes the slice
+// with coalesced stores.  Members beyond the LDS slice (a window grown by
+// one very large bucket) are written directly.
+constexpr int PACK_WIN = 8192;   // members per window (LDS slice)
+constexpr int PACK_CUR = 4096;   // buckets per window with LDS cursors
+
+__device__ __forceinline__ int32_t first_bucket_at(const int32_t* off, int32_t nb, int64_t pos) {
+    // smallest even b in [0, nb] with off[b] >= pos (nb when none)
+    int32_t lo = 0, hi = nb / 2;  // search over pair index
+    while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if ((int64_t)off[2 * mid] >= pos) hi = mid;
+        else lo = mid + 1;
+    }
+    return 2 * lo;
+}
+
+__global__ __launch_bounds__(PACK_THREADS) void k_pack_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem,
+                                                              uint32_t* gcur_all, int32_t nwin,
+                                                              const uint16_t* key16, int64_t ldk) {
+    extern __shared__ uint32_t sh[];
+    __shared__ int32_t s_b0, s_b1;
+    // (tree, window) -> workgroup: the windows of a tree are consecutive
+    // in dispatch order on one XCD
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid & 7, slot = bid >> 3;
+    const int64_t lin = (int64_t)xcd * (gridDim.x >> 3) + slot;
+    const int32_t t = (int32_t)(lin / nwin);
+    const int32_t w = (int32_t)(lin % nwin);
+    if (t >= v.T) return;
+    const int32_t nb = 2 * v.L;
+    const int32_t* off = goff_all + (int64_t)t * (nb + 1);
+    if (threadIdx.x == 0) {
+        s_b0 = first_bucket_at(off, nb, (int64_t)w * PACK_WIN);
+        s_b1 = first_bucket_at(off, nb, (int64_t)(w + 1) * PACK_WIN);
+    }
+    __syncthreads();
+    const int32_t b0 = s_b0, b1 = s_b1;
+    if (b0 >= b1) return;
+    const uint32_t base_pos = (uint32_t)off[b0];
+    const uint32_t end_pos = (uint32_t)off[b1];
+    if (end_pos == base_pos) return;
+    const int32_t nbk = b1 - b0;
+    const bool lds_cur = nbk <= PACK_CUR;
+    uint32_t* stage = sh;                 // PACK_WIN words
+    uint32_t* cur = sh + PACK_WIN;        // PACK_CUR words (relative cursors)
+    uint32_t* gcur = gcur_all + (int64_t)t * (nb + 1);
+    if (lds_cur) {
+        for (int32_t k = threadIdx.x; k < nbk; k += PACK_THREADS) cur[k] = (uint32_t)off[b0 + k] - base_pos;
+    } else {
+        for (int32_t k = threadIdx.x; k < nbk; k += PACK_THREADS) gcur[b0 + k] = (uint32_t)off[b0 + k] - base_pos;
+        __threadfence();
+    }
+    __syncthreads();
+    const int64_t N = v.N;
+    uint32_t* memt = mem + (int64_t)t * N;
+    auto place = [&](int64_t i, int32_t b) {
+        if (b < b0 || b >= b1) return;
+        const uint32_t rel = lds_cur ? atomicAdd(&cur[b - b0], 1u) : atomicAdd(&gcur[b], 1u);
+        const uint32_t bstart = (uint32_t)off[b] - base_pos;
+        const uint32_t end = (uint32_t)off[b + 1] - base_pos;
+        const uint32_t m = (uint32_t)(i + 1) | (rel + 1 == end && end - bstart >= REC_LONG ? MEM_LAST : 0u);
+        if (rel < (uint32_t)PACK_WIN) stage[rel] = m;
+        else memt[base_pos + rel] = m;
+    };
+    if (key16) {
+        // eight ids per thread per 16-byte load, two loads in flight
+        const uint4* k4 = (const uint4*)(key16 + (int64_t)t * ldk);
+        const int64_t n8 = ldk / 8;
+        for (int64_t q0 = threadIdx.x; q0 < n8; q0 += 2 * PACK_THREADS) {
+            const int64_t q1 = q0 + PACK_THREADS;
+            const uint4 x0 = k4[q0];
+            const uint4 x1 = q1 < n8 ? k4[q1] : make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
+            const uint32_t wv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int64_t i = 8 * (k < 4 ? q0 : q1) + 2 * (k & 3);
+                const uint32_t lo16 = wv[k] & 0xffffu, hi16 = wv[k] >> 16;
+                if (lo16 != 0xffffu) place(i, (int32_t)lo16);
+                if (hi16 != 0xffffu) place(i + 1, (int32_t)hi16);
+            }
+        }
+    } else {
+        const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+        for (int64_t base = 0; base < N; base += round) {
+            int32_t key[PACK_KR];
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                key[k] = i < N ? bucket_of(v, i, t) : -1;
+            }
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) place(base + (int64_t)k * PACK_THREADS + threadIdx.x, key[k]);
+        }
+    }
+    __syncthreads();
+    const uint32_t nst = min(end_pos - base_pos, (uint32_t)PACK_WIN);
+    for (uint32_t k = threadIdx.x; k < nst; k += PACK_THREADS) memt[base_pos + k] = stage[k];
+}
+
+__global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t val) {
+    int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; k < n; k += stride) p[k] = val;
+}
+
+// Partial OOB counts: grid (ceil(N/256), G), block g sums trees
+// [g*T/G, (g+1)*T/G) for 256 samples.
+__global__ __launch_bounds__(256) void k_nout_part(LeafView v, uint32_t* acc) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= v.N) return;
+    const int32_t G = gridDim.y;
+    const int32_t t0 = (int32_t)((int64_t)v.T * blockIdx.y / G);
+    const int32_t t1 = (int32_t)((int64_t)v.T * (blockIdx.y + 1) / G);
+    const uint32_t* w = v.oob + (i >> 5);
+    const uint32_t sh = (uint32_t)(i & 31);
+    uint32_t s = 0;
+    int32_t t = t0;
+    for (; t + 8 <= t1; t += 8) {
+        uint32_t x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = w[(int64_t)(t + k) * v.old];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += (x[k] >> sh) & 1u;
+    }
+    for (; t < t1; ++t) s += (w[(int64_t)t * v.old] >> sh) & 1u;
+    atomicAdd(&acc[i], s);
+}
+
+__global__ __launch_bounds__(256) void k_nout_final(int64_t N, const int32_t* nout_in, const uint32_t* acc,
+                                                   int32_t* nout, double* rinv, unsigned long long* rr) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    double r = 1.0;
+    bool ok = i < N;
+    if (ok) {
+        const int32_t n = nout_in ? nout_in[i] : (int32_t)acc[i];
+        nout[i] = n;
+        r = nout_recip(n);
+        rinv[i] = r;
+    }
+    // block-level min/max, then one atomic pair per block
+    __shared__ unsigned long long smin[256], smax[256];
+    const unsigned long long bits = (unsigned long long)__double_as_longlong(r);
+    smin[threadIdx.x] = ok ? bits : 0x7ff0000000000000ull;
+    smax[threadIdx.x] = ok ? bits : 0ull;
+    __syncthreads();
+    for (int d = 128; d > 0; d >>= 1) {
+        if (threadIdx.x < d) {
+            smin[threadIdx.x] = min(smin[threadIdx.x], smin[threadIdx.x + d]);
+            smax[threadIdx.x] = max(smax[threadIdx.x], smax[threadIdx.x + d]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        atomicMin(&rr[0], smin[0]);
+        atomicMax(&rr[1], smax[0]);
+    }
+}
+
+__global__ void k_rr_init(unsigned long long* rr) {
+    rr[0] = 0x7ff0000000000000ull;
+    rr[1] = 0ull;
+}
+
+static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
+    hipStream_t s = ctx->stream;
+    const int64_t N = v.N;
+    const int32_t T = v.T;
+    const int32_t nb = 2 * v.L;
+    {
+        LaunchTimer tm(ctx, "rr_init");
+        hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, ctx->rrange.p);
+    }
+    if (int rc = check_launch(ctx, "k_rr_init")) return rc;
+    if (N == 0) return RFXP_OK;
+    // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
+    const unsigned grid = (unsigned)(cdiv(T, 128) * 128);
+    const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
+    const bool lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= ctx->max_lds;
+    const int64_t nscr = (int64_t)T * 2 * (nb + 1);
+    RFXP_HIP(ctx, ctx->scratch.ensure((size_t)nscr));
+    // compact bucket ids for the second pass when they fit 16 bits
+    uint16_t* k16 = nullptr;
+    const int64_t ldk = cdiv(N, 8) * 8;
+    if (nb < 0xffff) {
+        RFXP_HIP(ctx, ctx->key16.ensure((size_t)T * ldk));
+        k16 = ctx->key16.p;
+    }
+    if (lds_path) {
+        if (lds_bytes > 32768)
+            RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_hist<true>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
+        LaunchTimer tm(ctx, "pack_hist");
+        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, ctx->bkt_off.p,
+                           ctx->roffT.p, ctx->rlenT.p, (uint32_t*)nullptr, k16, ldk);
+    } else {
+        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(nscr, 256), 65536)), dim3(256), 0, s,
+                           ctx->scratch.p, nscr, 0u);
+        LaunchTimer tm(ctx, "pack_hist");
+        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, ctx->bkt_off.p,
+                           ctx->roffT.p, ctx->rlenT.p, ctx->scratch.p, k16, ldk);
+    }
+    if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
+    {
+        LaunchTimer tm(ctx, "rec_transpose");
+        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s,
+                           ctx->roffT.p, ctx->rlenT.p, N, T, ctx->ldr, ctx->roff.p, ctx->rlen.p);
+    }
+    if (int rc = check_launch(ctx, "k_rec_transpose")) return rc;
+    {
+        // windows of PACK_WIN members, plus one for the slack a window can
+        // gain from keeping bucket pairs whole
+        const int32_t nwin = (int32_t)cdiv(N, PACK_WIN) + 1;
+        const int64_t nwg = cdiv((int64_t)T * nwin, 8) * 8;
+        const size_t lds2 = (size_t)(PACK_WIN + PACK_CUR) * 4;
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds2));
+        LaunchTimer tm(ctx, "pack_scatter");
+        hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, ctx->bkt_off.p,
+                           ctx->bkt_mem.p, ctx->scratch.p, nwin, (const uint16_t*)k16, ldk);
+    }
+    if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
+    if (!nout_in) {
+        RFXP_HIP(ctx, ctx->scratch2.ensure((size_t)N));
+        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(N, 256), 65536)), dim3(256), 0, s,
+                           ctx->scratch2.p, N, 0u);
+        const unsigned G = (unsigned)std::min<int32_t>(T, 16);
+        LaunchTimer tm(ctx, "nout");
+        hipLaunchKernelGGL(k_nout_part, dim3((unsigned)cdiv(N, 256), G), dim3(256), 0, s, v, ctx->scratch2.p);
+    }
+    if (int rc = check_launch(ctx, "k_nout_part")) return rc;
+    {
+        LaunchTimer tm(ctx, "nout_final");
+        hipLaunchKernelGGL(k_nout_final, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, s, N, nout_in,
+                           nout_in ? (const uint32_t*)nullptr : ctx->scratch2.p, ctx->nout.p, ctx->rinv.p,
+                           ctx->rrange.p);
+    }
+    return check_launch(ctx, "k_nout_final");
+}
+
+}  // namespace rfxp

@@ -7,18 +7,13 @@
 // cuda/rf_proximity_upper_triangle.cu:229-237 does gives, for i < j,
 //     U_ij = #{t : leaf_i(t) == leaf_j(t) valid, oob_i(t) != oob_j(t)}.
 //
-// Data layout in HBM (built by rfxp_set_forest):
-//   bkt_off [T][2L+1]  int32  per-tree offsets of bucket b = 2*leaf + oob
-//   bkt_mem [T][N]     int32  sample ids grouped by bucket
-//   rec     [N][T]     uint2  for sample i and tree t: (offset, length) of
-//                             the bucket holding i's leaf with the other
-//                             OOB bit -- exactly the j that pair with i
-//   nout [N] int32, rinv [N] double (1/nout or 1)
+// The forest index it reads (mem, rec, nout, rinv) is described in
+// rfxp_forest.hpp.
 //
 // Triangle kernel: one workgroup per (row i, column segment [lo, hi)) item.
 // It zeroes a byte counter per column in LDS, walks row i's T records,
 // gathers the member ids of each opposite bucket (one wave-wide coalesced
-// load per bucket, eight buckets in flight per wave) and bumps the LDS
+// load per bucket, sixteen buckets in flight per wave) and bumps the LDS
 // counter of every member j in the segment with j > i.  The epilogue turns
 // the counters into the output format and streams the row segment to HBM
 // with aligned 16-byte non-temporal stores.  Integer formats are
@@ -33,189 +28,26 @@
 #include <vector>
 
 #include "rfxp_device.hpp"
+#include "rfxp_forest.hpp"
 #include "rfxp_internal.hpp"
 
 namespace rfxp {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int PACK_THREADS = 1024;
-constexpr int TRI_THREADS = 512;
+constexpr int TRI_THREADS = 1024;
 constexpr int TRI_WAVES = TRI_THREADS / 64;
-
-struct LeafView {
-    const int32_t* leaf;
-    int64_t si, st;
-    const uint32_t* oob;
-    int64_t old;
-    int64_t N;
-    int32_t T;
-    int32_t L;
-};
-
-// Bucket id of sample i in tree t, -1 when its label is not a valid leaf.
-__device__ __forceinline__ int32_t bucket_of(const LeafView& v, int64_t i, int32_t t) {
-    int32_t l = v.leaf[i * v.si + (int64_t)t * v.st];
-    if (l < 0 || l >= v.L) return -1;
-    uint32_t w = v.oob[(int64_t)t * v.old + (i >> 5)];
-    return 2 * l + (int32_t)((w >> (i & 31)) & 1u);
-}
-
-// Exclusive scan of cnt[0..nb) in place (one workgroup), also written to
-// off[0..nb] with off[nb] = total.  `part` is PACK_THREADS words of scratch.
-template <class CntPtr>
-__device__ void block_exclusive_scan(CntPtr cnt, int32_t nb, uint32_t* part, int32_t* off) {
-    const int tid = threadIdx.x;
-    const int32_t chunk = (nb + PACK_THREADS - 1) / PACK_THREADS;
-    const int32_t b0 = tid * chunk;
-    const int32_t b1 = min(nb, b0 + chunk);
-    uint32_t s = 0;
-    for (int32_t b = b0; b < b1; ++b) s += cnt[b];
-    part[tid] = s;
-    __syncthreads();
-    for (int d = 1; d < PACK_THREADS; d <<= 1) {
-        uint32_t v = tid >= d ? part[tid - d] : 0u;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
-    }
-    uint32_t run = part[tid] - s;  // exclusive prefix of this thread's chunk
-    for (int32_t b = b0; b < b1; ++b) {
-        uint32_t c = cnt[b];
-        cnt[b] = run;
-        off[b] = (int32_t)run;
-        run += c;
-    }
-    if (tid == PACK_THREADS - 1) off[nb] = (int32_t)part[tid];
-    __syncthreads();
-}
-
-// One workgroup per tree: histogram of buckets in LDS, scan, then scatter of
-// the sample ids through LDS cursors.  Used when 2L counters fit in LDS.
-__global__ __launch_bounds__(PACK_THREADS) void k_bucket_lds(LeafView v, int32_t* bkt_off,
-                                                            int32_t* bkt_mem) {
-    extern __shared__ uint32_t sh[];
-    const int32_t t = blockIdx.x;
-    const int32_t nb = 2 * v.L;
-    uint32_t* cnt = sh;
-    uint32_t* part = sh + nb;
-    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) cnt[b] = 0;
-    __syncthreads();
-    for (int64_t i = threadIdx.x; i < v.N; i += PACK_THREADS) {
-        int32_t b = bucket_of(v, i, t);
-        if (b >= 0) atomicAdd(&cnt[b], 1u);
-    }
-    __syncthreads();
-    int32_t* off = bkt_off + (int64_t)t * (nb + 1);
-    block_exclusive_scan(cnt, nb, part, off);
-    int32_t* mem = bkt_mem + (int64_t)t * v.N;
-    for (int64_t i = threadIdx.x; i < v.N; i += PACK_THREADS) {
-        int32_t b = bucket_of(v, i, t);
-        if (b >= 0) {
-            uint32_t pos = atomicAdd(&cnt[b], 1u);
-            mem[pos] = (int32_t)i;
-        }
-    }
-}
-
-// Same with the counters in global memory (large leaf counts).  cnt is a
-// zeroed T x 2L scratch.
-__global__ __launch_bounds__(PACK_THREADS) void k_bucket_global(LeafView v, uint32_t* cnt_all,
-                                                               int32_t* bkt_off, int32_t* bkt_mem) {
-    __shared__ uint32_t part[PACK_THREADS];
-    const int32_t t = blockIdx.x;
-    const int32_t nb = 2 * v.L;
-    uint32_t* cnt = cnt_all + (int64_t)t * nb;
-    for (int64_t i = threadIdx.x; i < v.N; i += PACK_THREADS) {
-        int32_t b = bucket_of(v, i, t);
-        if (b >= 0) atomicAdd(&cnt[b], 1u);
-    }
-    __syncthreads();
-    __threadfence_block();
-    int32_t* off = bkt_off + (int64_t)t * (nb + 1);
-    block_exclusive_scan((volatile uint32_t*)cnt, nb, part, off);
-    __threadfence_block();
-    int32_t* mem = bkt_mem + (int64_t)t * v.N;
-    for (int64_t i = threadIdx.x; i < v.N; i += PACK_THREADS) {
-        int32_t b = bucket_of(v, i, t);
-        if (b >= 0) {
-            uint32_t pos = atomicAdd(&cnt[b], 1u);
-            mem[pos] = (int32_t)i;
-        }
-    }
-}
-
-__global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
-    int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (; k < n; k += stride) p[k] = v;
-}
-
-// rec[i][t] = (offset, length) of the opposite-OOB bucket of i's leaf, via a
-// 64 x 64 LDS tile so both the leaf reads and the rec writes are coalesced.
-__global__ __launch_bounds__(256) void k_records(LeafView v, const int32_t* bkt_off, uint2* rec) {
-    __shared__ uint2 tile[64][65];
-    const int64_t i0 = (int64_t)blockIdx.x * 64;
-    const int32_t t0 = blockIdx.y * 64;
-    const int32_t nb1 = 2 * v.L + 1;
-    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
-        int tl = k >> 6, il = k & 63;
-        int64_t i = i0 + il;
-        int32_t t = t0 + tl;
-        uint2 r = make_uint2(0u, 0u);
-        if (i < v.N && t < v.T) {
-            int32_t b = bucket_of(v, i, t);
-            if (b >= 0) {
-                const int32_t* off = bkt_off + (int64_t)t * nb1;
-                int32_t ob = b ^ 1;
-                int32_t s = off[ob];
-                r = make_uint2((uint32_t)s, (uint32_t)(off[ob + 1] - s));
-            }
-        }
-        tile[tl][il] = r;
-    }
-    __syncthreads();
-    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
-        int il = k >> 6, tl = k & 63;
-        int64_t i = i0 + il;
-        int32_t t = t0 + tl;
-        if (i < v.N && t < v.T) rec[i * v.T + t] = tile[tl][il];
-    }
-}
-
-// nout_i (counted from the OOB bits unless given), its reciprocal, and the
-// min/max reciprocal over all samples (as IEEE bits; positive doubles order
-// like their bit patterns).
-__global__ void k_nout(LeafView v, const int32_t* nout_in, int32_t* nout, double* rinv,
-                       unsigned long long* rr) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= v.N) return;
-    int32_t n = 0;
-    if (nout_in) {
-        n = nout_in[i];
-    } else {
-        for (int32_t t = 0; t < v.T; ++t) n += (int32_t)((v.oob[(int64_t)t * v.old + (i >> 5)] >> (i & 31)) & 1u);
-    }
-    nout[i] = n;
-    double r = nout_recip(n);
-    rinv[i] = r;
-    unsigned long long bits = (unsigned long long)__double_as_longlong(r);
-    atomicMin(&rr[0], bits);
-    atomicMax(&rr[1], bits);
-}
-
-__global__ void k_rr_init(unsigned long long* rr) {
-    rr[0] = 0x7ff0000000000000ull;
-    rr[1] = 0ull;
-}
 
 // ---------------------------------------------------------------------------
 // triangle
 // ---------------------------------------------------------------------------
 
 struct TriArgs {
-    const uint2* rec;
-    const int32_t* mem;
+    const uint32_t* roff;  // [N][T] bucket element offsets (+ REC_PAD)
+    const uint8_t* rlen;   // [N][T] bucket lengths (+ REC_PAD)
+    const uint32_t* mem;
+    uint32_t mem_bytes;  // readable bytes of mem (buffer-load range)
+    int64_t ldr;         // record row stride (T rounded up to 16)
     const double* rinv;
     const unsigned long long* rr;
     const int2* items;
@@ -288,64 +120,127 @@ __device__ __forceinline__ uint32_t code_word(uint32_t w, uint32_t lut_lo, uint3
 
 // Hit phase: every member j of row i's opposite buckets with lo <= j < hi
 // bumps its counter.  Counter c of column j sits at unit (j - lo + shift)
-// of the LDS array; BITS is 8 or 16.  Returns true when an 8-bit counter
-// wrapped (only checked when T can exceed 255).
-template <int BITS, bool CHECK>
-__device__ __forceinline__ bool hit_phase(const TriArgs& a, uint32_t* cnt, int64_t i, int64_t lo,
-                                          int32_t width, int32_t shift) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const uint2* recrow = a.rec + i * a.T;
-    bool wrapped = false;
-    auto hit = [&](int32_t j) {
-        uint32_t d = (uint32_t)(j - (int32_t)lo);
-        if (d < (uint32_t)width) {
-            uint32_t c = d + (uint32_t)shift;
-            if constexpr (BITS == 8) {
-                uint32_t sh = (c & 3u) * 8u;
-                if constexpr (CHECK) {
-                    uint32_t old = atomicAdd(&cnt[c >> 2], 1u << sh);
-                    wrapped |= ((old >> sh) & 0xffu) == 0xffu;
-                } else {
-                    atomicAdd(&cnt[c >> 2], 1u << sh);
+// of the LDS array (cap units); BITS is 8 or 16.  Returns the number of
+// counter increments this wave made (uniform; counted only when COUNT).
+//
+// Each wave owns a contiguous range of trees and walks it in groups of 16.
+// A group's records come in through scalar loads (16 offsets, 16 lengths);
+// its 16 bucket loads are buffer loads with the bucket offset in an SGPR and
+// one lane offset, lanes past the bucket end getting an out-of-range offset
+// (they read 0, which no stored id equals).  The loads of group q + 1 are
+// issued before group q is counted.  Counting is branch-free: lanes without
+// a hit add into a private dummy word past the counters.
+struct Group {
+    uint32_t m[16];
+    bool has_long;  // some bucket of the group has more than 64 members
+};
+
+__device__ __forceinline__ void load_group(__amdgpu_buffer_rsrc_t rs, const uint32_t* __restrict__ ro,
+                                           const uint8_t* __restrict__ rl, bool valid, uint32_t lane,
+                                           Group& G) {
+    // `valid` false issues the same 16 loads with every lane out of range
+    // (no memory access): the count of loads in flight stays static, so the
+    // wait for one group can leave the other outstanding.  Records of the
+    // padding trees (T..ldr-1) have length 0.
+    uint32_t off[16];
+    uint32_t len4[4];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) off[u] = __builtin_amdgcn_readfirstlane(ro[u]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) len4[k] = __builtin_amdgcn_readfirstlane(((const uint32_t*)rl)[k]) & (valid ? ~0u : 0u);
+    // any length byte above 64:  (b + 63) sets bit 7 for 65..192, b sets it for 128..255
+    uint32_t lng = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) lng |= ((len4[k] & 0x7f7f7f7fu) + 0x3f3f3f3fu) | len4[k];
+    G.has_long = (lng & 0x80808080u) != 0u;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const uint32_t len = (len4[u >> 2] >> (8 * (u & 3))) & 0xffu;
+        const uint32_t voff = lane < len ? lane * 4u : 0x7ffffff0u;
+        G.m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, voff, off[u], 0);
+    }
+}
+
+template <int BITS, bool COUNT>
+__device__ __forceinline__ uint32_t count_hits(uint32_t* cnt, uint32_t m, uint32_t base1, uint32_t cap,
+                                               uint32_t dummy) {
+    // m = j + 1 (0 for no member); c = j - lo + shift
+    const uint32_t c = m - base1;
+    const bool h = c < cap;
+    uint32_t addr, val;
+    if constexpr (BITS == 8) {
+        addr = c & ~3u;
+        val = 1u << ((c << 3) & 31u);
+    } else {
+        addr = (c << 1) & ~3u;
+        val = 1u << ((c << 4) & 16u);
+    }
+    atomicAdd((uint32_t*)((char*)cnt + (h ? addr : dummy)), val);
+    if constexpr (COUNT) return (uint32_t)__builtin_popcountll(__ballot(h));
+    else return 0u;
+}
+
+constexpr int TRI_DUMMY_BYTES = 256;  // per-lane dummy words after the counters
+
+template <int BITS, bool COUNT>
+__device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, uint32_t* cnt, int64_t i, int64_t lo,
+                                              uint32_t cap, int32_t shift, uint32_t dummy_base) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t lane4 = lane * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // whole groups of 16 trees per wave, so record rows stay 16-aligned
+    const int32_t ng = (a.T + 15) / 16;
+    const int32_t t_begin = 16 * (int32_t)(((int64_t)ng * wave) / TRI_WAVES);
+    const int32_t t_end = 16 * (int32_t)(((int64_t)ng * (wave + 1)) / TRI_WAVES);
+    const uint32_t* ro = a.roff + i * a.ldr;
+    const uint8_t* rl = a.rlen + i * a.ldr;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.mem, (short)0, (int)a.mem_bytes, 0x00020000);
+    const uint32_t base1 = (uint32_t)lo + 1u - (uint32_t)shift;
+    const uint32_t dummy = dummy_base + lane4;
+    uint32_t hits = 0;
+    // buckets of more than 64 members (rare for per-leaf buckets)
+    auto long_tail = [&](int32_t t0) {
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t len = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
+            if (len <= 64u) continue;
+            const uint32_t off = __builtin_amdgcn_readfirstlane(ro[t0 + u]);
+            if (len == REC_LONG) {
+                // 255 or more members: read on until the bucket's last-member mark
+                bool more = true;
+                for (uint32_t p = 64u; more; p += 64u) {
+                    const uint32_t m = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p * 4u + lane4, off, 0);
+                    const unsigned long long lastm = __ballot((m & MEM_LAST) != 0u);
+                    const uint32_t cut = lastm ? (uint32_t)__builtin_ctzll(lastm) : 64u;
+                    hits += count_hits<BITS, COUNT>(cnt, lane <= cut ? (m & MEM_ID) : 0u, base1, cap, dummy);
+                    more = (lastm == 0ull);
                 }
             } else {
-                atomicAdd(&cnt[c >> 1], 1u << ((c & 1u) * 16u));
+                for (uint32_t p = 64u; p < len; p += 64u) {
+                    const uint32_t voff = p + lane < len ? (p + lane) * 4u : 0x7ffffff0u;
+                    hits += count_hits<BITS, COUNT>(
+                        cnt, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, voff, off, 0), base1, cap, dummy);
+                }
             }
         }
     };
-    // Trees go to waves in groups of 8 (group g = trees 8g..8g+7, wave
-    // g % 8); one record load fetches a wave's next 8 groups.  Records of
-    // trees >= T read as (0, 0), so their buckets are empty.
-    const int32_t ngroup = (a.T + 7) / 8;
-    for (int32_t gb = wave; gb < ngroup; gb += 8 * TRI_WAVES) {
-        const int32_t t = 8 * (gb + TRI_WAVES * (lane >> 3)) + (lane & 7);
-        const uint2 r = t < a.T ? recrow[t] : make_uint2(0u, 0u);
-        for (int32_t q = 0; q < 8; ++q) {
-            const int32_t g = gb + TRI_WAVES * q;
-            if (g >= ngroup) break;
-            int32_t jv[8];
-            uint32_t len[8];
-            const int32_t* base[8];
+    // Two group buffers in ping-pong: one is counted while the other's 16
+    // loads are in flight (no register copies between them).
+    Group A, B;
+    load_group(rs, ro + t_begin, rl + t_begin, t_begin < t_end, lane, A);
+    for (int32_t t0 = t_begin; t0 < t_end; t0 += 32) {
+        load_group(rs, ro + t0 + 16, rl + t0 + 16, t0 + 16 < t_end, lane, B);
+        __builtin_amdgcn_sched_barrier(0);  // issue B's loads before touching A's data
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int kk = 8 * q + u;
-                const uint32_t st = (uint32_t)__builtin_amdgcn_readlane((int)r.x, kk);
-                len[u] = (uint32_t)__builtin_amdgcn_readlane((int)r.y, kk);
-                base[u] = a.mem + (int64_t)(8 * g + u) * a.N + st;
-                jv[u] = (uint32_t)lane < len[u] ? base[u][lane] : -1;
-            }
+        for (int u = 0; u < 16; ++u) hits += count_hits<BITS, COUNT>(cnt, A.m[u], base1, cap, dummy);
+        if (A.has_long) long_tail(t0);
+        load_group(rs, ro + t0 + 32, rl + t0 + 32, t0 + 32 < t_end, lane, A);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) hit(jv[u]);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (len[u] > 64u) {
-                    for (uint32_t p = 64u + lane; p < len[u]; p += 64u) hit(base[u][p]);
-                }
-            }
-        }
+        for (int u = 0; u < 16; ++u) hits += count_hits<BITS, COUNT>(cnt, B.m[u], base1, cap, dummy);
+        if (B.has_long) long_tail(t0 + 16);
     }
-    return wrapped;
+    return hits;
 }
 
 // Exact per-entry epilogue with 16-bit counters (segments whose 8-bit
@@ -361,6 +256,14 @@ __device__ void store_exact16(const TriArgs& a, const uint32_t* cnt, int64_t i, 
         const int64_t e = e0 + d;
         if constexpr (F == U16) {
             ((uint16_t*)a.out)[e] = diag ? 0 : (uint16_t)U;
+        } else if constexpr (F == NF4) {
+            const uint32_t c = code_of<NF4>(diag ? 1.0 : (U == 0 ? 0.0 : pair_p(U, ri, a.rinv[j])), 0.f, 0.f);
+            const int64_t g = e + (a.e_base & 1);
+            const uintptr_t ba = (uintptr_t)a.out + (uintptr_t)(g >> 1);
+            uint32_t* word = (uint32_t*)(ba & ~(uintptr_t)3);
+            const uint32_t sh = (uint32_t)((ba & 3u) * 8u + (uint32_t)(g & 1) * 4u);
+            atomicAnd(word, ~(0xfu << sh));
+            atomicOr(word, c << sh);
         } else {
             double P = diag ? 1.0 : (U == 0 ? 0.0 : pair_p(U, ri, a.rinv[j]));
             if constexpr (F == F32) ((float*)a.out)[e] = (float)P;
@@ -370,19 +273,79 @@ __device__ void store_exact16(const TriArgs& a, const uint32_t* cnt, int64_t i, 
     }
 }
 
+// Per-row table of the integer codes of U = 0..7 (I8, U8, NF4): uc is the
+// number of leading counts whose code does not depend on the column (the
+// code is monotone in r_j, so equal codes at the smallest and largest r_j
+// mean equal codes for every column).  Run by the first wave.
+template <int F>
+__device__ __forceinline__ void row_table(const TriArgs& a, double ri, uint32_t* s_lut, uint32_t* s_uc) {
+    if (threadIdx.x >= 64) return;
+    const int u = threadIdx.x & 7;
+    const double rmin = __longlong_as_double((long long)a.rr[0]);
+    const double rmax = __longlong_as_double((long long)a.rr[1]);
+    const uint32_t c0 = code_of<F>(pair_p(u, ri, rmin), a.scale, a.zp);
+    const uint32_t c1 = code_of<F>(pair_p(u, ri, rmax), a.scale, a.zp);
+    const unsigned long long eq = __ballot(c0 == c1 && threadIdx.x < 8);
+    uint32_t lo4 = 0, hi4 = 0;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const uint32_t cb = (uint32_t)__shfl((int)c0, b, 64);
+        if (b < 4) lo4 |= cb << (8 * b);
+        else hi4 |= cb << (8 * (b - 4));
+    }
+    if (threadIdx.x == 0) {
+        uint32_t uc = 0;
+        while (uc < 8 && ((eq >> uc) & 1ull)) ++uc;
+        *s_uc = uc;
+        s_lut[0] = lo4;
+        s_lut[1] = hi4;
+    }
+}
+
+// Common item prologue / hit phase / wrap check.  Returns true when the
+// 8-bit counters are exact; otherwise the item has been redone (16-bit
+// counters, exact stores) and the caller must return.
+struct ItemGeom {
+    int64_t i, lo;
+    int32_t width, shift, nchunk, nwords;
+    uint32_t dummy;  // byte offset of the per-lane dummy words in LDS
+};
+
+// After the optimistic epilogue, T > 255 items compare the sum of the 8-bit
+// counters with the number of increments: a counter that reached 256
+// wrapped (and carried into its neighbour), which changes the sum.  Such
+// items are recomputed with 16-bit counters and their entries rewritten.
+template <int F>
+__device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, double ri) {
+    if (threadIdx.x == 0) atomicAdd(&a.flags[0], 1);
+    const int32_t half_cap = gm.nwords * 2;  // 16-bit counters that fit
+    for (int32_t d0 = 0; d0 < gm.width; d0 += half_cap) {
+        const int32_t w2 = min(half_cap, gm.width - d0);
+        __syncthreads();
+        for (int32_t w = threadIdx.x; w < (w2 + 1) / 2; w += TRI_THREADS) cnt[w] = 0u;
+        __syncthreads();
+        hit_phase<16, false>(a, cnt, gm.i, gm.lo + d0, (uint32_t)w2, 0, gm.dummy);
+        __syncthreads();
+        store_exact16<F>(a, cnt, gm.i, gm.lo + d0, w2, ri);
+    }
+}
+
 template <int F>
 __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
     extern __shared__ uint32_t cnt[];
     __shared__ uint32_t s_lut[2];
     __shared__ uint32_t s_uc;
-    __shared__ int s_wrapped;
+    __shared__ uint32_t s_hits, s_sum;
     constexpr int esz = FmtInfo<F>::esz;
     constexpr int epc = 16 / esz;  // entries per 16-byte chunk
 
     const int2 it = a.items[blockIdx.x];
-    const int64_t i = it.x;
-    const int64_t lo = it.y;
-    const int32_t width = (int32_t)min((int64_t)a.S, a.N - lo);
+    ItemGeom gm;
+    gm.i = it.x;
+    gm.lo = it.y;
+    gm.width = (int32_t)min((int64_t)a.S, a.N - gm.lo);
+    const int64_t i = gm.i, lo = gm.lo;
+    const int32_t width = gm.width;
     const double ri = a.rinv[i];
 
     // Align counters to the output: chunk c of the LDS array maps to the
@@ -391,64 +354,29 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
     const int32_t shift = (int32_t)(((uintptr_t)dst0 & 15u) / esz);
     char* const dst_al = dst0 - shift * esz;
     const int32_t nchunk = (shift + width + epc - 1) / epc;
-    const int32_t nwords = nchunk * epc / 4;  // 8-bit counters
+    gm.shift = shift;
+    gm.nchunk = nchunk;
+    gm.nwords = nchunk * epc / 4;  // 8-bit counters
+    gm.dummy = (uint32_t)a.S + 64u;
 
-    for (int32_t w = threadIdx.x; w < nwords; w += TRI_THREADS) cnt[w] = 0u;
-    if (threadIdx.x == 0) s_wrapped = 0;
-    if constexpr (F == I8 || F == U8) {
-        // Per-row code table: U < uc give the same code for every column
-        // (the code is monotone in r_j, so equal codes at min and max r_j
-        // mean equal codes everywhere).
-        if (threadIdx.x < 64) {
-            const int u = threadIdx.x & 7;
-            const double rmin = __longlong_as_double((long long)a.rr[0]);
-            const double rmax = __longlong_as_double((long long)a.rr[1]);
-            const uint32_t c0 = code_of<F>(pair_p(u, ri, rmin), a.scale, a.zp);
-            const uint32_t c1 = code_of<F>(pair_p(u, ri, rmax), a.scale, a.zp);
-            const unsigned long long eq = __ballot(c0 == c1 && threadIdx.x < 8);
-            if (threadIdx.x == 0) {
-                uint32_t uc = 0;
-                while (uc < 8 && ((eq >> uc) & 1ull)) ++uc;
-                s_uc = uc;
-            }
-            uint32_t lo4 = 0, hi4 = 0;
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                uint32_t cb = (uint32_t)__shfl((int)c0, b, 64);
-                if (b < 4) lo4 |= cb << (8 * b);
-                else hi4 |= cb << (8 * (b - 4));
-            }
-            if (threadIdx.x == 0) {
-                s_lut[0] = lo4;
-                s_lut[1] = hi4;
-            }
-        }
+    for (int32_t w = threadIdx.x; w < gm.nwords; w += TRI_THREADS) cnt[w] = 0u;
+    if (threadIdx.x == 0) {
+        s_hits = 0u;
+        s_sum = 0u;
     }
+    if constexpr (F == I8 || F == U8) row_table<F>(a, ri, s_lut, &s_uc);
+    __syncthreads();
+    // counters cover units [0, nchunk * units-per-chunk): hits outside the
+    // item's columns but inside that range land in the unstored padding
+    const bool check = a.T > 255;
+    const uint32_t cap = (uint32_t)gm.nwords * 4u;
+    uint32_t nh;
+    if (check) nh = hit_phase<8, true>(a, cnt, i, lo, cap, shift, gm.dummy);
+    else nh = hit_phase<8, false>(a, cnt, i, lo, cap, shift, gm.dummy);
+    if (check && (threadIdx.x & 63) == 0) atomicAdd(&s_hits, nh);
     __syncthreads();
 
-    bool wrapped;
-    if (a.T > 255) wrapped = hit_phase<8, true>(a, cnt, i, lo, width, shift);
-    else wrapped = hit_phase<8, false>(a, cnt, i, lo, width, shift);
-    if (wrapped) s_wrapped = 1;
-    __syncthreads();
-
-    if (s_wrapped) {
-        // Some count reached 256: redo the segment with 16-bit counters in
-        // two halves of the same LDS space.
-        if (threadIdx.x == 0) atomicAdd(&a.flags[0], 1);
-        const int32_t half_cap = nwords * 2;  // 16-bit counters that fit
-        for (int32_t d0 = 0; d0 < width; d0 += half_cap) {
-            const int32_t w2 = min(half_cap, width - d0);
-            __syncthreads();
-            for (int32_t w = threadIdx.x; w < (w2 + 1) / 2; w += TRI_THREADS) cnt[w] = 0u;
-            __syncthreads();
-            hit_phase<16, false>(a, cnt, i, lo + d0, w2, 0);
-            __syncthreads();
-            store_exact16<F>(a, cnt, i, lo + d0, w2, ri);
-        }
-        return;
-    }
-
+    uint32_t bsum = 0;  // sum of the counter bytes this thread read
     const bool has_diag = (lo == i);
     const uint4* c4 = (const uint4*)cnt;
     if constexpr (F == I8 || F == U8) {
@@ -456,6 +384,12 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
         const uint32_t dcode = code_of<F>(1.0, a.scale, a.zp);
         for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS) {
             const uint4 w = c4[ck];
+            if (check) {
+                bsum = __builtin_amdgcn_sad_u8(w.x, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.y, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.z, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.w, 0u, bsum);
+            }
             const int64_t jb = lo + (int64_t)ck * 16 - shift;  // column of byte 0
             uint32_t o[4];
             o[0] = code_word<F>(w.x, lut_lo, lut_hi, uc, ri, a.rinv, jb + 0, a.scale, a.zp);
@@ -487,6 +421,10 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
             } else {
                 cw[0] = cnt[2 * ck];
                 cw[1] = cnt[2 * ck + 1];
+            }
+            if (check) {
+                bsum = __builtin_amdgcn_sad_u8(cw[0], 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(cw[1], 0u, bsum);
             }
             const int64_t jb = lo + (int64_t)ck * epc - shift;
             uint32_t o[4];
@@ -522,6 +460,11 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
             }
         }
     }
+    if (check) {
+        if (bsum) atomicAdd(&s_sum, bsum);
+        __syncthreads();
+        if (s_sum != s_hits) redo_wide<F>(a, cnt, gm, ri);
+    }
 }
 
 // NF4: two entries per byte.  Nibble position g(e) = e - e_base + (e_base & 1)
@@ -532,12 +475,15 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
     extern __shared__ uint32_t cnt[];
     __shared__ uint32_t s_lut[2];
     __shared__ uint32_t s_uc;
-    __shared__ int s_wrapped;
+    __shared__ uint32_t s_hits, s_sum;
 
     const int2 it = a.items[blockIdx.x];
-    const int64_t i = it.x;
-    const int64_t lo = it.y;
-    const int32_t width = (int32_t)min((int64_t)a.S, a.N - lo);
+    ItemGeom gm;
+    gm.i = it.x;
+    gm.lo = it.y;
+    gm.width = (int32_t)min((int64_t)a.S, a.N - gm.lo);
+    const int64_t i = gm.i, lo = gm.lo;
+    const int32_t width = gm.width;
     const double ri = a.rinv[i];
 
     const int64_t g0 = tri_idx(a.N, i, lo) - a.e_base + (a.e_base & 1);  // nibble index
@@ -545,66 +491,30 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
     const int32_t shift = (int32_t)(((uintptr_t)byte0 & 15u) * 2 + (g0 & 1));  // nibbles
     char* const dst_al = byte0 - ((uintptr_t)byte0 & 15u);
     const int32_t nchunk = (shift + width + 31) / 32;  // 32 nibbles per 16 bytes
-    const int32_t nwords = nchunk * 8;
+    gm.shift = shift;
+    gm.nchunk = nchunk;
+    gm.nwords = nchunk * 8;
+    gm.dummy = (uint32_t)a.S + 64u;
 
-    for (int32_t w = threadIdx.x; w < nwords; w += TRI_THREADS) cnt[w] = 0u;
-    if (threadIdx.x == 0) s_wrapped = 0;
-    if (threadIdx.x < 64) {
-        const int u = threadIdx.x & 7;
-        const double rmin = __longlong_as_double((long long)a.rr[0]);
-        const double rmax = __longlong_as_double((long long)a.rr[1]);
-        const uint32_t c0 = code_of<NF4>(pair_p(u, ri, rmin), 0.f, 0.f);
-        const uint32_t c1 = code_of<NF4>(pair_p(u, ri, rmax), 0.f, 0.f);
-        const unsigned long long eq = __ballot(c0 == c1 && threadIdx.x < 8);
-        uint32_t lo4 = 0, hi4 = 0;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            uint32_t cb = (uint32_t)__shfl((int)c0, b, 64);
-            if (b < 4) lo4 |= cb << (8 * b);
-            else hi4 |= cb << (8 * (b - 4));
-        }
-        if (threadIdx.x == 0) {
-            uint32_t uc = 0;
-            while (uc < 8 && ((eq >> uc) & 1ull)) ++uc;
-            s_uc = uc;
-            s_lut[0] = lo4;
-            s_lut[1] = hi4;
-        }
+    for (int32_t w = threadIdx.x; w < gm.nwords; w += TRI_THREADS) cnt[w] = 0u;
+    if (threadIdx.x == 0) {
+        s_hits = 0u;
+        s_sum = 0u;
     }
+    row_table<NF4>(a, ri, s_lut, &s_uc);
     __syncthreads();
-    bool wrapped;
-    if (a.T > 255) wrapped = hit_phase<8, true>(a, cnt, i, lo, width, shift);
-    else wrapped = hit_phase<8, false>(a, cnt, i, lo, width, shift);
-    if (wrapped) s_wrapped = 1;
+    // counters cover units [0, nchunk * units-per-chunk): hits outside the
+    // item's columns but inside that range land in the unstored padding
+    const bool check = a.T > 255;
+    const uint32_t cap = (uint32_t)gm.nwords * 4u;
+    uint32_t nh;
+    if (check) nh = hit_phase<8, true>(a, cnt, i, lo, cap, shift, gm.dummy);
+    else nh = hit_phase<8, false>(a, cnt, i, lo, cap, shift, gm.dummy);
+    if (check && (threadIdx.x & 63) == 0) atomicAdd(&s_hits, nh);
     __syncthreads();
 
+    uint32_t bsum = 0;
     const uint32_t dcode = code_of<NF4>(1.0, 0.f, 0.f);
-    if (s_wrapped) {
-        if (threadIdx.x == 0) atomicAdd(&a.flags[0], 1);
-        const int32_t half_cap = nwords * 2;
-        for (int32_t d0 = 0; d0 < width; d0 += half_cap) {
-            const int32_t w2 = min(half_cap, width - d0);
-            __syncthreads();
-            for (int32_t w = threadIdx.x; w < (w2 + 1) / 2; w += TRI_THREADS) cnt[w] = 0u;
-            __syncthreads();
-            hit_phase<16, false>(a, cnt, i, lo + d0, w2, 0);
-            __syncthreads();
-            for (int32_t d = threadIdx.x; d < w2; d += TRI_THREADS) {
-                const int64_t j = lo + d0 + d;
-                const uint32_t U = (cnt[d >> 1] >> ((d & 1) * 16)) & 0xffffu;
-                const uint32_t c = (j == i) ? dcode : (U == 0 ? code_of<NF4>(0.0, 0.f, 0.f)
-                                                              : code_of<NF4>(pair_p(U, ri, a.rinv[j]), 0.f, 0.f));
-                const int64_t g = g0 + d0 + d;
-                const uintptr_t ba = (uintptr_t)a.out + (uintptr_t)(g >> 1);
-                uint32_t* word = (uint32_t*)(ba & ~(uintptr_t)3);
-                const uint32_t sh = (uint32_t)((ba & 3u) * 8u + (uint32_t)(g & 1) * 4u);
-                atomicAnd(word, ~(0xfu << sh));
-                atomicOr(word, c << sh);
-            }
-        }
-        return;
-    }
-
     const uint32_t lut_lo = s_lut[0], lut_hi = s_lut[1], uc = s_uc;
     const bool has_diag = (lo == i);
     const uint4* c4 = (const uint4*)cnt;
@@ -614,6 +524,10 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
         const uint4 wa = c4[2 * ck], wb = c4[2 * ck + 1];
         cw[0] = wa.x; cw[1] = wa.y; cw[2] = wa.z; cw[3] = wa.w;
         cw[4] = wb.x; cw[5] = wb.y; cw[6] = wb.z; cw[7] = wb.w;
+        if (check) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) bsum = __builtin_amdgcn_sad_u8(cw[q], 0u, bsum);
+        }
         const int64_t jb = lo + (int64_t)ck * 32 - shift;
         uint32_t codes[8];
 #pragma unroll
@@ -653,6 +567,11 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
             }
         }
     }
+    if (check) {
+        if (bsum) atomicAdd(&s_sum, bsum);
+        __syncthreads();
+        if (s_sum != s_hits) redo_wide<NF4>(a, cnt, gm, ri);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -662,7 +581,7 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
 static int tri_segment_cols(rfxp_ctx* ctx, int fmt) {
     // Counter bytes per workgroup; leave room for the static LDS words and
     // for the 16-byte alignment shift.  Two workgroups per CU on gfx950.
-    int budget = std::min(ctx->max_lds, 160 * 1024) / 2 - 1024;
+    int budget = std::min(ctx->max_lds, 160 * 1024) / 2 - 1024 - TRI_DUMMY_BYTES;
     budget = std::max(budget, 4096);
     budget &= ~63;
     if (fmt == NF4) return budget;  // one counter byte per nibble entry
@@ -694,68 +613,37 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
                                const int32_t* nout) {
     if (!ctx) return RFXP_ERR_INVALID;
     ctx->forest_ready = false;
-    if (N < 0 || N > 0x7fffffffLL || T < 1 || T > 65535 || nleaf < 1 || nleaf > (1 << 29))
-        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: need 0 <= N < 2^31, 1 <= T <= 65535, 1 <= nleaf <= 2^29");
+    if (N < 0 || T < 1 || T > 65535 || nleaf < 1 || nleaf > (1 << 29))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: need N >= 0, 1 <= T <= 65535, 1 <= nleaf <= 2^29");
+    if (N > MAX_FOREST_N)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_forest: N above 2^24 - 1 is not supported");
     if (N > 0 && (!leaf || !oob_words))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: leaf / oob_words are NULL");
     if (oob_ld < (N + 31) / 32)
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: oob_ld < ceil(N/32)");
     if (N > 0 && (!is_device_pointer(leaf) || !is_device_pointer(oob_words) || (nout && !is_device_pointer(nout))))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: inputs must be device pointers");
-    if ((int64_t)N * T > 0xffffffffLL)
-        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_forest: N*T must stay below 2^32");
+    if ((int64_t)N * T + MEM_PAD > (1LL << 30) - 1)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_forest: N*T must stay below 2^30");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     ctx->N = N;
     ctx->T = T;
     ctx->L = nleaf;
-    const int32_t nb = 2 * nleaf;
+    const int64_t nb = 2 * (int64_t)nleaf;
+    const size_t n1 = (size_t)std::max<int64_t>(N, 1);
     RFXP_HIP(ctx, ctx->bkt_off.ensure((size_t)T * (nb + 1)));
-    RFXP_HIP(ctx, ctx->bkt_mem.ensure((size_t)T * (size_t)std::max<int64_t>(N, 1)));
-    RFXP_HIP(ctx, ctx->rec.ensure((size_t)std::max<int64_t>(N, 1) * T));
-    RFXP_HIP(ctx, ctx->nout.ensure((size_t)std::max<int64_t>(N, 1)));
-    RFXP_HIP(ctx, ctx->rinv.ensure((size_t)std::max<int64_t>(N, 1)));
+    RFXP_HIP(ctx, ctx->bkt_mem.ensure((size_t)T * n1 + MEM_PAD));
+    ctx->ldr = ((int64_t)T + 15) / 16 * 16;
+    RFXP_HIP(ctx, ctx->roff.ensure(n1 * ctx->ldr + REC_PAD));
+    RFXP_HIP(ctx, ctx->rlen.ensure(n1 * ctx->ldr + REC_PAD));
+    RFXP_HIP(ctx, ctx->roffT.ensure(n1 * T));
+    RFXP_HIP(ctx, ctx->rlenT.ensure(n1 * T));
+    RFXP_HIP(ctx, ctx->nout.ensure(n1));
+    RFXP_HIP(ctx, ctx->rinv.ensure(n1));
     RFXP_HIP(ctx, ctx->rrange.ensure(2));
     RFXP_HIP(ctx, ctx->flags.ensure(16));
     LeafView v{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf};
-    hipStream_t s = ctx->stream;
-    {
-        LaunchTimer tm(ctx, "rr_init");
-        hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, ctx->rrange.p);
-    }
-    if (int rc = check_launch(ctx, "k_rr_init")) return rc;
-    if (N == 0) {
-        ctx->forest_ready = true;
-        return RFXP_OK;
-    }
-    const size_t lds_bytes = (size_t)(nb + PACK_THREADS) * 4;
-    if ((int64_t)lds_bytes <= ctx->max_lds) {
-        if (lds_bytes > 65536)
-            RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_bucket_lds, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              (int)lds_bytes));
-        LaunchTimer tm(ctx, "bucket");
-        hipLaunchKernelGGL(k_bucket_lds, dim3(T), dim3(PACK_THREADS), lds_bytes, s, v, ctx->bkt_off.p, ctx->bkt_mem.p);
-    } else {
-        RFXP_HIP(ctx, ctx->bkt_cnt.ensure((size_t)T * nb));
-        const int64_t n = (int64_t)T * nb;
-        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 65536)), dim3(256), 0, s,
-                           ctx->bkt_cnt.p, n, 0u);
-        LaunchTimer tm(ctx, "bucket");
-        hipLaunchKernelGGL(k_bucket_global, dim3(T), dim3(PACK_THREADS), 0, s, v, ctx->bkt_cnt.p, ctx->bkt_off.p,
-                           ctx->bkt_mem.p);
-    }
-    if (int rc = check_launch(ctx, "k_bucket")) return rc;
-    {
-        LaunchTimer tm(ctx, "records");
-        hipLaunchKernelGGL(k_records, dim3((unsigned)ceil_div(N, 64), (unsigned)ceil_div(T, 64)), dim3(256), 0, s, v,
-                           ctx->bkt_off.p, ctx->rec.p);
-    }
-    if (int rc = check_launch(ctx, "k_records")) return rc;
-    {
-        LaunchTimer tm(ctx, "nout");
-        hipLaunchKernelGGL(k_nout, dim3((unsigned)ceil_div(N, 256)), dim3(256), 0, s, v, nout, ctx->nout.p,
-                           ctx->rinv.p, ctx->rrange.p);
-    }
-    if (int rc = check_launch(ctx, "k_nout")) return rc;
+    if (int rc = pack_forest(ctx, v, nout)) return rc;
     ctx->forest_ready = true;
     return RFXP_OK;
 }
@@ -809,8 +697,11 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
         ctx->items_key[3] = S;
     }
     TriArgs a;
-    a.rec = ctx->rec.p;
+    a.roff = ctx->roff.p;
+    a.rlen = ctx->rlen.p;
+    a.ldr = ctx->ldr;
     a.mem = ctx->bkt_mem.p;
+    a.mem_bytes = (uint32_t)(((uint64_t)ctx->T * (uint64_t)N + MEM_PAD) * 4u);
     a.rinv = ctx->rinv.p;
     a.rr = ctx->rrange.p;
     a.items = ctx->items.p;
@@ -824,7 +715,7 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     a.flags = ctx->flags.p;
     // counters: S units + up to one 16-byte chunk of alignment shift,
     // rounded to whole chunks (NF4: 32 nibbles per chunk)
-    const size_t lds = (size_t)S + 64;
+    const size_t lds = (size_t)S + 64 + TRI_DUMMY_BYTES;
     hipError_t e;
     {
         LaunchTimer tm(ctx, "tri");
