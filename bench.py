@@ -43,7 +43,37 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the bounded CPU-baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB a few times (the reference "
+                         "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
+
+
+def traffic_from_profile(config):
+    """HBM bytes per triangle launch measured with rocprofv3 --pmc FETCH_SIZE
+    and WRITE_SIZE (each scaled by the copy-kernel calibration), read from the
+    committed summary profiles/k_tri_<config>_traffic.md; None when absent."""
+    path = os.path.join(REPO, "profiles", f"k_tri_{config}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=")[1].strip().strip("`"))
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration(mib):
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
 def make_inputs(cfg, n, device):
@@ -110,6 +140,9 @@ def main():
                                    f"--gpus {args.gpus} is not supported (multi-GPU sharding is "
                                    "a design note only)"}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     import torch
 
     import rfxprox as R
@@ -154,8 +187,9 @@ def main():
     pairs = n * (n - 1) // 2
     value = pairs * t / (ms_step / 1e3)
     # algorithmic bytes of one triangle launch: 1 B per output entry written
-    # + 8 B per (sample, tree) bucket record read
-    tri_bytes = nbytes + n * t * 8
+    # + 5 B per (sample, tree) bucket record read (4 B offset, 1 B length)
+    # + 8 B per sample of 1/nout
+    tri_bytes = nbytes + n * t * 5 + n * 8
     achieved = tri_bytes / (tri_avg / 1e3) / 1e9
     rec = {
         "metric": "pair-tree comparisons/sec at N=100k,T=500 (uint8 OOB proximity triangle)",
@@ -176,7 +210,8 @@ def main():
         "kernels_ms": {"tri_avg": tri_avg, "pack_per_step": pack_ms / args.steps,
                        **{f"{k}_per_step": v for k, v in pack_each.items()}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic_from_profile(args.config) if n == cfg["n"] else None},
         "wall_s": wall,
     }
     ctx.set_timing(False)
