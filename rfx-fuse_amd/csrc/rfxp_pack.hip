@@ -61,7 +61,7 @@ __device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t*
 // then the records of every sample.  Keys are held in registers, PACK_KR per
 // thread per round, all loads of a round issued before the first atomic.
 template <bool LDS_PATH>
-__global__ __launch_bounds__(PACK_THREADS) void k_pack_hist(LeafView v, int32_t* goff_all, uint32_t* roffT,
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_hist(LeafView v, int32_t* goff_all, uint32_t* roffT,
                                                            uint8_t* rlenT, uint32_t* gscr, uint16_t* key16,
                                                            int64_t ldk) {
     extern __shared__ uint32_t sh[];
@@ -191,7 +191,7 @@ __device__ __forceinline__ int32_t first_bucket_at(const int32_t* off, int32_t n
     return 2 * lo;
 }
 
-__global__ __launch_bounds__(PACK_THREADS) void k_pack_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem,
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem,
                                                               uint32_t* gcur_all, int32_t nwin,
                                                               const uint16_t* key16, int64_t ldk) {
     extern __shared__ uint32_t sh[];

@@ -331,7 +331,7 @@ __device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, d
 }
 
 template <int F>
-__global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
+__global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri(TriArgs a) {
     extern __shared__ uint32_t cnt[];
     __shared__ uint32_t s_lut[2];
     __shared__ uint32_t s_uc;
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(TRI_THREADS) void k_tri(TriArgs a) {
 // relative to the byte `out`.  Bytes with both nibbles inside the item are
 // stored whole; a byte shared with a neighbouring item (row boundaries) is
 // merged with 32-bit atomics on its own nibble only.
-__global__ __launch_bounds__(TRI_THREADS) void k_tri_nf4(TriArgs a) {
+__global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri_nf4(TriArgs a) {
     extern __shared__ uint32_t cnt[];
     __shared__ uint32_t s_lut[2];
     __shared__ uint32_t s_uc;
