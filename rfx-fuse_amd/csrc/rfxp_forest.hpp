@@ -7,16 +7,19 @@
 //                         b = 2*leaf + oob (buckets hold the samples of one
 //                         leaf with one OOB bit, in no particular order); the
 //                         +1 keeps 0 free as "no member" for masked loads;
-//                         in buckets of 255 or more members bit 31 marks the
-//                         last member
+//                         in buckets of REC_LONG or more members bit 31 marks
+//                         the last member
 //   off  [T][2L+1] int32  per-tree bucket offsets into mem[t]
 //   roff [N][ldr] uint32  for sample i and tree t, the byte offset in mem
 //                         (4*(t*N + start)) of the bucket of i's leaf with the
 //                         other OOB bit -- exactly the samples that pair with
 //                         i in tree t (src/rf_proximity.cpp:179-230)
-//   rlen [N][ldr] uint8   that bucket's length, 255 meaning "255 or more,
-//                         read up to the bit-31 mark"; 0 when i has no valid
-//                         leaf in t.  Rows are ldr = T rounded up to 16 long
+//   rlen [N][ldr] uint16  that bucket's length in bytes, 4*min(len, REC_LONG);
+//                         4*REC_LONG means "REC_LONG or more members, read up
+//                         to the bit-31 mark"; 0 when i has no valid leaf in
+//                         t.  In bytes so that it serves directly as the
+//                         range of a buffer load.  Rows are ldr = T rounded
+//                         up to 16 long
 //                         (padding trees have empty records),
 //                         and both arrays have REC_PAD entries of slack
 //                         (whole-group record loads).
@@ -33,7 +36,7 @@ namespace rfxp {
 
 constexpr uint32_t MEM_LAST = 0x80000000u;
 constexpr uint32_t MEM_ID = 0x7fffffffu;
-constexpr uint32_t REC_LONG = 255u;
+constexpr uint32_t REC_LONG = 16383u;  // 4*REC_LONG fits the uint16 length
 constexpr int64_t MAX_FOREST_N = 0x7ffffffe;
 constexpr int REC_PAD = 64;
 constexpr int MEM_PAD = 64;                   // readable slack after mem

@@ -62,7 +62,7 @@ __device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t*
 // thread per round, all loads of a round issued before the first atomic.
 template <bool LDS_PATH>
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_hist(LeafView v, int32_t* goff_all, uint32_t* roffT,
-                                                           uint8_t* rlenT, uint32_t* gscr, uint16_t* key16,
+                                                           uint16_t* rlenT, uint32_t* gscr, uint16_t* key16,
                                                            int64_t ldk) {
     extern __shared__ uint32_t sh[];
     __shared__ uint32_t part[PACK_THREADS];
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     };
     // Records, tree-major (coalesced); k_rec_transpose makes them sample-major.
     uint32_t* ro = roffT + (int64_t)t * N;
-    uint8_t* rl = rlenT + (int64_t)t * N;
+    uint16_t* rl = rlenT + (int64_t)t * N;
     const uint32_t tbase = (uint32_t)t * (uint32_t)N;
     for (int64_t base = 0; base < N; base += round) {
         int32_t key[PACK_KR];
@@ -129,19 +129,19 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                 const int32_t ob = b ^ 1;
                 const uint32_t s = rd(ob);
                 o = (tbase + s) * 4u;
-                len = min(rd(ob + 1) - s, REC_LONG);
+                len = min(rd(ob + 1) - s, REC_LONG) * 4u;
             }
             ro[i] = o;
-            rl[i] = (uint8_t)len;
+            rl[i] = (uint16_t)len;
         }
     }
 }
 
 // [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
-__global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint8_t* rlenT, int64_t N,
-                                                      int32_t T, int64_t ldr, uint32_t* roff, uint8_t* rlen) {
+__global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint16_t* rlenT, int64_t N,
+                                                      int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen) {
     __shared__ uint32_t to[64][65];
-    __shared__ uint8_t tl[64][68];
+    __shared__ uint16_t tl[64][66];
     const int64_t i0 = (int64_t)blockIdx.x * 64;
     const int32_t t0 = blockIdx.y * 64;
     for (int k = threadIdx.x; k < 64 * 64; k += 256) {
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, co
         const int64_t i = i0 + c;
         const int32_t t = t0 + r;
         uint32_t o = 0u;
-        uint8_t l = 0;
+        uint16_t l = 0;
         if (i < N && t < T) {
             o = roffT[(int64_t)t * N + i];
             l = rlenT[(int64_t)t * N + i];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, co
         // padding trees T..ldr-1 get empty records
         if (i < N && t < ldr) {
             roff[i * ldr + t] = t < T ? to[c][r] : 0u;
-            rlen[i * ldr + t] = t < T ? tl[c][r] : (uint8_t)0;
+            rlen[i * ldr + t] = t < T ? tl[c][r] : (uint16_t)0;
         }
     }
 }

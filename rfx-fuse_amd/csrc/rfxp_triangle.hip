@@ -43,8 +43,8 @@ constexpr int TRI_WAVES = TRI_THREADS / 64;
 // ---------------------------------------------------------------------------
 
 struct TriArgs {
-    const uint32_t* roff;  // [N][T] bucket element offsets (+ REC_PAD)
-    const uint8_t* rlen;   // [N][T] bucket lengths (+ REC_PAD)
+    const uint32_t* roff;  // [N][ldr] bucket byte offsets in mem (+ REC_PAD)
+    const uint16_t* rlen;  // [N][ldr] bucket lengths in bytes (+ REC_PAD)
     const uint32_t* mem;
     uint32_t mem_bytes;  // readable bytes of mem (buffer-load range)
     int64_t ldr;         // record row stride (T rounded up to 16)
@@ -58,7 +58,30 @@ struct TriArgs {
     char* out;          // byte address of entry e_base (NF4: of its byte)
     float scale, zp;
     int32_t* flags;     // [0]: items redone with 16-bit counters
+    int32_t mode;       // TRI_MODE_*
 };
+
+// Counter width / exactness check per launch:
+//   EXACT8  T <= 255: 8-bit counters cannot wrap;
+//   CHECK8  8-bit counters, a byte-sum check after the hit phase, items
+//           whose counters wrapped are redone with 16-bit counters;
+//   WIDE16  every item counted with 16-bit counters (very many trees per
+//           wave, where the check's own dummy bytes could wrap).
+enum { TRI_MODE_EXACT8 = 0, TRI_MODE_CHECK8 = 1, TRI_MODE_WIDE16 = 2 };
+
+// LDS layout of one workgroup (dynamic shared memory, at address 0):
+//   [0, S + 64)                    counters (8-bit, or 16-bit when redoing)
+//   [dummy_off, dummy_off + 4096)  one word per thread: lanes without a hit
+//                                  add into their own word
+//   [dummy_off + 4096, +32)        item scalars (row table, sums)
+constexpr int TRI_DUMMY_BYTES = TRI_THREADS * 4;
+constexpr int TRI_MISC_WORDS = 8;
+enum { MISC_LUT_LO = 0, MISC_LUT_HI = 1, MISC_UC = 2, MISC_SUM = 3, MISC_SLOTS = 4 };
+
+__host__ __device__ constexpr uint32_t tri_dummy_off(int32_t S) { return ((uint32_t)S + 64u + 15u) & ~15u; }
+__host__ __device__ constexpr uint32_t tri_lds_bytes(int32_t S) {
+    return tri_dummy_off(S) + TRI_DUMMY_BYTES + TRI_MISC_WORDS * 4;
+}
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int b) { return (w >> (8 * b)) & 0xffu; }
 
@@ -97,15 +120,15 @@ __device__ __forceinline__ uint32_t float_entry(uint32_t U, double ri, const dou
     else return (uint32_t)f32_to_f16_bits(pf);
 }
 
-// Table-driven byte codes for I8 / U8 / NF4: lut_lo/lut_hi hold the codes
-// of U = 0..7, valid for U < uc.
+// Nonzero when some byte of w is >= uc (or >= 0x80): kuc = (0x80 - uc) * 0x01010101.
+__device__ __forceinline__ uint32_t over_uc(uint32_t w, uint32_t kuc) { return ((w + kuc) | w) & 0x80808080u; }
+
+// Byte codes of the four counts of w for I8 / U8 / NF4, exact path: counts
+// below uc come from the row table, the others from the closed form.
 template <int F>
-__device__ __forceinline__ uint32_t code_word(uint32_t w, uint32_t lut_lo, uint32_t lut_hi, uint32_t uc,
-                                              double ri, const double* rinv, int64_t j0, float scale,
-                                              float zp) {
-    // all four counts < uc  <=>  no byte has its top bit set after adding 0x80 - uc
-    const uint32_t k = (0x80u - uc) * 0x01010101u;
-    if ((((w + k) | w) & 0x80808080u) == 0u) return __builtin_amdgcn_perm(lut_hi, lut_lo, w);
+__device__ __noinline__ uint32_t code_word_exact(uint32_t w, uint32_t lut_lo, uint32_t lut_hi, uint32_t uc,
+                                                 double ri, const double* rinv, int64_t j0, float scale,
+                                                 float zp) {
     uint32_t o = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -121,49 +144,59 @@ __device__ __forceinline__ uint32_t code_word(uint32_t w, uint32_t lut_lo, uint3
 // Hit phase: every member j of row i's opposite buckets with lo <= j < hi
 // bumps its counter.  Counter c of column j sits at unit (j - lo + shift)
 // of the LDS array (cap units); BITS is 8 or 16.  Returns the number of
-// counter increments this wave made (uniform; counted only when COUNT).
+// 64-lane counting steps this wave made (wave-uniform).
 //
 // Each wave owns a contiguous range of trees and walks it in groups of 16.
 // A group's records come in through scalar loads (16 offsets, 16 lengths);
-// its 16 bucket loads are buffer loads with the bucket offset in an SGPR and
-// one lane offset, lanes past the bucket end getting an out-of-range offset
-// (they read 0, which no stored id equals).  The loads of group q + 1 are
-// issued before group q is counted.  Counting is branch-free: lanes without
-// a hit add into a private dummy word past the counters.
+// each bucket load is a buffer load with the bucket offset as its scalar
+// offset and a range (checked on scalar + lane offset) ending at the bucket
+// end, so lanes past the end read 0 (no stored id is 0) with no per-lane
+// masking.  The loads of group q + 1 are issued before group q is counted.
+// Counting is branch-free: a lane without a hit adds into its own dummy
+// word, so every lane of every step lands somewhere countable.
 struct Group {
     uint32_t m[16];
     bool has_long;  // some bucket of the group has more than 64 members
 };
 
-__device__ __forceinline__ void load_group(__amdgpu_buffer_rsrc_t rs, const uint32_t* __restrict__ ro,
-                                           const uint8_t* __restrict__ rl, bool valid, uint32_t lane,
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mem_rsrc(const uint32_t* mem, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)mem, (short)0, (int)nbytes, 0x00020000);
+}
+
+__device__ __forceinline__ void load_group(const uint32_t* mem, const uint32_t* __restrict__ ro,
+                                           const uint16_t* __restrict__ rl, bool valid, uint32_t lane4,
                                            Group& G) {
-    // `valid` false issues the same 16 loads with every lane out of range
-    // (no memory access): the count of loads in flight stays static, so the
-    // wait for one group can leave the other outstanding.  Records of the
-    // padding trees (T..ldr-1) have length 0.
+    // `valid` false issues the same 16 loads with an empty range (no memory
+    // access): the count of loads in flight stays static, so the wait for
+    // one group can leave the other outstanding.
     uint32_t off[16];
-    uint32_t len4[4];
+    uint32_t lw[8];
 #pragma unroll
     for (int u = 0; u < 16; ++u) off[u] = __builtin_amdgcn_readfirstlane(ro[u]);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) len4[k] = __builtin_amdgcn_readfirstlane(((const uint32_t*)rl)[k]) & (valid ? ~0u : 0u);
-    // any length byte above 64:  (b + 63) sets bit 7 for 65..192, b sets it for 128..255
+    for (int k = 0; k < 8; ++k) lw[k] = __builtin_amdgcn_readfirstlane(((const uint32_t*)rl)[k]) & (valid ? ~0u : 0u);
+    // any length above 256 bytes: v + (0x8000 - 257) sets bit 15 for 257..0x7fff, v sets it above
     uint32_t lng = 0u;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) lng |= ((len4[k] & 0x7f7f7f7fu) + 0x3f3f3f3fu) | len4[k];
-    G.has_long = (lng & 0x80808080u) != 0u;
+    for (int k = 0; k < 8; ++k) lng |= ((lw[k] & 0x7fff7fffu) + 0x7eff7effu) | lw[k];
+    G.has_long = (lng & 0x80008000u) != 0u;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-        const uint32_t len = (len4[u >> 2] >> (8 * (u & 3))) & 0xffu;
-        const uint32_t voff = lane < len ? lane * 4u : 0x7ffffff0u;
-        G.m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, voff, off[u], 0);
+        const uint32_t len4 = (lw[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+        G.m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(mem_rsrc(mem, off[u] + len4), lane4, off[u], 0);
     }
 }
 
-template <int BITS, bool COUNT>
-__device__ __forceinline__ uint32_t count_hits(uint32_t* cnt, uint32_t m, uint32_t base1, uint32_t cap,
-                                               uint32_t dummy) {
+// LDS atomic add at a byte address of the workgroup's LDS.  The counters are
+// the dynamic LDS array and the kernels declare no static LDS, so the array
+// starts at LDS address 0 and counter byte offsets are LDS addresses.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+__device__ __forceinline__ void lds_add(uint32_t addr, uint32_t val) {
+    __hip_atomic_fetch_add((lds_u32*)(uintptr_t)addr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int BITS>
+__device__ __forceinline__ void count_hits(uint32_t* cnt, uint32_t m, uint32_t base1, uint32_t cap, uint32_t dummy) {
     // m = j + 1 (0 for no member); c = j - lo + shift
     const uint32_t c = m - base1;
     const bool h = c < cap;
@@ -175,51 +208,49 @@ __device__ __forceinline__ uint32_t count_hits(uint32_t* cnt, uint32_t m, uint32
         addr = (c << 1) & ~3u;
         val = 1u << ((c << 4) & 16u);
     }
-    atomicAdd((uint32_t*)((char*)cnt + (h ? addr : dummy)), val);
-    if constexpr (COUNT) return (uint32_t)__builtin_popcountll(__ballot(h));
-    else return 0u;
+    (void)cnt;
+    lds_add(h ? addr : dummy, val);
 }
 
-constexpr int TRI_DUMMY_BYTES = 256;  // per-lane dummy words after the counters
-
-template <int BITS, bool COUNT>
-__device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, uint32_t* cnt, int64_t i, int64_t lo,
-                                              uint32_t cap, int32_t shift, uint32_t dummy_base) {
+template <int BITS>
+__device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, uint32_t* cnt, int64_t i, int64_t lo, uint32_t cap,
+                                              int32_t shift, uint32_t dummy) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lane4 = lane * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // whole groups of 16 trees per wave, so record rows stay 16-aligned
-    const int32_t ng = (a.T + 15) / 16;
-    const int32_t t_begin = 16 * (int32_t)(((int64_t)ng * wave) / TRI_WAVES);
-    const int32_t t_end = 16 * (int32_t)(((int64_t)ng * (wave + 1)) / TRI_WAVES);
+    const int32_t ng = (a.T + 15) >> 4;
+    const int32_t g0 = (ng * wave) / TRI_WAVES;
+    const int32_t g1 = (ng * (wave + 1)) / TRI_WAVES;
     const uint32_t* ro = a.roff + i * a.ldr;
-    const uint8_t* rl = a.rlen + i * a.ldr;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.mem, (short)0, (int)a.mem_bytes, 0x00020000);
+    const uint16_t* rl = a.rlen + i * a.ldr;
     const uint32_t base1 = (uint32_t)lo + 1u - (uint32_t)shift;
-    const uint32_t dummy = dummy_base + lane4;
-    uint32_t hits = 0;
+    uint32_t steps = 0;
     // buckets of more than 64 members (rare for per-leaf buckets)
     auto long_tail = [&](int32_t t0) {
         for (int u = 0; u < 16; ++u) {
-            const uint32_t len = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
-            if (len <= 64u) continue;
+            const uint32_t len4 = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
+            if (len4 <= 256u) continue;
             const uint32_t off = __builtin_amdgcn_readfirstlane(ro[t0 + u]);
-            if (len == REC_LONG) {
-                // 255 or more members: read on until the bucket's last-member mark
+            if (len4 == 4u * REC_LONG) {
+                // REC_LONG or more members: read on until the last-member mark
+                // (mem has MEM_PAD words of slack after its end)
+                const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, a.mem_bytes);
                 bool more = true;
-                for (uint32_t p = 64u; more; p += 64u) {
-                    const uint32_t m = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p * 4u + lane4, off, 0);
+                for (uint32_t p4 = 256u; more; p4 += 256u) {
+                    const uint32_t m = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0);
                     const unsigned long long lastm = __ballot((m & MEM_LAST) != 0u);
                     const uint32_t cut = lastm ? (uint32_t)__builtin_ctzll(lastm) : 64u;
-                    hits += count_hits<BITS, COUNT>(cnt, lane <= cut ? (m & MEM_ID) : 0u, base1, cap, dummy);
+                    count_hits<BITS>(cnt, lane <= cut ? (m & MEM_ID) : 0u, base1, cap, dummy);
+                    ++steps;
                     more = (lastm == 0ull);
                 }
             } else {
-                for (uint32_t p = 64u; p < len; p += 64u) {
-                    const uint32_t voff = p + lane < len ? (p + lane) * 4u : 0x7ffffff0u;
-                    hits += count_hits<BITS, COUNT>(
-                        cnt, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, voff, off, 0), base1, cap, dummy);
+                const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, off + len4);
+                for (uint32_t p4 = 256u; p4 < len4; p4 += 256u) {
+                    count_hits<BITS>(cnt, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0),
+                                     base1, cap, dummy);
+                    ++steps;
                 }
             }
         }
@@ -227,20 +258,21 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, uint32_t* cnt, i
     // Two group buffers in ping-pong: one is counted while the other's 16
     // loads are in flight (no register copies between them).
     Group A, B;
-    load_group(rs, ro + t_begin, rl + t_begin, t_begin < t_end, lane, A);
-    for (int32_t t0 = t_begin; t0 < t_end; t0 += 32) {
-        load_group(rs, ro + t0 + 16, rl + t0 + 16, t0 + 16 < t_end, lane, B);
+    load_group(a.mem, ro + 16 * g0, rl + 16 * g0, g0 < g1, lane4, A);
+    int32_t g = g0;
+    for (; g < g1; g += 2) {
+        load_group(a.mem, ro + 16 * (g + 1), rl + 16 * (g + 1), g + 1 < g1, lane4, B);
         __builtin_amdgcn_sched_barrier(0);  // issue B's loads before touching A's data
 #pragma unroll
-        for (int u = 0; u < 16; ++u) hits += count_hits<BITS, COUNT>(cnt, A.m[u], base1, cap, dummy);
-        if (A.has_long) long_tail(t0);
-        load_group(rs, ro + t0 + 32, rl + t0 + 32, t0 + 32 < t_end, lane, A);
+        for (int u = 0; u < 16; ++u) count_hits<BITS>(cnt, A.m[u], base1, cap, dummy);
+        if (A.has_long) long_tail(16 * g);
+        load_group(a.mem, ro + 16 * (g + 2), rl + 16 * (g + 2), g + 2 < g1, lane4, A);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) hits += count_hits<BITS, COUNT>(cnt, B.m[u], base1, cap, dummy);
-        if (B.has_long) long_tail(t0 + 16);
+        for (int u = 0; u < 16; ++u) count_hits<BITS>(cnt, B.m[u], base1, cap, dummy);
+        if (B.has_long) long_tail(16 * (g + 1));
     }
-    return hits;
+    return steps + 32u * (uint32_t)((g - g0) >> 1);
 }
 
 // Exact per-entry epilogue with 16-bit counters (segments whose 8-bit
@@ -278,7 +310,7 @@ __device__ void store_exact16(const TriArgs& a, const uint32_t* cnt, int64_t i, 
 // code is monotone in r_j, so equal codes at the smallest and largest r_j
 // mean equal codes for every column).  Run by the first wave.
 template <int F>
-__device__ __forceinline__ void row_table(const TriArgs& a, double ri, uint32_t* s_lut, uint32_t* s_uc) {
+__device__ __forceinline__ void row_table(const TriArgs& a, double ri, uint32_t* misc) {
     if (threadIdx.x >= 64) return;
     const int u = threadIdx.x & 7;
     const double rmin = __longlong_as_double((long long)a.rr[0]);
@@ -296,27 +328,22 @@ __device__ __forceinline__ void row_table(const TriArgs& a, double ri, uint32_t*
     if (threadIdx.x == 0) {
         uint32_t uc = 0;
         while (uc < 8 && ((eq >> uc) & 1ull)) ++uc;
-        *s_uc = uc;
-        s_lut[0] = lo4;
-        s_lut[1] = hi4;
+        misc[MISC_UC] = uc;
+        misc[MISC_LUT_LO] = lo4;
+        misc[MISC_LUT_HI] = hi4;
     }
 }
 
-// Common item prologue / hit phase / wrap check.  Returns true when the
-// 8-bit counters are exact; otherwise the item has been redone (16-bit
-// counters, exact stores) and the caller must return.
+// Item geometry shared by the prologue, the wrap check and the redo.
 struct ItemGeom {
     int64_t i, lo;
     int32_t width, shift, nchunk, nwords;
-    uint32_t dummy;  // byte offset of the per-lane dummy words in LDS
 };
 
-// After the optimistic epilogue, T > 255 items compare the sum of the 8-bit
-// counters with the number of increments: a counter that reached 256
-// wrapped (and carried into its neighbour), which changes the sum.  Such
-// items are recomputed with 16-bit counters and their entries rewritten.
+// 16-bit recount of an item (its 8-bit counters wrapped, or the launch is
+// WIDE16): passes of half the counter capacity, exact stores.
 template <int F>
-__device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, double ri) {
+__device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, double ri, uint32_t dummy) {
     if (threadIdx.x == 0) atomicAdd(&a.flags[0], 1);
     const int32_t half_cap = gm.nwords * 2;  // 16-bit counters that fit
     for (int32_t d0 = 0; d0 < gm.width; d0 += half_cap) {
@@ -324,20 +351,44 @@ __device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, d
         __syncthreads();
         for (int32_t w = threadIdx.x; w < (w2 + 1) / 2; w += TRI_THREADS) cnt[w] = 0u;
         __syncthreads();
-        hit_phase<16, false>(a, cnt, gm.i, gm.lo + d0, (uint32_t)w2, 0, gm.dummy);
+        hit_phase<16>(a, cnt, gm.i, gm.lo + d0, (uint32_t)w2, 0, dummy);
         __syncthreads();
         store_exact16<F>(a, cnt, gm.i, gm.lo + d0, w2, ri);
     }
 }
 
+// Zeroes counter words [0, nwords) (rounded up to 4) and this thread's dummy word.
+__device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords, uint32_t dummy) {
+    uint4* c4 = (uint4*)cnt;
+    const int32_t n4 = (nwords + 3) >> 2;
+    for (int32_t w = threadIdx.x; w < n4; w += TRI_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+    cnt[dummy >> 2] = 0u;
+}
+
+// After the hit phase of a CHECK8 item: every lane of every counting step
+// added 1 to exactly one byte, of a counter or of its dummy word, and a
+// counter byte that reached 256 wrapped (carrying into its neighbour), which
+// lowers the byte sum.  So the counters are exact iff
+//   sum of counter bytes + sum of dummy bytes == 64 * counting steps.
+// The dummy words cannot wrap: CHECK8 is used only while a wave makes at
+// most 255 steps.
+__device__ __forceinline__ bool counts_exact(uint32_t* misc, uint32_t bsum, const uint32_t* cnt, uint32_t dummy) {
+    bsum = __builtin_amdgcn_sad_u8(cnt[dummy >> 2], 0u, bsum);
+    // wave reduction, then one atomic per wave
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) bsum += (uint32_t)__shfl_xor((int)bsum, d, 64);
+    if ((threadIdx.x & 63) == 0 && bsum) atomicAdd(&misc[MISC_SUM], bsum);
+    __syncthreads();
+    return misc[MISC_SUM] == 64u * misc[MISC_SLOTS];
+}
+
 template <int F>
 __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri(TriArgs a) {
     extern __shared__ uint32_t cnt[];
-    __shared__ uint32_t s_lut[2];
-    __shared__ uint32_t s_uc;
-    __shared__ uint32_t s_hits, s_sum;
     constexpr int esz = FmtInfo<F>::esz;
     constexpr int epc = 16 / esz;  // entries per 16-byte chunk
+    uint32_t* const misc = cnt + (tri_dummy_off(a.S) + TRI_DUMMY_BYTES) / 4;
+    const uint32_t dummy = tri_dummy_off(a.S) + threadIdx.x * 4u;
 
     const int2 it = a.items[blockIdx.x];
     ItemGeom gm;
@@ -357,30 +408,29 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     gm.shift = shift;
     gm.nchunk = nchunk;
     gm.nwords = nchunk * epc / 4;  // 8-bit counters
-    gm.dummy = (uint32_t)a.S + 64u;
 
-    for (int32_t w = threadIdx.x; w < gm.nwords; w += TRI_THREADS) cnt[w] = 0u;
-    if (threadIdx.x == 0) {
-        s_hits = 0u;
-        s_sum = 0u;
+    if (a.mode == TRI_MODE_WIDE16) {
+        redo_wide<F>(a, cnt, gm, ri, dummy);
+        return;
     }
-    if constexpr (F == I8 || F == U8) row_table<F>(a, ri, s_lut, &s_uc);
+    zero_counters(cnt, gm.nwords, dummy);
+    if (threadIdx.x < TRI_MISC_WORDS) misc[threadIdx.x] = 0u;
+    if constexpr (F == I8 || F == U8) row_table<F>(a, ri, misc);
     __syncthreads();
     // counters cover units [0, nchunk * units-per-chunk): hits outside the
     // item's columns but inside that range land in the unstored padding
-    const bool check = a.T > 255;
+    const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    uint32_t nh;
-    if (check) nh = hit_phase<8, true>(a, cnt, i, lo, cap, shift, gm.dummy);
-    else nh = hit_phase<8, false>(a, cnt, i, lo, cap, shift, gm.dummy);
-    if (check && (threadIdx.x & 63) == 0) atomicAdd(&s_hits, nh);
+    const uint32_t steps = hit_phase<8>(a, cnt, i, lo, cap, shift, dummy);
+    if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
     uint32_t bsum = 0;  // sum of the counter bytes this thread read
     const bool has_diag = (lo == i);
     const uint4* c4 = (const uint4*)cnt;
     if constexpr (F == I8 || F == U8) {
-        const uint32_t lut_lo = s_lut[0], lut_hi = s_lut[1], uc = s_uc;
+        const uint32_t lut_lo = misc[MISC_LUT_LO], lut_hi = misc[MISC_LUT_HI], uc = misc[MISC_UC];
+        const uint32_t kuc = (0x80u - uc) * 0x01010101u;
         const uint32_t dcode = code_of<F>(1.0, a.scale, a.zp);
         for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS) {
             const uint4 w = c4[ck];
@@ -390,12 +440,20 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
                 bsum = __builtin_amdgcn_sad_u8(w.z, 0u, bsum);
                 bsum = __builtin_amdgcn_sad_u8(w.w, 0u, bsum);
             }
-            const int64_t jb = lo + (int64_t)ck * 16 - shift;  // column of byte 0
             uint32_t o[4];
-            o[0] = code_word<F>(w.x, lut_lo, lut_hi, uc, ri, a.rinv, jb + 0, a.scale, a.zp);
-            o[1] = code_word<F>(w.y, lut_lo, lut_hi, uc, ri, a.rinv, jb + 4, a.scale, a.zp);
-            o[2] = code_word<F>(w.z, lut_lo, lut_hi, uc, ri, a.rinv, jb + 8, a.scale, a.zp);
-            o[3] = code_word<F>(w.w, lut_lo, lut_hi, uc, ri, a.rinv, jb + 12, a.scale, a.zp);
+            if ((over_uc(w.x, kuc) | over_uc(w.y, kuc) | over_uc(w.z, kuc) | over_uc(w.w, kuc)) == 0u) {
+                // every count below uc: table lookup, four bytes at a time
+                o[0] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.x);
+                o[1] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.y);
+                o[2] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.z);
+                o[3] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.w);
+            } else {
+                const int64_t jb = lo + (int64_t)ck * 16 - shift;  // column of byte 0
+                o[0] = code_word_exact<F>(w.x, lut_lo, lut_hi, uc, ri, a.rinv, jb + 0, a.scale, a.zp);
+                o[1] = code_word_exact<F>(w.y, lut_lo, lut_hi, uc, ri, a.rinv, jb + 4, a.scale, a.zp);
+                o[2] = code_word_exact<F>(w.z, lut_lo, lut_hi, uc, ri, a.rinv, jb + 8, a.scale, a.zp);
+                o[3] = code_word_exact<F>(w.w, lut_lo, lut_hi, uc, ri, a.rinv, jb + 12, a.scale, a.zp);
+            }
             // the diagonal is column lo, byte `shift` of chunk 0
             if (has_diag && ck == 0) set_byte(o, shift, dcode);
             char* d = dst_al + (int64_t)ck * 16;
@@ -460,11 +518,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check) {
-        if (bsum) atomicAdd(&s_sum, bsum);
-        __syncthreads();
-        if (s_sum != s_hits) redo_wide<F>(a, cnt, gm, ri);
-    }
+    if (check && !counts_exact(misc, bsum, cnt, dummy)) redo_wide<F>(a, cnt, gm, ri, dummy);
 }
 
 // NF4: two entries per byte.  Nibble position g(e) = e - e_base + (e_base & 1)
@@ -473,9 +527,8 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
 // merged with 32-bit atomics on its own nibble only.
 __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri_nf4(TriArgs a) {
     extern __shared__ uint32_t cnt[];
-    __shared__ uint32_t s_lut[2];
-    __shared__ uint32_t s_uc;
-    __shared__ uint32_t s_hits, s_sum;
+    uint32_t* const misc = cnt + (tri_dummy_off(a.S) + TRI_DUMMY_BYTES) / 4;
+    const uint32_t dummy = tri_dummy_off(a.S) + threadIdx.x * 4u;
 
     const int2 it = a.items[blockIdx.x];
     ItemGeom gm;
@@ -494,28 +547,25 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     gm.shift = shift;
     gm.nchunk = nchunk;
     gm.nwords = nchunk * 8;
-    gm.dummy = (uint32_t)a.S + 64u;
 
-    for (int32_t w = threadIdx.x; w < gm.nwords; w += TRI_THREADS) cnt[w] = 0u;
-    if (threadIdx.x == 0) {
-        s_hits = 0u;
-        s_sum = 0u;
+    if (a.mode == TRI_MODE_WIDE16) {
+        redo_wide<NF4>(a, cnt, gm, ri, dummy);
+        return;
     }
-    row_table<NF4>(a, ri, s_lut, &s_uc);
+    zero_counters(cnt, gm.nwords, dummy);
+    if (threadIdx.x < TRI_MISC_WORDS) misc[threadIdx.x] = 0u;
+    row_table<NF4>(a, ri, misc);
     __syncthreads();
-    // counters cover units [0, nchunk * units-per-chunk): hits outside the
-    // item's columns but inside that range land in the unstored padding
-    const bool check = a.T > 255;
+    const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    uint32_t nh;
-    if (check) nh = hit_phase<8, true>(a, cnt, i, lo, cap, shift, gm.dummy);
-    else nh = hit_phase<8, false>(a, cnt, i, lo, cap, shift, gm.dummy);
-    if (check && (threadIdx.x & 63) == 0) atomicAdd(&s_hits, nh);
+    const uint32_t steps = hit_phase<8>(a, cnt, i, lo, cap, shift, dummy);
+    if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
     uint32_t bsum = 0;
     const uint32_t dcode = code_of<NF4>(1.0, 0.f, 0.f);
-    const uint32_t lut_lo = s_lut[0], lut_hi = s_lut[1], uc = s_uc;
+    const uint32_t lut_lo = misc[MISC_LUT_LO], lut_hi = misc[MISC_LUT_HI], uc = misc[MISC_UC];
+    const uint32_t kuc = (0x80u - uc) * 0x01010101u;
     const bool has_diag = (lo == i);
     const uint4* c4 = (const uint4*)cnt;
     for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS) {
@@ -524,15 +574,22 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
         const uint4 wa = c4[2 * ck], wb = c4[2 * ck + 1];
         cw[0] = wa.x; cw[1] = wa.y; cw[2] = wa.z; cw[3] = wa.w;
         cw[4] = wb.x; cw[5] = wb.y; cw[6] = wb.z; cw[7] = wb.w;
-        if (check) {
+        uint32_t over = 0u;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) bsum = __builtin_amdgcn_sad_u8(cw[q], 0u, bsum);
+        for (int q = 0; q < 8; ++q) {
+            if (check) bsum = __builtin_amdgcn_sad_u8(cw[q], 0u, bsum);
+            over |= over_uc(cw[q], kuc);
         }
-        const int64_t jb = lo + (int64_t)ck * 32 - shift;
         uint32_t codes[8];
+        if (over == 0u) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-            codes[q] = code_word<NF4>(cw[q], lut_lo, lut_hi, uc, ri, a.rinv, jb + 4 * q, 0.f, 0.f);
+            for (int q = 0; q < 8; ++q) codes[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, cw[q]);
+        } else {
+            const int64_t jb = lo + (int64_t)ck * 32 - shift;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                codes[q] = code_word_exact<NF4>(cw[q], lut_lo, lut_hi, uc, ri, a.rinv, jb + 4 * q, 0.f, 0.f);
+        }
         if (has_diag && ck == 0) set_byte(codes, shift, dcode);
         // pack byte codes c0..c3 of each word into two nibble-bytes
         uint32_t ob[4];
@@ -567,28 +624,33 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check) {
-        if (bsum) atomicAdd(&s_sum, bsum);
-        __syncthreads();
-        if (s_sum != s_hits) redo_wide<NF4>(a, cnt, gm, ri);
-    }
+    if (check && !counts_exact(misc, bsum, cnt, dummy)) redo_wide<NF4>(a, cnt, gm, ri, dummy);
 }
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 
-static int tri_segment_cols(rfxp_ctx* ctx, int fmt) {
-    // Counter bytes per workgroup; leave room for the static LDS words and
-    // for the 16-byte alignment shift.  Two workgroups per CU on gfx950.
-    int budget = std::min(ctx->max_lds, 160 * 1024) / 2 - 1024 - TRI_DUMMY_BYTES;
-    budget = std::max(budget, 4096);
-    budget &= ~63;
-    if (fmt == NF4) return budget;  // one counter byte per nibble entry
-    return budget;
+static int64_t ceil_div_i(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static int tri_segment_cols(rfxp_ctx* ctx) {
+    // Columns per item: one counter byte each (NF4: one per nibble entry),
+    // plus the alignment slack, the dummy words and the item scalars
+    // (tri_lds_bytes), two workgroups per CU (160 KB of LDS on gfx950).
+    const int half = std::min(ctx->max_lds, 160 * 1024) / 2;
+    int S = half - TRI_DUMMY_BYTES - TRI_MISC_WORDS * 4 - 64 - 16;
+    S = std::max(S, 4096) & ~63;
+    return S;
 }
 
-static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// Counter mode of a launch (TRI_MODE_*).
+static int tri_mode(int32_t T) {
+    if (T <= 255) return TRI_MODE_EXACT8;
+    // counting steps of the busiest wave: 16 trees per step, groups in pairs
+    const int64_t groups = ceil_div_i((T + 15) / 16, TRI_WAVES);
+    const int64_t steps = 32 * ((groups + 1) / 2);
+    return steps <= 192 ? TRI_MODE_CHECK8 : TRI_MODE_WIDE16;
+}
 
 }  // namespace rfxp
 
@@ -681,7 +743,7 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     if (((uintptr_t)out) % esz != 0) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: out is not aligned to its entry size");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
 
-    const int32_t S = tri_segment_cols(ctx, fmt);
+    const int32_t S = tri_segment_cols(ctx);
     // work list: rows in increasing order, each split into S-column segments
     if (ctx->items_key[0] != N || ctx->items_key[1] != r0 || ctx->items_key[2] != r1 || ctx->items_key[3] != S) {
         std::vector<int2> items;
@@ -713,9 +775,8 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     a.scale = scale;
     a.zp = zp;
     a.flags = ctx->flags.p;
-    // counters: S units + up to one 16-byte chunk of alignment shift,
-    // rounded to whole chunks (NF4: 32 nibbles per chunk)
-    const size_t lds = (size_t)S + 64 + TRI_DUMMY_BYTES;
+    a.mode = tri_mode(ctx->T);
+    const size_t lds = tri_lds_bytes(S);
     hipError_t e;
     {
         LaunchTimer tm(ctx, "tri");
