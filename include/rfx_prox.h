@@ -119,6 +119,34 @@ int64_t rfxp_upper_nbytes(int fmt, int64_t N, int64_t row_begin, int64_t row_end
 /* The per-sample nout actually used (device int32[N] copy into `nout`). */
 int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
 
+/* ---- top-K similarity retrieval ----------------------------------------- */
+
+/* Indexes a reference set (N samples x T trees of leaf labels, same layout
+ * rules as rfxp_set_forest, no OOB bits) for rfxp_topk.  Replaces the
+ * per-tree inverted index of RandomForest::get_top_k_similar
+ * (src/rf_random_forest.cpp:4644-4675) and the dense scan of
+ * predict_top_k_similar (python/randomforest_py.cpp:2534-2545).  T <= 65534. */
+int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t, int64_t N,
+                       int32_t T, int32_t nleaf);
+
+/* For each of Q queries (leaf labels q_leaf[q*q_stride_i + t*q_stride_t],
+ * device), the K (<= 64) reference indices with the largest
+ *   count(q, j) = #{t in trees(q) : leaf_q(t) == leaf_j(t), label valid}
+ * ordered by (count desc, index asc), into idx_out[q*K + k] (int32) and
+ * cnt_out[q*K + k] (uint16), device.
+ *   trees(q) = all trees when q_oob_words is NULL (new queries,
+ *              python/randomforest_py.cpp:2496-2568); otherwise the trees
+ *              whose bit (q & 31) of q_oob_words[t*q_oob_ld + q/32] is set
+ *              (OOB queries, src/rf_random_forest.cpp:4677-4782).
+ *   exclude_base >= 0: query q never returns reference exclude_base + q
+ *              (a training sample querying itself); < 0: nothing excluded.
+ *   positive_only: only counts > 0 are returned (OOB-query semantics);
+ *              otherwise zero counts fill the list in index order.
+ * Slots without a result get index -1 and count 0. */
+int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t q_stride_t, int64_t Q,
+              const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t exclude_base, int32_t K,
+              int positive_only, int32_t* idx_out, uint16_t* cnt_out);
+
 #ifdef __cplusplus
 }
 #endif

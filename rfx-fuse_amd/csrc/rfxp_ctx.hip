@@ -151,6 +151,8 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->rrange.release();
     ctx->items.release();
     ctx->flags.release();
+    ctx->ref_off.release();
+    ctx->ref_mem.release();
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();
     delete ctx;

@@ -49,17 +49,39 @@ struct LeafView {
     int64_t N;
     int32_t T;
     int32_t L;
+    // 0: forest buckets b = 2*leaf + oob.  > 0: reference-set buckets
+    // b = leaf*nseg + (i >> seg_shift) (top-K: one bucket per leaf and
+    // column segment, OOB bits unused).
+    int32_t nseg;
+    int32_t seg_shift;
 };
 
 // Bucket id of sample i in tree t, -1 when its label is not a valid leaf.
 __device__ __forceinline__ int32_t bucket_of(const LeafView& v, int64_t i, int32_t t) {
     int32_t l = v.leaf[i * v.si + (int64_t)t * v.st];
     if (l < 0 || l >= v.L) return -1;
+    if (v.nseg > 0) return l * v.nseg + (int32_t)(i >> v.seg_shift);
     uint32_t w = v.oob[(int64_t)t * v.old + (i >> 5)];
     return 2 * l + (int32_t)((w >> (i & 31)) & 1u);
 }
 
-// Builds mem/off/rec/nout/rinv/rr on ctx->stream (rfxp_pack.hip).
-int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in);
+// Buckets per tree of a view (even: packing windows split at even buckets).
+__host__ __device__ inline int32_t view_buckets(const LeafView& v) {
+    if (v.nseg == 0) return 2 * v.L;
+    const int64_t nb = (int64_t)v.L * v.nseg;
+    return (int32_t)((nb + 1) / 2 * 2);
+}
+
+// Where pack_forest writes: bucket offsets [T][nb+1] and members [T][N].
+// Forest mode (v.nseg == 0) also builds the per-sample records in ctx and
+// nout / rinv / rrange; reference mode builds buckets only.
+struct PackTarget {
+    int32_t* off;
+    uint32_t* mem;
+};
+
+// Builds the buckets (and, in forest mode, records and nout) on ctx->stream
+// (rfxp_pack.hip).
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst);
 
 }  // namespace rfxp

@@ -74,6 +74,13 @@ struct rfxp_ctx {
     int64_t n_items = 0;
     DevBuf<int32_t> flags;     // device status words
 
+    // reference set for top-K (rfxp_set_reference)
+    bool ref_ready = false;
+    int64_t ref_N = 0;
+    int32_t ref_T = 0, ref_L = 0, ref_nseg = 0, ref_shift = 0, ref_nb = 0;
+    DevBuf<int32_t> ref_off;   // T x (nb+1): bucket b = leaf*nseg + segment
+    DevBuf<uint32_t> ref_mem;  // T x N (+ padding)
+
     // timing
     bool timing = false;
     std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> pending;

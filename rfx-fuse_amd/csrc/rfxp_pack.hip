@@ -69,7 +69,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const uint32_t bid = blockIdx.x;
     const int32_t t = (int32_t)((((bid >> 3) >> 4) << 3) + (bid & 7)) * 16 + (int32_t)((bid >> 3) & 15);
     if (t >= v.T) return;
-    const int32_t nb = 2 * v.L;
+    const int32_t nb = view_buckets(v);
     uint32_t* cnt;
     if constexpr (LDS_PATH) cnt = sh;
     else cnt = gscr + (int64_t)t * 2 * (nb + 1);
@@ -109,6 +109,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         else return ((const volatile uint32_t*)off0)[k];
     };
     // Records, tree-major (coalesced); k_rec_transpose makes them sample-major.
+    if (!roffT) return;  // reference mode: buckets only
     uint32_t* ro = roffT + (int64_t)t * N;
     uint16_t* rl = rlenT + (int64_t)t * N;
     const uint32_t tbase = (uint32_t)t * (uint32_t)N;
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int32_t t = (int32_t)(lin / nwin);
     const int32_t w = (int32_t)(lin % nwin);
     if (t >= v.T) return;
-    const int32_t nb = 2 * v.L;
+    const int32_t nb = view_buckets(v);
     const int32_t* off = goff_all + (int64_t)t * (nb + 1);
     if (threadIdx.x == 0) {
         s_b0 = first_bucket_at(off, nb, (int64_t)w * PACK_WIN);
@@ -235,7 +236,8 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const uint32_t rel = lds_cur ? atomicAdd(&cur[b - b0], 1u) : atomicAdd(&gcur[b], 1u);
         const uint32_t bstart = (uint32_t)off[b] - base_pos;
         const uint32_t end = (uint32_t)off[b + 1] - base_pos;
-        const uint32_t m = (uint32_t)(i + 1) | (rel + 1 == end && end - bstart >= REC_LONG ? MEM_LAST : 0u);
+        const uint32_t m = (uint32_t)(i + 1) |
+                           (v.nseg == 0 && rel + 1 == end && end - bstart >= REC_LONG ? MEM_LAST : 0u);
         if (rel < (uint32_t)PACK_WIN) stage[rel] = m;
         else memt[base_pos + rel] = m;
     };
@@ -340,12 +342,13 @@ __global__ void k_rr_init(unsigned long long* rr) {
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
     const int32_t T = v.T;
-    const int32_t nb = 2 * v.L;
-    {
+    const int32_t nb = view_buckets(v);
+    const bool forest = v.nseg == 0;
+    if (forest) {
         LaunchTimer tm(ctx, "rr_init");
         hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, ctx->rrange.p);
     }
@@ -369,17 +372,17 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
             RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_hist<true>,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, ctx->bkt_off.p,
-                           ctx->roffT.p, ctx->rlenT.p, (uint32_t*)nullptr, k16, ldk);
+        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, dst.off,
+                           forest ? ctx->roffT.p : nullptr, ctx->rlenT.p, (uint32_t*)nullptr, k16, ldk);
     } else {
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(nscr, 256), 65536)), dim3(256), 0, s,
                            ctx->scratch.p, nscr, 0u);
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, ctx->bkt_off.p,
-                           ctx->roffT.p, ctx->rlenT.p, ctx->scratch.p, k16, ldk);
+        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, dst.off,
+                           forest ? ctx->roffT.p : nullptr, ctx->rlenT.p, ctx->scratch.p, k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
-    {
+    if (forest) {
         LaunchTimer tm(ctx, "rec_transpose");
         hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s,
                            ctx->roffT.p, ctx->rlenT.p, N, T, ctx->ldr, ctx->roff.p, ctx->rlen.p);
@@ -394,10 +397,11 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds2));
         LaunchTimer tm(ctx, "pack_scatter");
-        hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, ctx->bkt_off.p,
-                           ctx->bkt_mem.p, ctx->scratch.p, nwin, (const uint16_t*)k16, ldk);
+        hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, dst.off,
+                           dst.mem, ctx->scratch.p, nwin, (const uint16_t*)k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
+    if (!forest) return RFXP_OK;
     if (!nout_in) {
         RFXP_HIP(ctx, ctx->scratch2.ensure((size_t)N));
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(N, 256), 65536)), dim3(256), 0, s,

@@ -1,0 +1,433 @@
+// Per-query top-K of the most proximate reference samples, without the
+// query x reference proximity matrix.
+//
+// Reference semantics restated:
+//   * new queries, all trees (python/randomforest_py.cpp:2496-2568, and
+//     LoadedModel::get_top_k_similar :624-672): count(q, j) = #{t : leaf_q(t)
+//     == leaf_j(t)}; the top K over all N references, zero counts included;
+//   * OOB queries (src/rf_random_forest.cpp:4677-4782): only the trees where
+//     the query sample is out-of-bag, the query itself excluded, counts > 0
+//     only (the caller scales by 1/|OOB(q)|).
+// Ties are broken by the lower reference index (the reference leaves them to
+// std::partial_sort, whose order is unspecified).
+//
+// Layout: the reference set is packed like a forest, but bucket
+// b = leaf*nseg + (j >> seg_shift) holds the references of one leaf and one
+// column segment of S = 2^seg_shift references (rfxp_set_reference).  A
+// query's bucket in tree t and segment s is then one contiguous run, found
+// from its leaf label with two offset loads.
+//
+// Kernel k_topk: one workgroup per query walks the segments in order.  Per
+// segment, 16-bit LDS counters (one per reference of the segment) take the
+// query's T buckets exactly as the triangle's hit phase does; then the
+// counters become keys (count + 1, 0 for references that may not be chosen)
+// and only keys above the running K-th best key are looked at: entries of a
+// later segment lose every tie against the running list, which holds lower
+// indices.  Selection is exact: a binary search over key levels for the
+// threshold, ordered compaction of the winners, and a rank merge with the
+// running list by one wave.
+#include <algorithm>
+#include <string>
+
+#include "rfxp_device.hpp"
+#include "rfxp_forest.hpp"
+#include "rfxp_internal.hpp"
+
+namespace rfxp {
+
+constexpr int TOPK_THREADS = 1024;
+constexpr int TOPK_WAVES = TOPK_THREADS / 64;
+constexpr int TOPK_MAX_K = 64;
+constexpr int TOPK_MAX_SHIFT = 15;  // 32768 16-bit counters: 64 KB, two workgroups per CU
+constexpr int TOPK_MIN_SHIFT = 11;  // at least 2 counters per thread
+
+struct TopkArgs {
+    const uint32_t* mem;  // reference members (j + 1), [T][N]
+    uint32_t mem_bytes;
+    const int32_t* off;   // [T][nb + 1]
+    int32_t nb;
+    int64_t N;
+    int32_t T, L, nseg, shift;
+    const int32_t* qleaf;
+    int64_t qsi, qst;
+    const uint32_t* qoob;  // NULL: all trees
+    int64_t qold;
+    int64_t exclude_base;  // query q excludes reference exclude_base + q; < 0: none
+    int32_t K;
+    int32_t floor_key;     // smallest selectable key: 1 (zeros allowed) or 2 (counts > 0)
+    int32_t* idx_out;
+    uint16_t* cnt_out;
+};
+
+// LDS layout: counters (S/2 words) | dummy words (1024) | reduction scratch.
+__host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) { return (1u << shift) * 2u; }
+constexpr uint32_t TOPK_RED_WORDS = 64;                     // wave partials
+constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
+__host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
+    return topk_dummy_off(shift) + TOPK_THREADS * 4 + (TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
+}
+
+typedef __attribute__((address_space(3))) uint32_t lds_w;
+__device__ __forceinline__ void lds_add16(uint32_t addr, uint32_t val) {
+    __hip_atomic_fetch_add((lds_w*)(uintptr_t)addr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ref_rsrc(const uint32_t* mem, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)mem, (short)0, (int)nbytes, 0x00020000);
+}
+
+// Bucket (byte offset, byte length) of query q in tree t, segment s.
+__device__ __forceinline__ void query_bucket(const TopkArgs& a, int64_t q, int32_t t, int32_t s, uint32_t& soff,
+                                             uint32_t& len4) {
+    soff = 0u;
+    len4 = 0u;
+    if (t >= a.T) return;
+    const int32_t l = a.qleaf[q * a.qsi + (int64_t)t * a.qst];
+    if (l < 0 || l >= a.L) return;
+    if (a.qoob) {
+        const uint32_t w = a.qoob[(int64_t)t * a.qold + (q >> 5)];
+        if (((w >> (q & 31)) & 1u) == 0u) return;
+    }
+    const int32_t* ot = a.off + (int64_t)t * (a.nb + 1) + (int64_t)l * a.nseg + s;
+    const uint32_t o0 = (uint32_t)ot[0], o1 = (uint32_t)ot[1];
+    soff = 4u * ((uint32_t)t * (uint32_t)a.N + o0);
+    len4 = 4u * (o1 - o0);
+}
+
+// Counts the query's buckets of segment s into 16-bit counters: the
+// counter of reference lo + c is the 16-bit unit c.  Lanes past a bucket's
+// end read 0 (buffer range), which is no member; they and any member outside
+// the segment add into the thread's dummy word.
+__device__ void topk_hits(const TopkArgs& a, int64_t q, int32_t s, uint32_t lo, uint32_t width, uint32_t dummy) {
+    const uint32_t lane = threadIdx.x & 63, lane4 = lane * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t ng = (a.T + 15) >> 4;
+    const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
+    const uint32_t base1 = lo + 1u;
+    for (int32_t g = g0; g < g1; ++g) {
+        uint32_t m[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            uint32_t soff, len4;
+            query_bucket(a, q, 16 * g + u, s, soff, len4);
+            soff = __builtin_amdgcn_readfirstlane(soff);
+            len4 = __builtin_amdgcn_readfirstlane(len4);
+            m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, soff + len4), lane4, soff, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t c = m[u] - base1;
+            const bool h = c < width;
+            lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
+        }
+        // buckets of more than 64 references in this segment
+        for (int u = 0; u < 16; ++u) {
+            uint32_t soff, len4;
+            query_bucket(a, q, 16 * g + u, s, soff, len4);
+            soff = __builtin_amdgcn_readfirstlane(soff);
+            len4 = __builtin_amdgcn_readfirstlane(len4);
+            if (len4 <= 256u) continue;
+            const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, soff + len4);
+            for (uint32_t p4 = 256u; p4 < len4; p4 += 256u) {
+                const uint32_t mm = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, soff, 0);
+                const uint32_t c = mm - base1;
+                const bool h = c < width;
+                lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
+            }
+        }
+    }
+}
+
+// Block reductions through `red` (TOPK_RED_WORDS words); every thread gets
+// the result.  Each begins with a barrier-free wave step and uses two
+// barriers.
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += (uint32_t)__shfl_xor((int)v, d, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WAVES; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, d, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WAVES; ++w) t = max(t, red[w]);
+    __syncthreads();
+    return t;
+}
+
+// Exclusive prefix sum over threads in thread order; *total gets the sum.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+        if (lane >= (uint32_t)d) incl += o;
+    }
+    if (lane == 63) red[threadIdx.x >> 6] = incl;
+    __syncthreads();
+    uint32_t before = 0, t = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WAVES; ++w) {
+        const uint32_t x = red[w];
+        if (w < (int)(threadIdx.x >> 6)) before += x;
+        t += x;
+    }
+    __syncthreads();
+    *total = t;
+    return before + incl - v;
+}
+
+// Number of this thread's keys (16-bit halves of kw[0..nw)) >= c.
+template <int NW>
+__device__ __forceinline__ uint32_t count_ge(const uint32_t (&kw)[NW], uint32_t c) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) n += ((kw[k] & 0xffffu) >= c) + ((kw[k] >> 16) >= c);
+    return n;
+}
+
+// (key desc, index asc): does (ka, ia) come before (kb, ib)?
+__device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, uint32_t ib) {
+    return ka > kb || (ka == kb && ia < ib);
+}
+
+template <int NW>  // 16-bit words per thread: S = 2 * NW * TOPK_THREADS
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk(TopkArgs a) {
+    extern __shared__ uint32_t sm[];
+    const int32_t shift = a.shift;
+    const uint32_t S = 1u << shift;
+    uint32_t* const red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
+    uint32_t* const cand_k = red + TOPK_RED_WORDS;  // candidates of a segment
+    uint32_t* const cand_i = cand_k + TOPK_MAX_K;
+    uint32_t* const run_k = cand_i + TOPK_MAX_K;    // running top-K (sorted)
+    uint32_t* const run_i = run_k + TOPK_MAX_K;
+    uint32_t* const nrun_p = run_i + TOPK_MAX_K;
+    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
+    const int64_t q = blockIdx.x;
+    const uint32_t K = (uint32_t)a.K;
+    const int64_t ex = a.exclude_base >= 0 ? a.exclude_base + q : -1;
+
+    if (threadIdx.x == 0) *nrun_p = 0u;
+    uint32_t nrun = 0;      // entries in the running list (uniform)
+    uint32_t kmin = 0;      // key of the running K-th entry once the list is full
+    for (int32_t s = 0; s < a.nseg; ++s) {
+        const uint32_t lo = (uint32_t)s << shift;
+        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        uint4* c4 = (uint4*)sm;
+        for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+        sm[dummy >> 2] = 0u;
+        __syncthreads();
+        topk_hits(a, q, s, lo, width, dummy);
+        __syncthreads();
+        // this thread's counters: units [tid*2*NW, (tid+1)*2*NW) -> keys
+        uint32_t kw[NW];
+        const uint32_t u0 = threadIdx.x * 2u * NW;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            const uint32_t w = sm[threadIdx.x * NW + k];
+            const uint32_t ua = u0 + 2u * k, ub = ua + 1u;
+            const bool va = ua < width && (int64_t)(lo + ua) != ex;
+            const bool vb = ub < width && (int64_t)(lo + ub) != ex;
+            const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
+            const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
+            kw[k] = ka | (kb << 16);
+        }
+        // only keys above the running threshold can enter the list
+        const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+        uint32_t mloc = 0;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) mloc = max(mloc, max(kw[k] & 0xffffu, kw[k] >> 16));
+        const uint32_t M = block_max(mloc, red);
+        if (M >= lowest) {
+            // cstar: the largest level in [lowest, M] with at least `need`
+            // keys >= cstar (need = K - nothing: the merge keeps the best K
+            // of running + candidates, so K candidates always suffice)
+            uint32_t lo_c = lowest, hi_c = M;  // f(lo_c) > 0
+            uint32_t cstar = lowest;
+            if (block_sum(count_ge(kw, lowest), red) > K) {
+                // f(lowest) > K: binary search the largest c with f(c) >= K
+                while (lo_c < hi_c) {
+                    const uint32_t mid = (lo_c + hi_c + 1u) / 2u;
+                    if (block_sum(count_ge(kw, mid), red) >= K) lo_c = mid;
+                    else hi_c = mid - 1u;
+                }
+                cstar = lo_c;
+            }
+            // keys > cstar all go in; keys == cstar in index order up to K
+            const uint32_t ngt = count_ge(kw, cstar + 1u);
+            const uint32_t neq = count_ge(kw, cstar) - ngt;
+            uint32_t G, E;
+            const uint32_t pgt = block_excl_scan(ngt, red, &G);
+            const uint32_t peq = block_excl_scan(neq, red, &E);
+            const uint32_t take = min(E, K - G);
+            uint32_t rg = pgt, re = peq;
+#pragma unroll
+            for (int k = 0; k < 2 * NW; ++k) {
+                const uint32_t key = (kw[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                const uint32_t j = lo + u0 + (uint32_t)k;
+                if (key > cstar) {
+                    cand_k[rg] = key;
+                    cand_i[rg] = j;
+                    ++rg;
+                } else if (key == cstar && key >= lowest) {
+                    if (re < take) {
+                        cand_k[G + re] = key;
+                        cand_i[G + re] = j;
+                    }
+                    ++re;
+                }
+            }
+            __syncthreads();
+            // merge by rank (first wave): running entries precede candidates
+            // of equal key, since they have lower indices
+            const uint32_t nc = G + take;
+            if (threadIdx.x < 64) {
+                const uint32_t ntot = nrun + nc;
+                uint32_t mk[4], mi[4], rk[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t e = threadIdx.x + 64u * r;
+                    mk[r] = 0u;
+                    mi[r] = 0xffffffffu;
+                    if (e < nrun) {
+                        mk[r] = run_k[e];
+                        mi[r] = run_i[e];
+                    } else if (e < ntot) {
+                        mk[r] = cand_k[e - nrun];
+                        mi[r] = cand_i[e - nrun];
+                    }
+                    uint32_t rank = 0;
+                    for (uint32_t f = 0; f < ntot; ++f) {
+                        const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
+                        const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
+                        rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
+                    }
+                    rk[r] = e < ntot ? rank : 0xffffffffu;
+                }
+                // one wave: its reads of the old list precede these writes
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (rk[r] < K) {
+                        run_k[rk[r]] = mk[r];
+                        run_i[rk[r]] = mi[r];
+                    }
+                }
+                if (threadIdx.x == 0) *nrun_p = min(ntot, K);
+            }
+            __syncthreads();
+            nrun = *nrun_p;
+            kmin = nrun ? run_k[nrun - 1] : 0u;
+            __syncthreads();
+        }
+    }
+    if (threadIdx.x < K) {
+        const bool have = threadIdx.x < nrun;
+        a.idx_out[q * K + threadIdx.x] = have ? (int32_t)run_i[threadIdx.x] : -1;
+        a.cnt_out[q * K + threadIdx.x] = have ? (uint16_t)(run_k[threadIdx.x] - 1u) : (uint16_t)0;
+    }
+}
+
+template <int NW>
+static hipError_t launch_topk(rfxp_ctx* ctx, const TopkArgs& a, int64_t Q) {
+    const size_t lds = topk_lds_bytes(a.shift);
+    hipError_t e = hipFuncSetAttribute((const void*)k_topk<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_topk<NW>, dim3((unsigned)Q), dim3(TOPK_THREADS), lds, ctx->stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace rfxp
+
+using namespace rfxp;
+
+extern "C" int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t, int64_t N,
+                                  int32_t T, int32_t nleaf) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    ctx->ref_ready = false;
+    if (N < 1 || T < 1 || T > 65534 || nleaf < 1)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_reference: need N >= 1, 1 <= T <= 65534, nleaf >= 1");
+    if (!leaf || !is_device_pointer(leaf))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_reference: leaf must be a device pointer");
+    if (N * (int64_t)T + MEM_PAD > (1LL << 30) - 1)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_reference: N*T must stay below 2^30");
+    int32_t shift = TOPK_MIN_SHIFT;
+    while (shift < TOPK_MAX_SHIFT && (1LL << shift) < N) ++shift;
+    const int64_t nseg = (N + (1LL << shift) - 1) >> shift;
+    if ((int64_t)nleaf * nseg > (1LL << 29))
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_reference: nleaf * segments too large");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    LeafView v{leaf, stride_i, stride_t, nullptr, 0, N, T, nleaf, (int32_t)nseg, shift};
+    const int32_t nb = view_buckets(v);
+    RFXP_HIP(ctx, ctx->ref_off.ensure((size_t)T * (nb + 1)));
+    RFXP_HIP(ctx, ctx->ref_mem.ensure((size_t)T * N + MEM_PAD));
+    if (int rc = pack_forest(ctx, v, nullptr, PackTarget{ctx->ref_off.p, ctx->ref_mem.p})) return rc;
+    ctx->ref_N = N;
+    ctx->ref_T = T;
+    ctx->ref_L = nleaf;
+    ctx->ref_nseg = (int32_t)nseg;
+    ctx->ref_shift = shift;
+    ctx->ref_nb = nb;
+    ctx->ref_ready = true;
+    return RFXP_OK;
+}
+
+extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t q_stride_t, int64_t Q,
+                         const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t exclude_base, int32_t K,
+                         int positive_only, int32_t* idx_out, uint16_t* cnt_out) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (!ctx->ref_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_topk: no reference set");
+    if (Q < 0 || K < 1) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk: need Q >= 0, K >= 1");
+    if (K > TOPK_MAX_K) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_topk: K above 64 is not supported");
+    if (Q == 0) return RFXP_OK;
+    if (Q > 0x7fffffffLL) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_topk: too many queries");
+    if (!q_leaf || !idx_out || !cnt_out || !is_device_pointer(q_leaf) || !is_device_pointer(idx_out) ||
+        !is_device_pointer(cnt_out) || (q_oob_words && !is_device_pointer(q_oob_words)))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk: pointers must be device pointers");
+    if (q_oob_words && q_oob_ld < (Q + 31) / 32)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk: q_oob_ld < ceil(Q/32)");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    TopkArgs a;
+    a.mem = ctx->ref_mem.p;
+    a.mem_bytes = (uint32_t)(((uint64_t)ctx->ref_T * (uint64_t)ctx->ref_N + MEM_PAD) * 4u);
+    a.off = ctx->ref_off.p;
+    a.nb = ctx->ref_nb;
+    a.N = ctx->ref_N;
+    a.T = ctx->ref_T;
+    a.L = ctx->ref_L;
+    a.nseg = ctx->ref_nseg;
+    a.shift = ctx->ref_shift;
+    a.qleaf = q_leaf;
+    a.qsi = q_stride_i;
+    a.qst = q_stride_t;
+    a.qoob = q_oob_words;
+    a.qold = q_oob_ld;
+    a.exclude_base = exclude_base;
+    a.K = K;
+    a.floor_key = positive_only ? 2 : 1;
+    a.idx_out = idx_out;
+    a.cnt_out = cnt_out;
+    hipError_t e;
+    {
+        LaunchTimer tm(ctx, "topk");
+        switch (a.shift) {
+            case 11: e = launch_topk<1>(ctx, a, Q); break;
+            case 12: e = launch_topk<2>(ctx, a, Q); break;
+            case 13: e = launch_topk<4>(ctx, a, Q); break;
+            case 14: e = launch_topk<8>(ctx, a, Q); break;
+            default: e = launch_topk<16>(ctx, a, Q); break;
+        }
+    }
+    if (e != hipSuccess) return hip_error(ctx, e, "k_topk launch");
+    return RFXP_OK;
+}

@@ -704,8 +704,8 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     RFXP_HIP(ctx, ctx->rinv.ensure(n1));
     RFXP_HIP(ctx, ctx->rrange.ensure(2));
     RFXP_HIP(ctx, ctx->flags.ensure(16));
-    LeafView v{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf};
-    if (int rc = pack_forest(ctx, v, nout)) return rc;
+    LeafView v{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf, 0, 0};
+    if (int rc = pack_forest(ctx, v, nout, PackTarget{ctx->bkt_off.p, ctx->bkt_mem.p})) return rc;
     ctx->forest_ready = true;
     return RFXP_OK;
 }

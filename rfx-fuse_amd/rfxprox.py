@@ -68,6 +68,8 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_nbytes.argtypes = [C.c_int, i64, i64, i64]
     L.rfxp_upper_nbytes.restype = i64
     L.rfxp_get_nout.argtypes = [vp, vp]
+    L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
+    L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
     _lib = L
     return L
 
@@ -171,6 +173,41 @@ class Context:
                                             oob_words.shape[1], n, t, nleaf, nptr))
         self.n = n
         self.t = t
+
+    def set_reference(self, leaf, n: int, t: int, nleaf: int, layout: str = "tree"):
+        """Reference set for top-K: leaf int32 device tensor, (T, N) for
+        layout 'tree' or (N, T) for 'sample'."""
+        import torch
+
+        assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
+        si, st = (1, n) if layout == "tree" else (t, 1)
+        self._check(self._L.rfxp_set_reference(self.h, leaf.data_ptr(), si, st, n, t, nleaf))
+        self.ref_n = n
+
+    def topk(self, qleaf, k: int, layout: str = "sample", oob_words=None, exclude_base: int = -1,
+             positive_only: bool = False):
+        """Top-k references per query: qleaf int32 device tensor, (Q, T) for
+        layout 'sample' or (T, Q) for 'tree'; oob_words (T, ceil(Q/32))
+        int32 device tensor restricting each query to its OOB trees.
+        Returns (idx int32 (Q, k), counts int16-viewed-uint16 (Q, k))."""
+        import torch
+
+        assert qleaf.dtype == torch.int32 and qleaf.is_cuda and qleaf.is_contiguous()
+        if layout == "sample":
+            q, t = qleaf.shape
+            si, st = t, 1
+        else:
+            t, q = qleaf.shape
+            si, st = 1, q
+        idx = torch.empty((q, k), dtype=torch.int32, device=qleaf.device)
+        cnt = torch.empty((q, k), dtype=torch.int16, device=qleaf.device)
+        optr, old = None, 0
+        if oob_words is not None:
+            assert oob_words.dtype == torch.int32 and oob_words.is_cuda and oob_words.is_contiguous()
+            optr, old = oob_words.data_ptr(), oob_words.shape[1]
+        self._check(self._L.rfxp_topk(self.h, qleaf.data_ptr(), si, st, q, optr, old, exclude_base, k,
+                                      int(positive_only), idx.data_ptr(), cnt.data_ptr()))
+        return idx, cnt
 
     def upper(self, fmt: int, out, r0: int = 0, r1: int | None = None, scale: float = 1.0,
               zp: float = 0.0):
