@@ -30,6 +30,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 CONFIGS = {
     "c3": dict(workload="C3 quantized uint8 upper triangle", n=100_000, t=500, nleaf=2048,
                p_oob=0.368, seed=20261201 + 3),
+    # top-K retrieval: a parity/measurement case,
+    # not the driver's bench line
+    "c5": dict(workload="C5 top-K retrieval", n=1_000_000, q=100_000, t=500, nleaf=2048, k=20,
+               seed=20261201 + 5),
 }
 
 
@@ -40,6 +44,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--n", type=int, default=None, help="override N (smaller smoke runs)")
+    ap.add_argument("--q", type=int, default=None, help="override the query count (c5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the bounded CPU-baseline sample")
@@ -143,6 +148,13 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
+    if args.config == "c5":
+        run_c5(args)
+        return
+    run_c3(args)
+
+
+def run_c3(args):
     import torch
 
     import rfxprox as R
@@ -219,6 +231,107 @@ def main():
         leaf_np = leaf.cpu().numpy()
         oob_np = oob.to(torch.uint8).cpu().numpy()
         rec["cpu_baseline"] = cpu_baseline(cfg, leaf_np, oob_np, n, scale, zp, args.cpu_seconds)
+    else:
+        rec["cpu_baseline"] = None
+    print(json.dumps(rec), flush=True)
+    ctx.close()
+
+
+def cpu_baseline_topk(cfg, ref_tn, q_qt, k, target_s):
+    """The oracle's top-K (OpenMP over queries, a dense count scan per query
+    like python/randomforest_py.cpp:2534-2558) on a bounded query sample."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    n_q = threads
+    t0 = time.perf_counter()
+    O.topk_all(ref_tn, q_qt[:n_q], k, threads=threads)
+    dt = time.perf_counter() - t0
+    if dt < target_s:
+        n_q = min(q_qt.shape[0], max(n_q, int(n_q * target_s / max(dt, 1e-3)) // threads * threads))
+        t0 = time.perf_counter()
+        O.topk_all(ref_tn, q_qt[:n_q], k, threads=threads)
+        dt = time.perf_counter() - t0
+    t, n = ref_tn.shape
+    return {
+        "value": n_q * n * t / dt,
+        "unit": "pair-tree comparisons/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_q} queries against all {n} references ({dt:.1f} s)",
+    }
+
+
+def run_c5(args):
+    """Top-K of K=20 references per query for Q queries against N references
+    over T trees (all trees, zeros included, ties by lower index).  The
+    reference index (rfxp_set_reference) is built once outside the timed
+    region; one step = rfxp_topk over all Q queries."""
+    import numpy as np
+    import torch
+
+    import rfxprox as R
+
+    cfg = CONFIGS["c5"]
+    n = args.n or cfg["n"]
+    q = args.q or cfg["q"]
+    t, nleaf, k = cfg["t"], cfg["nleaf"], cfg["k"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg["seed"])
+    ref = torch.randint(0, nleaf, (t, n), generator=g, device=dev, dtype=torch.int32)
+    qs = torch.randint(0, nleaf, (q, t), generator=g, device=dev, dtype=torch.int32)
+    ctx = R.Context(0)
+    ctx.use_torch_stream()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ctx.set_reference(ref, n, t, nleaf)
+    torch.cuda.synchronize()
+    index_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(args.warmup):
+        ctx.topk(qs, k)
+    torch.cuda.synchronize()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        ctx.topk(qs, k)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    kms, kn = ctx.kernel_time("topk")
+    k_avg = kms / max(kn, 1)
+    # algorithmic bytes of one launch: every member id of the query's T
+    # buckets (N/nleaf per bucket on average, 4 B) + the query labels + outputs
+    alg = q * t * (n / nleaf) * 4 + q * t * 4 + q * k * 6
+    achieved = alg / (k_avg / 1e3) / 1e9
+    rec = {
+        "metric": "pair-tree comparisons/sec (C5 top-K retrieval, Q x N x T)",
+        "value": q * n * t / (ms_step / 1e3),
+        "unit": "pair-tree comparisons/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u16",
+        "data": "synthetic (uniform 2048-leaf assignment, seeded)",
+        "config": {"workload": cfg["workload"], "N": n, "Q": q, "T": t, "leaves_per_tree": nleaf, "K": k},
+        "queries_per_s": q / (ms_step / 1e3),
+        "index_build_ms": index_ms,
+        "kernels_ms": {"topk_avg": k_avg},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+    }
+    ctx.set_timing(False)
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline_topk(cfg, ref.cpu().numpy(), qs.cpu().numpy(), k, args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)

@@ -59,12 +59,15 @@ struct TopkArgs {
     uint16_t* cnt_out;
 };
 
-// LDS layout: counters (S/2 words) | dummy words (1024) | reduction scratch.
+// LDS layout: counters (S/2 words) | dummy words (1024) | per-segment
+// bucket records of up to 1024 trees (offset, length) | reduction scratch |
+// candidate and running lists.
 __host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) { return (1u << shift) * 2u; }
+constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
 constexpr uint32_t TOPK_RED_WORDS = 64;                     // wave partials
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
-    return topk_dummy_off(shift) + TOPK_THREADS * 4 + (TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
+    return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
 }
 
 typedef __attribute__((address_space(3))) uint32_t lds_w;
@@ -94,53 +97,43 @@ __device__ __forceinline__ void query_bucket(const TopkArgs& a, int64_t q, int32
     len4 = 4u * (o1 - o0);
 }
 
-// Counts the query's buckets of segment s into 16-bit counters: the
-// counter of reference lo + c is the 16-bit unit c.  Lanes past a bucket's
-// end read 0 (buffer range), which is no member; they and any member outside
-// the segment add into the thread's dummy word.
-__device__ void topk_hits(const TopkArgs& a, int64_t q, int32_t s, uint32_t lo, uint32_t width, uint32_t dummy) {
-    const uint32_t lane = threadIdx.x & 63, lane4 = lane * 4u;
-    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int32_t ng = (a.T + 15) >> 4;
-    const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
-    const uint32_t base1 = lo + 1u;
-    for (int32_t g = g0; g < g1; ++g) {
-        uint32_t m[16];
+__device__ __forceinline__ void count16(uint32_t m, uint32_t base1, uint32_t width, uint32_t dummy) {
+    // m = j + 1 (0: no member); 16-bit counter unit c = j - lo
+    const uint32_t c = m - base1;
+    const bool h = c < width;
+    lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
+}
+
+// 16 bucket loads of record group g (records rec_off/rec_len in LDS); a
+// group outside [.., g1) loads nothing.  Returns whether a bucket of the
+// group has more than 64 members.
+__device__ __forceinline__ bool load16(const TopkArgs& a, const uint32_t* rec_off, const uint32_t* rec_len, int32_t g,
+                                       bool ok, uint32_t lane4, uint32_t (&m)[16]) {
+    bool lng = false;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            uint32_t soff, len4;
-            query_bucket(a, q, 16 * g + u, s, soff, len4);
-            soff = __builtin_amdgcn_readfirstlane(soff);
-            len4 = __builtin_amdgcn_readfirstlane(len4);
-            m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, soff + len4), lane4, soff, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const uint32_t c = m[u] - base1;
-            const bool h = c < width;
-            lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
-        }
-        // buckets of more than 64 references in this segment
-        for (int u = 0; u < 16; ++u) {
-            uint32_t soff, len4;
-            query_bucket(a, q, 16 * g + u, s, soff, len4);
-            soff = __builtin_amdgcn_readfirstlane(soff);
-            len4 = __builtin_amdgcn_readfirstlane(len4);
-            if (len4 <= 256u) continue;
-            const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, soff + len4);
-            for (uint32_t p4 = 256u; p4 < len4; p4 += 256u) {
-                const uint32_t mm = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, soff, 0);
-                const uint32_t c = mm - base1;
-                const bool h = c < width;
-                lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
-            }
-        }
+    for (int u = 0; u < 16; ++u) {
+        const uint32_t soff = ok ? __builtin_amdgcn_readfirstlane(rec_off[16 * g + u]) : 0u;
+        const uint32_t len4 = ok ? __builtin_amdgcn_readfirstlane(rec_len[16 * g + u]) : 0u;
+        lng |= len4 > 256u;
+        m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, soff + len4), lane4, soff, 0);
+    }
+    return lng;
+}
+
+__device__ __forceinline__ void tails16(const TopkArgs& a, const uint32_t* rec_off, const uint32_t* rec_len, int32_t g,
+                                        uint32_t lane4, uint32_t base1, uint32_t width, uint32_t dummy) {
+    for (int u = 0; u < 16; ++u) {
+        const uint32_t len4 = __builtin_amdgcn_readfirstlane(rec_len[16 * g + u]);
+        if (len4 <= 256u) continue;
+        const uint32_t soff = __builtin_amdgcn_readfirstlane(rec_off[16 * g + u]);
+        const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, soff + len4);
+        for (uint32_t p4 = 256u; p4 < len4; p4 += 256u)
+            count16((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, soff, 0), base1, width, dummy);
     }
 }
 
 // Block reductions through `red` (TOPK_RED_WORDS words); every thread gets
-// the result.  Each begins with a barrier-free wave step and uses two
-// barriers.
+// the result.  Each uses two barriers.
 __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) v += (uint32_t)__shfl_xor((int)v, d, 64);
@@ -188,12 +181,15 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
     return before + incl - v;
 }
 
-// Number of this thread's keys (16-bit halves of kw[0..nw)) >= c.
+// Number of this thread's keys (16-bit halves of its NW key words) >= c.
 template <int NW>
-__device__ __forceinline__ uint32_t count_ge(const uint32_t (&kw)[NW], uint32_t c) {
+__device__ __forceinline__ uint32_t count_ge(const uint32_t* kw, uint32_t c) {
     uint32_t n = 0;
 #pragma unroll
-    for (int k = 0; k < NW; ++k) n += ((kw[k] & 0xffffu) >= c) + ((kw[k] >> 16) >= c);
+    for (int k = 0; k < NW; ++k) {
+        const uint32_t w = kw[k];
+        n += ((w & 0xffffu) >= c) + ((w >> 16) >= c);
+    }
     return n;
 }
 
@@ -207,72 +203,97 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     extern __shared__ uint32_t sm[];
     const int32_t shift = a.shift;
     const uint32_t S = 1u << shift;
-    uint32_t* const red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
+    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
+    uint32_t* const rec_len = rec_off + TOPK_THREADS;
+    uint32_t* const red = rec_len + TOPK_THREADS;
     uint32_t* const cand_k = red + TOPK_RED_WORDS;  // candidates of a segment
     uint32_t* const cand_i = cand_k + TOPK_MAX_K;
     uint32_t* const run_k = cand_i + TOPK_MAX_K;    // running top-K (sorted)
     uint32_t* const run_i = run_k + TOPK_MAX_K;
     uint32_t* const nrun_p = run_i + TOPK_MAX_K;
+    uint32_t* const kw = sm + threadIdx.x * NW;     // this thread's counter / key words
     const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
+    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t q = blockIdx.x;
     const uint32_t K = (uint32_t)a.K;
     const int64_t ex = a.exclude_base >= 0 ? a.exclude_base + q : -1;
 
-    if (threadIdx.x == 0) *nrun_p = 0u;
-    uint32_t nrun = 0;      // entries in the running list (uniform)
-    uint32_t kmin = 0;      // key of the running K-th entry once the list is full
+    uint32_t nrun = 0;  // entries in the running list (uniform)
+    uint32_t kmin = 0;  // key of the running K-th entry once the list is full
     for (int32_t s = 0; s < a.nseg; ++s) {
         const uint32_t lo = (uint32_t)s << shift;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        const uint32_t base1 = lo + 1u;
         uint4* c4 = (uint4*)sm;
         for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
         sm[dummy >> 2] = 0u;
-        __syncthreads();
-        topk_hits(a, q, s, lo, width, dummy);
-        __syncthreads();
-        // this thread's counters: units [tid*2*NW, (tid+1)*2*NW) -> keys
-        uint32_t kw[NW];
+        for (int32_t tc = 0; tc < a.T; tc += TOPK_THREADS) {
+            // the query's bucket records of trees tc .. tc+1023, one per thread
+            uint32_t soff, len4;
+            query_bucket(a, q, tc + (int32_t)threadIdx.x, s, soff, len4);
+            rec_off[threadIdx.x] = soff;
+            rec_len[threadIdx.x] = len4;
+            __syncthreads();
+            const int32_t nt = min(a.T - tc, TOPK_THREADS);
+            const int32_t ng = (nt + 15) >> 4;
+            const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
+            // two groups in ping-pong: one is counted while the other loads
+            uint32_t A[16], B[16];
+            bool la = load16(a, rec_off, rec_len, g0, g0 < g1, lane4, A);
+            for (int32_t g = g0; g < g1; g += 2) {
+                const bool lb = load16(a, rec_off, rec_len, g + 1, g + 1 < g1, lane4, B);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
+                if (la) tails16(a, rec_off, rec_len, g, lane4, base1, width, dummy);
+                la = load16(a, rec_off, rec_len, g + 2, g + 2 < g1, lane4, A);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
+                if (lb) tails16(a, rec_off, rec_len, g + 1, lane4, base1, width, dummy);
+            }
+            __syncthreads();
+        }
+        // counters -> keys in place: count + 1, or 0 where the reference may
+        // not be chosen (past the end, or excluded)
         const uint32_t u0 = threadIdx.x * 2u * NW;
+        uint32_t mloc = 0;
 #pragma unroll
         for (int k = 0; k < NW; ++k) {
-            const uint32_t w = sm[threadIdx.x * NW + k];
+            const uint32_t w = kw[k];
             const uint32_t ua = u0 + 2u * k, ub = ua + 1u;
             const bool va = ua < width && (int64_t)(lo + ua) != ex;
             const bool vb = ub < width && (int64_t)(lo + ub) != ex;
             const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
             const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
             kw[k] = ka | (kb << 16);
+            mloc = max(mloc, max(ka, kb));
         }
         // only keys above the running threshold can enter the list
         const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-        uint32_t mloc = 0;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) mloc = max(mloc, max(kw[k] & 0xffffu, kw[k] >> 16));
         const uint32_t M = block_max(mloc, red);
-        if (M >= lowest) {
-            // cstar: the largest level in [lowest, M] with at least `need`
-            // keys >= cstar (need = K - nothing: the merge keeps the best K
-            // of running + candidates, so K candidates always suffice)
-            uint32_t lo_c = lowest, hi_c = M;  // f(lo_c) > 0
-            uint32_t cstar = lowest;
-            if (block_sum(count_ge(kw, lowest), red) > K) {
-                // f(lowest) > K: binary search the largest c with f(c) >= K
-                while (lo_c < hi_c) {
-                    const uint32_t mid = (lo_c + hi_c + 1u) / 2u;
-                    if (block_sum(count_ge(kw, mid), red) >= K) lo_c = mid;
-                    else hi_c = mid - 1u;
-                }
-                cstar = lo_c;
+        if (M < lowest) continue;
+        // cstar: keys > cstar all enter, keys == cstar in index order up to K
+        uint32_t cstar = lowest;
+        if (block_sum(count_ge<NW>(kw, lowest), red) > K) {
+            uint32_t lo_c = lowest, hi_c = M;  // largest c with #(>= c) >= K
+            while (lo_c < hi_c) {
+                const uint32_t mid = (lo_c + hi_c + 1u) / 2u;
+                if (block_sum(count_ge<NW>(kw, mid), red) >= K) lo_c = mid;
+                else hi_c = mid - 1u;
             }
-            // keys > cstar all go in; keys == cstar in index order up to K
-            const uint32_t ngt = count_ge(kw, cstar + 1u);
-            const uint32_t neq = count_ge(kw, cstar) - ngt;
-            uint32_t G, E;
-            const uint32_t pgt = block_excl_scan(ngt, red, &G);
-            const uint32_t peq = block_excl_scan(neq, red, &E);
-            const uint32_t take = min(E, K - G);
-            uint32_t rg = pgt, re = peq;
-#pragma unroll
+            cstar = lo_c;
+        }
+        const uint32_t ngt = count_ge<NW>(kw, cstar + 1u);
+        const uint32_t neq = count_ge<NW>(kw, cstar) - ngt;
+        uint32_t G, E;
+        const uint32_t pgt = block_excl_scan(ngt, red, &G);
+        const uint32_t peq = block_excl_scan(neq, red, &E);
+        const uint32_t take = min(E, K - G);
+        uint32_t rg = pgt, re = peq;
+        if (ngt + neq) {
+#pragma unroll 1
             for (int k = 0; k < 2 * NW; ++k) {
                 const uint32_t key = (kw[k >> 1] >> (16 * (k & 1))) & 0xffffu;
                 const uint32_t j = lo + u0 + (uint32_t)k;
@@ -280,7 +301,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                     cand_k[rg] = key;
                     cand_i[rg] = j;
                     ++rg;
-                } else if (key == cstar && key >= lowest) {
+                } else if (key == cstar) {
                     if (re < take) {
                         cand_k[G + re] = key;
                         cand_i[G + re] = j;
@@ -288,48 +309,48 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                     ++re;
                 }
             }
-            __syncthreads();
-            // merge by rank (first wave): running entries precede candidates
-            // of equal key, since they have lower indices
-            const uint32_t nc = G + take;
-            if (threadIdx.x < 64) {
-                const uint32_t ntot = nrun + nc;
-                uint32_t mk[4], mi[4], rk[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t e = threadIdx.x + 64u * r;
-                    mk[r] = 0u;
-                    mi[r] = 0xffffffffu;
-                    if (e < nrun) {
-                        mk[r] = run_k[e];
-                        mi[r] = run_i[e];
-                    } else if (e < ntot) {
-                        mk[r] = cand_k[e - nrun];
-                        mi[r] = cand_i[e - nrun];
-                    }
-                    uint32_t rank = 0;
-                    for (uint32_t f = 0; f < ntot; ++f) {
-                        const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
-                        const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
-                        rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
-                    }
-                    rk[r] = e < ntot ? rank : 0xffffffffu;
-                }
-                // one wave: its reads of the old list precede these writes
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (rk[r] < K) {
-                        run_k[rk[r]] = mk[r];
-                        run_i[rk[r]] = mi[r];
-                    }
-                }
-                if (threadIdx.x == 0) *nrun_p = min(ntot, K);
-            }
-            __syncthreads();
-            nrun = *nrun_p;
-            kmin = nrun ? run_k[nrun - 1] : 0u;
-            __syncthreads();
         }
+        __syncthreads();
+        // merge by rank (first wave): running entries precede candidates of
+        // equal key, since they have lower indices
+        const uint32_t nc = G + take;
+        if (threadIdx.x < 64) {
+            const uint32_t ntot = nrun + nc;
+            uint32_t mk[4], mi[4], rk[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t e = threadIdx.x + 64u * r;
+                mk[r] = 0u;
+                mi[r] = 0xffffffffu;
+                if (e < nrun) {
+                    mk[r] = run_k[e];
+                    mi[r] = run_i[e];
+                } else if (e < ntot) {
+                    mk[r] = cand_k[e - nrun];
+                    mi[r] = cand_i[e - nrun];
+                }
+                uint32_t rank = 0;
+                for (uint32_t f = 0; f < ntot; ++f) {
+                    const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
+                    const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
+                    rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
+                }
+                rk[r] = e < ntot ? rank : 0xffffffffu;
+            }
+            // one wave: its reads of the old list precede these writes
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (rk[r] < K) {
+                    run_k[rk[r]] = mk[r];
+                    run_i[rk[r]] = mi[r];
+                }
+            }
+            if (threadIdx.x == 0) *nrun_p = min(ntot, K);
+        }
+        __syncthreads();
+        nrun = *nrun_p;
+        kmin = nrun ? run_k[nrun - 1] : 0u;
+        __syncthreads();
     }
     if (threadIdx.x < K) {
         const bool have = threadIdx.x < nrun;
