@@ -147,6 +147,25 @@ int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t 
               const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t exclude_base, int32_t K,
               int positive_only, int32_t* idx_out, uint16_t* cnt_out);
 
+/* ---- low-rank form of the all-trees proximity ---------------------------- */
+
+/* Y = P V with P = A A^T / T, A the N x (T*nleaf) one-hot leaf matrix of the
+ * reference set (rfxp_set_reference; P_ij = fraction of trees in which i and
+ * j share a leaf, P_ii = 1 for valid labels):
+ *   Y_i = (1/T) sum_t W_t[leaf_i(t)],  W_t[l] = sum_{j: leaf_j(t) = l} V_j.
+ * V, Y: device, N x r row-major fp32, 1 <= r <= 64, not aliased.  Reads the
+ * leaf matrix given to rfxp_set_reference, which must still be valid.
+ * The SpMM contract of the reference's LowRankProximityMatrix
+ * (include/rf_proximity_lowrank.hpp:27-433), without forming P. */
+int rfxp_lowrank_pv(rfxp_ctx* ctx, const float* V, int32_t r, float* Y);
+
+/* Subspace iteration for a rank-r factor of P (1 <= r <= 32):
+ *   Q_0 = orth(V0), Q_k = orth(P Q_{k-1}) for k = 1..iters, B = Q^T P Q,
+ * orth = QR with a positive diagonal of R (CholeskyQR2), so P ~ Q B Q^T.
+ * V0, Q: device N x r fp32 (distinct); B: host r x r double, row-major.
+ * Synchronises the context stream. */
+int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, int32_t iters, float* Q, double* B);
+
 #ifdef __cplusplus
 }
 #endif

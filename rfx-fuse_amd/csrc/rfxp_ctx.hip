@@ -153,6 +153,14 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->flags.release();
     ctx->ref_off.release();
     ctx->ref_mem.release();
+    ctx->lr_start.release();
+    ctx->lr_tot.release();
+    ctx->lr_pmap.release();
+    ctx->lr_w.release();
+    ctx->lr_z.release();
+    ctx->lr_tmp.release();
+    ctx->lr_part.release();
+    ctx->lr_rinv.release();
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();
     delete ctx;

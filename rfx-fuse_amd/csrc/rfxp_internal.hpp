@@ -80,6 +80,14 @@ struct rfxp_ctx {
     int32_t ref_T = 0, ref_L = 0, ref_nseg = 0, ref_shift = 0, ref_nb = 0;
     DevBuf<int32_t> ref_off;   // T x (nb+1): bucket b = leaf*nseg + segment
     DevBuf<uint32_t> ref_mem;  // T x N (+ padding)
+    const int32_t* ref_leaf = nullptr;  // the caller's leaf matrix (low-rank reads it)
+    int64_t ref_si = 0, ref_st = 0;
+
+    // low-rank (rfxp_lowrank_*)
+    bool lr_index_ready = false;
+    DevBuf<int32_t> lr_start, lr_tot, lr_pmap;  // piece index of the reference set
+    DevBuf<float> lr_w, lr_z, lr_tmp;           // W = A^T V, iteration block, scratch
+    DevBuf<double> lr_part, lr_rinv;            // Gram partials, R^-1
 
     // timing
     bool timing = false;

@@ -399,6 +399,10 @@ extern "C" int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t st
     ctx->ref_nseg = (int32_t)nseg;
     ctx->ref_shift = shift;
     ctx->ref_nb = nb;
+    ctx->ref_leaf = leaf;
+    ctx->ref_si = stride_i;
+    ctx->ref_st = stride_t;
+    ctx->lr_index_ready = false;
     ctx->ref_ready = true;
     return RFXP_OK;
 }

@@ -70,6 +70,8 @@ def load(path: str = LIB_PATH):
     L.rfxp_get_nout.argtypes = [vp, vp]
     L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
     L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
+    L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
+    L.rfxp_lowrank_subspace.argtypes = [vp, vp, i32, i32, vp, vp]
     _lib = L
     return L
 
@@ -208,6 +210,30 @@ class Context:
         self._check(self._L.rfxp_topk(self.h, qleaf.data_ptr(), si, st, q, optr, old, exclude_base, k,
                                       int(positive_only), idx.data_ptr(), cnt.data_ptr()))
         return idx, cnt
+
+    def lowrank_pv(self, V):
+        """Y = P V for the reference set (P = A A^T / T): V float32 device
+        tensor (N, r), r <= 64."""
+        import torch
+
+        assert V.dtype == torch.float32 and V.is_cuda and V.is_contiguous() and V.dim() == 2
+        Y = torch.empty_like(V)
+        self._check(self._L.rfxp_lowrank_pv(self.h, V.data_ptr(), V.shape[1], Y.data_ptr()))
+        return Y
+
+    def lowrank_subspace(self, V0, iters: int):
+        """Rank-r factor (Q, B) of P by subspace iteration; V0 float32 device
+        (N, r), r <= 32.  Returns Q (device, N x r) and B (numpy r x r)."""
+        import numpy as np
+        import torch
+
+        assert V0.dtype == torch.float32 and V0.is_cuda and V0.is_contiguous() and V0.dim() == 2
+        r = V0.shape[1]
+        Q = torch.empty_like(V0)
+        B = np.zeros((r, r), dtype=np.float64)
+        self._check(self._L.rfxp_lowrank_subspace(self.h, V0.data_ptr(), r, iters, Q.data_ptr(),
+                                                  B.ctypes.data))
+        return Q, B
 
     def upper(self, fmt: int, out, r0: int = 0, r1: int | None = None, scale: float = 1.0,
               zp: float = 0.0):

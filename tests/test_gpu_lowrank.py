@@ -1,0 +1,107 @@
+"""GPU low-rank path (rfxp_lowrank_pv, rfxp_lowrank_subspace) against the
+oracle's double-precision one-hot SpMM (pinned in tests/test_oracle.py to the
+dense product A A^T V / T) and a numpy subspace iteration in double.
+Tolerances: P V within 1e-5 relative Frobenius (fp32 sums of at most T*N
+terms); Q B Q^T V within 1e-4 relative Frobenius, as the north star states."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def zipf_leaves(rng, n, t, nleaf, s=1.1):
+    p = 1.0 / np.arange(1, nleaf + 1) ** s
+    p /= p.sum()
+    leaf = np.empty((t, n), dtype=np.int32)
+    for k in range(t):
+        perm = rng.permutation(nleaf).astype(np.int32)
+        leaf[k] = perm[rng.choice(nleaf, size=n, p=p)]
+    return leaf
+
+
+def dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def rel_fro(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("n,t,nleaf,r", [(1, 1, 1, 1), (300, 7, 5, 3), (5000, 20, 40, 32),
+                                         (20000, 12, 64, 17), (9000, 9, 3, 64)])
+def test_pv_matches_oracle(gpu_ctx, n, t, nleaf, r):
+    rng = np.random.default_rng(n + r)
+    leaf = zipf_leaves(rng, n, t, nleaf)   # skewed: the big leaves span several pieces
+    if n > 100:
+        leaf[rng.random((t, n)) < 0.03] = -1
+    V = rng.standard_normal((n, r)).astype(np.float32)
+    lt = dev(leaf)
+    gpu_ctx.set_reference(lt, n, t, nleaf)
+    Y = gpu_ctx.lowrank_pv(dev(V)).cpu().numpy()
+    want = O.lowrank_pv(leaf, nleaf, V.astype(np.float64))
+    assert rel_fro(Y.astype(np.float64), want) < 1e-5
+
+
+def numpy_subspace(leaf, nleaf, V0, iters):
+    def orth(X):
+        Q, R = np.linalg.qr(X)
+        return Q * np.sign(np.diag(R))
+
+    Q = orth(V0.astype(np.float64))
+    for _ in range(iters):
+        Q = orth(O.lowrank_pv(leaf, nleaf, Q))
+    B = Q.T @ O.lowrank_pv(leaf, nleaf, Q)
+    return Q, B
+
+
+def test_subspace_matches_numpy(gpu_ctx):
+    rng = np.random.default_rng(4)
+    n, t, nleaf, r, iters = 6000, 30, 24, 8, 5
+    leaf = zipf_leaves(rng, n, t, nleaf)
+    V0 = rng.standard_normal((n, r)).astype(np.float32)
+    lt = dev(leaf)
+    gpu_ctx.set_reference(lt, n, t, nleaf)
+    Q, B = gpu_ctx.lowrank_subspace(dev(V0), iters)
+    Q = Q.cpu().numpy().astype(np.float64)
+    Qw, Bw = numpy_subspace(leaf, nleaf, V0, iters)
+    assert np.abs(Q.T @ Q - np.eye(r)).max() < 1e-5
+    Vt = rng.standard_normal((n, r))
+    assert rel_fro(Q @ (B @ (Q.T @ Vt)), Qw @ (Bw @ (Qw.T @ Vt))) < 1e-4
+
+
+def test_c4_shape_properties(gpu_ctx):
+    """Config C4 shape (N=1M, T=500, 4096 leaves, Zipf(1.1) sizes, a label
+    permutation per tree) through properties the size does not change:
+    P 1 = (1/T) sum_t |leaf_i(t)| exactly (in fp32 rounding), and P is
+    symmetric (u . P v = v . P u)."""
+    import torch
+
+    n, t, nleaf = 1_000_000, 500, 4096
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(20261201 + 4)
+    p = 1.0 / torch.arange(1, nleaf + 1, dtype=torch.float64) ** 1.1
+    p = (p / p.sum()).to("cuda:0")
+    leaf = torch.empty((t, n), dtype=torch.int32, device="cuda:0")
+    for k in range(t):
+        perm = torch.randperm(nleaf, generator=g, device="cuda:0").to(torch.int32)
+        leaf[k] = perm[torch.multinomial(p, n, replacement=True, generator=g)]
+    gpu_ctx.set_reference(leaf, n, t, nleaf)
+    ones = torch.ones((n, 8), dtype=torch.float32, device="cuda:0")
+    Y = gpu_ctx.lowrank_pv(ones)
+    sizes = torch.zeros((t, nleaf), dtype=torch.float64, device="cuda:0")
+    sizes.scatter_add_(1, leaf.long(), torch.ones((t, n), dtype=torch.float64, device="cuda:0"))
+    want = torch.gather(sizes, 1, leaf.long()).sum(0) / t
+    err = ((Y[:, 0].double() - want).abs() / want).max().item()
+    assert err < 1e-5
+    assert (Y == Y[:, :1]).all()
+    u = torch.randn((n, 4), generator=g, device="cuda:0")
+    v = torch.randn((n, 4), generator=g, device="cuda:0")
+    Pu, Pv = gpu_ctx.lowrank_pv(u), gpu_ctx.lowrank_pv(v)
+    a = (u.double() * Pv.double()).sum(0)
+    b = (v.double() * Pu.double()).sum(0)
+    scale = u.double().norm(dim=0) * Pv.double().norm(dim=0)
+    assert ((a - b).abs() / scale).max().item() < 1e-5
