@@ -34,6 +34,9 @@ CONFIGS = {
     # not the driver's bench line
     "c5": dict(workload="C5 top-K retrieval", n=1_000_000, q=100_000, t=500, nleaf=2048, k=20,
                seed=20261201 + 5),
+    # low-rank SpMM: measurement case
+    "c4": dict(workload="C4 low-rank P V and rank-32 subspace iteration", n=1_000_000, t=500, nleaf=4096,
+               r=32, iters=5, zipf=1.1, seed=20261201 + 4),
 }
 
 
@@ -150,6 +153,9 @@ def main():
         return
     if args.config == "c5":
         run_c5(args)
+        return
+    if args.config == "c4":
+        run_c4(args)
         return
     run_c3(args)
 
@@ -332,6 +338,102 @@ def run_c5(args):
     ctx.set_timing(False)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline_topk(cfg, ref.cpu().numpy(), qs.cpu().numpy(), k, args.cpu_seconds)
+    else:
+        rec["cpu_baseline"] = None
+    print(json.dumps(rec), flush=True)
+    ctx.close()
+
+
+def run_c4(args):
+    """One step = rfxp_lowrank_pv (Y = A (A^T V) / T) on an N x 32 block;
+    also reported: the 5-iteration subspace run to a rank-32 factor.  The
+    reference index (rfxp_set_reference) is built once outside the timed
+    region."""
+    import numpy as np
+    import torch
+
+    import rfxprox as R
+
+    cfg = CONFIGS["c4"]
+    n = args.n or cfg["n"]
+    t, nleaf, r = cfg["t"], cfg["nleaf"], cfg["r"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg["seed"])
+    p = 1.0 / torch.arange(1, nleaf + 1, dtype=torch.float64) ** cfg["zipf"]
+    p = (p / p.sum()).to(dev)
+    leaf = torch.empty((t, n), dtype=torch.int32, device=dev)
+    for k in range(t):
+        perm = torch.randperm(nleaf, generator=g, device=dev).to(torch.int32)
+        leaf[k] = perm[torch.multinomial(p, n, replacement=True, generator=g)]
+    V = torch.randn((n, r), generator=g, device=dev, dtype=torch.float32)
+    ctx = R.Context(0)
+    ctx.use_torch_stream()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ctx.set_reference(leaf, n, t, nleaf)
+    ctx.lowrank_pv(V)            # also builds the piece index
+    torch.cuda.synchronize()
+    index_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(args.warmup):
+        ctx.lowrank_pv(V)
+    torch.cuda.synchronize()
+    ctx.set_timing(True)
+    ctx.reset_timing()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        ctx.lowrank_pv(V)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    w_ms = ctx.kernel_time("lr_w")[0] / args.steps
+    y_ms = ctx.kernel_time("lr_y")[0] / args.steps
+    ctx.set_timing(False)
+    t0 = time.perf_counter()
+    Q, B = ctx.lowrank_subspace(V, cfg["iters"])
+    torch.cuda.synchronize()
+    sub_ms = (time.perf_counter() - t0) * 1e3
+    # algorithmic bytes of one P V: leaves read twice (A^T V and A W), the V
+    # rows gathered once per (sample, tree) in A^T V and the W rows once per
+    # (sample, tree) in A W (r*4 B each), Y written
+    alg = 2 * n * t * 4 + 2 * n * t * r * 4 + n * r * 4
+    achieved = alg / (ms_step / 1e3) / 1e9
+    rec = {
+        "metric": "one-hot SpMM P V throughput (C4, N x T x r multiply-adds)",
+        "value": 2 * n * t * r / (ms_step / 1e3),
+        "unit": "multiply-adds/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (Zipf(1.1) leaf sizes, per-tree label permutation, V ~ N(0,1), seeded)",
+        "config": {"workload": cfg["workload"], "N": n, "T": t, "leaves_per_tree": nleaf, "r": r,
+                   "iters": cfg["iters"]},
+        "kernels_ms": {"lr_w": w_ms, "lr_y": y_ms},
+        "subspace_ms": sub_ms,
+        "index_build_ms": index_ms,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "ritz_top": float(np.max(np.linalg.eigvalsh((B + B.T) / 2))),
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+
+        # the oracle's single-thread SpMM on a tree subset, scaled to T trees
+        tt = 4
+        lf = leaf[:tt].cpu().numpy()
+        Vd = V.cpu().numpy().astype(np.float64)
+        c0 = time.perf_counter()
+        O.lowrank_pv(lf, nleaf, Vd)
+        dt = (time.perf_counter() - c0) * t / tt
+        rec["cpu_baseline"] = {"value": 2 * n * t * r / dt, "unit": "multiply-adds/s", "cores": 1, "kind": "port",
+                               "sample": f"{tt} of {t} trees at full N, scaled linearly"}
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)
