@@ -166,6 +166,62 @@ int rfxp_lowrank_pv(rfxp_ctx* ctx, const float* V, int32_t r, float* Y);
  * Synchronises the context stream. */
 int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, int32_t iters, float* Q, double* B);
 
+/* ---- per-tree and dense small-N operations -------------------------------
+ * A tree is (nodestatus[nnode], nodextr[N], nin[N]): sample n lies in node
+ * nodextr[n], which takes part when nodestatus of it is -1 (terminal);
+ * nin[n] is its bootstrap multiplicity, 0 when out-of-bag.  These arrays
+ * may be host or device pointers. */
+
+/* The OOB x in-bag pairs of one tree as (n + kk*N, w), the terms that
+ * rf::cpu_proximity adds into its column-major N x N matrix
+ * (src/rf_proximity.cpp:99-231, dense branch): OOB n, in-bag kk of n's
+ * terminal node, w = casewise ? nin[kk]/nodesize : 1, nodes with nodesize
+ * = 0 skipped when casewise.  *idx_host / *w_host point into host memory
+ * owned by the context, valid until its next call. */
+int rfxp_tree_pairs(rfxp_ctx* ctx, const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin,
+                    int32_t N, int32_t nnode, int casewise, int64_t** idx_host, double** w_host, int64_t* npairs);
+
+/* prox[idx] += w over the pairs of rfxp_tree_pairs: one call of
+ * rf::cpu_proximity / rf::gpu_proximity (include/rf_proximity.hpp:10-21) on
+ * the caller's host matrix prox (N x N, column-major). */
+int rfxp_tree_accumulate(rfxp_ctx* ctx, const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin,
+                         int32_t N, int32_t nnode, int casewise, double* prox);
+
+/* One tree's packed upper triangle over the first np samples (np = n_real
+ * when 0 < n_real < N, else N), zeroed first, host or device output, in the
+ * per-tree formats of cuda/rf_proximity_upper_triangle.cu:
+ *   RFXP_FMT_F16: OOB n x in-bag kk, entry = half(w), w as above in float
+ *                 (gpu_proximity_upper_triangle_fp16, :149-285);
+ *   RFXP_FMT_NF4: the same pairs, entry = fp32_to_nf4(w) (:368-519);
+ *   RFXP_FMT_I8:  every sample n with a terminal node x in-bag kk,
+ *                 entry += fp32_to_int8(nin[kk]/nodesize, scale, zp)
+ *                 modulo 256 (:288-365).
+ * A device output is written in place when 4-byte aligned with a byte size
+ * divisible by 4, else through a staging buffer; exactly the triangle's
+ * bytes are written either way. */
+int rfxp_tree_upper(rfxp_ctx* ctx, int fmt, const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin,
+                    int32_t N, int32_t nnode, int casewise, int32_t n_real, float scale, float zp, void* out);
+
+/* One tree's RF-GAP contributions as an FP16 packed upper triangle over the
+ * first np samples (cuda/rf_proximity_upper_triangle.cu:1621-1660): OOB i,
+ * in-bag j >= i of the same node (raw nodextr values, >= 0), entry =
+ * half(c_j / sum c over the node's in-bag samples). */
+int rfxp_rfgap_tree_upper(rfxp_ctx* ctx, const int32_t* nin, const int32_t* nodextr, int32_t N, int32_t n_real,
+                          uint16_t* out);
+
+/* rf::cpu_finishprox (src/rf_finishprox.cpp:12-74) on dense N x N
+ * column-major matrices (host or device): proxsym_ii = 1, and for i != j
+ * the reference's symmetrise / nout-normalise / symmetrise in the same IEEE
+ * double operations. */
+int rfxp_finishprox(rfxp_ctx* ctx, int32_t N, const int32_t* nout, const double* prox, double* proxsym);
+
+/* rf::cpu_proximity_rfgap (src/rf_proximity.cpp:238-397): RF-GAP proximity
+ * of T trees given tree-major nin / nodextr [t*N + i], into the dense N x N
+ * column-major prox (host or device), symmetrised; each entry summed over
+ * trees in ascending order as the reference does. */
+int rfxp_rfgap(rfxp_ctx* ctx, int32_t T, int32_t N, const int32_t* nin_flat, const int32_t* nodextr_flat,
+               double* prox);
+
 #ifdef __cplusplus
 }
 #endif

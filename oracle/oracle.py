@@ -81,6 +81,9 @@ def lib():
                                    _i32, _u16, _f32]
         L.orc_topk_oob.restype = C.c_int32
         L.orc_lowrank_pv.argtypes = [_i32, C.c_int64, C.c_int32, C.c_int32, _f64, C.c_int32, _f64]
+        L.orc_tree_upper.argtypes = [C.c_int, _i32, _i32, _i32, C.c_int32, C.c_int32, C.c_int, C.c_int32,
+                                     C.c_float, C.c_float, C.c_void_p]
+        L.orc_rfgap_tree_upper.argtypes = [_i32, _i32, C.c_int32, C.c_int32, C.c_void_p]
         _lib = L
     return _lib
 
@@ -271,6 +274,30 @@ def topk_oob(leaf_tn, oob_tn, q, K, exclude_self=True):
     m = lib().orc_topk_oob(_c(leaf_tn, np.int32).ravel(), _c(oob_tn, np.uint8).ravel(), n, t, q, K,
                            int(exclude_self), idx, cnt, sc)
     return idx[:m], cnt[:m], sc[:m]
+
+
+# ---- per-tree triangles -------------------------------------------------------
+
+def tree_upper(fmt, nodestatus, nodextr, nin, casewise=False, n_real=0, scale=1.0, zp=0.0):
+    """One tree's packed triangle in the reference per-tree formats
+    (FMT_F16 -> uint16, FMT_I8 -> int8, FMT_NF4 -> packed uint8)."""
+    n = len(nodextr)
+    np_ = n_real if 0 < n_real < n else n
+    ne = np_ * (np_ + 1) // 2
+    out = {FMT_F16: np.zeros(ne, np.uint16), FMT_I8: np.zeros(ne, np.int8),
+           FMT_NF4: np.zeros((ne + 1) // 2, np.uint8)}[fmt]
+    lib().orc_tree_upper(fmt, _c(nodestatus, np.int32), _c(nodextr, np.int32), _c(nin, np.int32), n,
+                         len(nodestatus), int(casewise), n_real, C.c_float(scale), C.c_float(zp),
+                         out.ctypes.data)
+    return out
+
+
+def rfgap_tree_upper(nin, nodextr, n_real=0):
+    n = len(nin)
+    np_ = n_real if 0 < n_real < n else n
+    out = np.zeros(np_ * (np_ + 1) // 2, np.uint16)
+    lib().orc_rfgap_tree_upper(_c(nin, np.int32), _c(nodextr, np.int32), n, n_real, out.ctypes.data)
+    return out
 
 
 # ---- low rank ---------------------------------------------------------------

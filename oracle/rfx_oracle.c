@@ -529,3 +529,103 @@ void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, co
     for (int64_t e = 0; e < N * r; ++e) Y[e] /= (double)T;
     free(W);
 }
+
+/* ------------------------------------------------------------------------ */
+/* a4: per-tree triangles, cuda/rf_proximity_upper_triangle.cu              */
+/* ------------------------------------------------------------------------ */
+
+static float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const int32_t ex = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ffu;
+    uint32_t bits;
+    if (ex == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal half -> normal float */
+            int32_t e = -1;
+            do {
+                man <<= 1;
+                ++e;
+            } while (!(man & 0x400u));
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (ex == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((uint32_t)(ex - 15 + 127) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* include/rf_quantization_kernels.hpp:53-65 */
+static float orc_nf4_to_f32(uint8_t q) {
+    if (q <= 7) return (float)q / 7.0f;
+    return -((float)(q - 8)) / 7.0f;
+}
+
+static int64_t tri_index64(int64_t n, int64_t i, int64_t j) { return i * n - i * (i + 1) / 2 + j; }
+
+void orc_tree_upper(int fmt, const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin, int32_t nsample,
+                    int32_t nnode, int casewise, int32_t n_real, float scale, float zp, void* out) {
+    const int64_t N = nsample;
+    const int64_t np = (n_real > 0 && n_real < nsample) ? n_real : nsample;
+    const int64_t ne = np * (np + 1) / 2;
+    if (fmt == 1) memset(out, 0, (size_t)(2 * ne));
+    else if (fmt == 2) memset(out, 0, (size_t)ne);
+    else memset(out, 0, (size_t)((ne + 1) / 2));
+    /* members of each node (node index as key), in sample order */
+    for (int64_t n = 0; n < np; ++n) {
+        if (fmt != 2 && nin[n] > 0) continue; /* F16 / NF4: OOB samples only */
+        const int32_t k = nodextr[n];
+        if (k < 0 || k >= nnode || nodestatus[k] != -1) continue;
+        int32_t nodesize = 0;
+        for (int64_t j = 0; j < N; ++j)
+            if (nodextr[j] == k && nin[j] > 0) nodesize += nin[j];
+        if (fmt == 2 ? !(nodesize > 0) : !(nodesize > 0 || !casewise)) continue;
+        for (int64_t kk = 0; kk < N; ++kk) {
+            if (nodextr[kk] != k || nin[kk] <= 0 || kk >= np) continue;
+            const int64_t e = tri_index64(np, n < kk ? n : kk, n < kk ? kk : n);
+            if (fmt == 1) {
+                const float w = casewise ? (float)nin[kk] / (float)nodesize : 1.0f;
+                uint16_t* o = (uint16_t*)out;
+                o[e] = orc_f32_to_f16(orc_f16_to_f32(o[e]) + w);
+            } else if (fmt == 3) {
+                const float w = casewise ? (float)nin[kk] / (float)nodesize : 1.0f;
+                uint8_t* o = (uint8_t*)out;
+                const int sh = (int)(e & 1) * 4;
+                const uint8_t old = (uint8_t)((o[e >> 1] >> sh) & 0xf);
+                const uint8_t nw = (uint8_t)(orc_q_nf4(orc_nf4_to_f32(old) + w) & 0xf);
+                o[e >> 1] = (uint8_t)((o[e >> 1] & ~(0xf << sh)) | (nw << sh));
+            } else {
+                const float w = (float)nin[kk] / (float)nodesize;
+                int8_t* o = (int8_t*)out;
+                o[e] = (int8_t)(uint8_t)((uint8_t)o[e] + (uint8_t)orc_q_i8(w, scale, zp));
+            }
+        }
+    }
+}
+
+void orc_rfgap_tree_upper(const int32_t* nin, const int32_t* nodextr, int32_t nsample, int32_t n_real,
+                          uint16_t* out) {
+    const int64_t N = nsample;
+    const int64_t np = (n_real > 0 && n_real < nsample) ? n_real : nsample;
+    memset(out, 0, sizeof(uint16_t) * (size_t)(np * (np + 1) / 2));
+    for (int64_t i = 0; i < np; ++i) {
+        if (nin[i] != 0) continue;
+        const int32_t node = nodextr[i];
+        if (node < 0) continue;
+        int32_t mult = 0;
+        for (int64_t j = 0; j < N; ++j)
+            if (nin[j] > 0 && nodextr[j] == node) mult += nin[j];
+        if (mult == 0) continue;
+        const float inv = 1.0f / (float)mult;
+        for (int64_t j = i; j < np; ++j) {
+            if (!(nin[j] > 0 && nodextr[j] == node)) continue;
+            const int64_t e = tri_index64(np, i, j);
+            out[e] = orc_f32_to_f16(orc_f16_to_f32(out[e]) + (float)nin[j] * inv);
+        }
+    }
+}

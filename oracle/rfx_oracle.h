@@ -119,6 +119,28 @@ int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t
                      int32_t K, int exclude_self, int32_t* idx_out, uint16_t* cnt_out,
                      float* score_out);
 
+/* ---- per-tree triangles (cuda/rf_proximity_upper_triangle.cu) ------------ */
+
+/* One tree's packed upper triangle over the first np samples (np = n_real
+ * when 0 < n_real < N, else N), zeroed first, as the reference's per-tree
+ * kernels update it (sample by sample, read-modify-write per pair):
+ *   fmt 1 (F16, :149-285): OOB n, in-bag kk of n's terminal node (nodes with
+ *         nodesize > 0 or not casewise), entry = half(half_to_float(entry) + w),
+ *         w = casewise ? (float)nin[kk]/(float)nodesize : 1;
+ *   fmt 3 (NF4, :368-519): the same pairs, nibble = fp32_to_nf4(
+ *         nf4_to_fp32(nibble) + w), entry e in byte e/2 at bit (e%2)*4;
+ *   fmt 2 (I8, :288-365): every sample n with a terminal node (no OOB test)
+ *         and in-bag kk, nodesize > 0, entry += fp32_to_int8(
+ *         (float)nin[kk]/(float)nodesize, scale, zp) modulo 256. */
+void orc_tree_upper(int fmt, const int32_t* nodestatus, const int32_t* nodextr, const int32_t* nin, int32_t nsample,
+                    int32_t nnode, int casewise, int32_t n_real, float scale, float zp, void* out);
+
+/* One tree's RF-GAP FP16 triangle (:1621-1660): OOB i < np with nodextr
+ * >= 0, mult = sum of nin over in-bag samples of that node, in-bag j of the
+ * node with i <= j < np: entry = half(half_to_float(entry) + nin[j] * (1/mult)). */
+void orc_rfgap_tree_upper(const int32_t* nin, const int32_t* nodextr, int32_t nsample, int32_t n_real,
+                          uint16_t* out);
+
 /* ---- low rank ------------------------------------------------------------ */
 
 /* Y = P V with P = A A^T / T, A the one-hot leaf matrix (all trees):

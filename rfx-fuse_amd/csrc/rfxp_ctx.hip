@@ -161,6 +161,14 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->lr_tmp.release();
     ctx->lr_part.release();
     ctx->lr_rinv.release();
+    for (auto* b : {&ctx->tr_status, &ctx->tr_nodextr, &ctx->tr_nin, &ctx->tr_term, &ctx->tr_members, &ctx->tr_node,
+                    &ctx->tr_pofs, &ctx->dn_nout})
+        b->release();
+    ctx->tr_idx.release();
+    ctx->tr_w.release();
+    ctx->tr_out.release();
+    ctx->dn_prox.release();
+    ctx->dn_out.release();
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();
     delete ctx;

@@ -89,6 +89,16 @@ struct rfxp_ctx {
     DevBuf<float> lr_w, lr_z, lr_tmp;           // W = A^T V, iteration block, scratch
     DevBuf<double> lr_part, lr_rinv;            // Gram partials, R^-1
 
+    // per-tree and dense small-N operations (rfxp_tree.hip)
+    DevBuf<int32_t> tr_status, tr_nodextr, tr_nin, tr_term, tr_members, tr_node, tr_pofs;
+    DevBuf<int64_t> tr_idx;
+    DevBuf<double> tr_w;
+    DevBuf<uint32_t> tr_out;
+    std::vector<int64_t> tr_idx_host;
+    std::vector<double> tr_w_host;
+    DevBuf<double> dn_prox, dn_out;
+    DevBuf<int32_t> dn_nout;
+
     // timing
     bool timing = false;
     std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> pending;

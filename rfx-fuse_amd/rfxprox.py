@@ -72,6 +72,13 @@ def load(path: str = LIB_PATH):
     L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
     L.rfxp_lowrank_subspace.argtypes = [vp, vp, i32, i32, vp, vp]
+    L.rfxp_tree_pairs.argtypes = [vp, vp, vp, vp, i32, i32, C.c_int, C.POINTER(C.POINTER(i64)),
+                                  C.POINTER(C.POINTER(C.c_double)), C.POINTER(i64)]
+    L.rfxp_tree_accumulate.argtypes = [vp, vp, vp, vp, i32, i32, C.c_int, vp]
+    L.rfxp_tree_upper.argtypes = [vp, C.c_int, vp, vp, vp, i32, i32, C.c_int, i32, C.c_float, C.c_float, vp]
+    L.rfxp_rfgap_tree_upper.argtypes = [vp, vp, vp, i32, i32, vp]
+    L.rfxp_finishprox.argtypes = [vp, i32, vp, vp, vp]
+    L.rfxp_rfgap.argtypes = [vp, i32, i32, vp, vp, vp]
     _lib = L
     return L
 
@@ -250,4 +257,93 @@ class Context:
 
         out = torch.empty(self.n, dtype=torch.int32, device=f"cuda:{self.device}")
         self._check(self._L.rfxp_get_nout(self.h, out.data_ptr()))
+        return out
+
+    # ---- per-tree and dense small-N operations (host numpy arrays) ----------
+
+    @staticmethod
+    def _i32(a):
+        import numpy as np
+
+        return np.ascontiguousarray(a, dtype=np.int32)
+
+    def tree_pairs(self, nodestatus, nodextr, nin, casewise: bool = False):
+        """OOB x in-bag pairs of one tree: (idx int64, w float64) numpy copies."""
+        import numpy as np
+
+        ns, nx, ni = self._i32(nodestatus), self._i32(nodextr), self._i32(nin)
+        pi, pw, cnt = C.POINTER(C.c_int64)(), C.POINTER(C.c_double)(), C.c_int64()
+        self._check(self._L.rfxp_tree_pairs(self.h, ns.ctypes.data, nx.ctypes.data, ni.ctypes.data, len(nx),
+                                            len(ns), int(casewise), C.byref(pi), C.byref(pw), C.byref(cnt)))
+        n = cnt.value
+        if n == 0:
+            return np.zeros(0, np.int64), np.zeros(0, np.float64)
+        return (np.ctypeslib.as_array(pi, (n,)).copy(), np.ctypeslib.as_array(pw, (n,)).copy())
+
+    def tree_accumulate(self, nodestatus, nodextr, nin, prox, casewise: bool = False):
+        """One tree into prox (Fortran-ordered N x N float64 numpy, in place)."""
+        import numpy as np
+
+        ns, nx, ni = self._i32(nodestatus), self._i32(nodextr), self._i32(nin)
+        n = len(nx)
+        assert prox.dtype == np.float64 and prox.shape == (n, n) and prox.flags.f_contiguous
+        self._check(self._L.rfxp_tree_accumulate(self.h, ns.ctypes.data, nx.ctypes.data, ni.ctypes.data, n,
+                                                 len(ns), int(casewise), prox.ctypes.data))
+        return prox
+
+    def tree_upper(self, fmt: int, nodestatus, nodextr, nin, casewise: bool = False, n_real: int = 0,
+                   scale: float = 1.0, zp: float = 0.0):
+        """One tree's packed triangle (host numpy: uint16 for F16, int8 for
+        I8, packed uint8 for NF4)."""
+        import numpy as np
+
+        ns, nx, ni = self._i32(nodestatus), self._i32(nodextr), self._i32(nin)
+        n = len(nx)
+        m = n_real if 0 < n_real < n else n
+        ne = m * (m + 1) // 2
+        out = {FMT_F16: lambda: np.zeros(ne, np.uint16), FMT_I8: lambda: np.zeros(ne, np.int8),
+               FMT_NF4: lambda: np.zeros((ne + 1) // 2, np.uint8)}.get(fmt, lambda: np.zeros(2 * ne, np.uint8))()
+        self._check(self._L.rfxp_tree_upper(self.h, fmt, ns.ctypes.data, nx.ctypes.data, ni.ctypes.data, n,
+                                            len(ns), int(casewise), n_real, scale, zp, out.ctypes.data))
+        return out
+
+    def tree_upper_device(self, fmt: int, nodestatus, nodextr, nin, out, casewise: bool = False,
+                          n_real: int = 0, scale: float = 1.0, zp: float = 0.0):
+        """rfxp_tree_upper into a device tensor `out` (4-byte aligned, byte
+        size a multiple of 4)."""
+        ns, nx, ni = self._i32(nodestatus), self._i32(nodextr), self._i32(nin)
+        self._check(self._L.rfxp_tree_upper(self.h, fmt, ns.ctypes.data, nx.ctypes.data, ni.ctypes.data,
+                                            len(nx), len(ns), int(casewise), n_real, scale, zp, out.data_ptr()))
+        return out
+
+    def rfgap_tree_upper(self, nin, nodextr, n_real: int = 0):
+        import numpy as np
+
+        ni, nx = self._i32(nin), self._i32(nodextr)
+        n = len(ni)
+        m = n_real if 0 < n_real < n else n
+        out = np.zeros(m * (m + 1) // 2, np.uint16)
+        self._check(self._L.rfxp_rfgap_tree_upper(self.h, ni.ctypes.data, nx.ctypes.data, n, n_real,
+                                                  out.ctypes.data))
+        return out
+
+    def finishprox(self, nout, prox):
+        """Dense symmetrised, nout-normalised proximity (Fortran N x N)."""
+        import numpy as np
+
+        no = self._i32(nout)
+        n = len(no)
+        src = np.asfortranarray(prox, dtype=np.float64)
+        out = np.zeros((n, n), np.float64, order="F")
+        self._check(self._L.rfxp_finishprox(self.h, n, no.ctypes.data, src.ctypes.data, out.ctypes.data))
+        return out
+
+    def rfgap(self, nin_tn, nodextr_tn):
+        """RF-GAP proximity of T trees, (T, N) inputs, Fortran N x N output."""
+        import numpy as np
+
+        ni, nx = self._i32(nin_tn), self._i32(nodextr_tn)
+        t, n = ni.shape
+        out = np.zeros((n, n), np.float64, order="F")
+        self._check(self._L.rfxp_rfgap(self.h, t, n, ni.ctypes.data, nx.ctypes.data, out.ctypes.data))
         return out

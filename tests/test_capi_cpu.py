@@ -51,3 +51,49 @@ def test_no_device_is_an_error_not_a_fallback():
     buf = ctypes.create_string_buffer(256)
     R.load().rfxp_last_error(None, buf, 256)
     assert b"no HIP device" in buf.value
+
+
+COMPAT_HDR = os.path.join(REPO, "include", "rfx_compat.hpp")
+
+
+def compat_functions():
+    """Function names declared in include/rfx_compat.hpp (reference signatures),
+    the inline device converters excluded."""
+    import re
+
+    src = open(COMPAT_HDR).read()
+    names = re.findall(r"^\s*(?:static\s+)?(?:void|size_t|__global__\s+void)\s+(\w+)\(", src, re.M)
+    return sorted(set(names) - {"rfx_compat_configure"})
+
+
+def test_library_exports_reference_signatures():
+    out = subprocess.run(["nm", "-DC", "--defined-only", R.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    names = compat_functions()
+    assert {"cpu_proximity", "gpu_proximity_upper_triangle_int8", "get_quantized_size",
+            "cuda_proximity_nf4_kernel"} <= set(names)
+    for n in names:
+        assert f"::{n}(" in out, f"{n} declared in rfx_compat.hpp, not exported"
+    assert " T rfx_compat_configure" in out and " T rfx_compat_last_error" in out
+    # the C++ entry points keep the reference's parameter types
+    assert "rf::cpu_proximity(int const*, int const*, int const*, int, int, double*, int*, int*, int*, int*, " \
+           "int*, int*)" in out
+    assert "rf::cpu_proximity_rfgap(int, int, std::vector<std::vector<int, std::allocator<int> >" in out
+
+
+def test_compat_entry_without_device_reports_error_and_leaves_output():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = ctypes.CDLL(R.LIB_PATH)
+    lib.rfx_compat_last_error.restype = ctypes.c_char_p
+    # rf::cpu_finishprox(int, const int*, double*, double*) by its mangled name
+    fn = getattr(lib, "_ZN2rf14cpu_finishproxEiPKiPdS2_")
+    n = 3
+    nout = (ctypes.c_int32 * n)(1, 1, 1)
+    prox = (ctypes.c_double * (n * n))(*([0.5] * 9))
+    sym = (ctypes.c_double * (n * n))(*([7.0] * 9))
+    fn(ctypes.c_int32(n), nout, prox, sym)
+    assert list(sym) == [7.0] * 9
+    assert b"no HIP device" in lib.rfx_compat_last_error()

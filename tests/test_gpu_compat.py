@@ -1,0 +1,228 @@
+"""GPU per-tree and dense small-N path (rfxp_tree_accumulate, rfxp_finishprox,
+rfxp_rfgap, rfxp_tree_upper, rfxp_rfgap_tree_upper) and the reference-signature
+C++ entry points (include/rfx_compat.hpp, through tests/compat/compat_driver)
+against the reference's golden fixtures and the oracle, bit-exact."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rfxprox as R
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+DRIVER = os.path.join(os.path.dirname(__file__), "compat", "compat_driver")
+
+
+def fixture():
+    g = np.load(os.path.join(GOLD, "cpu_prox_small.npz"))
+    return (g["nodestatus"].astype(np.int32), g["nodextr"].astype(np.int32), g["nin"].astype(np.int32), g)
+
+
+def random_tree(rng, n, nnode, p_term=0.7, oob=0.37):
+    ns = np.where(rng.random(nnode) < p_term, -1, rng.integers(1, 3, nnode)).astype(np.int32)
+    nx = rng.integers(-2, nnode + 2, n).astype(np.int32)
+    nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+    nin[rng.random(n) < oob - 0.37] = 0
+    return ns, nx, nin
+
+
+@pytest.mark.parametrize("cw", [0, 1])
+def test_tree_accumulate_and_finishprox_match_reference_fixture(gpu_ctx, cw):
+    ns, nx, nin, g = fixture()
+    n = nx.shape[1]
+    prox = np.zeros((n, n), order="F")
+    for k in range(nx.shape[0]):
+        gpu_ctx.tree_accumulate(ns[k], nx[k], nin[k], prox, casewise=bool(cw))
+    assert np.array_equal(prox, g[f"prox_cw{cw}"])
+    assert np.array_equal(gpu_ctx.finishprox(g["nout"], prox), g[f"proxsym_cw{cw}"])
+
+
+@pytest.mark.parametrize("n,nnode,seed", [(1, 1, 0), (37, 5, 1), (700, 40, 2), (2500, 9, 3)])
+def test_tree_accumulate_random_trees_match_oracle(gpu_ctx, n, nnode, seed):
+    rng = np.random.default_rng(seed)
+    for cw in (False, True):
+        want = np.zeros((n, n), order="F")
+        got = np.zeros((n, n), order="F")
+        nout = np.zeros(n, np.int32)
+        for _ in range(4):
+            ns, nx, nin = random_tree(rng, n, nnode)
+            nout += nin == 0
+            O.cpu_proximity(ns, nx, nin, nnode, want, cw)
+            gpu_ctx.tree_accumulate(ns, nx, nin, got, casewise=cw)
+        assert np.array_equal(got, want)
+        assert np.array_equal(gpu_ctx.finishprox(nout, got), O.finishprox(nout, want))
+
+
+def test_tree_pairs_sum_to_accumulate(gpu_ctx):
+    rng = np.random.default_rng(11)
+    n, nnode = 300, 12
+    ns, nx, nin = random_tree(rng, n, nnode)
+    idx, w = gpu_ctx.tree_pairs(ns, nx, nin, casewise=True)
+    want = np.zeros((n, n), order="F")
+    O.cpu_proximity(ns, nx, nin, nnode, want, True)
+    got = np.zeros(n * n)
+    np.add.at(got, idx, w)
+    assert np.array_equal(got.reshape((n, n), order="F"), want)
+
+
+def test_rfgap_matches_reference_fixture(gpu_ctx):
+    g = np.load(os.path.join(GOLD, "rfgap_small.npz"))
+    got = gpu_ctx.rfgap(g["nin"], g["nodextr"])
+    assert np.array_equal(got, g["prox"])
+
+
+@pytest.mark.parametrize("n,t,nnode,seed", [(1, 1, 1, 0), (90, 7, 6, 1), (1500, 12, 30, 2)])
+def test_rfgap_random_matches_oracle(gpu_ctx, n, t, nnode, seed):
+    rng = np.random.default_rng(seed)
+    nin = np.stack([np.bincount(rng.integers(0, n, n), minlength=n) for _ in range(t)]).astype(np.int32)
+    nx = rng.integers(-1, nnode, (t, n)).astype(np.int32)
+    if n > 1:
+        nin[:, 0] = 1   # sample 0 never OOB: diagonal 1, row from the symmetrisation only
+    assert np.array_equal(gpu_ctx.rfgap(nin, nx), O.rfgap(nin, nx))
+
+
+FMTS = [(R.FMT_F16, 1.0, 0.0), (R.FMT_NF4, 1.0, 0.0), (R.FMT_I8, 1.0 / 127.0, 0.0), (R.FMT_I8, 0.013, -3.5)]
+
+
+@pytest.mark.parametrize("fmt,scale,zp", FMTS)
+@pytest.mark.parametrize("cw", [False, True])
+def test_tree_upper_fixture_trees_match_oracle(gpu_ctx, fmt, scale, zp, cw):
+    ns, nx, nin, _ = fixture()
+    for k in range(0, nx.shape[0], 3):
+        want = O.tree_upper(fmt, ns[k], nx[k], nin[k], casewise=cw, scale=scale, zp=zp)
+        got = gpu_ctx.tree_upper(fmt, ns[k], nx[k], nin[k], casewise=cw, scale=scale, zp=zp)
+        assert np.array_equal(got, want), k
+
+
+@pytest.mark.parametrize("fmt,scale,zp", FMTS)
+@pytest.mark.parametrize("n,nnode,n_real,seed", [(1, 1, 0, 0), (2, 1, 0, 1), (333, 7, 0, 2),
+                                                 (2049, 25, 1999, 3), (3000, 3, 0, 4)])
+def test_tree_upper_random_trees_match_oracle(gpu_ctx, fmt, scale, zp, n, nnode, n_real, seed):
+    rng = np.random.default_rng(seed)
+    ns, nx, nin = random_tree(rng, n, nnode)
+    for cw in (False, True):
+        want = O.tree_upper(fmt, ns, nx, nin, casewise=cw, n_real=n_real, scale=scale, zp=zp)
+        got = gpu_ctx.tree_upper(fmt, ns, nx, nin, casewise=cw, n_real=n_real, scale=scale, zp=zp)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [1000, 1001])
+def test_tree_upper_device_output_matches_host_output(gpu_ctx, n):
+    """Word-sized outputs are written in place, others through staging; the
+    bytes after the triangle stay as they were."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    nnode = 17
+    ns, nx, nin = random_tree(rng, n, nnode)
+    ne = n * (n + 1) // 2
+    for fmt, nbytes, dt in ((R.FMT_F16, 2 * ne, np.uint16), (R.FMT_I8, ne, np.int8),
+                            (R.FMT_NF4, (ne + 1) // 2, np.uint8)):
+        buf = torch.full(((nbytes + 3) // 4,), -1, dtype=torch.int32, device="cuda:0")
+        gpu_ctx.tree_upper_device(fmt, ns, nx, nin, buf, casewise=True, scale=0.02, zp=1.0)
+        torch.cuda.synchronize()
+        raw = buf.cpu().numpy().view(np.uint8)
+        want = O.tree_upper(fmt, ns, nx, nin, casewise=True, scale=0.02, zp=1.0)
+        assert np.array_equal(raw[:nbytes].view(dt), want), fmt
+        assert (raw[nbytes:] == 0xFF).all()
+
+
+@pytest.mark.parametrize("n,n_real,seed", [(1, 0, 0), (80, 0, 1), (1200, 1000, 2)])
+def test_rfgap_tree_upper_matches_oracle(gpu_ctx, n, n_real, seed):
+    rng = np.random.default_rng(seed)
+    nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+    nx = rng.integers(-1, 9, n).astype(np.int32)
+    want = O.rfgap_tree_upper(nin, nx, n_real=n_real)
+    got = gpu_ctx.rfgap_tree_upper(nin, nx, n_real=n_real)
+    assert np.array_equal(got, want)
+
+
+def test_bad_arguments_are_errors(gpu_ctx):
+    ns, nx, nin, _ = fixture()
+    with pytest.raises(R.RfxpError):
+        gpu_ctx.tree_upper(17, ns[0], nx[0], nin[0])
+    L, h = gpu_ctx._L, gpu_ctx.h
+    z = np.zeros(4, np.int32)
+    assert L.rfxp_finishprox(h, -1, z.ctypes.data, z.ctypes.data, z.ctypes.data) == 1
+    assert L.rfxp_tree_upper(h, R.FMT_F16, ns[0].ctypes.data, nx[0].ctypes.data, nin[0].ctypes.data,
+                             nx.shape[1], ns.shape[1], 0, 0, 1.0, 0.0, None) == 1
+    assert L.rfxp_rfgap(h, 2, -5, z.ctypes.data, z.ctypes.data, z.ctypes.data) == 1
+    # empty inputs are no-ops, as in the reference
+    assert gpu_ctx.finishprox(np.zeros(0, np.int32), np.zeros((0, 0))).shape == (0, 0)
+
+
+def test_tree_upper_int8_zero_scale_saturates_like_reference(gpu_ctx):
+    """scale 0 is not rejected by the reference: w / 0 = +inf clamps to 127."""
+    ns, nx, nin, _ = fixture()
+    got = gpu_ctx.tree_upper(R.FMT_I8, ns[1], nx[1], nin[1], scale=0.0)
+    assert np.array_equal(got, O.tree_upper(O.FMT_I8, ns[1], nx[1], nin[1], scale=0.0))
+    assert set(np.unique(got)) <= {0, 127, -2}   # one or two adds of 127, modulo 256
+
+
+def write_driver_input(path, ns, nx, nin, nout, casewise):
+    t, n = nx.shape
+    with open(path, "wb") as f:
+        np.array([n, t, casewise], np.int32).tofile(f)
+        for k in range(t):
+            np.array([ns.shape[1]], np.int32).tofile(f)
+            ns[k].astype(np.int32).tofile(f)
+            nx[k].astype(np.int32).tofile(f)
+            nin[k].astype(np.int32).tofile(f)
+        nout.astype(np.int32).tofile(f)
+
+
+@pytest.mark.parametrize("cw", [0, 1])
+def test_reference_signatures_through_cpp_driver(tmp_path, cw):
+    """The rf:: functions, called with the reference's signatures from a C++
+    program linked against librfxprox.so, reproduce the reference fixture
+    and the oracle."""
+    assert os.path.exists(DRIVER), "tests/compat/compat_driver not built (make -C rfx-fuse_amd driver)"
+    ns, nx, nin, g = fixture()
+    t, n = nx.shape
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    write_driver_input(inp, ns, nx, nin, g["nout"], cw)
+    r = subprocess.run(["timeout", "-k", "10", "120", DRIVER, str(inp), str(outp)], capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    raw = np.fromfile(outp, np.uint8)
+    nn, ne = n * n, n * (n + 1) // 2
+    off = 0
+
+    def take(count, dt):
+        nonlocal off
+        nb = count * np.dtype(dt).itemsize
+        a = raw[off:off + nb].view(dt)
+        off += nb
+        return a
+
+    F = lambda a: a.reshape((n, n), order="F")  # noqa: E731
+    prox, sym, prox2, rg, rg2 = (F(take(nn, np.float64)) for _ in range(5))
+    f16, i8, nf4 = take(ne, np.uint16), take(ne, np.int8), take((ne + 1) // 2, np.uint8)
+    i8u, gap16 = take(ne, np.int8), take(ne, np.uint16)
+    qs, sc = take(4, np.uint64), take(4, np.float32)
+    assert off == raw.size
+    assert np.array_equal(prox, g[f"prox_cw{cw}"])
+    assert np.array_equal(prox2, g[f"prox_cw{cw}"])
+    assert np.array_equal(sym, g[f"proxsym_cw{cw}"])
+    want_rg = O.rfgap(nin, nx)
+    assert np.array_equal(rg, want_rg) and np.array_equal(rg2, want_rg)
+    assert np.array_equal(f16, O.tree_upper(O.FMT_F16, ns[0], nx[0], nin[0], casewise=bool(cw)))
+    assert np.array_equal(i8, O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
+                                           scale=np.float32(1.0 / 60.0), zp=0.5))
+    assert np.array_equal(nf4, O.tree_upper(O.FMT_NF4, ns[0], nx[0], nin[0], casewise=bool(cw)))
+    assert np.array_equal(i8u, O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
+                                            scale=np.float32(1.0) / np.float32(127.0), zp=0.0))
+    assert np.array_equal(gap16, O.rfgap_tree_upper(nin[0], nx[0]))
+    # cuda/rf_quantization_kernels.cu:393-406: FP32 counts sizeof(dp_t), NF4 one byte per entry
+    assert list(qs) == [8000, 2000, 1000, 1000]
+    col = g[f"proxsym_cw{cw}"][:, 0].astype(np.float32)
+    mn, mx = col.min(), col.max()
+    s = (mx - mn) / np.float32(255.0)
+    assert sc[0] == s and sc[1] == np.float32(-mn / s)
+    full = g[f"proxsym_cw{cw}"].astype(np.float32)
+    s2 = (full.max() - full.min()) / np.float32(255.0)
+    assert sc[2] == s2 and sc[3] == np.float32(-full.min() / s2)

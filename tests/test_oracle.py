@@ -300,3 +300,128 @@ def test_lowrank_pv_equals_dense_one_hot_product():
     want = (A @ (A.T @ V)) / t
     got = O.lowrank_pv(leaf, nleaf, V)
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+# ---- per-tree triangle formats (cuda/rf_proximity_upper_triangle.cu) -----------
+# The reference's per-tree kernels are CUDA and cannot run here; their
+# restatement is pinned to the reference's CPU accumulation (itself pinned to
+# the golden fixture above): each OOB x in-bag pair of a tree is the term that
+# rf::cpu_proximity adds, placed once at (min, max) of the pair.
+
+def tri_dense(vals, n):
+    D = np.zeros((n, n))
+    D[np.triu_indices(n)] = vals
+    return D
+
+
+def fixture_trees():
+    g = np.load(os.path.join(GOLD, "cpu_prox_small.npz"))
+    return (g["nodestatus"].astype(np.int32), g["nodextr"].astype(np.int32), g["nin"].astype(np.int32), g)
+
+
+def test_tree_upper_f16_trees_sum_to_reference_fixture():
+    ns, nx, nin, g = fixture_trees()
+    t, n = nx.shape
+    acc = np.zeros((n, n))
+    for k in range(t):
+        tri = O.tree_upper(O.FMT_F16, ns[k], nx[k], nin[k])
+        acc += tri_dense(tri.view(np.float16).astype(np.float64), n)
+    P = g["prox_cw0"]
+    assert acc.sum() > 0
+    assert np.array_equal(acc, np.triu(P + P.T))
+
+
+def casewise_tree_terms(ns, nx, nin):
+    """rf::cpu_proximity of one tree (casewise weights), symmetrised and
+    folded to the upper triangle: the weight of each OOB x in-bag pair."""
+    n = len(nx)
+    P = np.zeros((n, n), order="F")
+    O.cpu_proximity(ns, nx, nin, len(ns), P, True)
+    return np.triu(P + P.T)
+
+
+def test_tree_upper_casewise_f16_and_nf4_follow_cpu_pairs():
+    ns, nx, nin, _ = fixture_trees()
+    n = nx.shape[1]
+    for k in range(0, nx.shape[0], 4):
+        W = casewise_tree_terms(ns[k], nx[k], nin[k])
+        f16 = tri_dense(O.tree_upper(O.FMT_F16, ns[k], nx[k], nin[k], casewise=True).view(np.float16)
+                        .astype(np.float64), n)
+        assert np.array_equal(f16 > 0, W > 0)
+        assert np.abs(f16 - W).max() <= 2.0 ** -11 * W.max()
+        nf = O.tree_upper(O.FMT_NF4, ns[k], nx[k], nin[k], casewise=True)
+        ne = n * (n + 1) // 2
+        nib = np.stack([nf & 15, nf >> 4], axis=1).ravel()[:ne]
+        w32 = W[np.triu_indices(n)].astype(np.float32)
+        x = (w32 * np.float32(7)).astype(np.float64)
+        assert np.array_equal(nib, np.minimum(7, np.floor(x + 0.5)).astype(np.uint8))
+
+
+def i8_pair_brute(ns, nx, nin, scale, zp, n_real=0):
+    """The INT8 per-tree kernel summed pair by pair: entry (i, j), i <= j in
+    one terminal node, gets q(nin[j]/size) as (n=i, kk=j) when j is in-bag
+    and q(nin[i]/size) as (n=j, kk=i) when i is in-bag and i != j."""
+    n = len(nx)
+    m = n_real if 0 < n_real < n else n
+    out = np.zeros(m * (m + 1) // 2, np.int64)
+    term = lambda k: 0 <= k < len(ns) and ns[k] == -1  # noqa: E731
+    size = {}
+    for s in range(n):
+        if nin[s] > 0:
+            size[nx[s]] = size.get(nx[s], 0) + int(nin[s])
+
+    def q(w):
+        return int(np.int8(np.clip(np.float32(w) / np.float32(scale) + np.float32(zp), -128, 127)))
+
+    e = 0
+    for i in range(m):
+        for j in range(i, m):
+            k = nx[i]
+            if nx[j] == k and term(k) and size.get(k, 0) > 0:
+                v = 0
+                if nin[j] > 0:
+                    v += q(np.float32(nin[j]) / np.float32(size[k]))
+                if i != j and nin[i] > 0:
+                    v += q(np.float32(nin[i]) / np.float32(size[k]))
+                out[e] = v
+            e += 1
+    return (out % 256).astype(np.uint8).view(np.int8)
+
+
+@pytest.mark.parametrize("seed,scale,zp,n_real", [(1, 1 / 127.0, 0.0, 0), (2, 0.004, -20.0, 0), (3, 0.02, 3.0, 41)])
+def test_tree_upper_i8_matches_pairwise_brute_force(seed, scale, zp, n_real):
+    rng = np.random.default_rng(seed)
+    n, nnode = 64, 7
+    ns = np.where(rng.random(nnode) < 0.7, -1, 1).astype(np.int32)
+    nx = rng.integers(-1, nnode + 1, n).astype(np.int32)
+    nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+    got = O.tree_upper(O.FMT_I8, ns, nx, nin, scale=np.float32(scale), zp=np.float32(zp), n_real=n_real)
+    assert np.array_equal(got, i8_pair_brute(ns, nx, nin, scale, zp, n_real))
+
+
+def test_tree_upper_n_real_is_the_leading_block():
+    rng = np.random.default_rng(9)
+    n, nnode, m = 90, 5, 61
+    ns = -np.ones(nnode, np.int32)
+    nx = rng.integers(0, nnode, n).astype(np.int32)
+    nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+    for fmt in (O.FMT_F16, O.FMT_I8):
+        full = tri_dense(O.tree_upper(fmt, ns, nx, nin, casewise=True, scale=0.01).astype(np.float64), n)
+        part = tri_dense(O.tree_upper(fmt, ns, nx, nin, casewise=True, scale=0.01, n_real=m)
+                         .astype(np.float64), m)
+        assert np.array_equal(full[:m, :m], part)
+
+
+def test_rfgap_tree_upper_is_twice_single_tree_rfgap():
+    """With one tree, cpu_proximity_rfgap (pinned above) gives
+    (C_ij + C_ji)/2 for i != j, C_ij = nin[j]/size for OOB i and in-bag j of
+    one node; the per-tree triangle holds C_ij for i <= j."""
+    g = np.load(os.path.join(GOLD, "rfgap_small.npz"))
+    nin, nx = g["nin"].astype(np.int32), g["nodextr"].astype(np.int32)
+    n = nin.shape[1]
+    for k in range(0, nin.shape[0], 5):
+        dense = O.rfgap(nin[k:k + 1], nx[k:k + 1])
+        want = np.triu(2 * dense, 1) * (nin[k] == 0)[:, None]
+        got = tri_dense(O.rfgap_tree_upper(nin[k], nx[k]).view(np.float16).astype(np.float64), n)
+        assert np.array_equal(got > 0, want > 0)
+        assert np.abs(got - want).max() <= 2.0 ** -11 * max(want.max(), 1e-30)
