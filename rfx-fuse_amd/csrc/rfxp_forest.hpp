@@ -84,4 +84,7 @@ struct PackTarget {
 // (rfxp_pack.hip).
 int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst);
 
+// p[0..n) = val on ctx->stream (a fill kernel, capturable).
+void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val);
+
 }  // namespace rfxp

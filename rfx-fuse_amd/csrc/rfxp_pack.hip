@@ -342,6 +342,12 @@ __global__ void k_rr_init(unsigned long long* rr) {
 
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 65536)), dim3(256), 0, ctx->stream,
+                       p, n, val);
+}
+
 int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;

@@ -168,7 +168,9 @@ __device__ __forceinline__ void load_group(const uint32_t* mem, const uint32_t* 
                                            Group& G) {
     // `valid` false issues the same 16 loads with an empty range (no memory
     // access): the count of loads in flight stays static, so the wait for
-    // one group can leave the other outstanding.
+    // one group can leave the other outstanding.  Records past a row's T
+    // entries are the next row's, or after the last row the zeroed slack,
+    // so every offset read here lies inside mem.
     uint32_t off[16];
     uint32_t lw[8];
 #pragma unroll
@@ -698,6 +700,9 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     ctx->ldr = ((int64_t)T + 15) / 16 * 16;
     RFXP_HIP(ctx, ctx->roff.ensure(n1 * ctx->ldr + REC_PAD));
     RFXP_HIP(ctx, ctx->rlen.ensure(n1 * ctx->ldr + REC_PAD));
+    // the record slack after the last row reads as empty records
+    fill_u32(ctx, ctx->roff.p + n1 * ctx->ldr, REC_PAD, 0u);
+    fill_u32(ctx, (uint32_t*)(ctx->rlen.p + n1 * ctx->ldr), REC_PAD / 2, 0u);
     RFXP_HIP(ctx, ctx->roffT.ensure(n1 * T));
     RFXP_HIP(ctx, ctx->rlenT.ensure(n1 * T));
     RFXP_HIP(ctx, ctx->nout.ensure(n1));
