@@ -139,13 +139,13 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     for (hipEvent_t ev : ctx->event_pool) (void)hipEventDestroy(ev);
     ctx->bkt_off.release();
     ctx->bkt_mem.release();
+    ctx->roffT.release();
+    ctx->rlenT.release();
     ctx->scratch.release();
     ctx->scratch2.release();
     ctx->key16.release();
     ctx->roff.release();
     ctx->rlen.release();
-    ctx->roffT.release();
-    ctx->rlenT.release();
     ctx->nout.release();
     ctx->rinv.release();
     ctx->rrange.release();

@@ -61,9 +61,9 @@ struct rfxp_ctx {
     int64_t ldr = 0;           // record row stride: T rounded up to 16
     DevBuf<uint32_t> roff;     // N x ldr (+pad): offset of the opposite-OOB bucket of (i, t)
     DevBuf<uint16_t> rlen;     // N x ldr (+pad): its length in bytes (see rfxp_forest.hpp)
-    DevBuf<uint32_t> roffT;    // T x N: the same, tree-major (packing)
+    DevBuf<uint32_t> roffT;    // T x N: records, tree-major (packing)
     DevBuf<uint16_t> rlenT;
-    DevBuf<uint32_t> scratch;  // packing scratch (large leaf counts)
+    DevBuf<uint32_t> scratch;  // packing scratch (part histograms, large leaf counts)
     DevBuf<uint32_t> scratch2; // per-sample OOB counts
     DevBuf<uint16_t> key16;    // T x ceil8(N) bucket ids (packing pass B)
     DevBuf<int32_t> nout;      // N

@@ -1,13 +1,15 @@
 // Forest index construction (see rfxp_forest.hpp for the layout).
 //
-// k_pack_hist (one workgroup per tree): bucket histogram, offsets, and the
-// sample-major records.  k_pack_scatter (one workgroup per tree and window
-// of ~16k members): member lists built in LDS and written out coalesced --
-// scattering 4-byte ids straight to HBM costs a partial-line write each.
-// Trees are mapped to workgroups so that related work lands on one XCD:
-// 16 consecutive trees per XCD in the first kernel (they complete the same
-// record lines in L2), all windows of a tree in the second (they re-read
-// the tree's keys from L2).
+// k_pack_hist (one workgroup per tree): bucket histogram, offsets and the
+// tree's 16-bit bucket keys.  k_records (forest mode; 64 x 64 tiles of
+// trees x samples): the sample-major records, looked up from the keys and
+// the tree's offsets and written through an LDS transpose.  k_pack_scatter
+// (one workgroup per tree and window of ~12k members): member lists built
+// in LDS and written out coalesced -- scattering 4-byte ids straight to HBM
+// costs a partial-line write each.  Trees are mapped to workgroups so that
+// related work lands on one XCD: 16 consecutive trees per XCD in the first
+// kernel, all windows of a tree in the third (they re-read the tree's keys
+// from L2).
 //
 // k_nout_part / k_nout_final: nout_i = sum over trees of OOB bits
 // (src/rf_bootstrap.cpp:67-70), its reciprocal, and the reciprocal's range.
@@ -56,14 +58,13 @@ __device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t*
 
 // Pass A, one 1024-thread workgroup per tree: bucket histogram (LDS when
 // 2L+1 counters fit, else the zeroed global scratch `gscr`), exclusive scan
-// into the global offsets, the tree's bucket ids as uint16 (`key16`, rows
-// of ldk entries, pads 0xffff; written only when 2L < 0xffff, else NULL),
-// then the records of every sample.  Keys are held in registers, PACK_KR per
-// thread per round, all loads of a round issued before the first atomic.
+// into the global offsets, and the tree's bucket ids as uint16 (`key16`,
+// rows of ldk entries, pads 0xffff; written only when 2L < 0xffff, else
+// NULL).  Keys are held in registers, PACK_KR per thread per round, all
+// loads of a round issued before the first atomic.
 template <bool LDS_PATH>
-__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_hist(LeafView v, int32_t* goff_all, uint32_t* roffT,
-                                                           uint16_t* rlenT, uint32_t* gscr, uint16_t* key16,
-                                                           int64_t ldk) {
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_hist(
+    LeafView v, int32_t* goff_all, uint32_t* gscr, uint16_t* key16, int64_t ldk) {
     extern __shared__ uint32_t sh[];
     __shared__ uint32_t part[PACK_THREADS];
     const uint32_t bid = blockIdx.x;
@@ -104,69 +105,66 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         scan_offsets((volatile uint32_t*)cnt, (volatile uint32_t*)off0, nb, part, goff);
         __threadfence_block();
     }
-    auto rd = [&](int32_t k) -> uint32_t {
-        if constexpr (LDS_PATH) return off0[k];
-        else return ((const volatile uint32_t*)off0)[k];
-    };
-    // Records, tree-major (coalesced); k_rec_transpose makes them sample-major.
-    if (!roffT) return;  // reference mode: buckets only
-    uint32_t* ro = roffT + (int64_t)t * N;
-    uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
-    for (int64_t base = 0; base < N; base += round) {
-        int32_t key[PACK_KR];
-#pragma unroll
-        for (int k = 0; k < PACK_KR; ++k) {
-            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < N ? bucket_of(v, i, t) : -2;
-        }
-#pragma unroll
-        for (int k = 0; k < PACK_KR; ++k) {
-            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            const int32_t b = key[k];
-            if (b == -2) continue;
-            uint32_t o = 0u, len = 0u;
-            if (b >= 0) {
-                const int32_t ob = b ^ 1;
-                const uint32_t s = rd(ob);
-                o = (tbase + s) * 4u;
-                len = min(rd(ob + 1) - s, REC_LONG) * 4u;
-            }
-            ro[i] = o;
-            rl[i] = (uint16_t)len;
-        }
-    }
 }
 
-// [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
-__global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint16_t* rlenT, int64_t N,
-                                                      int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen) {
+// Sample-major records, one 256-thread workgroup per 64 x 64 tile of
+// (trees t0.., samples i0..): the bucket key of (i, t) from key16 (or from
+// the leaves when key16 is NULL), the start and length of the bucket with
+// the other OOB bit from the tree's offsets (L2-resident), then an LDS
+// transpose so that each sample's 64 records are written as one run.
+// Padding trees T..ldr-1 get empty records.
+__global__ __launch_bounds__(256) void k_records(LeafView v, const uint16_t* key16, int64_t ldk,
+                                                 const int32_t* goff_all, int64_t ldr, uint32_t* roff,
+                                                 uint16_t* rlen) {
     __shared__ uint32_t to[64][65];
     __shared__ uint16_t tl[64][66];
+    const int64_t N = v.N;
+    const int32_t T = v.T;
+    const int32_t nb = view_buckets(v);
     const int64_t i0 = (int64_t)blockIdx.x * 64;
     const int32_t t0 = blockIdx.y * 64;
-    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
-        const int r = k >> 6, c = k & 63;  // r: tree, c: sample
-        const int64_t i = i0 + c;
+    // thread -> (tree row r, 16 consecutive samples) for the lookups
+    for (int k = threadIdx.x; k < 64 * 4; k += 256) {
+        const int r = k >> 2, c0 = (k & 3) * 16;
         const int32_t t = t0 + r;
-        uint32_t o = 0u;
-        uint16_t l = 0;
-        if (i < N && t < T) {
-            o = roffT[(int64_t)t * N + i];
-            l = rlenT[(int64_t)t * N + i];
+        int32_t key[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const int64_t i = i0 + c0 + c;
+            int32_t b = -1;
+            if (t < T && i < N) {
+                if (key16) {
+                    const uint16_t kk = key16[(int64_t)t * ldk + i];
+                    b = kk == 0xffffu ? -1 : (int32_t)kk;
+                } else {
+                    b = bucket_of(v, i, t);
+                }
+            }
+            key[c] = b;
         }
-        to[r][c] = o;
-        tl[r][c] = l;
+        const int32_t* off = goff_all + (int64_t)(t < T ? t : 0) * (nb + 1);
+        const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            uint32_t o = 0u, len = 0u;
+            if (key[c] >= 0) {
+                const int32_t ob = key[c] ^ 1;
+                const uint32_t s = (uint32_t)off[ob];
+                o = (tbase + s) * 4u;
+                len = min((uint32_t)off[ob + 1] - s, REC_LONG) * 4u;
+            }
+            to[r][c0 + c] = o;
+            tl[r][c0 + c] = (uint16_t)len;
+        }
     }
     __syncthreads();
     for (int k = threadIdx.x; k < 64 * 64; k += 256) {
         const int r = k >> 6, c = k & 63;  // r: sample, c: tree
         const int64_t i = i0 + r;
         const int32_t t = t0 + c;
-        // padding trees T..ldr-1 get empty records
         if (i < N && t < ldr) {
-            roff[i * ldr + t] = t < T ? to[c][r] : 0u;
-            rlen[i * ldr + t] = t < T ? tl[c][r] : (uint16_t)0;
+            roff[i * ldr + t] = to[c][r];
+            rlen[i * ldr + t] = tl[c][r];
         }
     }
 }
@@ -178,8 +176,9 @@ __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, co
 // copy of its slice of mem[t] through LDS cursors, and writes the slice
 // with coalesced stores.  Members beyond the LDS slice (a window grown by
 // one very large bucket) are written directly.
-constexpr int PACK_WIN = 8192;   // members per window (LDS slice)
+constexpr int PACK_WIN = 12288;  // members per window (LDS slice; two workgroups per CU)
 constexpr int PACK_CUR = 4096;   // buckets per window with LDS cursors
+constexpr int SCAT_LOADS = 4;    // 16-byte key loads in flight per thread
 
 __device__ __forceinline__ int32_t first_bucket_at(const int32_t* off, int32_t nb, int64_t pos) {
     // smallest even b in [0, nb] with off[b] >= pos (nb when none)
@@ -242,20 +241,26 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         else memt[base_pos + rel] = m;
     };
     if (key16) {
-        // eight ids per thread per 16-byte load, two loads in flight
+        // eight ids per thread per 16-byte load, SCAT_LOADS loads in flight
         const uint4* k4 = (const uint4*)(key16 + (int64_t)t * ldk);
         const int64_t n8 = ldk / 8;
-        for (int64_t q0 = threadIdx.x; q0 < n8; q0 += 2 * PACK_THREADS) {
-            const int64_t q1 = q0 + PACK_THREADS;
-            const uint4 x0 = k4[q0];
-            const uint4 x1 = q1 < n8 ? k4[q1] : make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
-            const uint32_t wv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        for (int64_t q0 = threadIdx.x; q0 < n8; q0 += SCAT_LOADS * PACK_THREADS) {
+            uint4 x[SCAT_LOADS];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int64_t i = 8 * (k < 4 ? q0 : q1) + 2 * (k & 3);
-                const uint32_t lo16 = wv[k] & 0xffffu, hi16 = wv[k] >> 16;
-                if (lo16 != 0xffffu) place(i, (int32_t)lo16);
-                if (hi16 != 0xffffu) place(i + 1, (int32_t)hi16);
+            for (int u = 0; u < SCAT_LOADS; ++u) {
+                const int64_t q = q0 + (int64_t)u * PACK_THREADS;
+                x[u] = q < n8 ? k4[q] : make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
+            }
+#pragma unroll
+            for (int u = 0; u < SCAT_LOADS; ++u) {
+                const int64_t i8 = 8 * (q0 + (int64_t)u * PACK_THREADS);
+                const uint32_t wv[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t lo16 = wv[k] & 0xffffu, hi16 = wv[k] >> 16;
+                    if (lo16 != 0xffffu) place(i8 + 2 * k, (int32_t)lo16);
+                    if (hi16 != 0xffffu) place(i8 + 2 * k + 1, (int32_t)hi16);
+                }
             }
         }
     } else {
@@ -274,6 +279,193 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     __syncthreads();
     const uint32_t nst = min(end_pos - base_pos, (uint32_t)PACK_WIN);
     for (uint32_t k = threadIdx.x; k < nst; k += PACK_THREADS) memt[base_pos + k] = stage[k];
+}
+
+// ---------------------------------------------------------------------------
+// Forest path with per-part cursors (2L <= PART_MAX_NB): each tree's samples
+// are cut into PACK_PARTS contiguous parts.
+//   k_part_hist    (tree, part): LDS histogram of the part's buckets -> ph,
+//                  and the part's 16-bit keys;
+//   k_part_scan    (tree): bucket starts (off) and, per part, the start of
+//                  its members in each bucket (ph, in place);
+//   k_part_scatter (tree, part): LDS cursors from ph; each member goes
+//                  straight to its slot in mem[t], and each sample's record
+//                  to the tree-major arrays.  The parts of a tree run at
+//                  once on one XCD, eight trees per XCD: the 4-byte member
+//                  writes of those trees (8 x 4N bytes) merge in that XCD's
+//                  L2 before they reach HBM;
+//   k_rec_transpose: tree-major records -> sample-major.
+// ---------------------------------------------------------------------------
+constexpr int PACK_PARTS = 8;
+constexpr int PART_MAX_NB = 8192;
+
+__device__ __forceinline__ int64_t part_begin(int64_t N, int p) {
+    const int64_t chunk = (N + PACK_PARTS - 1) / PACK_PARTS;
+    return min(N, (int64_t)p * chunk);
+}
+
+// (tree, part) of a k_part_* workgroup: consecutive dispatch slots of one
+// XCD walk the parts of a tree, trees x, x + 8, x + 16, ... on XCD x.
+__device__ __forceinline__ void part_of_block(uint32_t bid, int32_t& t, int& p) {
+    const uint32_t xcd = bid & 7, slot = bid >> 3;
+    t = (int32_t)(xcd + 8 * (slot / PACK_PARTS));
+    p = (int)(slot % PACK_PARTS);
+}
+
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_hist(
+    LeafView v, uint32_t* ph, uint16_t* key16, int64_t ldk) {
+    extern __shared__ uint32_t sh[];
+    int32_t t;
+    int p;
+    part_of_block(blockIdx.x, t, p);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) sh[b] = 0u;
+    __syncthreads();
+    const int64_t i0 = part_begin(v.N, p), i1 = part_begin(v.N, p + 1);
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    uint16_t* kt = key16 + (int64_t)t * ldk;
+    for (int64_t base = i0; base < i1; base += round) {
+        int32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < i1 ? bucket_of(v, i, t) : -2;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            if (key[k] >= 0) atomicAdd(&sh[key[k]], 1u);
+            if (key[k] != -2) kt[i] = key[k] >= 0 ? (uint16_t)key[k] : (uint16_t)0xffffu;
+        }
+    }
+    // the row's padding keys (ldk > N) are written by the last part
+    if (p == PACK_PARTS - 1)
+        for (int64_t i = v.N + threadIdx.x; i < ldk; i += PACK_THREADS) kt[i] = (uint16_t)0xffffu;
+    __syncthreads();
+    uint32_t* out = ph + ((int64_t)t * PACK_PARTS + p) * nb;
+    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) out[b] = sh[b];
+}
+
+__global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, uint32_t* ph, int32_t* goff_all) {
+    __shared__ uint32_t part[PACK_THREADS];
+    const int32_t t = blockIdx.x;
+    if (t >= T) return;
+    uint32_t* pt = ph + (int64_t)t * PACK_PARTS * nb;
+    int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    const int tid = threadIdx.x;
+    const int32_t chunk = (nb + PACK_THREADS - 1) / PACK_THREADS;
+    const int32_t b0 = min(nb, tid * chunk);
+    const int32_t b1 = min(nb, b0 + chunk);
+    uint32_t s = 0;
+    for (int32_t b = b0; b < b1; ++b)
+#pragma unroll
+        for (int q = 0; q < PACK_PARTS; ++q) s += pt[(int64_t)q * nb + b];
+    part[tid] = s;
+    __syncthreads();
+    for (int d = 1; d < PACK_THREADS; d <<= 1) {
+        const uint32_t x = tid >= d ? part[tid - d] : 0u;
+        __syncthreads();
+        part[tid] += x;
+        __syncthreads();
+    }
+    uint32_t run = part[tid] - s;
+    for (int32_t b = b0; b < b1; ++b) {
+        goff[b] = (int32_t)run;
+#pragma unroll
+        for (int q = 0; q < PACK_PARTS; ++q) {
+            const uint32_t c = pt[(int64_t)q * nb + b];
+            pt[(int64_t)q * nb + b] = run;
+            run += c;
+        }
+    }
+    if (tid == PACK_THREADS - 1) goff[nb] = (int32_t)part[tid];
+}
+
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter(
+    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
+    uint32_t* roffT, uint16_t* rlenT) {
+    extern __shared__ uint32_t sh[];
+    int32_t t;
+    int p;
+    part_of_block(blockIdx.x, t, p);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    uint32_t* cur = sh;            // nb cursors
+    uint32_t* off = sh + nb;       // nb + 1 bucket starts
+    const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
+    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
+        if (b < nb) cur[b] = pp[b];
+        off[b] = (uint32_t)goff[b];
+    }
+    __syncthreads();
+    const int64_t N = v.N;
+    const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
+    uint32_t* memt = mem + (int64_t)t * N;
+    uint32_t* ro = roffT + (int64_t)t * N;
+    uint16_t* rl = rlenT + (int64_t)t * N;
+    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const uint16_t* kt = key16 + (int64_t)t * ldk;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    for (int64_t base = i0; base < i1; base += round) {
+        uint32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0x10000u;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            const uint32_t b = key[k];
+            if (b == 0x10000u) continue;
+            uint32_t o = 0u, len = 0u;
+            if (b != 0xffffu) {
+                const uint32_t pos = atomicAdd(&cur[b], 1u);
+                const uint32_t end = off[b + 1];
+                memt[pos] = (uint32_t)(i + 1) | (pos + 1 == end && end - off[b] >= REC_LONG ? MEM_LAST : 0u);
+                const uint32_t ob = b ^ 1u;
+                o = (tbase + off[ob]) * 4u;
+                len = min(off[ob + 1] - off[ob], REC_LONG) * 4u;
+            }
+            ro[i] = o;
+            rl[i] = (uint16_t)len;
+        }
+    }
+}
+
+// [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint16_t* rlenT, int64_t N,
+                                                      int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen) {
+    __shared__ uint32_t to[64][65];
+    __shared__ uint16_t tl[64][66];
+    const int64_t i0 = (int64_t)blockIdx.x * 64;
+    const int32_t t0 = blockIdx.y * 64;
+    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+        const int r = k >> 6, c = k & 63;  // r: tree, c: sample
+        const int64_t i = i0 + c;
+        const int32_t t = t0 + r;
+        uint32_t o = 0u;
+        uint16_t l = 0;
+        if (i < N && t < T) {
+            o = roffT[(int64_t)t * N + i];
+            l = rlenT[(int64_t)t * N + i];
+        }
+        to[r][c] = o;
+        tl[r][c] = l;
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+        const int r = k >> 6, c = k & 63;  // r: sample, c: tree
+        const int64_t i = i0 + r;
+        const int32_t t = t0 + c;
+        // padding trees T..ldr-1 get empty records
+        if (i < N && t < ldr) {
+            roff[i * ldr + t] = t < T ? to[c][r] : 0u;
+            rlen[i * ldr + t] = t < T ? tl[c][r] : (uint16_t)0;
+        }
+    }
 }
 
 __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t val) {
@@ -348,6 +540,9 @@ void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
                        p, n, val);
 }
 
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst);
+static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in);
+
 int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
@@ -360,6 +555,10 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     }
     if (int rc = check_launch(ctx, "k_rr_init")) return rc;
     if (N == 0) return RFXP_OK;
+    if (forest && nb <= PART_MAX_NB) {
+        if (int rc = pack_forest_parts(ctx, v, dst)) return rc;
+        return pack_nout(ctx, v, nout_in);
+    }
     // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
     const unsigned grid = (unsigned)(cdiv(T, 128) * 128);
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
@@ -379,21 +578,21 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
         LaunchTimer tm(ctx, "pack_hist");
         hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, dst.off,
-                           forest ? ctx->roffT.p : nullptr, ctx->rlenT.p, (uint32_t*)nullptr, k16, ldk);
+                           (uint32_t*)nullptr, k16, ldk);
     } else {
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(nscr, 256), 65536)), dim3(256), 0, s,
                            ctx->scratch.p, nscr, 0u);
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, dst.off,
-                           forest ? ctx->roffT.p : nullptr, ctx->rlenT.p, ctx->scratch.p, k16, ldk);
+        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, dst.off, ctx->scratch.p,
+                           k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
     if (forest) {
-        LaunchTimer tm(ctx, "rec_transpose");
-        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s,
-                           ctx->roffT.p, ctx->rlenT.p, N, T, ctx->ldr, ctx->roff.p, ctx->rlen.p);
+        LaunchTimer tm(ctx, "records");
+        hipLaunchKernelGGL(k_records, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s, v,
+                           (const uint16_t*)k16, ldk, (const int32_t*)dst.off, ctx->ldr, ctx->roff.p, ctx->rlen.p);
     }
-    if (int rc = check_launch(ctx, "k_rec_transpose")) return rc;
+    if (int rc = check_launch(ctx, "k_records")) return rc;
     {
         // windows of PACK_WIN members, plus one for the slack a window can
         // gain from keeping bucket pairs whole
@@ -408,6 +607,60 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     }
     if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
     if (!forest) return RFXP_OK;
+    return pack_nout(ctx, v, nout_in);
+}
+
+// Forest path for 2L <= PART_MAX_NB (see k_part_hist).
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst) {
+    hipStream_t s = ctx->stream;
+    const int64_t N = v.N;
+    const int32_t T = v.T;
+    const int32_t nb = view_buckets(v);
+    const int64_t ldk = cdiv(N, 8) * 8;
+    RFXP_HIP(ctx, ctx->key16.ensure((size_t)T * ldk));
+    RFXP_HIP(ctx, ctx->scratch.ensure((size_t)T * PACK_PARTS * nb));
+    RFXP_HIP(ctx, ctx->roffT.ensure((size_t)T * N));
+    RFXP_HIP(ctx, ctx->rlenT.ensure((size_t)T * N));
+    // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
+    const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
+    const size_t lds_h = (size_t)nb * 4, lds_s = (size_t)(2 * nb + 1) * 4;
+    if (lds_h > 32768)
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds_h));
+    if (lds_s > 32768)
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds_s));
+    {
+        LaunchTimer tm(ctx, "pack_hist");
+        hipLaunchKernelGGL(k_part_hist, dim3(grid), dim3(PACK_THREADS), lds_h, s, v, ctx->scratch.p, ctx->key16.p,
+                           ldk);
+    }
+    if (int rc = check_launch(ctx, "k_part_hist")) return rc;
+    {
+        LaunchTimer tm(ctx, "pack_scan");
+        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, ctx->scratch.p, dst.off);
+    }
+    if (int rc = check_launch(ctx, "k_part_scan")) return rc;
+    {
+        LaunchTimer tm(ctx, "pack_scatter");
+        hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v, (const uint32_t*)ctx->scratch.p,
+                           (const int32_t*)dst.off, (const uint16_t*)ctx->key16.p, ldk, dst.mem, ctx->roffT.p,
+                           ctx->rlenT.p);
+    }
+    if (int rc = check_launch(ctx, "k_part_scatter")) return rc;
+    {
+        LaunchTimer tm(ctx, "records");
+        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s,
+                           ctx->roffT.p, ctx->rlenT.p, N, T, ctx->ldr, ctx->roff.p, ctx->rlen.p);
+    }
+    return check_launch(ctx, "k_rec_transpose");
+}
+
+// nout, 1/nout and its range (forest mode).
+static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
+    hipStream_t s = ctx->stream;
+    const int64_t N = v.N;
+    const int32_t T = v.T;
     if (!nout_in) {
         RFXP_HIP(ctx, ctx->scratch2.ensure((size_t)N));
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(N, 256), 65536)), dim3(256), 0, s,

@@ -703,8 +703,6 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     // the record slack after the last row reads as empty records
     fill_u32(ctx, ctx->roff.p + n1 * ctx->ldr, REC_PAD, 0u);
     fill_u32(ctx, (uint32_t*)(ctx->rlen.p + n1 * ctx->ldr), REC_PAD / 2, 0u);
-    RFXP_HIP(ctx, ctx->roffT.ensure(n1 * T));
-    RFXP_HIP(ctx, ctx->rlenT.ensure(n1 * T));
     RFXP_HIP(ctx, ctx->nout.ensure(n1));
     RFXP_HIP(ctx, ctx->rinv.ensure(n1));
     RFXP_HIP(ctx, ctx->rrange.ensure(2));

@@ -57,7 +57,8 @@ def check_equal(got, want, what):
 
 
 @pytest.mark.parametrize("n,t,nleaf", [(1, 1, 1), (2, 3, 2), (37, 5, 3), (300, 64, 17),
-                                       (2000, 100, 64), (4099, 257, 300)])
+                                       (2000, 100, 64), (4099, 257, 300),
+                                       (6000, 20, 5000)])   # 2L > 8192: the whole-tree packing path
 def test_counts_u16_match_oracle(gpu_ctx, n, t, nleaf):
     leaf, oob = make_forest(n * 31 + t, n, t, nleaf)
     keep = upload(gpu_ctx, leaf, oob, nleaf)
