@@ -208,6 +208,35 @@ def test_c1_forest_matches_reference_digests(gpu_ctx):
     del keep
 
 
+@pytest.mark.skip(reason="written for a 4-bit counter variant of the triangle kernel (one item per row); "
+                         "that variant faulted the GPU at the C3 shape and is not in the library, and this "
+                         "test has not run against the shipped 8-bit kernel")
+@pytest.mark.parametrize("fmt,scale,zp", [(O.FMT_U8, 1.0 / 255.0, 0.0), (O.FMT_I8, 1.0 / 2000.0, -100.0)])
+def test_rows_wider_than_a_segment_with_wrapping_counts(gpu_ctx, fmt, scale, zp):
+    """N above the 8-bit segment width (rows split into two items).  A group
+    of 300 samples shares every leaf, so its pairs reach U >= 16."""
+    import torch
+
+    n, t, nleaf = 80_000, 40, 400
+    leaf, oob = make_forest(23, n, t, nleaf)
+    leaf[:, :300] = leaf[:, :1]
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
+    gpu_ctx.upper(fmt, out, 0, n, scale=np.float32(scale), zp=np.float32(zp))
+    torch.cuda.synchronize()
+    idx = O.RowIndex(leaf, oob, nleaf)
+    u = idx.rows(O.FMT_U16, 0, 1)
+    assert u[:300].max() >= 16
+    for r0 in (0, 1, 150, 299, 300, 2_500, 40_000, 79_990):
+        r1 = min(n, r0 + 10)
+        want = idx.rows(fmt, r0, r1, np.float32(scale), np.float32(zp))
+        e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
+        got = out[e0:e1].cpu().numpy().view(O.FMT_DTYPE[fmt])
+        check_equal(got, want, f"fmt {fmt} rows {r0}:{r1}")
+    idx.close()
+    del keep
+
+
 def test_c3_shape_sampled_rows(gpu_ctx):
     """Full north-star shape (N=100k, T=500, 2048 uniform leaves, uint8):
     rows spread over the triangle equal the oracle's; all codes are in the
