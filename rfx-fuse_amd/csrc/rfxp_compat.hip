@@ -107,6 +107,11 @@ void gpu_finishprox(integer_t nsample, const integer_t* nout, dp_t* prox, dp_t* 
 void cpu_proximity_rfgap(integer_t ntree, integer_t nsample, const std::vector<std::vector<integer_t>>& tree_nin,
                          const std::vector<std::vector<integer_t>>& tree_nodextr, dp_t* prox) {
     const char* fn = "rf::cpu_proximity_rfgap";
+    if (ntree < 0 || nsample < 0) {
+        t_last_error = std::string(fn) + ": negative ntree or nsample";
+        fprintf(stderr, "[rfxprox] %s\n", t_last_error.c_str());
+        return;
+    }
     if ((integer_t)tree_nin.size() < ntree || (integer_t)tree_nodextr.size() < ntree) {
         t_last_error = std::string(fn) + ": fewer tree arrays than ntree";
         fprintf(stderr, "[rfxprox] %s\n", t_last_error.c_str());
@@ -206,7 +211,13 @@ void gpu_proximity_rfgap_upper_triangle_fp16(const integer_t* nin_tree, const in
 // ---- quantization utilities (cuda/rf_quantization_kernels.cu:24-406) ------
 
 void QuantizationUtils::compute_int8_scaling(const float* data, size_t count, float& scale, float& zero_point) {
-    // host data, as cuda/rf_quantization_kernels.cu:107-119 (count >= 1)
+    // host data, as cuda/rf_quantization_kernels.cu:107-119, which reads
+    // data[0] unconditionally: an empty input is reported instead
+    if (count == 0 || !data) {
+        t_last_error = "rf::cuda::QuantizationUtils::compute_int8_scaling: no data";
+        fprintf(stderr, "[rfxprox] %s\n", t_last_error.c_str());
+        return;
+    }
     float mn = data[0], mx = data[0];
     for (size_t i = 1; i < count; ++i) {
         mn = std::min(mn, data[i]);

@@ -97,3 +97,25 @@ def test_compat_entry_without_device_reports_error_and_leaves_output():
     fn(ctypes.c_int32(n), nout, prox, sym)
     assert list(sym) == [7.0] * 9
     assert b"no HIP device" in lib.rfx_compat_last_error()
+
+
+def test_host_int8_scaling_matches_reference_formula_and_rejects_empty_input():
+    """rf::cuda::QuantizationUtils::compute_int8_scaling is host code: scale =
+    (max - min)/255, zero_point = -min/scale in float
+    (cuda/rf_quantization_kernels.cu:107-119); an empty input is reported and
+    leaves the outputs as they were (the reference reads data[0] regardless)."""
+    import numpy as np
+
+    lib = ctypes.CDLL(R.LIB_PATH)
+    lib.rfx_compat_last_error.restype = ctypes.c_char_p
+    fn = getattr(lib, "_ZN2rf4cuda17QuantizationUtils20compute_int8_scalingEPKfmRfS4_")
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+    data = np.array([0.25, -0.5, 0.75, 0.1], dtype=np.float32)
+    sc, zp = ctypes.c_float(0), ctypes.c_float(0)
+    fn(data.ctypes.data, data.size, ctypes.byref(sc), ctypes.byref(zp))
+    want_sc = (np.float32(0.75) - np.float32(-0.5)) / np.float32(255.0)
+    assert sc.value == want_sc and zp.value == np.float32(-np.float32(-0.5) / want_sc)
+    sc, zp = ctypes.c_float(3.0), ctypes.c_float(4.0)
+    fn(data.ctypes.data, 0, ctypes.byref(sc), ctypes.byref(zp))
+    assert (sc.value, zp.value) == (3.0, 4.0)
+    assert b"no data" in lib.rfx_compat_last_error()
