@@ -31,6 +31,9 @@
 namespace rfxp {
 
 constexpr int32_t NODE_TERMINAL = -1;  // nodestatus value of a terminal node
+// Dense N x N outputs: one thread per entry in a 1-D grid, whose work-item
+// count must stay below 2^32.
+constexpr int64_t DENSE_MAX_ENTRIES = (int64_t)1 << 31;
 
 struct TreeDev {
     const int32_t* status;  // [nnode]
@@ -467,6 +470,8 @@ extern "C" int rfxp_finishprox(rfxp_ctx* ctx, int32_t N, const int32_t* nout, co
     if (N < 0 || (N > 0 && (!nout || !prox || !proxsym)))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_finishprox: bad arguments");
     if (N == 0) return RFXP_OK;
+    if ((int64_t)N * N > DENSE_MAX_ENTRIES)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_finishprox: dense N x N above 2^31 entries (N > 46340)");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t nn = (int64_t)N * N;
     const double* pd;
@@ -494,6 +499,8 @@ extern "C" int rfxp_rfgap(rfxp_ctx* ctx, int32_t T, int32_t N, const int32_t* ni
     if (T < 0 || N < 0 || (N > 0 && T > 0 && (!nin_flat || !nodextr_flat)) || (N > 0 && !prox))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_rfgap: bad arguments");
     if (N == 0) return RFXP_OK;
+    if ((int64_t)N * N > DENSE_MAX_ENTRIES)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_rfgap: dense N x N above 2^31 entries (N > 46340)");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     const int64_t nn = (int64_t)N * N, tn = (int64_t)T * N;
     const int32_t *nind = nullptr, *ndxd = nullptr;
