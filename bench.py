@@ -29,7 +29,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 
 CONFIGS = {
     "c3": dict(workload="C3 quantized uint8 upper triangle", n=100_000, t=500, nleaf=2048,
-               p_oob=0.368, seed=20261201 + 3),
+               leaves=(2048, 2048), p_oob=0.368, fmt="u8", seed=20261201 + 3),
+    # mid-size fp32 triangle: a measurement case
+    "c2": dict(workload="C2 fp32 upper triangle", n=20_000, t=500, nleaf=4096,
+               leaves=(1000, 4096), p_oob=0.368, fmt="f32", seed=20261201 + 2),
     # top-K retrieval: a parity/measurement case,
     # not the driver's bench line
     "c5": dict(workload="C5 top-K retrieval", n=1_000_000, q=100_000, t=500, nleaf=2048, k=20,
@@ -38,6 +41,11 @@ CONFIGS = {
     "c4": dict(workload="C4 low-rank P V and rank-32 subspace iteration", n=1_000_000, t=500, nleaf=4096,
                r=32, iters=5, zipf=1.1, seed=20261201 + 4),
 }
+
+# Kernel sources whose rocprofv3 traffic summary (profiles/k_tri_<cfg>_traffic.md)
+# stays valid only as long as they are unchanged.
+TRI_SOURCES = ("rfx-fuse_amd/csrc/rfxp_triangle.hip", "rfx-fuse_amd/csrc/rfxp_pack.hip",
+               "rfx-fuse_amd/csrc/rfxp_forest.hpp", "rfx-fuse_amd/csrc/rfxp_device.hpp")
 
 
 def parse():
@@ -49,7 +57,7 @@ def parse():
     ap.add_argument("--n", type=int, default=None, help="override N (smaller smoke runs)")
     ap.add_argument("--q", type=int, default=None, help="override the query count (c5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
                     help="target CPU time of the bounded CPU-baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (the reference "
@@ -57,19 +65,57 @@ def parse():
     return ap.parse_args()
 
 
+def kernel_source_sha(paths=TRI_SOURCES):
+    """SHA-256 (first 16 hex digits) of the kernel sources, in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(REPO, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profile(config):
     """HBM bytes per triangle launch measured with rocprofv3 --pmc FETCH_SIZE
     and WRITE_SIZE (each scaled by the copy-kernel calibration), read from the
-    committed summary profiles/k_tri_<config>_traffic.md; None when absent."""
+    committed summary profiles/k_tri_<config>_traffic.md.  None when the file
+    is absent or was measured on other kernel sources than the ones built
+    now (its `kernel_source_sha` line differs)."""
     path = os.path.join(REPO, "profiles", f"k_tri_{config}_traffic.md")
+    vals = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.strip().startswith("traffic_bytes_per_launch"):
-                    return float(line.split("=")[1].strip().strip("`"))
+                line = line.strip().strip("`")
+                for key in ("traffic_bytes_per_launch", "kernel_source_sha"):
+                    if line.startswith(key) and "=" in line:
+                        vals[key] = line.split("=", 1)[1].strip().strip("`")
     except OSError:
         return None
-    return None
+    if vals.get("kernel_source_sha") != kernel_source_sha() or "traffic_bytes_per_launch" not in vals:
+        return None
+    return float(vals["traffic_bytes_per_launch"])
+
+
+def host_cpu():
+    """(CPU model, logical CPUs of the host, threads this process may use).
+    The threads are the OpenMP setting of the environment (on the GPU box:
+    the CPU share granted to one GPU), else every CPU of the host."""
+    model, ncpu = "unknown", os.cpu_count() or 1
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or ncpu
+    except ValueError:
+        threads = ncpu
+    return model, ncpu, max(1, min(threads, ncpu))
 
 
 def copy_calibration(mib):
@@ -85,6 +131,9 @@ def copy_calibration(mib):
 
 
 def make_inputs(cfg, n, device):
+    """Seeded synthetic forest on the device: per tree a leaf count L_t drawn
+    from cfg["leaves"] (inclusive), labels uniform on [0, L_t), OOB bits
+    Bernoulli(p_oob) iid."""
     import torch
 
     import rfxprox as R
@@ -92,52 +141,76 @@ def make_inputs(cfg, n, device):
     g = torch.Generator(device=device)
     g.manual_seed(cfg["seed"])
     t = cfg["t"]
-    leaf = torch.randint(0, cfg["nleaf"], (t, n), generator=g, device=device, dtype=torch.int32)
+    lo, hi = cfg["leaves"]
+    if lo == hi:
+        leaf = torch.randint(0, lo, (t, n), generator=g, device=device, dtype=torch.int32)
+    else:
+        lt = torch.randint(lo, hi + 1, (t, 1), generator=g, device=device, dtype=torch.int64)
+        leaf = (torch.rand((t, n), generator=g, device=device, dtype=torch.float64) * lt).to(torch.int32)
     oob = torch.rand((t, n), generator=g, device=device) < cfg["p_oob"]
     words = R.pack_oob_bits(oob)
     return leaf, oob, words
 
 
-def cpu_baseline(cfg, leaf_tn, oob_tn, n, scale, zp, target_s):
+def _rows_rate(idx, O, fmt, n, scale, zp, target_s, threads, seed, chunk=16):
+    """Pairs per second of the oracle's row pass on random chunks of rows
+    until ~target_s of wall time is spent."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    pairs_done, t_rows, nchunk = 0, 0.0, 0
+    while t_rows < target_s and nchunk < n // chunk:
+        r0 = int(rng.integers(0, n - chunk))
+        t0 = time.perf_counter()
+        idx.rows(fmt, r0, r0 + chunk, scale, zp, threads=threads)
+        t_rows += time.perf_counter() - t0
+        pairs_done += sum(n - 1 - i for i in range(r0, r0 + chunk))
+        nchunk += 1
+    return pairs_done / t_rows, nchunk, pairs_done, t_rows
+
+
+def cpu_baseline(cfg, leaf_tn, oob_tn, n, fmt, scale, zp, target_s):
     """The oracle (our OpenMP C restatement of the reference algorithm:
     per-tree leaf bucketing, OOB x in-bag co-occurrence, finishprox
-    normalisation, quantize) on a bounded sample of rows, extrapolated to
-    the whole triangle.  Host cores of the GPU box."""
-    import numpy as np
+    normalisation, quantize) on bounded samples of rows, extrapolated to the
+    whole triangle, on the GPU box's host cores.  Three runs on every thread
+    this process may use (median reported), then one single-thread run."""
+    import statistics
 
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
 
     t = cfg["t"]
-    threads = max(1, min(16, os.cpu_count() or 1))
+    model, ncpu, threads = host_cpu()
+    ofmt = {"u8": O.FMT_U8, "f32": O.FMT_F32}[fmt]
     # bucketing of all trees is paid once per triangle
     t0 = time.perf_counter()
     idx = O.RowIndex(leaf_tn, oob_tn, cfg["nleaf"], threads=threads)
     t_bucket = time.perf_counter() - t0
-    # rows: chunks at random offsets until ~target_s of CPU time is spent
-    pairs_done = 0
-    t_rows = 0.0
-    chunk = 16
-    rng = np.random.default_rng(cfg["seed"])
-    starts = []
-    while t_rows < target_s and len(starts) < n // chunk:
-        r0 = int(rng.integers(0, n - chunk))
-        starts.append(r0)
-        t0 = time.perf_counter()
-        idx.rows(O.FMT_U8, r0, r0 + chunk, scale, zp, threads=threads)
-        t_rows += time.perf_counter() - t0
-        pairs_done += sum(n - 1 - i for i in range(r0, r0 + chunk))
-    idx.close()
     total_pairs = n * (n - 1) // 2
-    est_s = t_bucket + t_rows * total_pairs / max(pairs_done, 1)
+    per_run = target_s / 4.0
+    runs = []
+    for k in range(3):
+        rate, nchunk, pairs, secs = _rows_rate(idx, O, ofmt, n, scale, zp, per_run, threads, cfg["seed"] + k)
+        runs.append((rate, nchunk, pairs, secs))
+    rate1, nchunk1, pairs1, secs1 = _rows_rate(idx, O, ofmt, n, scale, zp, per_run, 1, cfg["seed"] + 9)
+    idx.close()
+    med = statistics.median(r[0] for r in runs)
+    est_s = t_bucket + total_pairs / med
+    est1_s = t_bucket * threads + total_pairs / rate1
     return {
         "value": total_pairs * t / est_s,
         "unit": "pair-tree comparisons/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{len(starts)} chunks of {chunk} rows at random offsets "
-                   f"({pairs_done} of {total_pairs} pairs, {t_rows:.1f} s) + one full bucketing "
-                   f"pass ({t_bucket:.2f} s), extrapolated to the full triangle"),
+        "cpu_model": model,
+        "host_cpus": ncpu,
+        "single_thread_value": total_pairs * t / est1_s,
+        "runs": [total_pairs * t / (t_bucket + total_pairs / r[0]) for r in runs],
+        "sample": (f"median of 3 runs on {threads} threads, each {runs[0][1]}-{max(r[1] for r in runs)} "
+                   f"chunks of 16 rows at random offsets (~{per_run:.0f} s each), plus one full bucketing "
+                   f"pass ({t_bucket:.2f} s), extrapolated to the full triangle; single thread: "
+                   f"{nchunk1} chunks ({secs1:.1f} s)"),
     }
 
 
@@ -157,10 +230,12 @@ def main():
     if args.config == "c4":
         run_c4(args)
         return
-    run_c3(args)
+    run_triangle(args)
 
 
-def run_c3(args):
+def run_triangle(args):
+    """C3 (default) and C2: one step = rfxp_set_forest (bucket index over all
+    trees) + rfxp_upper (counting, normalisation, quantisation, stores)."""
     import torch
 
     import rfxprox as R
@@ -171,16 +246,22 @@ def run_c3(args):
     dev = torch.device("cuda:0")
     torch.cuda.init()
     leaf, oob, words = make_inputs(cfg, n, dev)
-    scale = float(torch.tensor(1.0, dtype=torch.float32) / 255.0)      # (max-min)/255
-    zp = float(-torch.tensor(0.0, dtype=torch.float32) / scale)         # -min/scale
-    nbytes = R.upper_nbytes(R.FMT_U8, n)
+    fmt = cfg["fmt"]
+    if fmt == "u8":
+        scale = float(torch.tensor(1.0, dtype=torch.float32) / 255.0)      # (max-min)/255
+        zp = float(-torch.tensor(0.0, dtype=torch.float32) / scale)         # -min/scale
+    else:
+        scale, zp = 1.0, 0.0
+    rfmt = R.FMT_NAMES[fmt]
+    esz = {"u8": 1, "f32": 4}[fmt]
+    nbytes = R.upper_nbytes(rfmt, n)
     out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     ctx = R.Context(0)
     ctx.use_torch_stream()
 
     def step():
         ctx.set_forest(leaf, words, n, t, cfg["nleaf"])
-        ctx.upper(R.FMT_U8, out, 0, n, scale=scale, zp=zp)
+        ctx.upper(rfmt, out, 0, n, scale=scale, zp=zp)
 
     for _ in range(args.warmup):
         step()
@@ -204,13 +285,14 @@ def run_c3(args):
     tri_avg = tri_ms / max(tri_n, 1)
     pairs = n * (n - 1) // 2
     value = pairs * t / (ms_step / 1e3)
-    # algorithmic bytes of one triangle launch: 1 B per output entry written
-    # + 5 B per (sample, tree) bucket record read (4 B offset, 1 B length)
-    # + 8 B per sample of 1/nout
-    tri_bytes = nbytes + n * t * 5 + n * 8
+    # algorithmic bytes of one triangle launch: the output entries written
+    # + 6 B per (sample, tree) record slot read (4 B offset, 2 B length; rows
+    # padded to ldr = T rounded up to 16) + 8 B per sample of 1/nout
+    ldr = (t + 15) // 16 * 16
+    tri_bytes = nbytes + n * ldr * 6 + n * 8
     achieved = tri_bytes / (tri_avg / 1e3) / 1e9
     rec = {
-        "metric": "pair-tree comparisons/sec at N=100k,T=500 (uint8 OOB proximity triangle)",
+        "metric": f"pair-tree comparisons/sec at N={n // 1000}k,T={t} ({fmt} OOB proximity triangle)",
         "value": value,
         "unit": "pair-tree comparisons/s",
         "n_gpus": 1,
@@ -220,23 +302,25 @@ def run_c3(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
-        "data": "synthetic (uniform 2048-leaf assignment, Bernoulli(0.368) OOB, seeded)",
-        "config": {"workload": cfg["workload"], "N": n, "T": t, "leaves_per_tree": cfg["nleaf"],
-                   "output_bytes": nbytes, "format": "u8", "scale": scale, "zp": zp},
+        "dtype": fmt,
+        "data": (f"synthetic ({cfg['leaves'][0]}-{cfg['leaves'][1]} uniform leaves per tree, "
+                 f"Bernoulli({cfg['p_oob']}) OOB, seeded)"),
+        "config": {"workload": cfg["workload"], "N": n, "T": t, "leaves_per_tree": list(cfg["leaves"]),
+                   "output_bytes": nbytes, "format": fmt, "scale": scale, "zp": zp},
         "output_GBps": nbytes / (ms_step / 1e3) / 1e9,
         "kernels_ms": {"tri_avg": tri_avg, "pack_per_step": pack_ms / args.steps,
                        **{f"{k}_per_step": v for k, v in pack_each.items()}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profile(args.config) if n == cfg["n"] else None},
+                     "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_launch": tri_bytes,
+                     "traffic": traffic_from_profile(args.config) if n == cfg["n"] else None,
+                     "kernel_source_sha": kernel_source_sha()},
         "wall_s": wall,
     }
     ctx.set_timing(False)
     if not args.no_cpu_baseline:
         leaf_np = leaf.cpu().numpy()
         oob_np = oob.to(torch.uint8).cpu().numpy()
-        rec["cpu_baseline"] = cpu_baseline(cfg, leaf_np, oob_np, n, scale, zp, args.cpu_seconds)
+        rec["cpu_baseline"] = cpu_baseline(cfg, leaf_np, oob_np, n, fmt, scale, zp, args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)
@@ -245,29 +329,44 @@ def run_c3(args):
 
 def cpu_baseline_topk(cfg, ref_tn, q_qt, k, target_s):
     """The oracle's top-K (OpenMP over queries, a dense count scan per query
-    like python/randomforest_py.cpp:2534-2558) on a bounded query sample."""
-    import numpy as np
+    like python/randomforest_py.cpp:2534-2558) on bounded query samples:
+    median of three runs on every thread this process may use, then one
+    single-thread run."""
+    import statistics
 
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    n_q = threads
-    t0 = time.perf_counter()
-    O.topk_all(ref_tn, q_qt[:n_q], k, threads=threads)
-    dt = time.perf_counter() - t0
-    if dt < target_s:
-        n_q = min(q_qt.shape[0], max(n_q, int(n_q * target_s / max(dt, 1e-3)) // threads * threads))
-        t0 = time.perf_counter()
-        O.topk_all(ref_tn, q_qt[:n_q], k, threads=threads)
-        dt = time.perf_counter() - t0
+    model, ncpu, threads = host_cpu()
     t, n = ref_tn.shape
+
+    def rate(nth, budget, seed_off):
+        n_q = nth
+        t0 = time.perf_counter()
+        O.topk_all(ref_tn, q_qt[seed_off:seed_off + n_q], k, threads=nth)
+        dt = time.perf_counter() - t0
+        if dt < budget:
+            n_q = min(q_qt.shape[0] - seed_off, max(n_q, int(n_q * budget / max(dt, 1e-3)) // nth * nth))
+            t0 = time.perf_counter()
+            O.topk_all(ref_tn, q_qt[seed_off:seed_off + n_q], k, threads=nth)
+            dt = time.perf_counter() - t0
+        return n_q * n * t / dt, n_q, dt
+
+    per_run = target_s / 4.0
+    runs = [rate(threads, per_run, 64 * j) for j in range(3)]
+    r1 = rate(1, per_run, 256)
     return {
-        "value": n_q * n * t / dt,
+        "value": statistics.median(r[0] for r in runs),
         "unit": "pair-tree comparisons/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n_q} queries against all {n} references ({dt:.1f} s)",
+        "cpu_model": model,
+        "host_cpus": ncpu,
+        "single_thread_value": r1[0],
+        "runs": [r[0] for r in runs],
+        "sample": (f"median of 3 runs on {threads} threads of {runs[0][1]}-{max(r[1] for r in runs)} queries "
+                   f"against all {n} references (~{per_run:.0f} s each); single thread: {r1[1]} queries "
+                   f"({r1[2]:.1f} s); linear in the query count"),
     }
 
 
@@ -394,10 +493,13 @@ def run_c4(args):
     Q, B = ctx.lowrank_subspace(V, cfg["iters"])
     torch.cuda.synchronize()
     sub_ms = (time.perf_counter() - t0) * 1e3
-    # algorithmic bytes of one P V: leaves read twice (A^T V and A W), the V
-    # rows gathered once per (sample, tree) in A^T V and the W rows once per
-    # (sample, tree) in A W (r*4 B each), Y written
-    alg = 2 * n * t * 4 + 2 * n * t * r * 4 + n * r * 4
+    # compulsory HBM bytes of one P V: the leaf labels read twice (A^T V
+    # and A W), the member lists once, V and Y once, W written once and
+    # gathered once per (tree, leaf); the per-(sample, tree) row gathers of V
+    # and W (2 N T r 4 B) are served from L2 / Infinity Cache and reported
+    # separately as the gather rate
+    alg = 2 * n * t * 4 + n * t * 4 + 2 * n * r * 4 + 2 * t * nleaf * r * 4
+    gather = 2 * n * t * r * 4
     achieved = alg / (ms_step / 1e3) / 1e9
     rec = {
         "metric": "one-hot SpMM P V throughput (C4, N x T x r multiply-adds)",
@@ -418,22 +520,34 @@ def run_c4(args):
         "subspace_ms": sub_ms,
         "index_build_ms": index_ms,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_step": alg, "traffic": None},
+        "gather_GBps": gather / (ms_step / 1e3) / 1e9,
         "ritz_top": float(np.max(np.linalg.eigvalsh((B + B.T) / 2))),
     }
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
         import oracle as O
 
-        # the oracle's single-thread SpMM on a tree subset, scaled to T trees
-        tt = 4
+        # the oracle's SpMM on a tree subset at full N, scaled to T trees:
+        # median of three runs on every thread this process may use, then
+        # one single-thread run
+        import statistics
+
+        model, ncpu, threads = host_cpu()
+        tt = 8
         lf = leaf[:tt].cpu().numpy()
         Vd = V.cpu().numpy().astype(np.float64)
-        c0 = time.perf_counter()
-        O.lowrank_pv(lf, nleaf, Vd)
-        dt = (time.perf_counter() - c0) * t / tt
-        rec["cpu_baseline"] = {"value": 2 * n * t * r / dt, "unit": "multiply-adds/s", "cores": 1, "kind": "port",
-                               "sample": f"{tt} of {t} trees at full N, scaled linearly"}
+
+        def one(nth):
+            c0 = time.perf_counter()
+            O.lowrank_pv(lf, nleaf, Vd, threads=nth)
+            return 2 * n * t * r / ((time.perf_counter() - c0) * t / tt)
+
+        runs = [one(threads) for _ in range(3)]
+        rec["cpu_baseline"] = {"value": statistics.median(runs), "unit": "multiply-adds/s", "cores": threads,
+                               "kind": "port", "cpu_model": model, "host_cpus": ncpu,
+                               "single_thread_value": one(1), "runs": runs,
+                               "sample": f"{tt} of {t} trees at full N, scaled linearly; median of 3 runs"}
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)

@@ -119,6 +119,18 @@ int64_t rfxp_upper_nbytes(int fmt, int64_t N, int64_t row_begin, int64_t row_end
 /* The per-sample nout actually used (device int32[N] copy into `nout`). */
 int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
 
+/* Work decomposition of rfxp_upper, host-only (no device needed): row i of
+ * the band [row_begin, row_end) is cut into segments of S columns starting
+ * at i, i + S, ...; one workgroup per segment.  Returns the number of
+ * segments (-1 for bad arguments) and, when 0 <= e < that number, the row
+ * and first column of segment e.  rfxp_upper_launches is the number of
+ * kernel launches n_items segments take (at most 2^22 - 1 workgroups of
+ * 1024 threads each).  Lets callers size row bands for several devices; no
+ * reference counterpart. */
+int64_t rfxp_upper_work_item(int64_t N, int32_t S, int64_t row_begin, int64_t row_end, int64_t e,
+                             int64_t* row, int64_t* col);
+int64_t rfxp_upper_launches(int64_t n_items);
+
 /* ---- top-K similarity retrieval ----------------------------------------- */
 
 /* Indexes a reference set (N samples x T trees of leaf labels, same layout

@@ -88,6 +88,11 @@ def lib():
     return _lib
 
 
+def ref_available() -> bool:
+    """Whether the compiled reference was built here (no library is loaded)."""
+    return os.path.exists(os.path.join(HERE, "_ref", "libref.so"))
+
+
 def ref():
     """The compiled reference (build container only); None when absent."""
     global _ref
@@ -302,10 +307,11 @@ def rfgap_tree_upper(nin, nodextr, n_real=0):
 
 # ---- low rank ---------------------------------------------------------------
 
-def lowrank_pv(leaf_tn, nleaf, V):
+def lowrank_pv(leaf_tn, nleaf, V, threads=0):
+    """Y = A (A^T V) / T in double (same result for every thread count)."""
     t, n = leaf_tn.shape
     V = _c(V, np.float64)
     r = V.shape[1]
     Y = np.empty_like(V)
-    lib().orc_lowrank_pv(_c(leaf_tn, np.int32).ravel(), n, t, nleaf, V.ravel(), r, Y.ravel())
+    lib().orc_lowrank_pv(_c(leaf_tn, np.int32).ravel(), n, t, nleaf, V.ravel(), r, Y.ravel(), threads)
     return Y

@@ -509,24 +509,34 @@ int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t
 /* low rank: P V with P = A A^T / T                                          */
 /* ------------------------------------------------------------------------ */
 void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, const double* V,
-                    int32_t r, double* Y) {
-    double* W = (double*)malloc(sizeof(double) * (size_t)nleaf * (size_t)r);
-    memset(Y, 0, sizeof(double) * (size_t)(N * r));
+                    int32_t r, double* Y, int threads) {
+    /* W_t[l] = sum over j ascending of V_j (one tree per thread), then
+     * Y_i = sum over t ascending of W_t[leaf_i(t)] (rows split over threads):
+     * the same additions in the same order for any thread count. */
+    const int nth = threads > 0 ? threads : omp_get_max_threads();
+    double* W = (double*)calloc((size_t)T * (size_t)nleaf * (size_t)r, sizeof(double));
+#pragma omp parallel for num_threads(nth) schedule(dynamic, 1)
     for (int32_t t = 0; t < T; ++t) {
         const int32_t* lab = leaf + (int64_t)t * N;
-        memset(W, 0, sizeof(double) * (size_t)nleaf * (size_t)r);
+        double* Wt = W + (size_t)t * (size_t)nleaf * (size_t)r;
         for (int64_t j = 0; j < N; ++j) {
             int32_t l = lab[j];
             if (l < 0 || l >= nleaf) continue;
-            for (int32_t c = 0; c < r; ++c) W[(int64_t)l * r + c] += V[j * r + c];
-        }
-        for (int64_t i = 0; i < N; ++i) {
-            int32_t l = lab[i];
-            if (l < 0 || l >= nleaf) continue;
-            for (int32_t c = 0; c < r; ++c) Y[i * r + c] += W[(int64_t)l * r + c];
+            for (int32_t c = 0; c < r; ++c) Wt[(int64_t)l * r + c] += V[j * r + c];
         }
     }
-    for (int64_t e = 0; e < N * r; ++e) Y[e] /= (double)T;
+#pragma omp parallel for num_threads(nth) schedule(static)
+    for (int64_t i = 0; i < N; ++i) {
+        double* y = Y + i * r;
+        for (int32_t c = 0; c < r; ++c) y[c] = 0.0;
+        for (int32_t t = 0; t < T; ++t) {
+            int32_t l = leaf[(int64_t)t * N + i];
+            if (l < 0 || l >= nleaf) continue;
+            const double* w = W + ((size_t)t * (size_t)nleaf + (size_t)l) * (size_t)r;
+            for (int32_t c = 0; c < r; ++c) y[c] += w[c];
+        }
+        for (int32_t c = 0; c < r; ++c) y[c] /= (double)T;
+    }
     free(W);
 }
 

@@ -145,9 +145,10 @@ void orc_rfgap_tree_upper(const int32_t* nin, const int32_t* nodextr, int32_t ns
 
 /* Y = P V with P = A A^T / T, A the one-hot leaf matrix (all trees):
  * Y[i] = (1/T) sum_t W_t[leaf_i(t)], W_t[l] = sum_{j: leaf_j(t)=l} V[j].
- * V and Y are N x r row-major double; labels outside [0,nleaf) take no part. */
+ * V and Y are N x r row-major double; labels outside [0,nleaf) take no part.
+ * threads <= 0: all OpenMP threads; results do not depend on the count. */
 void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, const double* V,
-                    int32_t r, double* Y);
+                    int32_t r, double* Y, int threads);
 
 #ifdef __cplusplus
 }

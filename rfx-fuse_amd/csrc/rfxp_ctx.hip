@@ -146,10 +146,11 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->key16.release();
     ctx->roff.release();
     ctx->rlen.release();
+    ctx->lng.release();
+    ctx->lngn.release();
     ctx->nout.release();
     ctx->rinv.release();
     ctx->rrange.release();
-    ctx->items.release();
     ctx->flags.release();
     ctx->ref_off.release();
     ctx->ref_mem.release();

@@ -5,24 +5,29 @@
 // low-rank kernels.  Layout in HBM:
 //   mem  [T][N]   uint32  sample ids + 1 grouped, per tree, by bucket
 //                         b = 2*leaf + oob (buckets hold the samples of one
-//                         leaf with one OOB bit, in no particular order); the
-//                         +1 keeps 0 free as "no member" for masked loads;
-//                         in buckets of REC_LONG or more members bit 31 marks
-//                         the last member
+//                         leaf with one OOB bit); the +1 keeps 0 free as "no
+//                         member" for masked loads
 //   off  [T][2L+1] int32  per-tree bucket offsets into mem[t]
 //   roff [N][ldr] uint32  for sample i and tree t, the byte offset in mem
-//                         (4*(t*N + start)) of the bucket of i's leaf with the
-//                         other OOB bit -- exactly the samples that pair with
-//                         i in tree t (src/rf_proximity.cpp:179-230)
-//   rlen [N][ldr] uint16  that bucket's length in bytes, 4*min(len, REC_LONG);
-//                         4*REC_LONG means "REC_LONG or more members, read up
-//                         to the bit-31 mark"; 0 when i has no valid leaf in
-//                         t.  In bytes so that it serves directly as the
-//                         range of a buffer load.  Rows are ldr = T rounded
-//                         up to 16 long
-//                         (padding trees have empty records),
-//                         and both arrays have REC_PAD entries of slack
-//                         (whole-group record loads).
+//                         (4*(t*N + start)) of the run of i: the bucket of
+//                         i's leaf with the other OOB bit holds exactly the
+//                         samples that pair with i in tree t
+//                         (src/rf_proximity.cpp:179-230).  Members are placed
+//                         part by part (contiguous sample ranges, ascending),
+//                         so the run starts where the members from i's own
+//                         part begin: every member j > i is in the run, and
+//                         of the members j < i only those of i's part
+//   rlen [N][ldr] uint16  the run's length in bytes, 4*min(len, REC_LONG);
+//                         4*REC_LONG means "REC_LONG or more members: the run
+//                         ends where its bucket ends", found in lng below; 0
+//                         when i has no valid leaf in t.  In bytes so that
+//                         it serves directly as the range of a buffer load.
+//                         Rows are ldr = T rounded up to 16 long (padding
+//                         trees have empty records), and both arrays have
+//                         REC_PAD entries of slack (whole-group record loads)
+//   lng  [T][lmax] uint2  per tree, the start and end byte offsets in mem of
+//                         the buckets of REC_LONG or more members (lngn[t]
+//                         of them, lmax = N / REC_LONG + 1)
 //   nout [N] int32, rinv [N] double (nout > 0 ? 1/nout : 1), and the min and
 //   max of rinv as IEEE bits.
 #pragma once
@@ -34,8 +39,7 @@
 
 namespace rfxp {
 
-constexpr uint32_t MEM_LAST = 0x80000000u;
-constexpr uint32_t MEM_ID = 0x7fffffffu;
+constexpr uint32_t MEM_ID = 0x7fffffffu;  // the id bits of a mem entry
 constexpr uint32_t REC_LONG = 16383u;  // 4*REC_LONG fits the uint16 length
 constexpr int64_t MAX_FOREST_N = 0x7ffffffe;
 constexpr int REC_PAD = 64;

@@ -61,6 +61,9 @@ struct rfxp_ctx {
     int64_t ldr = 0;           // record row stride: T rounded up to 16
     DevBuf<uint32_t> roff;     // N x ldr (+pad): offset of the opposite-OOB bucket of (i, t)
     DevBuf<uint16_t> rlen;     // N x ldr (+pad): its length in bytes (see rfxp_forest.hpp)
+    DevBuf<uint2> lng;         // T x lmax: start, end byte offsets of buckets of REC_LONG+ members
+    DevBuf<int32_t> lngn;      // T: entries of lng per tree
+    int32_t lmax = 0;
     DevBuf<uint32_t> roffT;    // T x N: records, tree-major (packing)
     DevBuf<uint16_t> rlenT;
     DevBuf<uint32_t> scratch;  // packing scratch (part histograms, large leaf counts)
@@ -69,9 +72,6 @@ struct rfxp_ctx {
     DevBuf<int32_t> nout;      // N
     DevBuf<double> rinv;       // N: nout > 0 ? 1/nout : 1
     DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits
-    DevBuf<int2> items;        // work list of the triangle kernel
-    int64_t items_key[4] = {-1, -1, -1, -1};
-    int64_t n_items = 0;
     DevBuf<int32_t> flags;     // device status words
 
     // reference set for top-K (rfxp_set_reference)

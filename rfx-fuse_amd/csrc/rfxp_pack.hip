@@ -233,10 +233,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     auto place = [&](int64_t i, int32_t b) {
         if (b < b0 || b >= b1) return;
         const uint32_t rel = lds_cur ? atomicAdd(&cur[b - b0], 1u) : atomicAdd(&gcur[b], 1u);
-        const uint32_t bstart = (uint32_t)off[b] - base_pos;
-        const uint32_t end = (uint32_t)off[b + 1] - base_pos;
-        const uint32_t m = (uint32_t)(i + 1) |
-                           (v.nseg == 0 && rel + 1 == end && end - bstart >= REC_LONG ? MEM_LAST : 0u);
+        const uint32_t m = (uint32_t)(i + 1);
         if (rel < (uint32_t)PACK_WIN) stage[rel] = m;
         else memt[base_pos + rel] = m;
     };
@@ -347,39 +344,56 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) out[b] = sh[b];
 }
 
+// One workgroup per tree.  Buckets are taken 1024 at a time, one per
+// thread, so that every load and store of the part table is coalesced; a
+// workgroup-wide exclusive scan per chunk and a running carry give the
+// bucket starts, and each part's start in each bucket replaces its count.
 __global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, uint32_t* ph, int32_t* goff_all) {
-    __shared__ uint32_t part[PACK_THREADS];
+    __shared__ uint32_t wsum[PACK_THREADS / 64];
     const int32_t t = blockIdx.x;
     if (t >= T) return;
     uint32_t* pt = ph + (int64_t)t * PACK_PARTS * nb;
     int32_t* goff = goff_all + (int64_t)t * (nb + 1);
-    const int tid = threadIdx.x;
-    const int32_t chunk = (nb + PACK_THREADS - 1) / PACK_THREADS;
-    const int32_t b0 = min(nb, tid * chunk);
-    const int32_t b1 = min(nb, b0 + chunk);
-    uint32_t s = 0;
-    for (int32_t b = b0; b < b1; ++b)
-#pragma unroll
-        for (int q = 0; q < PACK_PARTS; ++q) s += pt[(int64_t)q * nb + b];
-    part[tid] = s;
-    __syncthreads();
-    for (int d = 1; d < PACK_THREADS; d <<= 1) {
-        const uint32_t x = tid >= d ? part[tid - d] : 0u;
-        __syncthreads();
-        part[tid] += x;
-        __syncthreads();
-    }
-    uint32_t run = part[tid] - s;
-    for (int32_t b = b0; b < b1; ++b) {
-        goff[b] = (int32_t)run;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t carry = 0;
+    for (int32_t c0 = 0; c0 < nb; c0 += PACK_THREADS) {
+        const int32_t b = c0 + tid;
+        uint32_t v[PACK_PARTS];
+        uint32_t s = 0;
 #pragma unroll
         for (int q = 0; q < PACK_PARTS; ++q) {
-            const uint32_t c = pt[(int64_t)q * nb + b];
-            pt[(int64_t)q * nb + b] = run;
-            run += c;
+            v[q] = b < nb ? pt[(int64_t)q * nb + b] : 0u;
+            s += v[q];
         }
+        // inclusive scan within the wave, then across the waves
+        uint32_t incl = s;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < PACK_THREADS / 64; ++w) {
+            const uint32_t x = wsum[w];
+            before += w < wave ? x : 0u;
+            total += x;
+        }
+        __syncthreads();
+        uint32_t run = carry + before + incl - s;
+        if (b < nb) {
+            goff[b] = (int32_t)run;
+#pragma unroll
+            for (int q = 0; q < PACK_PARTS; ++q) {
+                pt[(int64_t)q * nb + b] = run;
+                run += v[q];
+            }
+        }
+        carry += total;
     }
-    if (tid == PACK_THREADS - 1) goff[nb] = (int32_t)part[tid];
+    if (tid == 0) goff[nb] = (int32_t)carry;
 }
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter(
@@ -393,10 +407,15 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int32_t nb = view_buckets(v);
     uint32_t* cur = sh;            // nb cursors
     uint32_t* off = sh + nb;       // nb + 1 bucket starts
+    uint32_t* ps0 = off + nb + 1;  // nb: where this part's members start in each bucket
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
     const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
     for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
-        if (b < nb) cur[b] = pp[b];
+        if (b < nb) {
+            const uint32_t x = pp[b];
+            cur[b] = x;
+            ps0[b] = x;
+        }
         off[b] = (uint32_t)goff[b];
     }
     __syncthreads();
@@ -423,11 +442,14 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             uint32_t o = 0u, len = 0u;
             if (b != 0xffffu) {
                 const uint32_t pos = atomicAdd(&cur[b], 1u);
-                const uint32_t end = off[b + 1];
-                memt[pos] = (uint32_t)(i + 1) | (pos + 1 == end && end - off[b] >= REC_LONG ? MEM_LAST : 0u);
+                memt[pos] = (uint32_t)(i + 1);
+                // the run of (i, t): members of the opposite bucket placed
+                // by this part and the later ones, i.e. every member j with
+                // j >= the part's first sample, and some j < i of the part
                 const uint32_t ob = b ^ 1u;
-                o = (tbase + off[ob]) * 4u;
-                len = min(off[ob + 1] - off[ob], REC_LONG) * 4u;
+                const uint32_t rs = ps0[ob], rem = off[ob + 1] - rs;
+                o = (tbase + rs) * 4u;
+                len = min(rem, REC_LONG) * 4u;
             }
             ro[i] = o;
             rl[i] = (uint16_t)len;
@@ -532,6 +554,22 @@ __global__ void k_rr_init(unsigned long long* rr) {
     rr[1] = 0ull;
 }
 
+// Buckets of REC_LONG or more members (forest mode): their start and end
+// byte offsets in mem, per tree, in lng[t][0 .. lngn[t]) (lngn zeroed
+// first).  One thread per (tree, bucket).
+__global__ __launch_bounds__(256) void k_long_runs(const int32_t* goff_all, int32_t nb, int32_t T, int64_t N,
+                                                   uint2* lng, int32_t* lngn, int32_t lmax) {
+    const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (k >= (int64_t)T * nb) return;
+    const int32_t t = (int32_t)(k / nb), b = (int32_t)(k % nb);
+    const int32_t* off = goff_all + (int64_t)t * (nb + 1);
+    const uint32_t s = (uint32_t)off[b], e = (uint32_t)off[b + 1];
+    if (e - s < REC_LONG) return;
+    const int32_t slot = atomicAdd(&lngn[t], 1);
+    const uint32_t base = (uint32_t)t * (uint32_t)N;
+    if (slot < lmax) lng[(int64_t)t * lmax + slot] = make_uint2(4u * (base + s), 4u * (base + e));
+}
+
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
@@ -542,6 +580,20 @@ void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
 
 static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst);
 static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in);
+
+// The table of long buckets (forest mode), once the offsets are known.
+static int pack_long_runs(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst) {
+    const int32_t nb = view_buckets(v);
+    const int32_t lmax = (int32_t)(v.N / REC_LONG + 1);
+    RFXP_HIP(ctx, ctx->lng.ensure((size_t)v.T * lmax));
+    RFXP_HIP(ctx, ctx->lngn.ensure((size_t)v.T));
+    ctx->lmax = lmax;
+    fill_u32(ctx, (uint32_t*)ctx->lngn.p, v.T, 0u);
+    const int64_t n = (int64_t)v.T * nb;
+    hipLaunchKernelGGL(k_long_runs, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, ctx->stream, (const int32_t*)dst.off,
+                       nb, v.T, v.N, ctx->lng.p, ctx->lngn.p, lmax);
+    return check_launch(ctx, "k_long_runs");
+}
 
 int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst) {
     hipStream_t s = ctx->stream;
@@ -557,6 +609,7 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     if (N == 0) return RFXP_OK;
     if (forest && nb <= PART_MAX_NB) {
         if (int rc = pack_forest_parts(ctx, v, dst)) return rc;
+        if (int rc = pack_long_runs(ctx, v, dst)) return rc;
         return pack_nout(ctx, v, nout_in);
     }
     // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
@@ -607,6 +660,7 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     }
     if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
     if (!forest) return RFXP_OK;
+    if (int rc = pack_long_runs(ctx, v, dst)) return rc;
     return pack_nout(ctx, v, nout_in);
 }
 
@@ -623,7 +677,7 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget&
     RFXP_HIP(ctx, ctx->rlenT.ensure((size_t)T * N));
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
     const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
-    const size_t lds_h = (size_t)nb * 4, lds_s = (size_t)(2 * nb + 1) * 4;
+    const size_t lds_h = (size_t)nb * 4, lds_s = (size_t)(3 * nb + 1) * 4;
     if (lds_h > 32768)
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds_h));

@@ -42,18 +42,93 @@ constexpr int TRI_WAVES = TRI_THREADS / 64;
 // triangle
 // ---------------------------------------------------------------------------
 
+
+// Work items of a row band [r0, r1): row i is cut into segments of S
+// columns starting at i, i + S, ...; segment k of row i starts at i + k*S
+// and exists while N - i > k*S.  Rows are taken in groups of 8 (group g:
+// rows r0 + 8g .. r0 + 8g + 7); a group occupies 8 * n_g consecutive
+// workgroup slots, level-major (slot 8k + r: segment k of row r of the
+// group), n_g = the number of segments of its first row.  Workgroups are
+// dealt to the 8 XCDs round-robin by index, so every segment of a row runs
+// on the same XCD, one slot after the other, and the later segments find
+// the row's records and bucket runs -- which they read in full, as the
+// first segment does -- in that XCD's L2.  Slots of rows past the band or
+// of segments a row does not have are idle.
+//
+// G_k = number of groups with a segment k = min(G, ceil((N - r0 - k*S)/8)),
+// slots before group g = 8 * sum_k min(g, G_k); tri_slot() inverts that by
+// binary search over g.  The divisions (G, nlev) are done on the host.
+struct TriLevels {
+    int64_t N, S, r0, r1, G, nlev;
+};
+
+__host__ __device__ inline TriLevels tri_levels_of(int64_t N, int64_t S, int64_t r0, int64_t r1) {
+    TriLevels L;
+    L.N = N;
+    L.S = S;
+    L.r0 = r0;
+    L.r1 = r1;
+    L.G = (r1 - r0 + 7) / 8;
+    L.nlev = (N - r0 + S - 1) / S;
+    return L;
+}
+
+__host__ __device__ inline int64_t tri_groups_with_level(const TriLevels& L, int64_t k) {
+    const int64_t rem = L.N - L.r0 - k * L.S;
+    if (rem <= 0) return 0;
+    const int64_t g = (rem + 7) >> 3;
+    return g < L.G ? g : L.G;
+}
+
+__host__ __device__ inline int64_t tri_slots_before(const TriLevels& L, int64_t g) {
+    int64_t s = 0;
+    for (int64_t k = 0; k < L.nlev; ++k) {
+        const int64_t gk = tri_groups_with_level(L, k);
+        s += g < gk ? g : gk;
+    }
+    return 8 * s;
+}
+
+// Row i and segment k of slot b; false for an idle slot.  Groups
+// [G_m, G_{m-1}) have exactly m segments (G_nlev = 0), so the slots are
+// walked segment count by segment count, most segments (first groups)
+// first.
+__host__ __device__ inline bool tri_slot(const TriLevels& L, int64_t b, int64_t& i, int64_t& k) {
+    int64_t start = 0, g0 = 0;
+    for (int64_t m = L.nlev; m >= 1; --m) {
+        const int64_t g1 = tri_groups_with_level(L, m - 1);
+        const int64_t per = 8 * m;
+        const int64_t cnt = (g1 - g0) * per;
+        if (b < start + cnt) {
+            const int64_t off = b - start;
+            const int64_t gq = (int64_t)((uint64_t)off / (uint64_t)per);
+            const int64_t loc = off - gq * per;
+            k = loc >> 3;
+            i = L.r0 + 8 * (g0 + gq) + (loc & 7);
+            return i < L.r1 && L.N - i > k * L.S;
+        }
+        start += cnt;
+        g0 = g1;
+    }
+    return false;
+}
+
 struct TriArgs {
-    const uint32_t* roff;  // [N][ldr] bucket byte offsets in mem (+ REC_PAD)
-    const uint16_t* rlen;  // [N][ldr] bucket lengths in bytes (+ REC_PAD)
+    const uint32_t* roff;  // [N][ldr] run byte offsets in mem (+ REC_PAD)
+    const uint16_t* rlen;  // [N][ldr] run lengths in bytes (+ REC_PAD)
     const uint32_t* mem;
     uint32_t mem_bytes;  // readable bytes of mem (buffer-load range)
     int64_t ldr;         // record row stride (T rounded up to 16)
+    const uint2* lng;    // [T][lmax] long buckets: start, end byte offsets in mem
+    const int32_t* lngn; // [T] entries of lng per tree
+    int32_t lmax;
     const double* rinv;
     const unsigned long long* rr;
-    const int2* items;
     int64_t N;
     int32_t T;
     int32_t S;          // columns per item
+    TriLevels lev;      // work decomposition of the row band
+    int64_t item_base;  // item index of blockIdx.x == 0 (launches in chunks)
     int64_t e_base;     // idx(row_begin, row_begin)
     char* out;          // byte address of entry e_base (NF4: of its byte)
     float scale, zp;
@@ -70,18 +145,23 @@ struct TriArgs {
 enum { TRI_MODE_EXACT8 = 0, TRI_MODE_CHECK8 = 1, TRI_MODE_WIDE16 = 2 };
 
 // LDS layout of one workgroup (dynamic shared memory, at address 0):
-//   [0, S + 64)                    counters (8-bit, or 16-bit when redoing)
-//   [dummy_off, dummy_off + 4096)  one word per thread: lanes without a hit
-//                                  add into their own word
-//   [dummy_off + 4096, +32)        item scalars (row table, sums)
+//   [0, cap)                 the item's counters, cap = 16 * chunks <= S + 32
+//                            (8-bit, or 16-bit when redoing)
+//   [cap, cap + 4096)        one dummy word per thread (see count_hits)
+//   [misc_off, +64)          item scalars (geometry, row table, sums),
+//                            misc_off = round16(S + 64) + 4096
 constexpr int TRI_DUMMY_BYTES = TRI_THREADS * 4;
-constexpr int TRI_MISC_WORDS = 8;
-enum { MISC_LUT_LO = 0, MISC_LUT_HI = 1, MISC_UC = 2, MISC_SUM = 3, MISC_SLOTS = 4 };
+constexpr int TRI_MISC_WORDS = 16;
+enum {
+    MISC_LUT_LO = 0, MISC_LUT_HI = 1, MISC_UC = 2, MISC_SUM = 3, MISC_SLOTS = 4,  // cleared per item
+    MISC_ROW = 5, MISC_LO = 6, MISC_WIDTH = 7, MISC_SHIFT = 8, MISC_NCHUNK = 9, MISC_DST_LO = 10, MISC_DST_HI = 11
+};
+constexpr int TRI_MISC_ZEROED = 5;  // words cleared per item (the row table and the sums)
 
-__host__ __device__ constexpr uint32_t tri_dummy_off(int32_t S) { return ((uint32_t)S + 64u + 15u) & ~15u; }
-__host__ __device__ constexpr uint32_t tri_lds_bytes(int32_t S) {
-    return tri_dummy_off(S) + TRI_DUMMY_BYTES + TRI_MISC_WORDS * 4;
+__host__ __device__ constexpr uint32_t tri_misc_off(int32_t S) {
+    return (((uint32_t)S + 64u + 15u) & ~15u) + TRI_DUMMY_BYTES;
 }
+__host__ __device__ constexpr uint32_t tri_lds_bytes(int32_t S) { return tri_misc_off(S) + TRI_MISC_WORDS * 4; }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int b) { return (w >> (8 * b)) & 0xffu; }
 
@@ -156,32 +236,27 @@ __device__ __noinline__ uint32_t code_word_exact(uint32_t w, uint32_t lut_lo, ui
 // word, so every lane of every step lands somewhere countable.
 struct Group {
     uint32_t m[16];
-    bool has_long;  // some bucket of the group has more than 64 members
+    bool has_long;  // some run of the group may have more than 63 members
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t mem_rsrc(const uint32_t* mem, uint32_t nbytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)mem, (short)0, (int)nbytes, 0x00020000);
 }
 
+// The 16 bucket loads of one record group (ro, rl point at its records).
 __device__ __forceinline__ void load_group(const uint32_t* mem, const uint32_t* __restrict__ ro,
-                                           const uint16_t* __restrict__ rl, bool valid, uint32_t lane4,
-                                           Group& G) {
-    // `valid` false issues the same 16 loads with an empty range (no memory
-    // access): the count of loads in flight stays static, so the wait for
-    // one group can leave the other outstanding.  Records past a row's T
-    // entries are the next row's, or after the last row the zeroed slack,
-    // so every offset read here lies inside mem.
+                                           const uint16_t* __restrict__ rl, uint32_t lane4, Group& G) {
     uint32_t off[16];
     uint32_t lw[8];
 #pragma unroll
     for (int u = 0; u < 16; ++u) off[u] = __builtin_amdgcn_readfirstlane(ro[u]);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) lw[k] = __builtin_amdgcn_readfirstlane(((const uint32_t*)rl)[k]) & (valid ? ~0u : 0u);
-    // any length above 256 bytes: v + (0x8000 - 257) sets bit 15 for 257..0x7fff, v sets it above
+    for (int k = 0; k < 8; ++k) lw[k] = __builtin_amdgcn_readfirstlane(((const uint32_t*)rl)[k]);
+    // a length of 256 bytes or more (64+ members) may need the tail loop
     uint32_t lng = 0u;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) lng |= ((lw[k] & 0x7fff7fffu) + 0x7eff7effu) | lw[k];
-    G.has_long = (lng & 0x80008000u) != 0u;
+    for (int k = 0; k < 8; ++k) lng |= lw[k];
+    G.has_long = (lng & 0xff00ff00u) != 0u;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const uint32_t len4 = (lw[u >> 1] >> (16 * (u & 1))) & 0xffffu;
@@ -197,84 +272,86 @@ __device__ __forceinline__ void lds_add(uint32_t addr, uint32_t val) {
     __hip_atomic_fetch_add((lds_u32*)(uintptr_t)addr, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// One counting step: m = j + 1 of a member (0: no member); counter unit
+// c = j - lo + shift.  Units c >= xlim -- members outside the item, empty
+// lanes -- are clamped to xlim, the unit of this thread's dummy word, which
+// sits with the other dummy words right after the item's counters; units
+// between the counters and xlim fall on other threads' dummy words.  Every
+// lane of every step thus adds 1 to some byte (16-bit unit) of the
+// counter-and-dummy area, without a compare or select.
 template <int BITS>
-__device__ __forceinline__ void count_hits(uint32_t* cnt, uint32_t m, uint32_t base1, uint32_t cap, uint32_t dummy) {
-    // m = j + 1 (0 for no member); c = j - lo + shift
-    const uint32_t c = m - base1;
-    const bool h = c < cap;
-    uint32_t addr, val;
-    if constexpr (BITS == 8) {
-        addr = c & ~3u;
-        val = 1u << ((c << 3) & 31u);
-    } else {
-        addr = (c << 1) & ~3u;
-        val = 1u << ((c << 4) & 16u);
-    }
-    (void)cnt;
-    lds_add(h ? addr : dummy, val);
+__device__ __forceinline__ void count_hits(uint32_t m, uint32_t base1, uint32_t xlim) {
+    const uint32_t c = min(m - base1, xlim);
+    if constexpr (BITS == 8) lds_add(c & ~3u, 1u << ((c << 3) & 31u));
+    else lds_add((c << 1) & ~3u, 1u << ((c << 4) & 31u));
 }
 
+// Runs of REC_LONG or more members: their end, from the per-tree table of
+// long buckets (start and end byte offsets in mem) that contains `off`.
+__device__ __forceinline__ uint32_t long_run_end(const TriArgs& a, int32_t t, uint32_t off, uint32_t fallback) {
+    const uint2* L = a.lng + (int64_t)t * a.lmax;
+    const int32_t n = min(a.lngn[t], a.lmax);
+    for (int32_t e = 0; e < n; ++e) {
+        const uint2 r = L[e];
+        if (r.x <= off && off < r.y) return r.y;
+    }
+    return fallback;
+}
+
+// Hit phase of one item: every member j of row i's runs bumps counter unit
+// j - lo + shift (see count_hits).  Each wave owns a contiguous range of
+// record groups (16 trees each) and keeps two groups' loads in flight; no
+// load is issued past its range.  Returns the wave's 64-lane counting steps
+// (uniform).
 template <int BITS>
-__device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, uint32_t* cnt, int64_t i, int64_t lo, uint32_t cap,
-                                              int32_t shift, uint32_t dummy) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t lane4 = lane * 4u;
+__device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64_t lo, int32_t shift, uint32_t xlim) {
+    const uint32_t lane4 = (threadIdx.x & 63) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // whole groups of 16 trees per wave, so record rows stay 16-aligned
     const int32_t ng = (a.T + 15) >> 4;
     const int32_t g0 = (ng * wave) / TRI_WAVES;
     const int32_t g1 = (ng * (wave + 1)) / TRI_WAVES;
+    if (g0 >= g1) return 0u;
     const uint32_t* ro = a.roff + i * a.ldr;
     const uint16_t* rl = a.rlen + i * a.ldr;
     const uint32_t base1 = (uint32_t)lo + 1u - (uint32_t)shift;
     uint32_t steps = 0;
-    // buckets of more than 64 members (rare for per-leaf buckets)
+    // members past the first 64 of a run (rare for per-leaf buckets)
     auto long_tail = [&](int32_t t0) {
         for (int u = 0; u < 16; ++u) {
             const uint32_t len4 = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
             if (len4 <= 256u) continue;
             const uint32_t off = __builtin_amdgcn_readfirstlane(ro[t0 + u]);
-            if (len4 == 4u * REC_LONG) {
-                // REC_LONG or more members: read on until the last-member mark
-                // (mem has MEM_PAD words of slack after its end)
-                const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, a.mem_bytes);
-                bool more = true;
-                for (uint32_t p4 = 256u; more; p4 += 256u) {
-                    const uint32_t m = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0);
-                    const unsigned long long lastm = __ballot((m & MEM_LAST) != 0u);
-                    const uint32_t cut = lastm ? (uint32_t)__builtin_ctzll(lastm) : 64u;
-                    count_hits<BITS>(cnt, lane <= cut ? (m & MEM_ID) : 0u, base1, cap, dummy);
-                    ++steps;
-                    more = (lastm == 0ull);
-                }
-            } else {
-                const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, off + len4);
-                for (uint32_t p4 = 256u; p4 < len4; p4 += 256u) {
-                    count_hits<BITS>(cnt, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0),
-                                     base1, cap, dummy);
-                    ++steps;
-                }
+            const uint32_t end = len4 == 4u * REC_LONG ? long_run_end(a, t0 + u, off, off + len4) : off + len4;
+            const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, end);
+            for (uint32_t p4 = 256u; off + p4 < end; p4 += 256u) {
+                count_hits<BITS>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0), base1, xlim);
+                ++steps;
             }
         }
     };
-    // Two group buffers in ping-pong: one is counted while the other's 16
-    // loads are in flight (no register copies between them).
+    // A and B in ping-pong: one group is counted while the other's loads
+    // are in flight (no register copies between them)
     Group A, B;
-    load_group(a.mem, ro + 16 * g0, rl + 16 * g0, g0 < g1, lane4, A);
-    int32_t g = g0;
-    for (; g < g1; g += 2) {
-        load_group(a.mem, ro + 16 * (g + 1), rl + 16 * (g + 1), g + 1 < g1, lane4, B);
-        __builtin_amdgcn_sched_barrier(0);  // issue B's loads before touching A's data
-#pragma unroll
-        for (int u = 0; u < 16; ++u) count_hits<BITS>(cnt, A.m[u], base1, cap, dummy);
-        if (A.has_long) long_tail(16 * g);
-        load_group(a.mem, ro + 16 * (g + 2), rl + 16 * (g + 2), g + 2 < g1, lane4, A);
+    load_group(a.mem, ro + 16 * g0, rl + 16 * g0, lane4, A);
+    if (g0 + 1 < g1) load_group(a.mem, ro + 16 * (g0 + 1), rl + 16 * (g0 + 1), lane4, B);
+    for (int32_t g = g0;; g += 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) count_hits<BITS>(cnt, B.m[u], base1, cap, dummy);
+        for (int u = 0; u < 16; ++u) count_hits<BITS>(A.m[u], base1, xlim);
+        steps += 16;
+        if (A.has_long) long_tail(16 * g);
+        if (g + 2 < g1) load_group(a.mem, ro + 16 * (g + 2), rl + 16 * (g + 2), lane4, A);
+        if (g + 1 >= g1) break;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) count_hits<BITS>(B.m[u], base1, xlim);
+        steps += 16;
         if (B.has_long) long_tail(16 * (g + 1));
+        if (g + 3 < g1) load_group(a.mem, ro + 16 * (g + 3), rl + 16 * (g + 3), lane4, B);
+        if (g + 2 >= g1) break;
     }
-    return steps + 32u * (uint32_t)((g - g0) >> 1);
+    return steps;
 }
 
 // Exact per-entry epilogue with 16-bit counters (segments whose 8-bit
@@ -336,46 +413,101 @@ __device__ __forceinline__ void row_table(const TriArgs& a, double ri, uint32_t*
     }
 }
 
-// Item geometry shared by the prologue, the wrap check and the redo.
+// Item geometry, worked out by thread 0 (tri_slot, the 64-bit entry index
+// and the output alignment) and read by every wave from LDS.
 struct ItemGeom {
     int64_t i, lo;
     int32_t width, shift, nchunk, nwords;
+    int64_t dst;  // byte offset of the item's first 16-byte output chunk from a.out
 };
 
+// Thread 0: the item of this workgroup into misc (MISC_ROW = ~0 when idle).
+// Byte formats: entries of esz bytes, a counter byte per entry, epc entries
+// per 16-byte chunk.  NF4 (esz = 0): a counter byte per nibble entry, 32
+// entries per 16-byte chunk.
+template <int esz>
+__device__ __forceinline__ void item_to_lds(const TriArgs& a, uint32_t* misc) {
+    int64_t i, k;
+    if (!tri_slot(a.lev, a.item_base + blockIdx.x, i, k)) {
+        misc[MISC_ROW] = 0xffffffffu;
+        return;
+    }
+    const int64_t lo = i + k * a.S;
+    const int32_t width = (int32_t)min((int64_t)a.S, a.N - lo);
+    int64_t dst;
+    int32_t shift, nchunk;
+    if constexpr (esz == 0) {
+        const int64_t g0 = tri_idx(a.N, i, lo) - a.e_base + (a.e_base & 1);  // nibble index
+        const int64_t b0 = (g0 >> 1) + (int64_t)((uintptr_t)a.out & 15u);
+        shift = (int32_t)((b0 & 15) * 2 + (g0 & 1));
+        dst = (b0 & ~(int64_t)15) - (int64_t)((uintptr_t)a.out & 15u);
+        nchunk = (shift + width + 31) / 32;
+    } else {
+        constexpr int epc = 16 / esz;
+        const int64_t b0 = (tri_idx(a.N, i, lo) - a.e_base) * esz + (int64_t)((uintptr_t)a.out & 15u);
+        shift = (int32_t)((b0 & 15) / esz);
+        dst = (b0 & ~(int64_t)15) - (int64_t)((uintptr_t)a.out & 15u);
+        nchunk = (shift + width + epc - 1) / epc;
+    }
+    misc[MISC_ROW] = (uint32_t)i;
+    misc[MISC_LO] = (uint32_t)lo;
+    misc[MISC_WIDTH] = (uint32_t)width;
+    misc[MISC_SHIFT] = (uint32_t)shift;
+    misc[MISC_NCHUNK] = (uint32_t)nchunk;
+    misc[MISC_DST_LO] = (uint32_t)(uint64_t)dst;
+    misc[MISC_DST_HI] = (uint32_t)((uint64_t)dst >> 32);
+}
+
+template <int esz>
+__device__ __forceinline__ bool item_from_lds(const uint32_t* misc, ItemGeom& gm) {
+    const uint32_t row = misc[MISC_ROW];
+    if (row == 0xffffffffu) return false;
+    gm.i = row;
+    gm.lo = misc[MISC_LO];
+    gm.width = (int32_t)misc[MISC_WIDTH];
+    gm.shift = (int32_t)misc[MISC_SHIFT];
+    gm.nchunk = (int32_t)misc[MISC_NCHUNK];
+    gm.dst = (int64_t)(((uint64_t)misc[MISC_DST_HI] << 32) | misc[MISC_DST_LO]);
+    gm.nwords = esz == 0 ? gm.nchunk * 8 : gm.nchunk * (16 / esz) / 4;
+    return true;
+}
+
 // 16-bit recount of an item (its 8-bit counters wrapped, or the launch is
-// WIDE16): passes of half the counter capacity, exact stores.
+// WIDE16): passes of half the counter capacity, exact stores.  The dummy
+// words follow the pass's counters, 16-byte aligned, inside the item's
+// counter-and-dummy area.
 template <int F>
-__device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, double ri, uint32_t dummy) {
+__device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, double ri) {
     if (threadIdx.x == 0) atomicAdd(&a.flags[0], 1);
     const int32_t half_cap = gm.nwords * 2;  // 16-bit counters that fit
     for (int32_t d0 = 0; d0 < gm.width; d0 += half_cap) {
         const int32_t w2 = min(half_cap, gm.width - d0);
+        const uint32_t cap16 = ((uint32_t)w2 + 7u) & ~7u;
         __syncthreads();
-        for (int32_t w = threadIdx.x; w < (w2 + 1) / 2; w += TRI_THREADS) cnt[w] = 0u;
+        for (int32_t w = threadIdx.x; w < (int32_t)cap16 / 2; w += TRI_THREADS) cnt[w] = 0u;
         __syncthreads();
-        hit_phase<16>(a, cnt, gm.i, gm.lo + d0, (uint32_t)w2, 0, dummy);
+        hit_phase<16>(a, gm.i, gm.lo + d0, 0, cap16 + 2u * threadIdx.x);
         __syncthreads();
         store_exact16<F>(a, cnt, gm.i, gm.lo + d0, w2, ri);
     }
 }
 
-// Zeroes counter words [0, nwords) (rounded up to 4) and this thread's dummy word.
-__device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords, uint32_t dummy) {
+// Zeroes the item's counter words [0, nwords) (nwords a multiple of 4) and
+// the dummy words after them.
+__device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords) {
     uint4* c4 = (uint4*)cnt;
-    const int32_t n4 = (nwords + 3) >> 2;
+    const int32_t n4 = (nwords >> 2) + TRI_THREADS / 4;
     for (int32_t w = threadIdx.x; w < n4; w += TRI_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
-    cnt[dummy >> 2] = 0u;
 }
 
 // After the hit phase of a CHECK8 item: every lane of every counting step
-// added 1 to exactly one byte, of a counter or of its dummy word, and a
-// counter byte that reached 256 wrapped (carrying into its neighbour), which
-// lowers the byte sum.  So the counters are exact iff
+// added 1 to exactly one byte of the counter-and-dummy area, and a byte that
+// reached 256 wrapped (carrying into its neighbour), which lowers the byte
+// sum.  So the counters are exact iff
 //   sum of counter bytes + sum of dummy bytes == 64 * counting steps.
-// The dummy words cannot wrap: CHECK8 is used only while a wave makes at
-// most 255 steps.
-__device__ __forceinline__ bool counts_exact(uint32_t* misc, uint32_t bsum, const uint32_t* cnt, uint32_t dummy) {
-    bsum = __builtin_amdgcn_sad_u8(cnt[dummy >> 2], 0u, bsum);
+// (A dummy byte that wraps only costs a recount.)
+__device__ __forceinline__ bool counts_exact(uint32_t* misc, uint32_t bsum, const uint32_t* cnt, uint32_t nwords) {
+    bsum = __builtin_amdgcn_sad_u8(cnt[nwords + threadIdx.x], 0u, bsum);
     // wave reduction, then one atomic per wave
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) bsum += (uint32_t)__shfl_xor((int)bsum, d, 64);
@@ -389,41 +521,30 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     extern __shared__ uint32_t cnt[];
     constexpr int esz = FmtInfo<F>::esz;
     constexpr int epc = 16 / esz;  // entries per 16-byte chunk
-    uint32_t* const misc = cnt + (tri_dummy_off(a.S) + TRI_DUMMY_BYTES) / 4;
-    const uint32_t dummy = tri_dummy_off(a.S) + threadIdx.x * 4u;
+    uint32_t* const misc = cnt + tri_misc_off(a.S) / 4;
 
-    const int2 it = a.items[blockIdx.x];
+    if (threadIdx.x == 0) item_to_lds<esz>(a, misc);
+    __syncthreads();
     ItemGeom gm;
-    gm.i = it.x;
-    gm.lo = it.y;
-    gm.width = (int32_t)min((int64_t)a.S, a.N - gm.lo);
+    if (!item_from_lds<esz>(misc, gm)) return;
     const int64_t i = gm.i, lo = gm.lo;
-    const int32_t width = gm.width;
+    const int32_t width = gm.width, shift = gm.shift, nchunk = gm.nchunk;
+    char* const dst_al = a.out + gm.dst;
     const double ri = a.rinv[i];
 
-    // Align counters to the output: chunk c of the LDS array maps to the
-    // 16-byte aligned output chunk c.
-    char* const dst0 = a.out + (tri_idx(a.N, i, lo) - a.e_base) * esz;
-    const int32_t shift = (int32_t)(((uintptr_t)dst0 & 15u) / esz);
-    char* const dst_al = dst0 - shift * esz;
-    const int32_t nchunk = (shift + width + epc - 1) / epc;
-    gm.shift = shift;
-    gm.nchunk = nchunk;
-    gm.nwords = nchunk * epc / 4;  // 8-bit counters
-
     if (a.mode == TRI_MODE_WIDE16) {
-        redo_wide<F>(a, cnt, gm, ri, dummy);
+        redo_wide<F>(a, cnt, gm, ri);
         return;
     }
-    zero_counters(cnt, gm.nwords, dummy);
-    if (threadIdx.x < TRI_MISC_WORDS) misc[threadIdx.x] = 0u;
+    zero_counters(cnt, gm.nwords);
+    if (threadIdx.x < TRI_MISC_ZEROED) misc[threadIdx.x] = 0u;
     if constexpr (F == I8 || F == U8) row_table<F>(a, ri, misc);
     __syncthreads();
     // counters cover units [0, nchunk * units-per-chunk): hits outside the
     // item's columns but inside that range land in the unstored padding
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = hit_phase<8>(a, cnt, i, lo, cap, shift, dummy);
+    const uint32_t steps = hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x);
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -520,7 +641,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check && !counts_exact(misc, bsum, cnt, dummy)) redo_wide<F>(a, cnt, gm, ri, dummy);
+    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords)) redo_wide<F>(a, cnt, gm, ri);
 }
 
 // NF4: two entries per byte.  Nibble position g(e) = e - e_base + (e_base & 1)
@@ -529,38 +650,28 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
 // merged with 32-bit atomics on its own nibble only.
 __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri_nf4(TriArgs a) {
     extern __shared__ uint32_t cnt[];
-    uint32_t* const misc = cnt + (tri_dummy_off(a.S) + TRI_DUMMY_BYTES) / 4;
-    const uint32_t dummy = tri_dummy_off(a.S) + threadIdx.x * 4u;
+    uint32_t* const misc = cnt + tri_misc_off(a.S) / 4;
 
-    const int2 it = a.items[blockIdx.x];
+    if (threadIdx.x == 0) item_to_lds<0>(a, misc);
+    __syncthreads();
     ItemGeom gm;
-    gm.i = it.x;
-    gm.lo = it.y;
-    gm.width = (int32_t)min((int64_t)a.S, a.N - gm.lo);
+    if (!item_from_lds<0>(misc, gm)) return;
     const int64_t i = gm.i, lo = gm.lo;
-    const int32_t width = gm.width;
+    const int32_t width = gm.width, shift = gm.shift, nchunk = gm.nchunk;
+    char* const dst_al = a.out + gm.dst;
     const double ri = a.rinv[i];
 
-    const int64_t g0 = tri_idx(a.N, i, lo) - a.e_base + (a.e_base & 1);  // nibble index
-    char* const byte0 = a.out + (g0 >> 1);
-    const int32_t shift = (int32_t)(((uintptr_t)byte0 & 15u) * 2 + (g0 & 1));  // nibbles
-    char* const dst_al = byte0 - ((uintptr_t)byte0 & 15u);
-    const int32_t nchunk = (shift + width + 31) / 32;  // 32 nibbles per 16 bytes
-    gm.shift = shift;
-    gm.nchunk = nchunk;
-    gm.nwords = nchunk * 8;
-
     if (a.mode == TRI_MODE_WIDE16) {
-        redo_wide<NF4>(a, cnt, gm, ri, dummy);
+        redo_wide<NF4>(a, cnt, gm, ri);
         return;
     }
-    zero_counters(cnt, gm.nwords, dummy);
-    if (threadIdx.x < TRI_MISC_WORDS) misc[threadIdx.x] = 0u;
+    zero_counters(cnt, gm.nwords);
+    if (threadIdx.x < TRI_MISC_ZEROED) misc[threadIdx.x] = 0u;
     row_table<NF4>(a, ri, misc);
     __syncthreads();
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = hit_phase<8>(a, cnt, i, lo, cap, shift, dummy);
+    const uint32_t steps = hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x);
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -626,7 +737,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check && !counts_exact(misc, bsum, cnt, dummy)) redo_wide<NF4>(a, cnt, gm, ri, dummy);
+    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords)) redo_wide<NF4>(a, cnt, gm, ri);
 }
 
 // ---------------------------------------------------------------------------
@@ -648,9 +759,10 @@ static int tri_segment_cols(rfxp_ctx* ctx) {
 // Counter mode of a launch (TRI_MODE_*).
 static int tri_mode(int32_t T) {
     if (T <= 255) return TRI_MODE_EXACT8;
-    // counting steps of the busiest wave: 16 trees per step, groups in pairs
+    // counting steps of the busiest wave: one per group of 16 trees and
+    // record (runs past 64 members add steps, which at worst cost a recount)
     const int64_t groups = ceil_div_i((T + 15) / 16, TRI_WAVES);
-    const int64_t steps = 32 * ((groups + 1) / 2);
+    const int64_t steps = 16 * groups;
     return steps <= 192 ? TRI_MODE_CHECK8 : TRI_MODE_WIDE16;
 }
 
@@ -680,7 +792,7 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     if (N < 0 || T < 1 || T > 65535 || nleaf < 1 || nleaf > (1 << 29))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: need N >= 0, 1 <= T <= 65535, 1 <= nleaf <= 2^29");
     if (N > MAX_FOREST_N)
-        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_forest: N above 2^24 - 1 is not supported");
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_forest: N above 2^31 - 2 is not supported");
     if (N > 0 && (!leaf || !oob_words))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_forest: leaf / oob_words are NULL");
     if (oob_ld < (N + 31) / 32)
@@ -713,23 +825,49 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     return RFXP_OK;
 }
 
-template <int F>
-static hipError_t launch_tri(rfxp_ctx* ctx, const TriArgs& a, int64_t n_items, size_t lds) {
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_tri<F>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(k_tri<F>, dim3((unsigned)n_items), dim3(TRI_THREADS), lds, ctx->stream, a);
-    return hipGetLastError();
+// Workgroups per launch: gridDim.x * blockDim.x must stay below 2^32, and a
+// multiple of 8 keeps the slot -> XCD mapping of every chunk aligned.
+constexpr int64_t TRI_MAX_GRID = (int64_t)((1ull << 32) / TRI_THREADS) - 8;
+
+// Number of workgroup slots of a row band (idle slots included).
+static int64_t tri_slot_count(int64_t N, int32_t S, int64_t r0, int64_t r1) {
+    if (r0 >= r1) return 0;
+    const TriLevels L = tri_levels_of(N, S, r0, r1);
+    return tri_slots_before(L, L.G);
 }
 
-static hipError_t launch_tri_nf4(rfxp_ctx* ctx, const TriArgs& a, int64_t n_items, size_t lds) {
+extern "C" int64_t rfxp_upper_work_item(int64_t N, int32_t S, int64_t r0, int64_t r1, int64_t e, int64_t* row,
+                                        int64_t* col) {
+    if (N < 1 || S < 1 || r0 < 0 || r1 > N || r0 >= r1) return -1;
+    const int64_t n = tri_slot_count(N, S, r0, r1);
+    if (e >= 0 && e < n && row && col) {
+        int64_t i, k;
+        const bool ok = tri_slot(tri_levels_of(N, S, r0, r1), e, i, k);
+        *row = ok ? i : -1;
+        *col = ok ? i + k * S : -1;
+    }
+    return n;
+}
+
+extern "C" int64_t rfxp_upper_launches(int64_t n_items) {
+    return n_items <= 0 ? 0 : (n_items + TRI_MAX_GRID - 1) / TRI_MAX_GRID;
+}
+
+template <class K>
+static hipError_t launch_items(rfxp_ctx* ctx, K kernel, TriArgs a, int64_t n_items, size_t lds) {
     if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_tri_nf4, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(k_tri_nf4, dim3((unsigned)n_items), dim3(TRI_THREADS), lds, ctx->stream, a);
-    return hipGetLastError();
+    // items in chunks of at most TRI_MAX_GRID workgroups, in stream order
+    for (int64_t b = 0; b < n_items; b += TRI_MAX_GRID) {
+        a.item_base = b;
+        const int64_t n = std::min<int64_t>(TRI_MAX_GRID, n_items - b);
+        hipLaunchKernelGGL(kernel, dim3((unsigned)n), dim3(TRI_THREADS), lds, ctx->stream, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t r0, int64_t r1, void* out) {
@@ -746,50 +884,43 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     if (((uintptr_t)out) % esz != 0) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: out is not aligned to its entry size");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
 
+    // The kernels derive each item's (row, segment) from its index, so
+    // consecutive calls on one stream share no host-written state.
     const int32_t S = tri_segment_cols(ctx);
-    // work list: rows in increasing order, each split into S-column segments
-    if (ctx->items_key[0] != N || ctx->items_key[1] != r0 || ctx->items_key[2] != r1 || ctx->items_key[3] != S) {
-        std::vector<int2> items;
-        for (int64_t i = r0; i < r1; ++i)
-            for (int64_t lo = i; lo < N; lo += S) items.push_back(make_int2((int)i, (int)lo));
-        if ((int64_t)items.size() > 0x7fffffffLL) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_upper: too many work items");
-        RFXP_HIP(ctx, ctx->items.ensure(items.size()));
-        RFXP_HIP(ctx, hipMemcpy(ctx->items.p, items.data(), items.size() * sizeof(int2), hipMemcpyHostToDevice));
-        ctx->n_items = (int64_t)items.size();
-        ctx->items_key[0] = N;
-        ctx->items_key[1] = r0;
-        ctx->items_key[2] = r1;
-        ctx->items_key[3] = S;
-    }
     TriArgs a;
     a.roff = ctx->roff.p;
     a.rlen = ctx->rlen.p;
     a.ldr = ctx->ldr;
+    a.lng = ctx->lng.p;
+    a.lngn = ctx->lngn.p;
+    a.lmax = ctx->lmax;
     a.mem = ctx->bkt_mem.p;
     a.mem_bytes = (uint32_t)(((uint64_t)ctx->T * (uint64_t)N + MEM_PAD) * 4u);
     a.rinv = ctx->rinv.p;
     a.rr = ctx->rrange.p;
-    a.items = ctx->items.p;
     a.N = N;
     a.T = ctx->T;
     a.S = S;
+    a.lev = tri_levels_of(N, S, r0, r1);
+    a.item_base = 0;
     a.e_base = tri_idx(N, r0, r0);
     a.out = (char*)out;
     a.scale = scale;
     a.zp = zp;
     a.flags = ctx->flags.p;
     a.mode = tri_mode(ctx->T);
+    const int64_t n_items = tri_slot_count(N, S, r0, r1);
     const size_t lds = tri_lds_bytes(S);
     hipError_t e;
     {
         LaunchTimer tm(ctx, "tri");
         switch (fmt) {
-            case F32: e = launch_tri<F32>(ctx, a, ctx->n_items, lds); break;
-            case F16: e = launch_tri<F16>(ctx, a, ctx->n_items, lds); break;
-            case I8: e = launch_tri<I8>(ctx, a, ctx->n_items, lds); break;
-            case U8: e = launch_tri<U8>(ctx, a, ctx->n_items, lds); break;
-            case U16: e = launch_tri<U16>(ctx, a, ctx->n_items, lds); break;
-            default: e = launch_tri_nf4(ctx, a, ctx->n_items, lds); break;
+            case F32: e = launch_items(ctx, k_tri<F32>, a, n_items, lds); break;
+            case F16: e = launch_items(ctx, k_tri<F16>, a, n_items, lds); break;
+            case I8: e = launch_items(ctx, k_tri<I8>, a, n_items, lds); break;
+            case U8: e = launch_items(ctx, k_tri<U8>, a, n_items, lds); break;
+            case U16: e = launch_items(ctx, k_tri<U16>, a, n_items, lds); break;
+            default: e = launch_items(ctx, k_tri_nf4, a, n_items, lds); break;
         }
     }
     if (e != hipSuccess) return hip_error(ctx, e, "k_tri launch");

@@ -68,6 +68,10 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_nbytes.argtypes = [C.c_int, i64, i64, i64]
     L.rfxp_upper_nbytes.restype = i64
     L.rfxp_get_nout.argtypes = [vp, vp]
+    L.rfxp_upper_work_item.argtypes = [i64, i32, i64, i64, i64, C.POINTER(i64), C.POINTER(i64)]
+    L.rfxp_upper_work_item.restype = i64
+    L.rfxp_upper_launches.argtypes = [i64]
+    L.rfxp_upper_launches.restype = i64
     L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
     L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
@@ -89,6 +93,21 @@ def upper_nbytes(fmt: int, n: int, r0: int = 0, r1: int | None = None) -> int:
     if v < 0:
         raise ValueError("bad format or row range")
     return v
+
+
+def upper_work_items(n: int, s: int, r0: int, r1: int):
+    """Segments (row, first column) of rfxp_upper's decomposition of rows
+    [r0, r1) into S-column segments, in launch order (host only)."""
+    L = load()
+    cnt = L.rfxp_upper_work_item(n, s, r0, r1, -1, None, None)
+    if cnt < 0:
+        raise ValueError("bad arguments")
+    out = []
+    row, col = C.c_int64(), C.c_int64()
+    for e in range(cnt):
+        L.rfxp_upper_work_item(n, s, r0, r1, e, C.byref(row), C.byref(col))
+        out.append((row.value, col.value))
+    return out
 
 
 def pack_oob_bits(oob_tn):

@@ -119,3 +119,71 @@ def test_host_int8_scaling_matches_reference_formula_and_rejects_empty_input():
     fn(data.ctypes.data, 0, ctypes.byref(sc), ctypes.byref(zp))
     assert (sc.value, zp.value) == (3.0, 4.0)
     assert b"no data" in lib.rfx_compat_last_error()
+
+
+def _all_segments(n, s, r0, r1):
+    """Every (row, first column) segment of rows [r0, r1): segment k of row i
+    starts at i + k*S while N - i > k*S."""
+    return {(i, i + k * s) for i in range(r0, r1) for k in range((n - i + s - 1) // s)}
+
+
+@pytest.mark.parametrize("n,s,r0,r1", [(1, 1, 0, 1), (5, 2, 0, 5), (5, 2, 1, 3), (17, 4, 0, 17),
+                                       (17, 4, 16, 17), (100, 7, 3, 98), (100, 100, 0, 100),
+                                       (100, 1000, 0, 100), (1000, 77, 0, 1000), (1000, 77, 500, 501),
+                                       (999, 64, 937, 999), (64, 64, 0, 1), (300, 41, 9, 290)])
+def test_upper_work_items_cover_the_band_once(n, s, r0, r1):
+    """Slots of rfxp_upper's decomposition: the non-idle ones cover every
+    segment of the band exactly once; all segments of a row sit on slots
+    congruent mod 8 (one XCD), in increasing column order one slot-group of
+    8 apart; each segment's output range lies inside the band's buffer."""
+    slots = R.upper_work_items(n, s, r0, r1)
+    assert len(slots) % 8 == 0
+    real = [(b, i, lo) for b, (i, lo) in enumerate(slots) if i >= 0]
+    assert len({(i, lo) for _, i, lo in real}) == len(real)
+    assert {(i, lo) for _, i, lo in real} == _all_segments(n, s, r0, r1)
+    by_row = {}
+    for b, i, lo in real:
+        assert b % 8 == (i - r0) % 8
+        by_row.setdefault(i, []).append((b, lo))
+    for i, lst in by_row.items():
+        lst.sort()
+        assert [lo for _, lo in lst] == [i + k * s for k in range(len(lst))]
+        assert all(b1 - b0 == 8 for (b0, _), (b1, _) in zip(lst, lst[1:]))
+    e_base = r0 * n - r0 * (r0 + 1) // 2 + r0
+    e_end = r1 * n - r1 * (r1 + 1) // 2 + r1
+    covered = 0
+    for _, i, lo in real:
+        width = min(s, n - lo)
+        e0 = i * n - i * (i + 1) // 2 + lo
+        assert e_base <= e0 and e0 + width <= e_end
+        covered += width
+    assert covered == e_end - e_base
+    # idle slots are a small share
+    assert len(slots) - len(real) <= 8 * ((n - r0 + s - 1) // s) + 7
+
+
+def test_upper_work_items_at_large_sizes():
+    """Closed form at sizes where enumeration is too long: slot counts, a
+    sample of slots, and the launch split at 2^22 - 8 workgroups."""
+    L = R.load()
+    import ctypes as C
+
+    row, col = C.c_int64(), C.c_int64()
+    n, s = 100_000, 77_696
+    cnt = L.rfxp_upper_work_item(n, s, 0, n, -1, None, None)
+    # groups of 8 rows: two segments while the group's first row is below N - S
+    g2 = (n - s + 7) // 8
+    assert cnt == 8 * ((n + 7) // 8) + 8 * g2
+    n = 5_000_000
+    cnt = L.rfxp_upper_work_item(n, s, 0, n, -1, None, None)
+    segs = sum(max(0, n - k * s) for k in range((n + s - 1) // s))
+    assert segs <= cnt <= segs + 8 * 65 and cnt > (1 << 22)
+    big = (1 << 22) - 8
+    assert L.rfxp_upper_launches(cnt) == (cnt + big - 1) // big
+    assert L.rfxp_upper_launches(big) == 1 and L.rfxp_upper_launches(big + 1) == 2
+    for e in (0, 1, 8, cnt // 3, cnt // 2, cnt - 9, cnt - 1):
+        L.rfxp_upper_work_item(n, s, 0, n, e, C.byref(row), C.byref(col))
+        i, lo = row.value, col.value
+        if i >= 0:
+            assert 0 <= i <= lo < n and (lo - i) % s == 0 and e % 8 == i % 8
+    assert L.rfxp_upper_work_item(n, s, 7, 3, 0, None, None) == -1

@@ -270,3 +270,101 @@ def test_c3_shape_sampled_rows(gpu_ctx):
     diag = torch.tensor([O.tri_idx(n, i, i) for i in range(0, n, 997)], device="cuda:0")
     assert bool((out[diag] == dcode).all())
     idx.close()
+
+
+def test_c2_shape_full_triangle_f32(gpu_ctx):
+    """BASELINE config 2 shape: N=20,000, T=500, 1,000-4,096 leaves per tree
+    (the per-part packing path), fp32 output.  The whole triangle (2e8
+    entries) equals the oracle's bit for bit, and so do the raw counts."""
+    import torch
+
+    n, t = 20_000, 500
+    rng = np.random.default_rng(20261203)
+    lt = rng.integers(1000, 4097, size=t)
+    leaf = (rng.random((t, n)) * lt[:, None]).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    nleaf = 4096
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for fmt in (O.FMT_F32, O.FMT_U16):
+        out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper(fmt, out, 0, n)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(O.FMT_DTYPE[fmt])
+        want = idx.rows(fmt, 0, n)
+        if fmt == O.FMT_F32:
+            check_equal(got.view(np.uint32), want.view(np.uint32), "C2 f32 triangle")
+        else:
+            check_equal(got, want, "C2 u16 triangle")
+            assert int(want.max()) <= t
+        del out
+    idx.close()
+    del keep
+
+
+@pytest.mark.parametrize("case", ["parts", "whole_tree"])
+def test_buckets_beyond_16383_members(gpu_ctx, case):
+    """Buckets of 16,383 or more members take the read-to-the-mark path of
+    the hit phase.  'parts': two leaves at N=60,000 (per-part packing);
+    'whole_tree': 2L > 8192 with one leaf holding 40,000 samples (whole-tree
+    packing)."""
+    import torch
+
+    n = 60_000
+    rng = np.random.default_rng(31 if case == "parts" else 37)
+    if case == "parts":
+        t, nleaf = 20, 2
+        leaf = rng.integers(0, nleaf, size=(t, n)).astype(np.int32)
+    else:
+        t, nleaf = 12, 5000
+        leaf = rng.integers(1, nleaf, size=(t, n)).astype(np.int32)
+        big = rng.random((t, n)) < 40_000 / n
+        leaf[big] = 0
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for fmt, scale in ((O.FMT_U16, 1.0), (O.FMT_U8, float(np.float32(1) / np.float32(255)))):
+        out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper(fmt, out, 0, n, scale=scale)
+        torch.cuda.synchronize()
+        esz = 2 if fmt == O.FMT_U16 else 1
+        for r0 in (0, 1, 4_999, 16_383, 30_000, 59_990):
+            r1 = min(n, r0 + 10)
+            e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
+            got = out[e0 * esz:e1 * esz].cpu().numpy().view(O.FMT_DTYPE[fmt])
+            check_equal(got, idx.rows(fmt, r0, r1, scale, 0.0), f"{case} fmt {fmt} rows {r0}:{r1}")
+        del out
+    idx.close()
+    del keep
+
+
+def test_row_bands_back_to_back_on_the_context_stream():
+    """Two row bands queued on the context's own (non-blocking) stream with
+    no synchronisation between them, the second band no larger than the
+    first: each equals the oracle, and nothing is written outside either
+    buffer."""
+    import torch
+
+    n, t, nleaf = 3000, 60, 40
+    leaf, oob = make_forest(41, n, t, nleaf)
+    ctx = R.Context(0)  # own stream
+    lt = torch.from_numpy(leaf).to("cuda:0")
+    ow = R.pack_oob_bits(torch.from_numpy(oob).to("cuda:0"))
+    torch.cuda.synchronize()
+    ctx.set_forest(lt, ow, n, t, nleaf)
+    bands = [(0, 1800), (1800, 3000), (100, 900)]
+    bufs = []
+    for r0, r1 in bands:
+        nb = R.upper_nbytes(O.FMT_U16, n, r0, r1)
+        bufs.append(torch.full((nb + 64,), 0xA5, dtype=torch.uint8, device="cuda:0"))
+    torch.cuda.synchronize()
+    for (r0, r1), b in zip(bands, bufs):
+        ctx.upper(O.FMT_U16, b[:R.upper_nbytes(O.FMT_U16, n, r0, r1)], r0, r1)
+    ctx.sync()
+    for (r0, r1), b in zip(bands, bufs):
+        host = b.cpu().numpy()
+        nb = R.upper_nbytes(O.FMT_U16, n, r0, r1)
+        check_equal(host[:nb].view(np.uint16), O.upper_rows(leaf, oob, nleaf, O.FMT_U16, r0=r0, r1=r1),
+                    f"band {r0}:{r1}")
+        assert (host[nb:] == 0xA5).all()
+    ctx.close()
