@@ -121,15 +121,41 @@ int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
 
 /* Work decomposition of rfxp_upper, host-only (no device needed): row i of
  * the band [row_begin, row_end) is cut into segments of S columns starting
- * at i, i + S, ...; one workgroup per segment.  Returns the number of
- * segments (-1 for bad arguments) and, when 0 <= e < that number, the row
- * and first column of segment e.  rfxp_upper_launches is the number of
- * kernel launches n_items segments take (at most 2^22 - 1 workgroups of
- * 1024 threads each).  Lets callers size row bands for several devices; no
- * reference counterpart. */
+ * at i, i + S, ...; one workgroup slot per segment, rows taken in groups of
+ * 8 so that all segments of a row run on one XCD, plus idle slots where a
+ * group's rows have fewer segments than its first.  Returns the number of
+ * slots (-1 for bad arguments) and, when 0 <= e < that number, the row and
+ * first column of the segment of slot e (-1, -1 for an idle slot).
+ * rfxp_upper_launches is the number of kernel launches n slots take (at
+ * most 2^22 - 8 workgroups of 1024 threads each).  Lets callers size row
+ * bands for several devices; no reference counterpart. */
 int64_t rfxp_upper_work_item(int64_t N, int32_t S, int64_t row_begin, int64_t row_end, int64_t e,
                              int64_t* row, int64_t* col);
 int64_t rfxp_upper_launches(int64_t n_items);
+
+/* ---- allocation-free one-shot triangle ------------------------------------ */
+
+/* Maximum device workspace of rfxp_upper_noalloc, per GPU (64 MiB). */
+#define RFXP_UPPER_NOALLOC_MAX_BYTES (64LL << 20)
+
+/* rfxp_set_forest + rfxp_upper (same arguments, same output) in one call
+ * that allocates no device memory: the forest index goes to a static
+ * workspace of RFXP_UPPER_NOALLOC_MAX_BYTES per GPU, which each GPU the
+ * library runs on holds until the process ends.  No counterpart in the
+ * reference: it is for callers that cannot allocate (stream capture, tight
+ * loops over many small forests, harnesses that forbid hipMalloc).  Forests
+ * whose index exceeds the workspace (rfxp_upper_noalloc_workspace) are
+ * rejected with RFXP_ERR_UNSUPPORTED.  All calls on one GPU share its
+ * workspace: calls that overlap on one GPU race, so callers serialise them
+ * (one stream, one host thread at a time).  The context's forest of
+ * rfxp_set_forest is left as it was. */
+int rfxp_upper_noalloc(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t,
+                       const uint32_t* oob_words, int64_t oob_ld, int64_t N, int32_t T, int32_t nleaf,
+                       const int32_t* nout, int fmt, float scale, float zp, int64_t row_begin, int64_t row_end,
+                       void* out);
+/* Workspace bytes rfxp_upper_noalloc needs for a forest (host only; -1 for
+ * bad arguments); nout_given: a caller nout is passed. */
+int64_t rfxp_upper_noalloc_workspace(int64_t N, int32_t T, int32_t nleaf, int nout_given);
 
 /* ---- top-K similarity retrieval ----------------------------------------- */
 

@@ -124,6 +124,7 @@ int rfxp_ctx_create(int device, rfxp_ctx** out) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess)
         ctx->n_cu = v;
     (void)hipGetLastError();
+    rfxp::noalloc_setup(device);  // the static workspace's address on this device
     *out = ctx;
     return RFXP_OK;
 }

@@ -76,17 +76,42 @@ __host__ __device__ inline int32_t view_buckets(const LeafView& v) {
     return (int32_t)((nb + 1) / 2 * 2);
 }
 
-// Where pack_forest writes: bucket offsets [T][nb+1] and members [T][N].
-// Forest mode (v.nseg == 0) also builds the per-sample records in ctx and
-// nout / rinv / rrange; reference mode builds buckets only.
-struct PackTarget {
-    int32_t* off;
-    uint32_t* mem;
+// Every buffer of a forest index, as pointers into device memory (the
+// context's own buffers, or a static workspace).  Forest mode (v.nseg == 0)
+// builds buckets, records, the long-bucket table and nout / rinv / rrange;
+// reference mode (top-K, low rank) builds the buckets only.
+enum ForestBuf {
+    FB_OFF, FB_MEM, FB_ROFF, FB_RLEN, FB_ROFFT, FB_RLENT, FB_SCRATCH, FB_SCRATCH2, FB_KEY16, FB_NOUT, FB_RINV,
+    FB_RRANGE, FB_LNG, FB_LNGN, FB_FLAGS, FB_COUNT
 };
 
-// Builds the buckets (and, in forest mode, records and nout) on ctx->stream
-// (rfxp_pack.hip).
-int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst);
+// Element counts of each buffer (n[FB_*], 0 when unused) for a view.
+struct ForestSizes {
+    size_t n[FB_COUNT] = {};
+    int64_t ldr = 0;
+    int32_t lmax = 0;
+    bool part_path = false;  // per-part packing (forest mode, 2L <= 8192)
+    bool lds_path = false;   // whole-tree histogram in LDS
+};
+ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds);
+size_t forest_elem_bytes(int k);
+
+// The context's own buffers for sizes z (grown as needed), with off / mem
+// the given ones (forest or reference set).
+int ctx_forest_bufs(rfxp_ctx* ctx, const ForestSizes& z, DevBuf<int32_t>& off, DevBuf<uint32_t>& mem,
+                    ForestBufs& fb);
+
+// Builds the index into fb on ctx->stream (rfxp_pack.hip).  nout_in
+// (device int32[N]) or NULL: counted from the OOB bits.
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb);
+
+// Argument checks of rfxp_upper-like calls (status, message on ctx), and
+// rows [r0, r1) of the triangle of index fb into out on ctx->stream
+// (rfxp_triangle.hip).
+int upper_check_args(rfxp_ctx* ctx, const char* who, int64_t N, int fmt, float scale, float zp, int64_t r0,
+                     int64_t r1, const void* out);
+int upper_launch(rfxp_ctx* ctx, const ForestBufs& fb, int64_t N, int32_t T, int fmt, float scale, float zp,
+                 int64_t r0, int64_t r1, void* out);
 
 // p[0..n) = val on ctx->stream (a fill kernel, capturable).
 void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val);

@@ -37,6 +37,28 @@ struct DevBuf {
     }
 };
 
+// Every buffer of a forest index (rfxp_forest.hpp, ForestBuf), as pointers
+// into device memory: the context's own buffers, or a static workspace.
+struct ForestBufs {
+    int32_t* off = nullptr;        // [T][nb+1] bucket offsets
+    uint32_t* mem = nullptr;       // [T][N] + MEM_PAD members
+    uint32_t* roff = nullptr;      // [N][ldr] + REC_PAD records (forest mode)
+    uint16_t* rlen = nullptr;
+    uint32_t* roffT = nullptr;     // [T][N] tree-major records (per-part packing)
+    uint16_t* rlenT = nullptr;
+    uint32_t* scratch = nullptr;   // part histograms, or whole-tree counters / cursors
+    uint32_t* scratch2 = nullptr;  // [N] OOB counts (nout not given)
+    uint16_t* key16 = nullptr;     // [T][ceil8(N)] bucket ids
+    int32_t* nout = nullptr;       // [N]
+    double* rinv = nullptr;        // [N]
+    unsigned long long* rrange = nullptr;  // [2]
+    uint2* lng = nullptr;          // [T][lmax] long buckets
+    int32_t* lngn = nullptr;       // [T]
+    int32_t* flags = nullptr;      // [16] device status words
+    int64_t ldr = 0;
+    int32_t lmax = 0;
+};
+
 struct KernelTiming {
     double ms = 0.0;
     int64_t launches = 0;
@@ -73,6 +95,7 @@ struct rfxp_ctx {
     DevBuf<double> rinv;       // N: nout > 0 ? 1/nout : 1
     DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits
     DevBuf<int32_t> flags;     // device status words
+    ForestBufs fb;             // the forest index of rfxp_set_forest (pointers into the buffers above)
 
     // reference set for top-K (rfxp_set_reference)
     bool ref_ready = false;
@@ -119,6 +142,9 @@ struct LaunchTimer {
     ~LaunchTimer();
 };
 int check_launch(rfxp_ctx* ctx, const char* what);
+// Device address of rfxp_upper_noalloc's static workspace on `device`
+// (current), taken once per device (rfxp_noalloc.hip).
+void noalloc_setup(int device);
 bool is_device_pointer(const void* p);
 
 }  // namespace rfxp

@@ -578,72 +578,142 @@ void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
                        p, n, val);
 }
 
-static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst);
-static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in);
+ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
+    ForestSizes z;
+    const int64_t N = v.N, n1 = std::max<int64_t>(N, 1);
+    const int32_t T = v.T;
+    const int32_t nb = view_buckets(v);
+    const bool forest = v.nseg == 0;
+    const int64_t ldk = cdiv(N, 8) * 8;
+    z.ldr = ((int64_t)T + 15) / 16 * 16;
+    z.lmax = (int32_t)(N / REC_LONG + 1);
+    z.part_path = forest && nb <= PART_MAX_NB;
+    const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
+    z.lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= max_lds;
+    z.n[FB_OFF] = (size_t)T * (nb + 1);
+    z.n[FB_MEM] = (size_t)T * n1 + MEM_PAD;
+    if (z.part_path) {
+        z.n[FB_KEY16] = (size_t)T * ldk;
+        z.n[FB_SCRATCH] = (size_t)T * PACK_PARTS * nb;
+        z.n[FB_ROFFT] = (size_t)T * N;
+        z.n[FB_RLENT] = (size_t)T * N;
+    } else {
+        z.n[FB_KEY16] = nb < 0xffff ? (size_t)T * ldk : 0;
+        z.n[FB_SCRATCH] = (size_t)T * 2 * (nb + 1);
+    }
+    if (forest) {
+        z.n[FB_ROFF] = (size_t)n1 * z.ldr + REC_PAD;
+        z.n[FB_RLEN] = (size_t)n1 * z.ldr + REC_PAD;
+        z.n[FB_SCRATCH2] = count_nout ? (size_t)n1 : 0;
+        z.n[FB_NOUT] = (size_t)n1;
+        z.n[FB_RINV] = (size_t)n1;
+        z.n[FB_RRANGE] = 2;
+        z.n[FB_LNG] = (size_t)T * z.lmax;
+        z.n[FB_LNGN] = (size_t)T;
+        z.n[FB_FLAGS] = 16;
+    }
+    return z;
+}
+
+int ctx_forest_bufs(rfxp_ctx* ctx, const ForestSizes& z, DevBuf<int32_t>& off, DevBuf<uint32_t>& mem,
+                    ForestBufs& fb) {
+    fb = ForestBufs();
+    fb.ldr = z.ldr;
+    fb.lmax = z.lmax;
+#define RFXP_FB(K, buf, field)                                  \
+    if (z.n[K]) {                                               \
+        RFXP_HIP(ctx, (buf).ensure(z.n[K]));                    \
+        fb.field = (buf).p;                                     \
+    }
+    RFXP_FB(FB_OFF, off, off)
+    RFXP_FB(FB_MEM, mem, mem)
+    RFXP_FB(FB_ROFF, ctx->roff, roff)
+    RFXP_FB(FB_RLEN, ctx->rlen, rlen)
+    RFXP_FB(FB_ROFFT, ctx->roffT, roffT)
+    RFXP_FB(FB_RLENT, ctx->rlenT, rlenT)
+    RFXP_FB(FB_SCRATCH, ctx->scratch, scratch)
+    RFXP_FB(FB_SCRATCH2, ctx->scratch2, scratch2)
+    RFXP_FB(FB_KEY16, ctx->key16, key16)
+    RFXP_FB(FB_NOUT, ctx->nout, nout)
+    RFXP_FB(FB_RINV, ctx->rinv, rinv)
+    RFXP_FB(FB_RRANGE, ctx->rrange, rrange)
+    RFXP_FB(FB_LNG, ctx->lng, lng)
+    RFXP_FB(FB_LNGN, ctx->lngn, lngn)
+    RFXP_FB(FB_FLAGS, ctx->flags, flags)
+#undef RFXP_FB
+    return RFXP_OK;
+}
+
+size_t forest_elem_bytes(int k) {
+    switch (k) {
+        case FB_OFF: case FB_NOUT: case FB_LNGN: case FB_FLAGS: return 4;
+        case FB_MEM: case FB_ROFF: case FB_ROFFT: case FB_SCRATCH: case FB_SCRATCH2: return 4;
+        case FB_RLEN: case FB_RLENT: case FB_KEY16: return 2;
+        case FB_RINV: case FB_RRANGE: case FB_LNG: return 8;
+        default: return 0;
+    }
+}
+
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb);
+static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb);
 
 // The table of long buckets (forest mode), once the offsets are known.
-static int pack_long_runs(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst) {
+static int pack_long_runs(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
     const int32_t nb = view_buckets(v);
-    const int32_t lmax = (int32_t)(v.N / REC_LONG + 1);
-    RFXP_HIP(ctx, ctx->lng.ensure((size_t)v.T * lmax));
-    RFXP_HIP(ctx, ctx->lngn.ensure((size_t)v.T));
-    ctx->lmax = lmax;
-    fill_u32(ctx, (uint32_t*)ctx->lngn.p, v.T, 0u);
+    fill_u32(ctx, (uint32_t*)fb.lngn, v.T, 0u);
     const int64_t n = (int64_t)v.T * nb;
-    hipLaunchKernelGGL(k_long_runs, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, ctx->stream, (const int32_t*)dst.off,
-                       nb, v.T, v.N, ctx->lng.p, ctx->lngn.p, lmax);
+    hipLaunchKernelGGL(k_long_runs, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, ctx->stream, (const int32_t*)fb.off,
+                       nb, v.T, v.N, fb.lng, fb.lngn, fb.lmax);
     return check_launch(ctx, "k_long_runs");
 }
 
-int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const PackTarget& dst) {
+int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
     const int32_t T = v.T;
     const int32_t nb = view_buckets(v);
     const bool forest = v.nseg == 0;
+    const ForestSizes z = forest_sizes(v, nout_in == nullptr, ctx->max_lds);
     if (forest) {
+        // the record slack after the last row reads as empty records
+        const int64_t n1 = std::max<int64_t>(N, 1);
+        fill_u32(ctx, fb.roff + n1 * fb.ldr, REC_PAD, 0u);
+        fill_u32(ctx, (uint32_t*)(fb.rlen + n1 * fb.ldr), REC_PAD / 2, 0u);
         LaunchTimer tm(ctx, "rr_init");
-        hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, ctx->rrange.p);
+        hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, fb.rrange);
     }
     if (int rc = check_launch(ctx, "k_rr_init")) return rc;
     if (N == 0) return RFXP_OK;
-    if (forest && nb <= PART_MAX_NB) {
-        if (int rc = pack_forest_parts(ctx, v, dst)) return rc;
-        if (int rc = pack_long_runs(ctx, v, dst)) return rc;
-        return pack_nout(ctx, v, nout_in);
+    if (z.part_path) {
+        if (int rc = pack_forest_parts(ctx, v, fb)) return rc;
+        if (int rc = pack_long_runs(ctx, v, fb)) return rc;
+        return pack_nout(ctx, v, nout_in, fb);
     }
     // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
     const unsigned grid = (unsigned)(cdiv(T, 128) * 128);
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
-    const bool lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= ctx->max_lds;
     const int64_t nscr = (int64_t)T * 2 * (nb + 1);
-    RFXP_HIP(ctx, ctx->scratch.ensure((size_t)nscr));
     // compact bucket ids for the second pass when they fit 16 bits
-    uint16_t* k16 = nullptr;
+    uint16_t* k16 = z.n[FB_KEY16] ? fb.key16 : nullptr;
     const int64_t ldk = cdiv(N, 8) * 8;
-    if (nb < 0xffff) {
-        RFXP_HIP(ctx, ctx->key16.ensure((size_t)T * ldk));
-        k16 = ctx->key16.p;
-    }
-    if (lds_path) {
+    if (z.lds_path) {
         if (lds_bytes > 32768)
             RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_hist<true>,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, dst.off,
+        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, fb.off,
                            (uint32_t*)nullptr, k16, ldk);
     } else {
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(nscr, 256), 65536)), dim3(256), 0, s,
-                           ctx->scratch.p, nscr, 0u);
+                           fb.scratch, nscr, 0u);
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, dst.off, ctx->scratch.p,
-                           k16, ldk);
+        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, fb.off, fb.scratch, k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
     if (forest) {
         LaunchTimer tm(ctx, "records");
-        hipLaunchKernelGGL(k_records, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s, v,
-                           (const uint16_t*)k16, ldk, (const int32_t*)dst.off, ctx->ldr, ctx->roff.p, ctx->rlen.p);
+        hipLaunchKernelGGL(k_records, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s, v,
+                           (const uint16_t*)k16, ldk, (const int32_t*)fb.off, fb.ldr, fb.roff, fb.rlen);
     }
     if (int rc = check_launch(ctx, "k_records")) return rc;
     {
@@ -655,26 +725,22 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds2));
         LaunchTimer tm(ctx, "pack_scatter");
-        hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, dst.off,
-                           dst.mem, ctx->scratch.p, nwin, (const uint16_t*)k16, ldk);
+        hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, fb.off, fb.mem,
+                           fb.scratch, nwin, (const uint16_t*)k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
     if (!forest) return RFXP_OK;
-    if (int rc = pack_long_runs(ctx, v, dst)) return rc;
-    return pack_nout(ctx, v, nout_in);
+    if (int rc = pack_long_runs(ctx, v, fb)) return rc;
+    return pack_nout(ctx, v, nout_in, fb);
 }
 
 // Forest path for 2L <= PART_MAX_NB (see k_part_hist).
-static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget& dst) {
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
     const int32_t T = v.T;
     const int32_t nb = view_buckets(v);
     const int64_t ldk = cdiv(N, 8) * 8;
-    RFXP_HIP(ctx, ctx->key16.ensure((size_t)T * ldk));
-    RFXP_HIP(ctx, ctx->scratch.ensure((size_t)T * PACK_PARTS * nb));
-    RFXP_HIP(ctx, ctx->roffT.ensure((size_t)T * N));
-    RFXP_HIP(ctx, ctx->rlenT.ensure((size_t)T * N));
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
     const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
     const size_t lds_h = (size_t)nb * 4, lds_s = (size_t)(3 * nb + 1) * 4;
@@ -686,49 +752,45 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const PackTarget&
                                           (int)lds_s));
     {
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_part_hist, dim3(grid), dim3(PACK_THREADS), lds_h, s, v, ctx->scratch.p, ctx->key16.p,
-                           ldk);
+        hipLaunchKernelGGL(k_part_hist, dim3(grid), dim3(PACK_THREADS), lds_h, s, v, fb.scratch, fb.key16, ldk);
     }
     if (int rc = check_launch(ctx, "k_part_hist")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scan");
-        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, ctx->scratch.p, dst.off);
+        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.scratch, fb.off);
     }
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
-        hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v, (const uint32_t*)ctx->scratch.p,
-                           (const int32_t*)dst.off, (const uint16_t*)ctx->key16.p, ldk, dst.mem, ctx->roffT.p,
-                           ctx->rlenT.p);
+        hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v, (const uint32_t*)fb.scratch,
+                           (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk, fb.mem, fb.roffT, fb.rlenT);
     }
     if (int rc = check_launch(ctx, "k_part_scatter")) return rc;
     {
         LaunchTimer tm(ctx, "records");
-        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(ctx->ldr, 64)), dim3(256), 0, s,
-                           ctx->roffT.p, ctx->rlenT.p, N, T, ctx->ldr, ctx->roff.p, ctx->rlen.p);
+        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s,
+                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen);
     }
     return check_launch(ctx, "k_rec_transpose");
 }
 
 // nout, 1/nout and its range (forest mode).
-static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in) {
+static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
     const int32_t T = v.T;
     if (!nout_in) {
-        RFXP_HIP(ctx, ctx->scratch2.ensure((size_t)N));
         hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(N, 256), 65536)), dim3(256), 0, s,
-                           ctx->scratch2.p, N, 0u);
+                           fb.scratch2, N, 0u);
         const unsigned G = (unsigned)std::min<int32_t>(T, 16);
         LaunchTimer tm(ctx, "nout");
-        hipLaunchKernelGGL(k_nout_part, dim3((unsigned)cdiv(N, 256), G), dim3(256), 0, s, v, ctx->scratch2.p);
+        hipLaunchKernelGGL(k_nout_part, dim3((unsigned)cdiv(N, 256), G), dim3(256), 0, s, v, fb.scratch2);
     }
     if (int rc = check_launch(ctx, "k_nout_part")) return rc;
     {
         LaunchTimer tm(ctx, "nout_final");
         hipLaunchKernelGGL(k_nout_final, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, s, N, nout_in,
-                           nout_in ? (const uint32_t*)nullptr : ctx->scratch2.p, ctx->nout.p, ctx->rinv.p,
-                           ctx->rrange.p);
+                           nout_in ? (const uint32_t*)nullptr : fb.scratch2, fb.nout, fb.rinv, fb.rrange);
     }
     return check_launch(ctx, "k_nout_final");
 }

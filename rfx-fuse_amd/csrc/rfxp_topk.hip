@@ -390,9 +390,10 @@ extern "C" int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t st
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     LeafView v{leaf, stride_i, stride_t, nullptr, 0, N, T, nleaf, (int32_t)nseg, shift};
     const int32_t nb = view_buckets(v);
-    RFXP_HIP(ctx, ctx->ref_off.ensure((size_t)T * (nb + 1)));
-    RFXP_HIP(ctx, ctx->ref_mem.ensure((size_t)T * N + MEM_PAD));
-    if (int rc = pack_forest(ctx, v, nullptr, PackTarget{ctx->ref_off.p, ctx->ref_mem.p})) return rc;
+    const ForestSizes z = forest_sizes(v, false, ctx->max_lds);
+    ForestBufs fb;
+    if (int rc = ctx_forest_bufs(ctx, z, ctx->ref_off, ctx->ref_mem, fb)) return rc;
+    if (int rc = pack_forest(ctx, v, nullptr, fb)) return rc;
     ctx->ref_N = N;
     ctx->ref_T = T;
     ctx->ref_L = nleaf;

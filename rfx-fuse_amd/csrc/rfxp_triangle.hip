@@ -805,22 +805,12 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     ctx->N = N;
     ctx->T = T;
     ctx->L = nleaf;
-    const int64_t nb = 2 * (int64_t)nleaf;
-    const size_t n1 = (size_t)std::max<int64_t>(N, 1);
-    RFXP_HIP(ctx, ctx->bkt_off.ensure((size_t)T * (nb + 1)));
-    RFXP_HIP(ctx, ctx->bkt_mem.ensure((size_t)T * n1 + MEM_PAD));
-    ctx->ldr = ((int64_t)T + 15) / 16 * 16;
-    RFXP_HIP(ctx, ctx->roff.ensure(n1 * ctx->ldr + REC_PAD));
-    RFXP_HIP(ctx, ctx->rlen.ensure(n1 * ctx->ldr + REC_PAD));
-    // the record slack after the last row reads as empty records
-    fill_u32(ctx, ctx->roff.p + n1 * ctx->ldr, REC_PAD, 0u);
-    fill_u32(ctx, (uint32_t*)(ctx->rlen.p + n1 * ctx->ldr), REC_PAD / 2, 0u);
-    RFXP_HIP(ctx, ctx->nout.ensure(n1));
-    RFXP_HIP(ctx, ctx->rinv.ensure(n1));
-    RFXP_HIP(ctx, ctx->rrange.ensure(2));
-    RFXP_HIP(ctx, ctx->flags.ensure(16));
     LeafView v{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf, 0, 0};
-    if (int rc = pack_forest(ctx, v, nout, PackTarget{ctx->bkt_off.p, ctx->bkt_mem.p})) return rc;
+    const ForestSizes z = forest_sizes(v, nout == nullptr, ctx->max_lds);
+    if (int rc = ctx_forest_bufs(ctx, z, ctx->bkt_off, ctx->bkt_mem, ctx->fb)) return rc;
+    ctx->ldr = z.ldr;
+    ctx->lmax = z.lmax;
+    if (int rc = pack_forest(ctx, v, nout, ctx->fb)) return rc;
     ctx->forest_ready = true;
     return RFXP_OK;
 }
@@ -870,36 +860,43 @@ static hipError_t launch_items(rfxp_ctx* ctx, K kernel, TriArgs a, int64_t n_ite
     return hipSuccess;
 }
 
-extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t r0, int64_t r1, void* out) {
-    if (!ctx) return RFXP_ERR_INVALID;
-    if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_upper: no forest set");
-    const int64_t N = ctx->N;
-    if (fmt < F32 || fmt > U16) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: unknown format");
-    if (r0 < 0 || r1 > N || r0 > r1) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: bad row range");
-    if ((fmt == I8 || fmt == U8) && (!std::isfinite(scale) || scale == 0.0f || !std::isfinite(zp)))
-        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: scale must be finite and non-zero, zp finite");
-    if (r0 == r1) return RFXP_OK;
-    if (!out || !is_device_pointer(out)) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: out must be a device pointer");
-    const int esz = (fmt == F32) ? 4 : (fmt == F16 || fmt == U16) ? 2 : 1;
-    if (((uintptr_t)out) % esz != 0) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper: out is not aligned to its entry size");
-    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+namespace rfxp {
 
-    // The kernels derive each item's (row, segment) from its index, so
-    // consecutive calls on one stream share no host-written state.
+int upper_check_args(rfxp_ctx* ctx, const char* who, int64_t N, int fmt, float scale, float zp, int64_t r0,
+                     int64_t r1, const void* out) {
+    if (fmt < F32 || fmt > U16) return set_error(ctx, RFXP_ERR_INVALID, std::string(who) + ": unknown format");
+    if (r0 < 0 || r1 > N || r0 > r1) return set_error(ctx, RFXP_ERR_INVALID, std::string(who) + ": bad row range");
+    if ((fmt == I8 || fmt == U8) && (!std::isfinite(scale) || scale == 0.0f || !std::isfinite(zp)))
+        return set_error(ctx, RFXP_ERR_INVALID, std::string(who) + ": scale must be finite and non-zero, zp finite");
+    if (r0 == r1) return RFXP_OK;
+    if (!out || !is_device_pointer(out))
+        return set_error(ctx, RFXP_ERR_INVALID, std::string(who) + ": out must be a device pointer");
+    const int esz = (fmt == F32) ? 4 : (fmt == F16 || fmt == U16) ? 2 : 1;
+    if (((uintptr_t)out) % esz != 0)
+        return set_error(ctx, RFXP_ERR_INVALID, std::string(who) + ": out is not aligned to its entry size");
+    return RFXP_OK;
+}
+
+// Rows [r0, r1) of the triangle of the forest index fb (N samples, T trees)
+// on ctx->stream.  The kernels derive each item's (row, segment) from its
+// index, so consecutive calls on one stream share no host-written state.
+int upper_launch(rfxp_ctx* ctx, const ForestBufs& fb, int64_t N, int32_t T, int fmt, float scale, float zp,
+                 int64_t r0, int64_t r1, void* out) {
+    if (r0 == r1) return RFXP_OK;
     const int32_t S = tri_segment_cols(ctx);
     TriArgs a;
-    a.roff = ctx->roff.p;
-    a.rlen = ctx->rlen.p;
-    a.ldr = ctx->ldr;
-    a.lng = ctx->lng.p;
-    a.lngn = ctx->lngn.p;
-    a.lmax = ctx->lmax;
-    a.mem = ctx->bkt_mem.p;
-    a.mem_bytes = (uint32_t)(((uint64_t)ctx->T * (uint64_t)N + MEM_PAD) * 4u);
-    a.rinv = ctx->rinv.p;
-    a.rr = ctx->rrange.p;
+    a.roff = fb.roff;
+    a.rlen = fb.rlen;
+    a.ldr = fb.ldr;
+    a.lng = fb.lng;
+    a.lngn = fb.lngn;
+    a.lmax = fb.lmax;
+    a.mem = fb.mem;
+    a.mem_bytes = (uint32_t)(((uint64_t)T * (uint64_t)N + MEM_PAD) * 4u);
+    a.rinv = fb.rinv;
+    a.rr = fb.rrange;
     a.N = N;
-    a.T = ctx->T;
+    a.T = T;
     a.S = S;
     a.lev = tri_levels_of(N, S, r0, r1);
     a.item_base = 0;
@@ -907,8 +904,8 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     a.out = (char*)out;
     a.scale = scale;
     a.zp = zp;
-    a.flags = ctx->flags.p;
-    a.mode = tri_mode(ctx->T);
+    a.flags = fb.flags;
+    a.mode = tri_mode(T);
     const int64_t n_items = tri_slot_count(N, S, r0, r1);
     const size_t lds = tri_lds_bytes(S);
     hipError_t e;
@@ -925,6 +922,17 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     }
     if (e != hipSuccess) return hip_error(ctx, e, "k_tri launch");
     return RFXP_OK;
+}
+
+}  // namespace rfxp
+
+extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t r0, int64_t r1, void* out) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_upper: no forest set");
+    if (int rc = upper_check_args(ctx, "rfxp_upper", ctx->N, fmt, scale, zp, r0, r1, out)) return rc;
+    if (r0 == r1) return RFXP_OK;
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    return upper_launch(ctx, ctx->fb, ctx->N, ctx->T, fmt, scale, zp, r0, r1, out);
 }
 
 extern "C" int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout) {

@@ -72,6 +72,10 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_work_item.restype = i64
     L.rfxp_upper_launches.argtypes = [i64]
     L.rfxp_upper_launches.restype = i64
+    L.rfxp_upper_noalloc.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, C.c_int, C.c_float, C.c_float,
+                                     i64, i64, vp]
+    L.rfxp_upper_noalloc_workspace.argtypes = [i64, i32, i32, C.c_int]
+    L.rfxp_upper_noalloc_workspace.restype = i64
     L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
     L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
@@ -108,6 +112,14 @@ def upper_work_items(n: int, s: int, r0: int, r1: int):
         L.rfxp_upper_work_item(n, s, r0, r1, e, C.byref(row), C.byref(col))
         out.append((row.value, col.value))
     return out
+
+
+def upper_noalloc_workspace(n: int, t: int, nleaf: int, nout_given: bool = False) -> int:
+    """Device workspace bytes rfxp_upper_noalloc needs for a forest."""
+    return load().rfxp_upper_noalloc_workspace(n, t, nleaf, int(nout_given))
+
+
+NOALLOC_MAX_BYTES = 64 << 20
 
 
 def pack_oob_bits(oob_tn):
@@ -269,6 +281,27 @@ class Context:
         if have < need:
             raise ValueError(f"output buffer has {have} bytes, rows need {need}")
         self._check(self._L.rfxp_upper(self.h, fmt, scale, zp, r0, r1, out.data_ptr()))
+        return out
+
+    def upper_noalloc(self, leaf, oob_words, n: int, t: int, nleaf: int, fmt: int, out, r0: int = 0,
+                      r1: int | None = None, scale: float = 1.0, zp: float = 0.0, layout: str = "tree",
+                      nout=None):
+        """rfxp_upper_noalloc: set_forest + upper in one call, with the forest
+        index in the library's static device workspace (no allocation)."""
+        import torch
+
+        assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
+        assert oob_words.dtype == torch.int32 and oob_words.is_cuda and oob_words.is_contiguous()
+        si, st = (1, n) if layout == "tree" else (t, 1)
+        r1 = n if r1 is None else r1
+        need = upper_nbytes(fmt, n, r0, r1)
+        have = out.numel() * out.element_size()
+        if have < need:
+            raise ValueError(f"output buffer has {have} bytes, rows need {need}")
+        nptr = None if nout is None else nout.data_ptr()
+        self._check(self._L.rfxp_upper_noalloc(self.h, leaf.data_ptr(), si, st, oob_words.data_ptr(),
+                                               oob_words.shape[1], n, t, nleaf, nptr, fmt, scale, zp, r0, r1,
+                                               out.data_ptr()))
         return out
 
     def nout(self):
