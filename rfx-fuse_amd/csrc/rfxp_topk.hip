@@ -53,6 +53,7 @@ struct TopkArgs {
     const uint32_t* qoob;  // NULL: all trees
     int64_t qold;
     int64_t exclude_base;  // query q excludes reference exclude_base + q; < 0: none
+    int64_t q0;            // query of workgroup 0 of this launch
     int32_t K;
     int32_t floor_key;     // smallest selectable key: 1 (zeros allowed) or 2 (counts > 0)
     int32_t* idx_out;
@@ -132,64 +133,100 @@ __device__ __forceinline__ void tails16(const TopkArgs& a, const uint32_t* rec_o
     }
 }
 
-// Block reductions through `red` (TOPK_RED_WORDS words); every thread gets
-// the result.  Each uses two barriers.
-__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
+// Per-thread level counts of keys >= c0 + d for d = 0..3, two 16-bit fields
+// per word (a thread holds at most 32 keys, a workgroup at most 32768, so
+// the fields of a block sum do not carry into each other).
+template <int NW>
+__device__ __forceinline__ void level_counts(const uint32_t (&key)[NW], uint32_t c0, uint32_t& w01, uint32_t& w23) {
+    uint32_t n0 = 0, n1 = 0, n2 = 0, n3 = 0;
 #pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v += (uint32_t)__shfl_xor((int)v, d, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    uint32_t t = 0;
+    for (int k = 0; k < NW; ++k) {
 #pragma unroll
-    for (int w = 0; w < TOPK_WAVES; ++w) t += red[w];
-    __syncthreads();
-    return t;
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t v = (key[k] >> (16 * h)) & 0xffffu;
+            n0 += v >= c0;
+            n1 += v >= c0 + 1u;
+            n2 += v >= c0 + 2u;
+            n3 += v >= c0 + 3u;
+        }
+    }
+    w01 = n0 | (n1 << 16);
+    w23 = n2 | (n3 << 16);
 }
 
-__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
+// Wave-wide sum / maximum through DPP lane moves (no lane-index registers):
+// quad swaps, then half-row and row mirrors leave every lane with its
+// 16-lane row total; the four row totals are read as scalars.  The whole
+// wave must be active.
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, int ctrl) {
+    switch (ctrl) {
+        case 0: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+        case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+        case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+        default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false); // row_mirror
+    }
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
 #pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, d, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    uint32_t t = 0;
+    for (int c = 0; c < 4; ++c) v += dpp_mov(v, c);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+           (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 #pragma unroll
-    for (int w = 0; w < TOPK_WAVES; ++w) t = max(t, red[w]);
-    __syncthreads();
-    return t;
+    for (int c = 0; c < 4; ++c) v = max(v, dpp_mov(v, c));
+    return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+               max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
 }
 
-// Exclusive prefix sum over threads in thread order; *total gets the sum.
+// Block sums of w01 and w23 and block maximum of m through `red` (48
+// words); every thread gets the results.  Two barriers.
+__device__ __forceinline__ void block_levels(uint32_t& w01, uint32_t& w23, uint32_t& m, uint32_t* red) {
+    const uint32_t s01 = wave_sum(w01), s23 = wave_sum(w23), mx = wave_max(m);
+    if ((threadIdx.x & 63) == 0) {
+        red[3 * (threadIdx.x >> 6)] = s01;
+        red[3 * (threadIdx.x >> 6) + 1] = s23;
+        red[3 * (threadIdx.x >> 6) + 2] = mx;
+    }
+    __syncthreads();
+    // lane w < 16 of every wave picks up wave w's partials
+    const uint32_t l = threadIdx.x & 63u;
+    const bool have = l < (uint32_t)TOPK_WAVES;
+    const uint32_t a = have ? red[3 * l] : 0u, b = have ? red[3 * l + 1] : 0u, c = have ? red[3 * l + 2] : 0u;
+    w01 = wave_sum(a);
+    w23 = wave_sum(b);
+    m = wave_max(c);
+    __syncthreads();
+}
+
+// Exclusive prefix sum over threads in thread order of v = a | (b << 16)
+// with a, b <= 63; *total gets the sum.  Within a wave the prefix is built
+// bit by bit from ballots (mbcnt counts the set lanes below this one).
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
-    const uint32_t lane = threadIdx.x & 63;
-    uint32_t incl = v;
+    uint32_t pre = 0, wt = 0;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
-        if (lane >= (uint32_t)d) incl += o;
+    for (int b = 0; b < 22; ++b) {
+        if (b >= 6 && b < 16) continue;
+        const uint64_t m = __ballot((v >> b) & 1u);
+        pre += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+        wt += (uint32_t)__popcll(m) << b;
     }
-    if (lane == 63) red[threadIdx.x >> 6] = incl;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = wt;
     __syncthreads();
-    uint32_t before = 0, t = 0;
-#pragma unroll
-    for (int w = 0; w < TOPK_WAVES; ++w) {
-        const uint32_t x = red[w];
-        if (w < (int)(threadIdx.x >> 6)) before += x;
-        t += x;
-    }
+    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t x = l < (uint32_t)TOPK_WAVES ? red[l] : 0u;
+    const uint32_t before = wave_sum(l < wave ? x : 0u);
+    *total = wave_sum(x);
     __syncthreads();
-    *total = t;
-    return before + incl - v;
+    return before + pre;
 }
 
 // Number of this thread's keys (16-bit halves of its NW key words) >= c.
 template <int NW>
-__device__ __forceinline__ uint32_t count_ge(const uint32_t* kw, uint32_t c) {
+__device__ __forceinline__ uint32_t count_ge(const uint32_t (&key)[NW], uint32_t c) {
     uint32_t n = 0;
 #pragma unroll
-    for (int k = 0; k < NW; ++k) {
-        const uint32_t w = kw[k];
-        n += ((w & 0xffffu) >= c) + ((w >> 16) >= c);
-    }
+    for (int k = 0; k < NW; ++k) n += ((key[k] & 0xffffu) >= c) + ((key[k] >> 16) >= c);
     return n;
 }
 
@@ -215,7 +252,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t q = blockIdx.x;
+    const int64_t q = a.q0 + blockIdx.x;
     const uint32_t K = (uint32_t)a.K;
     const int64_t ex = a.exclude_base >= 0 ? a.exclude_base + q : -1;
 
@@ -255,55 +292,84 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             }
             __syncthreads();
         }
-        // counters -> keys in place: count + 1, or 0 where the reference may
-        // not be chosen (past the end, or excluded)
+        // counters -> keys, held in registers from here on: count + 1, or
+        // 0 where the reference may not be chosen (past the end, or excluded)
         const uint32_t u0 = threadIdx.x * 2u * NW;
+        uint32_t key[NW];
+        if constexpr (NW >= 4) {
+#pragma unroll
+            for (int k = 0; k < NW; k += 4) {
+                const uint4 x = *(const uint4*)(kw + k);
+                key[k] = x.x;
+                key[k + 1] = x.y;
+                key[k + 2] = x.z;
+                key[k + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) key[k] = kw[k];
+        }
+        // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
+        // excluded unit `exu` (offsets against constants keep no per-unit
+        // index live across the segment loop)
+        const int32_t rem = (int32_t)width - (int32_t)u0;
+        const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
+        const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
         uint32_t mloc = 0;
 #pragma unroll
         for (int k = 0; k < NW; ++k) {
-            const uint32_t w = kw[k];
-            const uint32_t ua = u0 + 2u * k, ub = ua + 1u;
-            const bool va = ua < width && (int64_t)(lo + ua) != ex;
-            const bool vb = ub < width && (int64_t)(lo + ub) != ex;
+            const uint32_t w = key[k];
+            const bool va = 2 * k < rem && 2 * k != exu;
+            const bool vb = 2 * k + 1 < rem && 2 * k + 1 != exu;
             const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
             const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
-            kw[k] = ka | (kb << 16);
+            key[k] = ka | (kb << 16);
             mloc = max(mloc, max(ka, kb));
         }
-        // only keys above the running threshold can enter the list
+        // only keys above the running threshold can enter the list.  cstar:
+        // keys > cstar all enter, keys == cstar in index order up to K; it is
+        // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
+        // keys reach `lowest`.  Each round counts four levels at once.
         const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-        const uint32_t M = block_max(mloc, red);
+        uint32_t c0 = lowest, w01, w23, M = mloc;
+        level_counts<NW>(key, c0, w01, w23);
+        block_levels(w01, w23, M, red);  // also orders the key reads before the next segment's clear
         if (M < lowest) continue;
-        // cstar: keys > cstar all enter, keys == cstar in index order up to K
         uint32_t cstar = lowest;
-        if (block_sum(count_ge<NW>(kw, lowest), red) > K) {
-            uint32_t lo_c = lowest, hi_c = M;  // largest c with #(>= c) >= K
-            while (lo_c < hi_c) {
-                const uint32_t mid = (lo_c + hi_c + 1u) / 2u;
-                if (block_sum(count_ge<NW>(kw, mid), red) >= K) lo_c = mid;
-                else hi_c = mid - 1u;
+        if ((w01 & 0xffffu) > K) {
+            for (;;) {
+                const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
+                const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
+                if (d < 3u || c0 + 3u >= M) {
+                    cstar = c0 + d;
+                    break;
+                }
+                c0 += 3u;
+                uint32_t m2 = 0;
+                level_counts<NW>(key, c0, w01, w23);
+                block_levels(w01, w23, m2, red);
             }
-            cstar = lo_c;
         }
-        const uint32_t ngt = count_ge<NW>(kw, cstar + 1u);
-        const uint32_t neq = count_ge<NW>(kw, cstar) - ngt;
-        uint32_t G, E;
-        const uint32_t pgt = block_excl_scan(ngt, red, &G);
-        const uint32_t peq = block_excl_scan(neq, red, &E);
+        const uint32_t ngt = count_ge<NW>(key, cstar + 1u);
+        const uint32_t neq = count_ge<NW>(key, cstar) - ngt;
+        uint32_t tot;
+        const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
+        const uint32_t G = tot & 0xffffu, E = tot >> 16;
         const uint32_t take = min(E, K - G);
-        uint32_t rg = pgt, re = peq;
+        uint32_t rg = pre & 0xffffu, re = pre >> 16;
         if (ngt + neq) {
-#pragma unroll 1
+            const uint32_t j0 = lo + u0;
+#pragma unroll
             for (int k = 0; k < 2 * NW; ++k) {
-                const uint32_t key = (kw[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                const uint32_t j = lo + u0 + (uint32_t)k;
-                if (key > cstar) {
-                    cand_k[rg] = key;
+                const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                const uint32_t j = j0 + (uint32_t)k;
+                if (kk > cstar) {
+                    cand_k[rg] = kk;
                     cand_i[rg] = j;
                     ++rg;
-                } else if (key == cstar) {
+                } else if (kk == cstar) {
                     if (re < take) {
-                        cand_k[G + re] = key;
+                        cand_k[G + re] = kk;
                         cand_i[G + re] = j;
                     }
                     ++re;
@@ -359,13 +425,21 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     }
 }
 
+// Queries per launch: gridDim.x * blockDim.x must stay below 2^32.
+constexpr int64_t TOPK_MAX_GRID = 1LL << 21;
+
 template <int NW>
-static hipError_t launch_topk(rfxp_ctx* ctx, const TopkArgs& a, int64_t Q) {
+static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
     const size_t lds = topk_lds_bytes(a.shift);
     hipError_t e = hipFuncSetAttribute((const void*)k_topk<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_topk<NW>, dim3((unsigned)Q), dim3(TOPK_THREADS), lds, ctx->stream, a);
-    return hipGetLastError();
+    for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
+        a.q0 = q0;
+        const unsigned nq = (unsigned)std::min(TOPK_MAX_GRID, Q - q0);
+        hipLaunchKernelGGL(k_topk<NW>, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace rfxp
