@@ -185,6 +185,54 @@ int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t 
               const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t exclude_base, int32_t K,
               int positive_only, int32_t* idx_out, uint16_t* cnt_out);
 
+/* Float scores of rfxp_topk results (Q x K, device): for OOB queries
+ * (q_oob_words as given to rfxp_topk) (float)count * (1.0f / |OOB(q)|),
+ * the score of RandomForest::get_top_k_similar
+ * (src/rf_random_forest.cpp:4744, 4775-4778); for new queries
+ * (q_oob_words NULL) (float)count / (float)T, the similarity of
+ * predict_top_k_similar (python/randomforest_py.cpp:2538-2550).  Slots
+ * without a result (idx < 0) get 0. */
+int rfxp_topk_scores(rfxp_ctx* ctx, const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t Q, int32_t T,
+                     int32_t K, const int32_t* idx, const uint16_t* cnt, float* score_out);
+
+/* RandomForest::compute_proximity_from_leaves (src/rf_random_forest.cpp:4605-4642)
+ * for npairs pairs (pair_i[p], pair_j[p]) (device int64): the float quotient
+ *   #{t : i OOB in t, leaf_i(t) == leaf_j(t) valid} / |OOB(i)|
+ * into out[p] (device float); 0 when an index is out of range or i is never
+ * OOB.  Leaf matrix and OOB bits as for rfxp_set_forest. */
+int rfxp_pair_proximity(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t,
+                        const uint32_t* oob_words, int64_t oob_ld, int64_t N, int32_t T, int32_t nleaf,
+                        const int64_t* pair_i, const int64_t* pair_j, int64_t npairs, float* out);
+
+/* ---- outlier scores ----------------------------------------------------- */
+
+/* Raw outlier measure of RandomForest::compute_outlier_scores
+ * (src/rf_random_forest.cpp:4100-4193) for Q queries against the current
+ * reference set (rfxp_set_reference), all trees:
+ *   s_q = sum over references j != excluded of (c_qj / T)^2,
+ *   c_qj = #{t : leaf_q(t) == leaf_j(t) valid},
+ *   raw_q = s_q > 1e-10 ? numerator / s_q : isolated     (device float[Q]).
+ * (c/T) is a float division and its square a float product, as in the
+ * reference; the sum runs in double and is rounded to float (the
+ * reference's float sum runs in hash-map order).  Full mode: the reference
+ * set is the training forest, queries = its samples, exclude_base = 0,
+ * numerator = N - 1, isolated = N * 1e10.  Anchor ("greedy") mode: the
+ * reference set is the anchors' leaf rows, exclude_idx[q] = the anchor
+ * position of sample q or -1 (device int32[Q]; NULL uses exclude_base as in
+ * rfxp_topk), numerator = number of anchors, isolated = anchors * 1e10. */
+int rfxp_outlier_raw(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t q_stride_t, int64_t Q,
+                     int64_t exclude_base, const int32_t* exclude_idx, float numerator, float isolated,
+                     float* raw_out);
+
+/* Host only (no device): the robust normalisation of the raw scores
+ * (src/rf_random_forest.cpp:4196-4273).  classes (host int32[N]) or NULL;
+ * per class in ascending class order (one group when NULL): median = the
+ * sorted group's element size/2, MAD = the sorted |raw - median|'s element
+ * size/2 (1 when below 1e-10), scores[n] = (raw[n] - median) / MAD.
+ * medians / mads (host float, one per group) may be NULL. */
+int rfxp_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, float* scores, float* medians,
+                           float* mads);
+
 /* ---- low-rank form of the all-trees proximity ---------------------------- */
 
 /* Y = P V with P = A A^T / T, A the N x (T*nleaf) one-hot leaf matrix of the

@@ -84,6 +84,12 @@ def lib():
         L.orc_tree_upper.argtypes = [C.c_int, _i32, _i32, _i32, C.c_int32, C.c_int32, C.c_int, C.c_int32,
                                      C.c_float, C.c_float, C.c_void_p]
         L.orc_rfgap_tree_upper.argtypes = [_i32, _i32, C.c_int32, C.c_int32, C.c_void_p]
+        L.orc_dispatch_prox.argtypes = [C.c_int, _i32, _i32, C.c_int32, _i32, _i32, C.c_void_p]
+        L.orc_pair_proximity.argtypes = [_i32, _u8, C.c_int64, C.c_int32, C.c_int32, C.c_int64, C.c_int64]
+        L.orc_pair_proximity.restype = C.c_float
+        L.orc_outlier_raw.argtypes = [_i32, C.c_int64, C.c_int32, C.c_int32, _i32, C.c_int64, C.c_void_p,
+                                      C.c_float, C.c_float, _f32, C.c_int]
+        L.orc_outlier_normalize.argtypes = [_f32, C.c_int64, C.c_void_p, _f32]
         _lib = L
     return _lib
 
@@ -315,3 +321,44 @@ def lowrank_pv(leaf_tn, nleaf, V, threads=0):
     Y = np.empty_like(V)
     lib().orc_lowrank_pv(_c(leaf_tn, np.int32).ravel(), n, t, nleaf, V.ravel(), r, Y.ravel(), threads)
     return Y
+
+
+# ---- quantization dispatcher --------------------------------------------------
+
+DISPATCH_DTYPE = {0: np.float64, 1: np.uint16, 2: np.int8, 3: np.uint8}
+
+
+def dispatch_prox(level, nodexb, nin, ndbegin, npcase):
+    """One launch of QuantizationDispatcher::launch_proximity_kernel at
+    ``level`` into a zeroed column-major N x N array of that level's type."""
+    n = len(nodexb)
+    out = np.zeros(n * n, dtype=DISPATCH_DTYPE[level])
+    lib().orc_dispatch_prox(level, _c(nodexb, np.int32), _c(nin, np.int32), n, _c(ndbegin, np.int32),
+                            _c(npcase, np.int32), out.ctypes.data)
+    return out.reshape((n, n), order="F")
+
+
+# ---- pair proximity and outlier scores ------------------------------------------
+
+def pair_proximity(leaf_tn, oob_tn, nleaf, i, j):
+    t, n = leaf_tn.shape
+    return lib().orc_pair_proximity(_c(leaf_tn, np.int32).ravel(), _c(oob_tn, np.uint8).ravel(), n, t, nleaf,
+                                    int(i), int(j))
+
+
+def outlier_raw(ref_leaf_tn, nleaf, qleaf_qt, exclude=None, numerator=1.0, isolated=1e10, threads=0):
+    t, n = ref_leaf_tn.shape
+    q = qleaf_qt.shape[0]
+    out = np.empty(q, np.float32)
+    ex = None if exclude is None else _c(exclude, np.int32)
+    lib().orc_outlier_raw(_c(ref_leaf_tn, np.int32).ravel(), n, t, nleaf, _c(qleaf_qt, np.int32).ravel(), q,
+                          ex.ctypes.data if ex is not None else None, numerator, isolated, out, threads)
+    return out
+
+
+def outlier_normalize(raw, classes=None):
+    raw = _c(raw, np.float32)
+    out = np.empty_like(raw)
+    cl = None if classes is None else _c(classes, np.int32)
+    lib().orc_outlier_normalize(raw, len(raw), cl.ctypes.data if cl is not None else None, out)
+    return out

@@ -639,3 +639,139 @@ void orc_rfgap_tree_upper(const int32_t* nin, const int32_t* nodextr, int32_t ns
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* a5: QuantizationDispatcher::launch_proximity_kernel,                       */
+/* cuda/rf_quantization_kernels.cu:195-355 (one launch)                      */
+/* ------------------------------------------------------------------------ */
+void orc_dispatch_prox(int level, const int32_t* nodexb, const int32_t* nin, int32_t nsample,
+                       const int32_t* ndbegin, const int32_t* npcase, void* out) {
+    /* every sample n with a terminal ordinal k = nodexb[n] >= 0: nodesize =
+     * sum of nin over the in-bag members of k (first pass, :207-213); then
+     * each in-bag member kk with n <= kk adds its weight at n + kk*N
+     * (second pass, :216-227).  The reference adds through type-punned
+     * 32-bit atomics; the entries here take the width of the level. */
+    const int64_t N = nsample;
+    for (int64_t n = 0; n < N; ++n) {
+        const int32_t k = nodexb[n];
+        if (k < 0) continue;
+        int32_t nsz = 0;
+        for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j)
+            if (nin[npcase[j]] > 0) nsz += nin[npcase[j]];
+        if (nsz <= 0) continue;
+        for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j) {
+            const int32_t kk = npcase[j];
+            if (nin[kk] <= 0 || n > kk) continue;
+            const int64_t e = n + (int64_t)kk * N;
+            if (level == 0) {          /* FP32: double weight (:236-270) */
+                ((double*)out)[e] += (double)nin[kk] / (double)nsz;
+            } else if (level == 1) {   /* FP16: half(weight) (:195-231) */
+                uint16_t* o = (uint16_t*)out;
+                const float w = orc_f16_to_f32(orc_f32_to_f16((float)nin[kk] / (float)nsz));
+                o[e] = orc_f32_to_f16(orc_f16_to_f32(o[e]) + w);
+            } else if (level == 2) {   /* INT8: fp32_to_int8(w, 1/127, 0) (:273-310, dispatcher :372-378) */
+                uint8_t* o = (uint8_t*)out;
+                o[e] = (uint8_t)(o[e] + (uint8_t)orc_q_i8((float)nin[kk] / (float)nsz, 1.0f / 127.0f, 0.0f));
+            } else {                   /* NF4: one byte per entry, + fp32_to_nf4(w) (:313-355) */
+                uint8_t* o = (uint8_t*)out;
+                o[e] = (uint8_t)(o[e] + orc_q_nf4((float)nin[kk] / (float)nsz));
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a8: compute_proximity_from_leaves, src/rf_random_forest.cpp:4605-4642     */
+/* ------------------------------------------------------------------------ */
+float orc_pair_proximity(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int64_t i,
+                         int64_t j) {
+    if (i < 0 || i >= N || j < 0 || j >= N) return 0.0f;            /* :4610-4613 */
+    int32_t matches = 0, noob = 0;
+    for (int32_t t = 0; t < T; ++t) {                                /* oob_trees_[i], ascending */
+        if (!oob[(int64_t)t * N + i]) continue;
+        ++noob;
+        const int32_t li = leaf[(int64_t)t * N + i], lj = leaf[(int64_t)t * N + j];
+        if (li == lj && li >= 0 && li < nleaf) ++matches;            /* :4628-4636 */
+    }
+    if (noob == 0) return 0.0f;                                      /* :4619-4621 */
+    return (float)matches / (float)noob;                             /* :4641 */
+}
+
+/* ------------------------------------------------------------------------ */
+/* f2: outlier scores, src/rf_random_forest.cpp:4100-4273                    */
+/* ------------------------------------------------------------------------ */
+void orc_outlier_raw(const int32_t* ref_leaf, int64_t N, int32_t T, int32_t nleaf, const int32_t* qleaf, int64_t Q,
+                     const int32_t* exclude, float numerator, float isolated, float* raw_out, int threads) {
+    const int nth = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel num_threads(nth)
+    {
+        uint16_t* cnt = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(N > 0 ? N : 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t q = 0; q < Q; ++q) {
+            memset(cnt, 0, sizeof(uint16_t) * (size_t)N);
+            for (int32_t t = 0; t < T; ++t) {   /* the query's leaf members in every tree (:4167-4178) */
+                const int32_t ql = qleaf[q * T + t];
+                if (ql < 0 || ql >= nleaf) continue;
+                const int32_t* rl = ref_leaf + (int64_t)t * N;
+                for (int64_t j = 0; j < N; ++j) cnt[j] += (uint16_t)(rl[j] == ql);
+            }
+            const int64_t ex = exclude ? exclude[q] : -1;
+            double s = 0.0;                     /* prox = count / ntree, squared, summed (:4179-4183) */
+            for (int64_t j = 0; j < N; ++j) {
+                if (j == ex || cnt[j] == 0) continue;
+                const float p = (float)cnt[j] / (float)T;
+                s += (double)(p * p);
+            }
+            const float sq = (float)s;
+            raw_out[q] = sq > 1e-10f ? numerator / sq : isolated; /* :4184-4188 */
+        }
+        free(cnt);
+    }
+}
+
+static int cmp_f32(const void* a, const void* b) {
+    const float x = *(const float*)a, y = *(const float*)b;
+    return (x > y) - (x < y);
+}
+
+void orc_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, float* scores) {
+    /* groups: ascending class values (std::map order, :4198-4203), or all */
+    int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * (size_t)N);
+    int64_t ng = 0;
+    if (classes) {
+        for (int64_t n = 0; n < N; ++n) {
+            int found = 0;
+            for (int64_t g = 0; g < ng; ++g) found |= keys[g] == classes[n];
+            if (!found) keys[ng++] = classes[n];
+        }
+        /* insertion sort of the class keys */
+        for (int64_t a = 1; a < ng; ++a)
+            for (int64_t b = a; b > 0 && keys[b - 1] > keys[b]; --b) {
+                const int32_t t = keys[b];
+                keys[b] = keys[b - 1];
+                keys[b - 1] = t;
+            }
+    } else {
+        ng = 1;
+    }
+    float* v = (float*)malloc(sizeof(float) * (size_t)N);
+    float* d = (float*)malloc(sizeof(float) * (size_t)N);
+    for (int64_t g = 0; g < ng; ++g) {
+        int64_t m = 0;
+        for (int64_t n = 0; n < N; ++n)
+            if (!classes || classes[n] == keys[g]) v[m++] = raw[n];
+        qsort(v, (size_t)m, sizeof(float), cmp_f32);
+        const float median = v[m / 2];                             /* :4218-4219, :4249-4250 */
+        int64_t k = 0;
+        for (int64_t n = 0; n < N; ++n)
+            if (!classes || classes[n] == keys[g]) d[k++] = fabsf(raw[n] - median);
+        qsort(d, (size_t)m, sizeof(float), cmp_f32);
+        float mad = d[m / 2];                                      /* :4221-4228 */
+        if (mad < 1e-10f) mad = 1.0f;
+        for (int64_t n = 0; n < N; ++n)
+            if (!classes || classes[n] == keys[g]) scores[n] = (raw[n] - median) / mad;
+    }
+    free(v);
+    free(d);
+    free(keys);
+}

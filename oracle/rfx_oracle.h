@@ -150,6 +150,38 @@ void orc_rfgap_tree_upper(const int32_t* nin, const int32_t* nodextr, int32_t ns
 void orc_lowrank_pv(const int32_t* leaf, int64_t N, int32_t T, int32_t nleaf, const double* V,
                     int32_t r, double* Y, int threads);
 
+/* ---- quantization dispatcher (cuda/rf_quantization_kernels.cu:195-406) --- */
+
+/* One launch of QuantizationDispatcher::launch_proximity_kernel at `level`
+ * (0 FP32 -> double, 1 FP16 -> uint16 half bits, 2 INT8 -> int8 with the
+ * dispatcher's scale 1/127 and zero point 0, 3 NF4 -> one byte per entry)
+ * into the caller-zeroed column-major N x N `out`: for every sample n with a
+ * terminal ordinal k = nodexb[n] >= 0 and every in-bag member kk >= n of
+ * node k (CSR ndbegin / npcase as src/rf_proximity.cpp:110-171 builds it),
+ * entry n + kk*N takes the weight nin[kk] / nodesize in that level's type. */
+void orc_dispatch_prox(int level, const int32_t* nodexb, const int32_t* nin, int32_t nsample,
+                       const int32_t* ndbegin, const int32_t* npcase, void* out);
+
+/* ---- pair proximity and outlier scores ------------------------------------ */
+
+/* src/rf_random_forest.cpp:4605-4642: #{t : oob_i(t), leaf_i(t) == leaf_j(t)
+ * valid} / |OOB(i)| as a float division; 0 for bad indices or no OOB tree. */
+float orc_pair_proximity(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int64_t i,
+                         int64_t j);
+
+/* src/rf_random_forest.cpp:4100-4193 (full / anchor modes): for query q
+ * (qleaf[q*T + t], sample-major) against the references (ref_leaf[t*N + j]),
+ * c_j = #{t : labels equal and valid}; s = sum over j != exclude[q], c_j > 0,
+ * ascending j, in double, of the float (c_j / (float)T)^2; raw_q = (float)s
+ * > 1e-10 ? numerator / (float)s : isolated.  exclude may be NULL. */
+void orc_outlier_raw(const int32_t* ref_leaf, int64_t N, int32_t T, int32_t nleaf, const int32_t* qleaf, int64_t Q,
+                     const int32_t* exclude, float numerator, float isolated, float* raw_out, int threads);
+
+/* src/rf_random_forest.cpp:4196-4273: per class (ascending) or overall,
+ * median = sorted[size/2], MAD = sorted |raw - median|[size/2] (1 below
+ * 1e-10), score = (raw - median) / MAD.  classes may be NULL. */
+void orc_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, float* scores);
+
 #ifdef __cplusplus
 }
 #endif

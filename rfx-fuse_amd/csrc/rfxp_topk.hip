@@ -27,7 +27,9 @@
 // threshold, ordered compaction of the winners, and a rank merge with the
 // running list by one wave.
 #include <algorithm>
+#include <cmath>
 #include <string>
+#include <vector>
 
 #include "rfxp_device.hpp"
 #include "rfxp_forest.hpp"
@@ -53,6 +55,7 @@ struct TopkArgs {
     const uint32_t* qoob;  // NULL: all trees
     int64_t qold;
     int64_t exclude_base;  // query q excludes reference exclude_base + q; < 0: none
+    const int32_t* exclude_idx;  // or, when not NULL, reference exclude_idx[q] (< 0: none)
     int64_t q0;            // query of workgroup 0 of this launch
     int32_t K;
     int32_t floor_key;     // smallest selectable key: 1 (zeros allowed) or 2 (counts > 0)
@@ -230,9 +233,54 @@ __device__ __forceinline__ uint32_t count_ge(const uint32_t (&key)[NW], uint32_t
     return n;
 }
 
+// The reference query q may not return (< 0: none).
+__device__ __forceinline__ int64_t query_exclusion(const TopkArgs& a, int64_t q) {
+    if (a.exclude_idx) return a.exclude_idx[q];
+    return a.exclude_base >= 0 ? a.exclude_base + q : -1;
+}
+
 // (key desc, index asc): does (ka, ia) come before (kb, ib)?
 __device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, uint32_t ib) {
     return ka > kb || (ka == kb && ia < ib);
+}
+
+// Clears the 16-bit LDS counters of a segment of S references and counts
+// into them, for query q, the members of the query's buckets of segment s
+// (counter unit j - lo for member j; base1 = lo + 1, width = references in
+// the segment).  Ends with a barrier: every count is in LDS.
+__device__ __forceinline__ void count_segment(const TopkArgs& a, int64_t q, int32_t s, uint32_t S, uint32_t* sm,
+                                              uint32_t* rec_off, uint32_t* rec_len, uint32_t dummy, uint32_t lane4,
+                                              int32_t wave, uint32_t base1, uint32_t width) {
+    uint4* c4 = (uint4*)sm;
+    for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+    sm[dummy >> 2] = 0u;
+    for (int32_t tc = 0; tc < a.T; tc += TOPK_THREADS) {
+        // the query's bucket records of trees tc .. tc+1023, one per thread
+        uint32_t soff, len4;
+        query_bucket(a, q, tc + (int32_t)threadIdx.x, s, soff, len4);
+        rec_off[threadIdx.x] = soff;
+        rec_len[threadIdx.x] = len4;
+        __syncthreads();
+        const int32_t nt = min(a.T - tc, TOPK_THREADS);
+        const int32_t ng = (nt + 15) >> 4;
+        const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
+        // two groups in ping-pong: one is counted while the other loads
+        uint32_t A[16], B[16];
+        bool la = load16(a, rec_off, rec_len, g0, g0 < g1, lane4, A);
+        for (int32_t g = g0; g < g1; g += 2) {
+            const bool lb = load16(a, rec_off, rec_len, g + 1, g + 1 < g1, lane4, B);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
+            if (la) tails16(a, rec_off, rec_len, g, lane4, base1, width, dummy);
+            la = load16(a, rec_off, rec_len, g + 2, g + 2 < g1, lane4, A);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
+            if (lb) tails16(a, rec_off, rec_len, g + 1, lane4, base1, width, dummy);
+        }
+        __syncthreads();
+    }
 }
 
 template <int NW>  // 16-bit words per thread: S = 2 * NW * TOPK_THREADS
@@ -254,7 +302,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t q = a.q0 + blockIdx.x;
     const uint32_t K = (uint32_t)a.K;
-    const int64_t ex = a.exclude_base >= 0 ? a.exclude_base + q : -1;
+    const int64_t ex = query_exclusion(a, q);
 
     uint32_t nrun = 0;  // entries in the running list (uniform)
     uint32_t kmin = 0;  // key of the running K-th entry once the list is full
@@ -262,36 +310,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const uint32_t lo = (uint32_t)s << shift;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
         const uint32_t base1 = lo + 1u;
-        uint4* c4 = (uint4*)sm;
-        for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
-        sm[dummy >> 2] = 0u;
-        for (int32_t tc = 0; tc < a.T; tc += TOPK_THREADS) {
-            // the query's bucket records of trees tc .. tc+1023, one per thread
-            uint32_t soff, len4;
-            query_bucket(a, q, tc + (int32_t)threadIdx.x, s, soff, len4);
-            rec_off[threadIdx.x] = soff;
-            rec_len[threadIdx.x] = len4;
-            __syncthreads();
-            const int32_t nt = min(a.T - tc, TOPK_THREADS);
-            const int32_t ng = (nt + 15) >> 4;
-            const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
-            // two groups in ping-pong: one is counted while the other loads
-            uint32_t A[16], B[16];
-            bool la = load16(a, rec_off, rec_len, g0, g0 < g1, lane4, A);
-            for (int32_t g = g0; g < g1; g += 2) {
-                const bool lb = load16(a, rec_off, rec_len, g + 1, g + 1 < g1, lane4, B);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
-                if (la) tails16(a, rec_off, rec_len, g, lane4, base1, width, dummy);
-                la = load16(a, rec_off, rec_len, g + 2, g + 2 < g1, lane4, A);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
-                if (lb) tails16(a, rec_off, rec_len, g + 1, lane4, base1, width, dummy);
-            }
-            __syncthreads();
-        }
+        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, base1, width);
         // counters -> keys, held in registers from here on: count + 1, or
         // 0 where the reference may not be chosen (past the end, or excluded)
         const uint32_t u0 = threadIdx.x * 2u * NW;
@@ -425,6 +444,145 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     }
 }
 
+// Outlier scores, full and anchor modes of RandomForest::compute_outlier_scores
+// (src/rf_random_forest.cpp:4100-4193): for query q, with c_j the all-trees
+// co-occurrence count of q and reference j (every j except the excluded
+// one),
+//     s_q = sum_j (c_j / T)^2,   raw_q = s_q > 1e-10 ? numerator / s_q : isolated
+// with c_j / T a float division and its square a float product, as the
+// reference computes them; the terms are summed in double (the reference
+// sums floats in hash-map order, which no order reproduces), then rounded
+// to float.  The counts come from count_segment, exactly as for top-K.
+struct OutlierArgs {
+    float numerator, isolated;
+    float* raw_out;
+};
+
+template <int NW>
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_outlier(TopkArgs a,
+                                                                                                    OutlierArgs o) {
+    extern __shared__ uint32_t sm[];
+    const int32_t shift = a.shift;
+    const uint32_t S = 1u << shift;
+    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
+    uint32_t* const rec_len = rec_off + TOPK_THREADS;
+    double* const red = (double*)(rec_len + TOPK_THREADS);  // TOPK_WAVES doubles
+    const uint32_t* const kw = sm + threadIdx.x * NW;
+    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
+    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t q = a.q0 + blockIdx.x;
+    const int64_t ex = query_exclusion(a, q);
+    const float fT = (float)a.T;
+
+    double acc = 0.0;
+    for (int32_t s = 0; s < a.nseg; ++s) {
+        const uint32_t lo = (uint32_t)s << shift;
+        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
+        const uint32_t u0 = threadIdx.x * 2u * NW;
+        const int32_t rem = (int32_t)width - (int32_t)u0;
+        const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
+        const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            const uint32_t w = kw[k];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t c = (w >> (16 * h)) & 0xffffu;
+                if (c != 0u && 2 * k + h < rem && 2 * k + h != exu) {
+                    const float p = (float)c / fT;
+                    acc += (double)(p * p);
+                }
+            }
+        }
+        __syncthreads();  // counters read before the next segment clears them
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d, 64);
+    if ((threadIdx.x & 63) == 0) red[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < TOPK_WAVES; ++w) t += red[w];
+        const float sq = (float)t;
+        o.raw_out[q] = sq > 1e-10f ? o.numerator / sq : o.isolated;
+    }
+}
+
+// compute_proximity_from_leaves (src/rf_random_forest.cpp:4605-4642) for a
+// batch of pairs: #{t : i OOB in t, leaf_i(t) == leaf_j(t)} / |OOB(i)| as a
+// float division; 0 for indices out of range or |OOB(i)| = 0.  One wave per
+// pair, lanes over trees.
+struct PairArgs {
+    const int32_t* leaf;
+    int64_t si, st;
+    const uint32_t* oob;
+    int64_t old;
+    int64_t N;
+    int32_t T, L;
+    const int64_t* pi;
+    const int64_t* pj;
+    int64_t npairs;
+    float* out;
+};
+
+__global__ __launch_bounds__(256) void k_pair_prox(PairArgs a) {
+    const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= a.npairs) return;
+    const int64_t i = a.pi[p], j = a.pj[p];
+    const bool ok = i >= 0 && i < a.N && j >= 0 && j < a.N;
+    uint32_t match = 0, noob = 0;
+    if (ok) {
+        for (int32_t t = threadIdx.x & 63; t < a.T; t += 64) {
+            const uint32_t w = a.oob[(int64_t)t * a.old + (i >> 5)];
+            if (!((w >> (i & 31)) & 1u)) continue;
+            ++noob;
+            const int32_t li = a.leaf[i * a.si + (int64_t)t * a.st];
+            const int32_t lj = a.leaf[j * a.si + (int64_t)t * a.st];
+            match += (li == lj && li >= 0 && li < a.L) ? 1u : 0u;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        match += (uint32_t)__shfl_xor((int)match, d, 64);
+        noob += (uint32_t)__shfl_xor((int)noob, d, 64);
+    }
+    if ((threadIdx.x & 63) == 0) a.out[p] = (ok && noob) ? (float)match / (float)noob : 0.0f;
+}
+
+// Float scores of top-K results (src/rf_random_forest.cpp:4744, 4775-4778
+// for OOB queries: (float)count * (1.0f / |OOB(q)|);
+// python/randomforest_py.cpp:2538-2550 for new queries: the count summed
+// as floats, divided by (float)T); 0 where a slot holds no result.
+struct ScoreArgs {
+    const uint32_t* qoob;
+    int64_t qold;
+    int64_t Q;
+    int32_t T, K;
+    const int32_t* idx;
+    const uint16_t* cnt;
+    float* score;
+};
+
+__global__ __launch_bounds__(256) void k_topk_scores(ScoreArgs a) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.Q * a.K) return;
+    const int64_t q = e / a.K;
+    float sc = 0.0f;
+    if (a.idx[e] >= 0) {
+        const float c = (float)a.cnt[e];
+        if (a.qoob) {
+            uint32_t n = 0;
+            for (int32_t t = 0; t < a.T; ++t) n += (a.qoob[(int64_t)t * a.qold + (q >> 5)] >> (q & 31)) & 1u;
+            sc = n ? c * (1.0f / (float)n) : 0.0f;
+        } else {
+            sc = c / (float)a.T;
+        }
+    }
+    a.score[e] = sc;
+}
+
 // Queries per launch: gridDim.x * blockDim.x must stay below 2^32.
 constexpr int64_t TOPK_MAX_GRID = 1LL << 21;
 
@@ -440,6 +598,49 @@ static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+template <int NW>
+static hipError_t launch_outlier(rfxp_ctx* ctx, TopkArgs a, const OutlierArgs& o, int64_t Q) {
+    const size_t lds = topk_lds_bytes(a.shift);
+    hipError_t e = hipFuncSetAttribute((const void*)k_outlier<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
+        a.q0 = q0;
+        const unsigned nq = (unsigned)std::min(TOPK_MAX_GRID, Q - q0);
+        hipLaunchKernelGGL(k_outlier<NW>, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a, o);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Arguments of a query launch over the context's reference set.
+static TopkArgs ref_args(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t q_stride_t,
+                         const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t exclude_base,
+                         const int32_t* exclude_idx) {
+    TopkArgs a;
+    a.mem = ctx->ref_mem.p;
+    a.mem_bytes = (uint32_t)(((uint64_t)ctx->ref_T * (uint64_t)ctx->ref_N + MEM_PAD) * 4u);
+    a.off = ctx->ref_off.p;
+    a.nb = ctx->ref_nb;
+    a.N = ctx->ref_N;
+    a.T = ctx->ref_T;
+    a.L = ctx->ref_L;
+    a.nseg = ctx->ref_nseg;
+    a.shift = ctx->ref_shift;
+    a.qleaf = q_leaf;
+    a.qsi = q_stride_i;
+    a.qst = q_stride_t;
+    a.qoob = q_oob_words;
+    a.qold = q_oob_ld;
+    a.exclude_base = exclude_base;
+    a.exclude_idx = exclude_idx;
+    a.q0 = 0;
+    a.K = 1;
+    a.floor_key = 1;
+    a.idx_out = nullptr;
+    a.cnt_out = nullptr;
+    return a;
 }
 
 }  // namespace rfxp
@@ -497,22 +698,7 @@ extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
     if (q_oob_words && q_oob_ld < (Q + 31) / 32)
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk: q_oob_ld < ceil(Q/32)");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
-    TopkArgs a;
-    a.mem = ctx->ref_mem.p;
-    a.mem_bytes = (uint32_t)(((uint64_t)ctx->ref_T * (uint64_t)ctx->ref_N + MEM_PAD) * 4u);
-    a.off = ctx->ref_off.p;
-    a.nb = ctx->ref_nb;
-    a.N = ctx->ref_N;
-    a.T = ctx->ref_T;
-    a.L = ctx->ref_L;
-    a.nseg = ctx->ref_nseg;
-    a.shift = ctx->ref_shift;
-    a.qleaf = q_leaf;
-    a.qsi = q_stride_i;
-    a.qst = q_stride_t;
-    a.qoob = q_oob_words;
-    a.qold = q_oob_ld;
-    a.exclude_base = exclude_base;
+    TopkArgs a = ref_args(ctx, q_leaf, q_stride_i, q_stride_t, q_oob_words, q_oob_ld, exclude_base, nullptr);
     a.K = K;
     a.floor_key = positive_only ? 2 : 1;
     a.idx_out = idx_out;
@@ -529,5 +715,112 @@ extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
         }
     }
     if (e != hipSuccess) return hip_error(ctx, e, "k_topk launch");
+    return RFXP_OK;
+}
+
+extern "C" int rfxp_topk_scores(rfxp_ctx* ctx, const uint32_t* q_oob_words, int64_t q_oob_ld, int64_t Q, int32_t T,
+                                int32_t K, const int32_t* idx, const uint16_t* cnt, float* score_out) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (Q < 0 || K < 1 || T < 1) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk_scores: need Q >= 0, K >= 1, T >= 1");
+    if (Q == 0) return RFXP_OK;
+    if (Q > (1LL << 40) / K) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_topk_scores: Q * K too large");
+    if (!idx || !cnt || !score_out || !is_device_pointer(idx) || !is_device_pointer(cnt) ||
+        !is_device_pointer(score_out) || (q_oob_words && !is_device_pointer(q_oob_words)))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk_scores: pointers must be device pointers");
+    if (q_oob_words && q_oob_ld < (Q + 31) / 32)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk_scores: q_oob_ld < ceil(Q/32)");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    ScoreArgs a{q_oob_words, q_oob_ld, Q, T, K, idx, cnt, score_out};
+    const int64_t nb = (Q * K + 255) / 256;
+    if (nb > 0x7fffffffLL) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_topk_scores: Q * K too large");
+    hipLaunchKernelGGL(k_topk_scores, dim3((unsigned)nb), dim3(256), 0, ctx->stream, a);
+    return check_launch(ctx, "k_topk_scores launch");
+}
+
+extern "C" int rfxp_pair_proximity(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t,
+                                   const uint32_t* oob_words, int64_t oob_ld, int64_t N, int32_t T, int32_t nleaf,
+                                   const int64_t* pair_i, const int64_t* pair_j, int64_t npairs, float* out) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (N < 0 || T < 1 || nleaf < 1 || npairs < 0)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_pair_proximity: need N >= 0, T >= 1, nleaf >= 1, npairs >= 0");
+    if (npairs == 0) return RFXP_OK;
+    if (oob_ld < (N + 31) / 32) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_pair_proximity: oob_ld < ceil(N/32)");
+    if (!leaf || !oob_words || !pair_i || !pair_j || !out || !is_device_pointer(leaf) ||
+        !is_device_pointer(oob_words) || !is_device_pointer(pair_i) || !is_device_pointer(pair_j) ||
+        !is_device_pointer(out))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_pair_proximity: pointers must be device pointers");
+    if ((npairs + 3) / 4 > 0x7fffffffLL)
+        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_pair_proximity: too many pairs");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    PairArgs a{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf, pair_i, pair_j, npairs, out};
+    hipLaunchKernelGGL(k_pair_prox, dim3((unsigned)((npairs + 3) / 4)), dim3(256), 0, ctx->stream, a);
+    return check_launch(ctx, "k_pair_prox launch");
+}
+
+extern "C" int rfxp_outlier_raw(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_i, int64_t q_stride_t,
+                                int64_t Q, int64_t exclude_base, const int32_t* exclude_idx, float numerator,
+                                float isolated, float* raw_out) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (!ctx->ref_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_outlier_raw: no reference set");
+    if (Q < 0) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_outlier_raw: need Q >= 0");
+    if (Q == 0) return RFXP_OK;
+    if (Q > 0x7fffffffLL) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_outlier_raw: too many queries");
+    if (!q_leaf || !raw_out || !is_device_pointer(q_leaf) || !is_device_pointer(raw_out) ||
+        (exclude_idx && !is_device_pointer(exclude_idx)))
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_outlier_raw: pointers must be device pointers");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    const TopkArgs a = ref_args(ctx, q_leaf, q_stride_i, q_stride_t, nullptr, 0, exclude_base, exclude_idx);
+    const OutlierArgs o{numerator, isolated, raw_out};
+    hipError_t e;
+    {
+        LaunchTimer tm(ctx, "outlier");
+        switch (a.shift) {
+            case 11: e = launch_outlier<1>(ctx, a, o, Q); break;
+            case 12: e = launch_outlier<2>(ctx, a, o, Q); break;
+            case 13: e = launch_outlier<4>(ctx, a, o, Q); break;
+            case 14: e = launch_outlier<8>(ctx, a, o, Q); break;
+            default: e = launch_outlier<16>(ctx, a, o, Q); break;
+        }
+    }
+    if (e != hipSuccess) return hip_error(ctx, e, "k_outlier launch");
+    return RFXP_OK;
+}
+
+// src/rf_random_forest.cpp:4196-4273: robust normalisation of the raw
+// scores, per class in ascending class order when classes are given (else
+// over all samples): median = the sorted values' element size/2, MAD = the
+// sorted absolute deviations' element size/2 (1 when below 1e-10),
+// score = (raw - median) / MAD.  Host memory, no device needed.
+extern "C" int rfxp_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, float* scores,
+                                      float* medians, float* mads) {
+    if (N < 1 || !raw || !scores) return RFXP_ERR_INVALID;
+    std::vector<int32_t> cls;
+    if (classes) {
+        cls.assign(classes, classes + N);
+        std::sort(cls.begin(), cls.end());
+        cls.erase(std::unique(cls.begin(), cls.end()), cls.end());
+    } else {
+        cls.push_back(-1);
+    }
+    std::vector<int64_t> members;
+    std::vector<float> v, dev;
+    for (size_t c = 0; c < cls.size(); ++c) {
+        members.clear();
+        for (int64_t n = 0; n < N; ++n)
+            if (!classes || classes[n] == cls[c]) members.push_back(n);
+        v.resize(members.size());
+        for (size_t k = 0; k < members.size(); ++k) v[k] = raw[members[k]];
+        std::vector<float> sorted = v;
+        std::sort(sorted.begin(), sorted.end());
+        const float median = sorted[sorted.size() / 2];
+        dev.resize(v.size());
+        for (size_t k = 0; k < v.size(); ++k) dev[k] = std::fabs(v[k] - median);
+        std::sort(dev.begin(), dev.end());
+        float mad = dev[dev.size() / 2];
+        if (mad < 1e-10f) mad = 1.0f;
+        if (medians) medians[c] = median;
+        if (mads) mads[c] = mad;
+        for (size_t k = 0; k < members.size(); ++k) scores[members[k]] = (raw[members[k]] - median) / mad;
+    }
     return RFXP_OK;
 }

@@ -78,6 +78,10 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_noalloc_workspace.restype = i64
     L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
     L.rfxp_topk.argtypes = [vp, vp, i64, i64, i64, vp, i64, i64, i32, C.c_int, vp, vp]
+    L.rfxp_topk_scores.argtypes = [vp, vp, i64, i64, i32, i32, vp, vp, vp]
+    L.rfxp_pair_proximity.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, vp, i64, vp]
+    L.rfxp_outlier_raw.argtypes = [vp, vp, i64, i64, i64, i64, vp, C.c_float, C.c_float, vp]
+    L.rfxp_outlier_normalize.argtypes = [vp, i64, vp, vp, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
     L.rfxp_lowrank_subspace.argtypes = [vp, vp, i32, i32, vp, vp]
     L.rfxp_tree_pairs.argtypes = [vp, vp, vp, vp, i32, i32, C.c_int, C.POINTER(C.POINTER(i64)),
@@ -120,6 +124,25 @@ def upper_noalloc_workspace(n: int, t: int, nleaf: int, nout_given: bool = False
 
 
 NOALLOC_MAX_BYTES = 64 << 20
+
+
+def outlier_normalize(raw, classes=None):
+    """Host: (scores, medians, mads) of rfxp_outlier_normalize (numpy in/out)."""
+    import numpy as np
+
+    L = load()
+    raw = np.ascontiguousarray(raw, dtype=np.float32)
+    n = raw.shape[0]
+    cls = None if classes is None else np.ascontiguousarray(classes, dtype=np.int32)
+    ng = 1 if cls is None else len(np.unique(cls))
+    sc = np.empty(n, np.float32)
+    med = np.empty(ng, np.float32)
+    mad = np.empty(ng, np.float32)
+    rc = L.rfxp_outlier_normalize(raw.ctypes.data, n, None if cls is None else cls.ctypes.data, sc.ctypes.data,
+                                  med.ctypes.data, mad.ctypes.data)
+    if rc != 0:
+        raise RfxpError(rc, "rfxp_outlier_normalize: bad arguments")
+    return sc, med, mad
 
 
 def pack_oob_bits(oob_tn):
@@ -248,6 +271,52 @@ class Context:
         self._check(self._L.rfxp_topk(self.h, qleaf.data_ptr(), si, st, q, optr, old, exclude_base, k,
                                       int(positive_only), idx.data_ptr(), cnt.data_ptr()))
         return idx, cnt
+
+    def topk_scores(self, idx, cnt, t: int, oob_words=None):
+        """Float scores of topk results (OOB queries when oob_words is the
+        topk call's OOB words, else new queries over t trees)."""
+        import torch
+
+        q, k = idx.shape
+        sc = torch.empty((q, k), dtype=torch.float32, device=idx.device)
+        optr, old = None, 0
+        if oob_words is not None:
+            optr, old = oob_words.data_ptr(), oob_words.shape[1]
+        self._check(self._L.rfxp_topk_scores(self.h, optr, old, q, t, k, idx.data_ptr(), cnt.data_ptr(),
+                                             sc.data_ptr()))
+        return sc
+
+    def pair_proximity(self, leaf, oob_words, n: int, t: int, nleaf: int, pi, pj, layout: str = "tree"):
+        """compute_proximity_from_leaves for pairs (pi[p], pj[p]) (int64
+        device tensors); leaf int32 (T, N) for layout 'tree' or (N, T)."""
+        import torch
+
+        assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
+        si, st = (1, n) if layout == "tree" else (t, 1)
+        assert pi.dtype == torch.int64 and pj.dtype == torch.int64 and pi.shape == pj.shape
+        out = torch.empty(pi.shape[0], dtype=torch.float32, device=leaf.device)
+        self._check(self._L.rfxp_pair_proximity(self.h, leaf.data_ptr(), si, st, oob_words.data_ptr(),
+                                                oob_words.shape[1], n, t, nleaf, pi.data_ptr(), pj.data_ptr(),
+                                                pi.shape[0], out.data_ptr()))
+        return out
+
+    def outlier_raw(self, qleaf, layout: str = "sample", exclude_base: int = -1, exclude_idx=None,
+                    numerator: float = 1.0, isolated: float = 1e10):
+        """Raw outlier measure of each query against the reference set."""
+        import torch
+
+        assert qleaf.dtype == torch.int32 and qleaf.is_cuda and qleaf.is_contiguous()
+        if layout == "sample":
+            q, t = qleaf.shape
+            si, st = t, 1
+        else:
+            t, q = qleaf.shape
+            si, st = 1, q
+        raw = torch.empty(q, dtype=torch.float32, device=qleaf.device)
+        ex = None if exclude_idx is None else exclude_idx.data_ptr()
+        self._check(self._L.rfxp_outlier_raw(self.h, qleaf.data_ptr(), si, st, q, exclude_base, ex,
+                                             numerator, isolated, raw.data_ptr()))
+        return raw
 
     def lowrank_pv(self, V):
         """Y = P V for the reference set (P = A A^T / T): V float32 device

@@ -13,7 +13,10 @@
 // triangles: fp16 (ne u16), int8 (ne i8), nf4 ((ne+1)/2 u8), unified INT8
 // (ne i8), RF-GAP fp16 (ne u16); get_quantized_size for 4 levels x 1000
 // (4 x u64); compute_int8_scaling of proxsym's first column (2 f32) and
-// compute_int8_scaling_gpu of proxsym (2 f32).
+// compute_int8_scaling_gpu of proxsym (2 f32); proxsym via gpu_finishprox
+// (N*N f64); tree 0's terminal CSR: nterm (i32), nodexb[N], ndbegin[nterm+1],
+// npcase[N]; launch_proximity_kernel at FP32, FP16, INT8, NF4 for tree 0
+// (N*N f64, u16, i8, u8).
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -108,6 +111,62 @@ int main(int argc, char** argv) {
     if (hipMemcpy(sc + 2, dsz, 8, hipMemcpyDeviceToHost) != hipSuccess) return 3;
     (void)hipFree(dsym);
     (void)hipFree(dsz);
+
+    // rf::gpu_finishprox on the accumulated prox (its only form is the
+    // reference's; no caller in the reference, include/rf_finishprox.hpp:12)
+    std::vector<double> sym2(nn, 0.0);
+    rf::gpu_finishprox(N, nout.data(), prox.data(), sym2.data());
+
+    // QuantizationDispatcher::launch_proximity_kernel for tree 0 at all four
+    // levels, the way cuda/rf_proximity.cu:440-485 calls it: terminal CSR of
+    // the tree built on the host (src/rf_proximity.cpp:110-171), device
+    // inputs, a zeroed get_quantized_size(level, N*N) output, 256-thread
+    // blocks over the samples.
+    const std::vector<int32_t>& st0 = status[0];
+    std::vector<int32_t> nod(nnode[0] > 0 ? nnode[0] : 1, -1), ncount(N, 0), ncn(N, 0), nodexb(N, -1);
+    int32_t nterm = 0;
+    for (int32_t k = 0; k < nnode[0]; ++k)
+        if (st0[k] == -1) nod[k] = nterm++;
+    for (int32_t n = 0; n < N; ++n) {
+        const int32_t nd = nodextr[0][n];
+        if (nd >= 0 && nd < nnode[0] && nod[nd] >= 0) {
+            const int32_t k = nod[nd];
+            ncn[n] = ++ncount[k];
+            nodexb[n] = k;
+        }
+    }
+    std::vector<int32_t> ndbegin(nterm + 1, 0), npcase(N, -1);
+    for (int32_t k = 1; k <= nterm; ++k) ndbegin[k] = ndbegin[k - 1] + ncount[k - 1];
+    for (int32_t n = 0; n < N; ++n)
+        if (nodexb[n] >= 0) npcase[ndbegin[nodexb[n]] + ncn[n] - 1] = n;
+    int32_t *d_xb = nullptr, *d_nin = nullptr, *d_beg = nullptr, *d_pc = nullptr;
+    if (hipMalloc((void**)&d_xb, 4 * (size_t)N) != hipSuccess || hipMalloc((void**)&d_nin, 4 * (size_t)N) != hipSuccess ||
+        hipMalloc((void**)&d_beg, 4 * (size_t)(nterm + 1)) != hipSuccess ||
+        hipMalloc((void**)&d_pc, 4 * (size_t)N) != hipSuccess)
+        return 3;
+    if (hipMemcpy(d_xb, nodexb.data(), 4 * (size_t)N, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_nin, nin[0].data(), 4 * (size_t)N, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_beg, ndbegin.data(), 4 * (size_t)(nterm + 1), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_pc, npcase.data(), 4 * (size_t)N, hipMemcpyHostToDevice) != hipSuccess)
+        return 3;
+    std::vector<std::vector<uint8_t>> lev(4);
+    for (int l = 0; l < 4; ++l) {
+        const auto q = (rf::cuda::QuantizationLevel)l;
+        const size_t nb = rf::cuda::QuantizationDispatcher::get_quantized_size(q, nn);
+        void* d = nullptr;
+        if (hipMalloc(&d, nb) != hipSuccess || hipMemset(d, 0, nb) != hipSuccess) return 3;
+        rf::cuda::QuantizationDispatcher::launch_proximity_kernel(q, d_xb, d_nin, N, d_beg, d_pc, d, (N + 255) / 256,
+                                                                  256);
+        if (hipDeviceSynchronize() != hipSuccess) return 3;
+        lev[l].resize(nb);
+        if (hipMemcpy(lev[l].data(), d, nb, hipMemcpyDeviceToHost) != hipSuccess) return 3;
+        (void)hipFree(d);
+    }
+    (void)hipFree(d_xb);
+    (void)hipFree(d_nin);
+    (void)hipFree(d_beg);
+    (void)hipFree(d_pc);
+
     if (rfx_compat_last_error()[0]) {
         fprintf(stderr, "compat error: %s\n", rfx_compat_last_error());
         return 4;
@@ -127,6 +186,12 @@ int main(int argc, char** argv) {
     fwrite(gap16.data(), 2, ne, o);
     fwrite(qs, 8, 4, o);
     fwrite(sc, 4, 4, o);
+    fwrite(sym2.data(), 8, nn, o);
+    fwrite(&nterm, 4, 1, o);
+    fwrite(nodexb.data(), 4, N, o);
+    fwrite(ndbegin.data(), 4, nterm + 1, o);
+    fwrite(npcase.data(), 4, N, o);
+    for (int l = 0; l < 4; ++l) fwrite(lev[l].data(), 1, lev[l].size(), o);
     fclose(o);
     printf("compat_driver ok N=%d T=%d\n", N, T);
     return 0;

@@ -5,6 +5,7 @@ import ctypes
 import os
 import subprocess
 
+import numpy as np
 import pytest
 
 import rfxprox as R
@@ -187,3 +188,17 @@ def test_upper_work_items_at_large_sizes():
         if i >= 0:
             assert 0 <= i <= lo < n and (lo - i) % s == 0 and e % 8 == i % 8
     assert L.rfxp_upper_work_item(n, s, 7, 3, 0, None, None) == -1
+
+
+def test_outlier_normalize_host_matches_oracle():
+    """rfxp_outlier_normalize is host-only: it runs without a device."""
+    import oracle as O
+
+    rng = np.random.default_rng(3)
+    raw = rng.gamma(2.0, 3.0, 1001).astype(np.float32)
+    cls = rng.integers(0, 4, 1001).astype(np.int32)
+    for c in (None, cls):
+        got, med, mad = R.outlier_normalize(raw, c)
+        assert np.array_equal(got, O.outlier_normalize(raw, c))
+    got, med, mad = R.outlier_normalize(np.array([5, 1, 3, 2, 4], np.float32))
+    assert med[0] == 3 and mad[0] == 1

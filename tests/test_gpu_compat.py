@@ -204,6 +204,10 @@ def test_reference_signatures_through_cpp_driver(tmp_path, cw):
     f16, i8, nf4 = take(ne, np.uint16), take(ne, np.int8), take((ne + 1) // 2, np.uint8)
     i8u, gap16 = take(ne, np.int8), take(ne, np.uint16)
     qs, sc = take(4, np.uint64), take(4, np.float32)
+    sym2 = F(take(nn, np.float64))
+    nterm = int(take(1, np.int32)[0])
+    nodexb, ndbegin, npcase = take(n, np.int32), take(nterm + 1, np.int32), take(n, np.int32)
+    lev = [F(take(nn, dt)) for dt in (np.float64, np.uint16, np.int8, np.uint8)]
     assert off == raw.size
     assert np.array_equal(prox, g[f"prox_cw{cw}"])
     assert np.array_equal(prox2, g[f"prox_cw{cw}"])
@@ -226,3 +230,13 @@ def test_reference_signatures_through_cpp_driver(tmp_path, cw):
     full = g[f"proxsym_cw{cw}"].astype(np.float32)
     s2 = (full.max() - full.min()) / np.float32(255.0)
     assert sc[2] == s2 and sc[3] == np.float32(-full.min() / s2)
+    # rf::gpu_finishprox = the fixture's proxsym (src/rf_finishprox.cpp:12-74)
+    assert np.array_equal(sym2, g[f"proxsym_cw{cw}"])
+    # the driver's terminal CSR is the reference's (src/rf_proximity.cpp:110-171)
+    assert np.array_equal(nodexb, O.terminal_leaf(ns[0], nx[0]))
+    assert ndbegin[0] == 0 and ndbegin[-1] == int((nodexb >= 0).sum())
+    for k in range(nterm):
+        assert np.array_equal(npcase[ndbegin[k]:ndbegin[k + 1]], np.flatnonzero(nodexb == k))
+    # QuantizationDispatcher::launch_proximity_kernel at the four levels
+    for level in range(4):
+        assert np.array_equal(lev[level], O.dispatch_prox(level, nodexb, nin[0], ndbegin, npcase)), level

@@ -117,3 +117,104 @@ def test_topk_rejects_bad_arguments(gpu_ctx):
     rc = L.rfxp_topk(gpu_ctx.h, host.ctypes.data_as(ctypes.c_void_p), 4, 1, 2, None, 0, -1, 4, 0,
                      out_i.data_ptr(), out_c.data_ptr())
     assert rc == 1  # host pointer
+
+
+def test_topk_scores_match_reference_formulas(gpu_ctx):
+    """OOB queries: (float)count * (1.0f/|OOB(q)|) exactly as O.topk_oob;
+    new queries: (float)count / (float)T."""
+    import torch
+
+    rng = np.random.default_rng(31)
+    n, t, nleaf, k = 1200, 45, 7, 9
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    oob[:, 11] = 0
+    gpu_ctx.set_reference(dev(leaf), n, t, nleaf)
+    words = R.pack_oob_bits(dev(oob).to(torch.bool))
+    idx, cnt = gpu_ctx.topk(dev(leaf), k, layout="tree", oob_words=words, exclude_base=0, positive_only=True)
+    sc = gpu_ctx.topk_scores(idx, cnt, t, oob_words=words).cpu().numpy()
+    for q in range(0, n, 7):
+        wi, wc, ws = O.topk_oob(leaf, oob, q, k)
+        m = len(wi)
+        assert np.array_equal(sc[q, :m], ws) and (sc[q, m:] == 0).all(), q
+    qs = rng.integers(0, nleaf, size=(50, t), dtype=np.int32)
+    idx, cnt = gpu_ctx.topk(dev(qs), k)
+    sc = gpu_ctx.topk_scores(idx, cnt, t).cpu().numpy()
+    c = cnt.cpu().numpy().view(np.uint16).astype(np.float32)
+    assert np.array_equal(sc, c / np.float32(t))
+
+
+def test_pair_proximity_matches_oracle(gpu_ctx):
+    import torch
+
+    rng = np.random.default_rng(32)
+    n, t, nleaf = 3000, 130, 9
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    leaf[rng.random((t, n)) < 0.05] = -1
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    oob[:, 17] = 0
+    words = R.pack_oob_bits(dev(oob).to(torch.bool))
+    pi = rng.integers(-2, n + 2, 700).astype(np.int64)
+    pj = rng.integers(-2, n + 2, 700).astype(np.int64)
+    pi[:5], pj[:5] = [17, 4, 9, 9, 0], [3, 4, 9, 17, n - 1]
+    for layout in ("tree", "sample"):
+        lf = leaf if layout == "tree" else np.ascontiguousarray(leaf.T)
+        got = gpu_ctx.pair_proximity(dev(lf), words, n, t, nleaf, dev(pi), dev(pj), layout=layout).cpu().numpy()
+        want = np.array([O.pair_proximity(leaf, oob, nleaf, a, b) for a, b in zip(pi, pj)], np.float32)
+        assert np.array_equal(got, want), layout
+
+
+@pytest.mark.parametrize("n,t,nleaf", [(2000, 100, 40), (70001, 12, 900)])
+def test_outlier_full_mode_matches_oracle(gpu_ctx, n, t, nleaf):
+    """Full mode: every training sample against the forest, itself excluded;
+    raw within 1e-6 relative (float terms, double sums in different order),
+    normalised scores by the host rule."""
+    rng = np.random.default_rng(n + t)
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    gpu_ctx.set_reference(dev(leaf), n, t, nleaf)
+    raw = gpu_ctx.outlier_raw(dev(leaf), layout="tree", exclude_base=0, numerator=float(n - 1),
+                              isolated=float(n) * 1e10).cpu().numpy()
+    sel = np.arange(n) if n <= 2000 else np.sort(rng.choice(n, 40, replace=False))
+    want = O.outlier_raw(leaf, nleaf, np.ascontiguousarray(leaf[:, sel].T), exclude=sel.astype(np.int32),
+                         numerator=float(n - 1), isolated=float(n) * 1e10)
+    assert np.allclose(raw[sel], want, rtol=1e-6, atol=0)
+    if n <= 2000:
+        cls = (np.arange(n) % 3).astype(np.int32)
+        for c in (None, cls):
+            sc, _, _ = R.outlier_normalize(raw, c)
+            assert np.allclose(sc, O.outlier_normalize(want, c), rtol=1e-5, atol=1e-5)
+
+
+def test_outlier_anchor_mode_matches_oracle(gpu_ctx):
+    rng = np.random.default_rng(33)
+    n, t, nleaf = 5000, 60, 25
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    anchors = np.sort(rng.choice(n, 300, replace=False)).astype(np.int64)
+    ex = np.full(n, -1, np.int32)
+    ex[anchors] = np.arange(len(anchors))
+    aleaf = np.ascontiguousarray(leaf[:, anchors])
+    gpu_ctx.set_reference(dev(aleaf), len(anchors), t, nleaf)
+    raw = gpu_ctx.outlier_raw(dev(leaf), layout="tree", exclude_idx=dev(ex), numerator=300.0,
+                              isolated=300.0 * 1e10).cpu().numpy()
+    want = O.outlier_raw(aleaf, nleaf, np.ascontiguousarray(leaf.T), exclude=ex, numerator=300.0,
+                         isolated=300.0 * 1e10)
+    assert np.allclose(raw, want, rtol=1e-6, atol=0)
+
+
+def test_outlier_c5_scale_sampled_queries(gpu_ctx):
+    """Full mode at the C5 reference size (N=1M, T=500, 2048 leaves) on a
+    few training samples; the oracle costs N*T compares per query."""
+    import torch
+
+    n, t, nleaf = 1_000_000, 500, 2048
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(20261201 + 50)
+    ref = torch.randint(0, nleaf, (t, n), generator=g, device="cuda:0", dtype=torch.int32)
+    sel = np.array([0, 1, 500_000, 999_999], np.int64)
+    gpu_ctx.set_reference(ref, n, t, nleaf)
+    qs = ref[:, torch.from_numpy(sel).to("cuda:0")].T.contiguous()
+    raw = gpu_ctx.outlier_raw(qs, exclude_idx=dev(sel.astype(np.int32)), numerator=float(n - 1),
+                              isolated=float(n) * 1e10).cpu().numpy()
+    want = O.outlier_raw(ref.cpu().numpy(), nleaf, qs.cpu().numpy(), exclude=sel.astype(np.int32),
+                         numerator=float(n - 1), isolated=float(n) * 1e10)
+    assert np.allclose(raw, want, rtol=1e-6, atol=0)

@@ -432,3 +432,117 @@ def test_rfgap_tree_upper_is_twice_single_tree_rfgap():
         got = tri_dense(O.rfgap_tree_upper(nin[k], nx[k]).view(np.float16).astype(np.float64), n)
         assert np.array_equal(got > 0, want > 0)
         assert np.abs(got - want).max() <= 2.0 ** -11 * max(want.max(), 1e-30)
+
+
+# ---- QuantizationDispatcher::launch_proximity_kernel ---------------------------
+
+def terminal_csr(ns, nx):
+    """ndbegin / npcase of the terminal ordinals (src/rf_proximity.cpp:110-171)."""
+    xb = O.terminal_leaf(ns, nx)
+    nterm = int((np.asarray(ns) == -1).sum())
+    cnt = np.bincount(xb[xb >= 0], minlength=nterm)
+    beg = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
+    pc = np.concatenate([np.flatnonzero(xb == k) for k in range(nterm)] + [np.zeros(0, np.int64)]).astype(np.int32)
+    return xb, beg, pc
+
+
+@pytest.mark.parametrize("seed", [4, 5])
+def test_dispatch_prox_levels(seed):
+    """FP32 level: rows of OOB samples equal the compiled reference's casewise
+    cpu_proximity (n <= kk); every entry equals a pair-by-pair brute force.
+    The other levels are the reference converters of the float weight."""
+    rng = np.random.default_rng(seed)
+    n, nnode = 97, 9
+    ns = np.where(rng.random(nnode) < 0.7, -1, 1).astype(np.int32)
+    nx = rng.integers(-1, nnode + 1, n).astype(np.int32)
+    nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+    xb, beg, pc = terminal_csr(ns, nx)
+    D = O.dispatch_prox(0, xb, nin, beg, pc)
+    size = np.array([nin[(xb == k) & (nin > 0)].sum() for k in range(len(beg) - 1)], np.int64)
+    want = np.zeros((n, n))
+    for a in range(n):
+        for b in range(a, n):
+            if xb[a] >= 0 and xb[a] == xb[b] and nin[b] > 0 and size[xb[a]] > 0:
+                want[a, b] = nin[b] / size[xb[a]]
+    assert np.array_equal(D, want)
+    if O.ref_available():
+        R = compiled_reference()
+        R.ref_set_config(1, 0, 2)
+        C = np.zeros((n, n), order="F")
+        R.ref_cpu_proximity(ns, nx, nin, n, nnode, C.reshape(-1, order="F"))
+        oob = nin == 0
+        up = np.triu(np.ones((n, n), bool))
+        assert np.array_equal(D[oob][up[oob]], C[oob][up[oob]])
+        assert C[oob].any()
+    hit = want > 0
+    w32 = (np.float32(1) * nin[None, :].repeat(n, 0)).astype(np.float32)
+    w32 = np.where(hit, w32 / np.where(xb >= 0, size[xb], 1).astype(np.float32)[:, None], np.float32(0))
+    f16 = O.dispatch_prox(1, xb, nin, beg, pc)
+    assert np.array_equal(f16, np.where(hit, w32.astype(np.float16).view(np.uint16), 0))
+    i8 = O.dispatch_prox(2, xb, nin, beg, pc)
+    q = np.clip(w32 / np.float32(1.0 / 127.0), -128, 127).astype(np.int8)
+    assert np.array_equal(i8, np.where(hit, q, 0))
+    nf = O.dispatch_prox(3, xb, nin, beg, pc)
+    assert np.array_equal(nf, np.where(hit, np.minimum(7, np.floor(w32.astype(np.float64) * 7 + 0.5)), 0))
+
+
+# ---- pair proximity and outlier scores ---------------------------------------
+
+def test_pair_proximity_is_oob_match_fraction():
+    rng = np.random.default_rng(21)
+    n, t, nleaf = 120, 37, 5
+    leaf = rng.integers(-1, nleaf, (t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    oob[:, 3] = 0
+    for i, j in [(0, 1), (5, 5), (17, 90), (3, 4), (119, 0), (-1, 2), (2, 120)]:
+        got = O.pair_proximity(leaf, oob, nleaf, i, j)
+        if not (0 <= i < n and 0 <= j < n) or oob[:, i].sum() == 0:
+            assert got == 0.0
+            continue
+        m = int((oob[:, i].astype(bool) & (leaf[:, i] == leaf[:, j]) & (leaf[:, i] >= 0)).sum())
+        assert got == np.float32(m) / np.float32(oob[:, i].sum())
+
+
+def test_outlier_raw_equals_dense_cooccurrence():
+    """raw = numerator / sum_j (C_ij / T)^2 with C the all-trees co-occurrence
+    matrix taken as a dense one-hot product (an independent route)."""
+    rng = np.random.default_rng(22)
+    n, t, nleaf = 300, 23, 6
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    leaf[0, :40] = np.arange(40) % nleaf
+    C = np.zeros((n, n))
+    for k in range(t):
+        A = np.zeros((n, nleaf))
+        A[np.arange(n), leaf[k]] = 1
+        C += A @ A.T
+    np.fill_diagonal(C, 0)
+    p = (C.astype(np.float32) / np.float32(t))
+    s = (p.astype(np.float32) * p.astype(np.float32)).astype(np.float64).sum(axis=1).astype(np.float32)
+    want = np.float32(n - 1) / s
+    got = O.outlier_raw(leaf, nleaf, np.ascontiguousarray(leaf.T), exclude=np.arange(n, dtype=np.int32),
+                        numerator=float(n - 1), isolated=float(n) * 1e10)
+    assert np.allclose(got, want, rtol=1e-6, atol=0)
+    # anchors: a subset as the reference set, excluding a query's own anchor
+    anchors = np.array([3, 50, 77, 200], np.int32)
+    ex = np.full(n, -1, np.int32)
+    ex[anchors] = np.arange(len(anchors))
+    ga = O.outlier_raw(np.ascontiguousarray(leaf[:, anchors]), nleaf, np.ascontiguousarray(leaf.T), exclude=ex,
+                       numerator=4.0, isolated=4e10)
+    pa = p[:, anchors]
+    sa = (pa * pa).astype(np.float64).sum(axis=1).astype(np.float32)
+    wa = np.where(sa > np.float32(1e-10), np.float32(4.0) / np.maximum(sa, np.float32(1e-30)), np.float32(4e10))
+    assert np.allclose(ga, wa, rtol=1e-6, atol=0)
+
+
+def test_outlier_normalize_reference_median_rule():
+    """median = sorted[size/2] (upper median), MAD likewise, 1 below 1e-10."""
+    got = O.outlier_normalize(np.array([5, 1, 3, 2, 4], np.float32))
+    assert np.array_equal(got, np.array([2, -2, 0, -1, 1], np.float32))
+    got = O.outlier_normalize(np.array([1, 2, 3, 4], np.float32))           # median 3, MAD 1
+    assert np.array_equal(got, np.array([-2, -1, 0, 1], np.float32))
+    got = O.outlier_normalize(np.array([7, 7, 7, 9], np.float32))           # MAD 0 -> 1
+    assert np.array_equal(got, np.array([0, 0, 0, 2], np.float32))
+    raw = np.array([10, 1, 20, 2, 30, 3], np.float32)
+    cls = np.array([1, 0, 1, 0, 1, 0], np.int32)                            # medians 20 / 2, MADs 10 / 1
+    got = O.outlier_normalize(raw, cls)
+    assert np.array_equal(got, np.array([-1, -1, 0, 0, 1, 1], np.float32))
