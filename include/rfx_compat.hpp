@@ -5,6 +5,9 @@
 // rf_finishprox.hpp, rf_proximity_upper_triangle.hpp,
 // rf_quantization_kernels.hpp) links these definitions unchanged; this
 // header declares the same functions for code built without those headers.
+// The low-rank class (rf_proximity_lowrank.hpp) keeps its public interface
+// but not the reference's private members, so its callers compile against
+// this header; the helpers of rf_lowrank_helpers.hpp are declared here too.
 // The declarations follow the reference's (file:line at each group); the
 // definitions run on the GPU through the C ABI of rfx_prox.h.
 //
@@ -141,6 +144,80 @@ void gpu_proximity_upper_triangle(const integer_t* nodestatus, const integer_t* 
 // contributions as an FP16 triangle (host output).
 void gpu_proximity_rfgap_upper_triangle_fp16(const integer_t* nin_tree, const integer_t* nodextr_tree,
                                              integer_t nsample, __half* prox_upper_fp16);
+
+// include/rf_proximity_lowrank.hpp:27-433: the low-rank proximity object.
+// Public interface as the reference's; the private state is this build's.
+// Contributions (per-tree packed triangles in FP16 / INT8 / NF4, FP32 read
+// as FP16 as the reference does, or dense N x N doubles) are accumulated
+// exactly as a sparse symmetric matrix M on the device; the factor A (N x
+// rank, column-major double, B = A) is the rank-`rank` positive part of M
+// from block subspace iteration with power_iterations products
+// (rfxp_symacc_factor), computed when first needed after new
+// contributions.  With final_call, finalize_accumulation stores the factors
+// at the object's quantization level (FP16 / INT8 / NF4); get_factors then
+// returns their dequantised values, as the reference's does.
+class LowRankProximityMatrix {
+   public:
+    LowRankProximityMatrix(integer_t nsample, integer_t initial_rank = 100,
+                           QuantizationLevel quant_level = QuantizationLevel::FP16, integer_t max_rank = 1000,
+                           integer_t power_iterations = 30);
+    ~LowRankProximityMatrix();
+    LowRankProximityMatrix(const LowRankProximityMatrix&) = delete;
+    LowRankProximityMatrix& operator=(const LowRankProximityMatrix&) = delete;
+
+    // false when no HIP device can be used (the reference always says true)
+    bool initialize();
+    void add_tree_contribution(const dp_t* tree_proximity, integer_t nsample, bool use_incremental = false);
+    void add_tree_contribution_incremental(const dp_t* tree_proximity, integer_t nsample);
+    void add_tree_contribution_incremental_upper_triangle(const void* tree_proximity_upper, integer_t nsample,
+                                                          QuantizationLevel quant_level,
+                                                          float int8_scale = 1.0f / 127.0f,
+                                                          float int8_zero_point = 0.0f);
+    void add_tree_contribution_incremental_upper_triangle_fp16(const __half* tree_proximity_upper_fp16,
+                                                               integer_t nsample);
+    void finalize_accumulation(integer_t n_trees_processed = 0, bool final_call = false);
+    void get_accumulated_proximity(dp_t* output_prox, integer_t nsample);
+    void reconstruct_full_matrix(dp_t* output_prox, integer_t nsample,
+                                 QuantizationLevel quant_level = QuantizationLevel::FP32);
+    void quantize_factors(QuantizationLevel quant_level);
+    void dequantize_factors();
+    bool is_quantized() const { return current_quant_level_ != QuantizationLevel::FP32; }
+    QuantizationLevel get_quantization_level() const { return current_quant_level_; }
+    void get_factors(dp_t** A_gpu, dp_t** B_gpu, integer_t* rank);
+    void compute_distances_from_factors(dp_t* output_distances, integer_t nsample);
+    void set_oob_counts_for_rfgap(const integer_t* oob_counts);
+    std::vector<double> compute_mds_from_factors(integer_t k = 3);
+    std::vector<double> compute_mds_3d_from_factors() { return compute_mds_from_factors(3); }
+    integer_t auto_adjust_rank(double target_variance = 0.95);
+    size_t get_memory_usage() const;
+    size_t get_memory_usage(QuantizationLevel quant_level) const;
+    static bool should_use_incremental(integer_t nsample, size_t available_memory = 0);
+
+    struct State;  // opaque: the library's device state of the object
+
+   private:
+    State* st_;
+    integer_t nsample_;
+    integer_t rank_;
+    integer_t max_rank_;
+    integer_t power_iterations_;
+    QuantizationLevel current_quant_level_;
+};
+
+// include/rf_proximity_lowrank.hpp:433: min(max_rank, floor(sqrt(nsample))), at least 1
+integer_t estimate_optimal_rank(integer_t nsample, integer_t max_rank = 1000);
+
+// include/rf_lowrank_helpers.hpp:13-34 (lowrank_proximity_ptr is a
+// LowRankProximityMatrix*): host copies of the factors (new[], the caller
+// deletes), MDS coordinates (empty on failure), and the reconstructed
+// N x N matrix (new[], refused above 50000 samples).
+bool get_lowrank_factors_host(void* lowrank_proximity_ptr, dp_t** A_host, dp_t** B_host, integer_t* rank,
+                              integer_t nsamples);
+std::vector<double> compute_mds_from_factors_host(void* lowrank_proximity_ptr, integer_t k);
+inline std::vector<double> compute_mds_3d_from_factors_host(void* lowrank_proximity_ptr) {
+    return compute_mds_from_factors_host(lowrank_proximity_ptr, 3);
+}
+bool reconstruct_proximity_matrix_host(void* lowrank_proximity_ptr, dp_t** output_prox, integer_t nsamples);
 
 }  // namespace cuda
 }  // namespace rf

@@ -252,6 +252,73 @@ int rfxp_lowrank_pv(rfxp_ctx* ctx, const float* V, int32_t r, float* Y);
  * Synchronises the context stream. */
 int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, int32_t iters, float* Q, double* B);
 
+/* ---- accumulated symmetric proximity and its factor ----------------------
+ * The engine of the reference's LowRankProximityMatrix class
+ * (include/rf_proximity_lowrank.hpp:27-433, rf_lowrank_helpers.hpp:13-34),
+ * which is built on these calls in the same library.  The context holds one
+ * accumulator: M = sum of the symmetric contributions added since
+ * rfxp_symacc_reset, kept exactly as a sparse matrix in device memory. */
+
+/* Empties the accumulator and sets its order N (1 <= N < 2^31 - 1). */
+int rfxp_symacc_reset(rfxp_ctx* ctx, int64_t N);
+/* Number of stored entries (i <= j) so far; -1 for a NULL context. */
+int64_t rfxp_symacc_nnz(rfxp_ctx* ctx);
+/* Adds the symmetric matrix whose packed upper triangle (N(N+1)/2 entries,
+ * host or device) is `tri`, read as the reference's low-rank path reads
+ * per-tree triangles (cuda/rf_proximity_lowrank.cu:687-789):
+ *   RFXP_FMT_F16  IEEE half entries;
+ *   RFXP_FMT_F32  float entries;
+ *   RFXP_FMT_I8   half((q - zp) * scale) (int8_to_fp32, then FP16);
+ *   RFXP_FMT_NF4  half(nf4_to_fp32(nibble)), entry e in byte e/2 at bit (e%2)*4. */
+int rfxp_symacc_add_upper(rfxp_ctx* ctx, int fmt, const void* tri, float scale, float zp);
+/* Adds the symmetric matrix with upper triangle half((float)full[i*N + j])
+ * for i <= j from a dense N x N double (host or device), as
+ * add_tree_contribution_incremental reads it (:654-685). */
+int rfxp_symacc_add_dense(rfxp_ctx* ctx, const double* full);
+/* Y = M X for X, Y device N x b row-major doubles (b >= 1). */
+int rfxp_symacc_apply(rfxp_ctx* ctx, const double* X, int32_t b, double* Y);
+/* Rank-r factor of M: block subspace iteration (block b = 2r + 16, capped
+ * at N, room for the negative eigenvalues of an indefinite M among the
+ * largest magnitudes; random normal start from `seed`; `iters` products,
+ * each followed by CholeskyQR2 or, for a singular Gram matrix, SVQB), then
+ * Rayleigh-Ritz: A[:, c] = Q u_c sqrt(lambda_c) for the r largest Ritz
+ * values (descending), a zero column where lambda_c <= 0, so that A A^T is
+ * the rank-r positive part of M.  A: device N x r column-major double
+ * (the layout of LowRankProximityMatrix::get_factors); evals: host r
+ * doubles (the Ritz values) or NULL.  1 <= r <= min(N, 4096). */
+int rfxp_symacc_factor(rfxp_ctx* ctx, int32_t rank, int32_t iters, uint64_t seed, double* A, double* evals);
+
+/* P = A B^T (A, B device N x rank column-major) into the device column-major
+ * N x N `out`, as reconstruct_full_matrix forms it
+ * (cuda/rf_proximity_lowrank.cu:1274-1376): P_ii = 1; with oob_counts (host
+ * int32[N], RF-GAP) and w_i = 1/s_i where s_i > 0 (else 1): P_ii = w_i and,
+ * for i != j, 0.5 * (P_ij w_lo + P_ij w_hi), lo = min(i,j), hi = max(i,j). */
+int rfxp_factor_reconstruct(rfxp_ctx* ctx, const double* A, const double* B, int64_t N, int32_t rank,
+                            const int32_t* oob_counts, double* out);
+/* Classical MDS from a factor (compute_mds_from_factors, :1902-2498), never
+ * forming an N x N matrix: P = A A^T (RF-GAP counts: 0.5 (W P + P W),
+ * W = diag(w) as above), m = max_i P_ii (1 when below 1e-10),
+ * D = 1 - P/m, C = -1/2 J (D o D) J, J the centring matrix.  The k largest
+ * eigenpairs of C by block subspace iteration with Rayleigh-Ritz (block
+ * k + 4, at most `iters` products, stopping when the Ritz values settle to
+ * 1e-12 relative); coords (host, N x k row-major) = v_c sqrt(|lambda_c|) in
+ * descending eigenvalue order; evals (host k) or NULL. */
+int rfxp_factor_mds(rfxp_ctx* ctx, const double* A, int64_t N, int32_t rank, int32_t k, const int32_t* oob_counts,
+                    int32_t iters, double* coords, double* evals);
+/* Factor storage of the reference's quantize_factors / dequantize_factors
+ * (:242-400, :1379-1718): F32 and F16 as IEEE halves, I8 as
+ * fp32_to_int8((float)a, scale, zp) with (scale, zp) in device memory
+ * (scale_zp[0], scale_zp[1]), NF4 two per byte (element e in byte e/2, bits
+ * (e%2)*4).  Bytes of `count` quantized elements, or -1. */
+int64_t rfxp_factor_quantized_bytes(int level, int64_t count);
+int rfxp_factor_quantize(rfxp_ctx* ctx, int level, const double* A, int64_t count, const float* scale_zp, void* q);
+int rfxp_factor_dequantize(rfxp_ctx* ctx, int level, const void* q, int64_t count, const float* scale_zp, double* A);
+
+/* Host only: eigenvalues (descending) and, when v is not NULL, eigenvectors
+ * (columns of the row-major n x n v) of the symmetric row-major n x n `a`
+ * by cyclic Jacobi rotations; the b x b eigensolver of the calls above. */
+int rfxp_host_symeig(int32_t n, const double* a, double* w, double* v);
+
 /* ---- per-tree and dense small-N operations -------------------------------
  * A tree is (nodestatus[nnode], nodextr[N], nin[N]): sample n lies in node
  * nodextr[n], which takes part when nodestatus of it is -1 (terminal);

@@ -64,6 +64,16 @@ bool ok(const char* fn, rfxp_ctx* ctx, int rc) {
 
 }  // namespace
 
+namespace rfxp {
+// Failure reporting of the reference-signature layer, for the other
+// translation units that implement part of it (rfxp_lrclass.hip).
+void compat_report(const char* fn, rfxp_ctx* ctx, int rc) { report(fn, ctx, rc); }
+void compat_report_msg(const char* fn, const char* msg) {
+    t_last_error = std::string(fn) + ": " + msg;
+    fprintf(stderr, "[rfxprox] %s\n", t_last_error.c_str());
+}
+}  // namespace rfxp
+
 extern "C" void rfx_compat_configure(int use_casewise, int32_t n_real_samples) {
     g_compat.use_casewise = use_casewise ? 1 : 0;
     g_compat.n_real = n_real_samples > 0 ? n_real_samples : 0;
@@ -145,8 +155,11 @@ static void tree_upper(const char* fn, int fmt, const integer_t* nodestatus, con
                        const integer_t* nin, integer_t nsample, integer_t nnode, float scale, float zp, void* out) {
     rfxp_ctx* ctx = compat_ctx(fn);
     if (!ctx) return;
-    ok(fn, ctx, rfxp_tree_upper(ctx, fmt, nodestatus, nodextr, nin, nsample, nnode, g_compat.use_casewise,
-                                g_compat.n_real, scale, zp, out));
+    // complete on return, as the reference's device synchronisation makes
+    // it (cuda/rf_proximity_upper_triangle.cu uses cudaDeviceSynchronize)
+    if (ok(fn, ctx, rfxp_tree_upper(ctx, fmt, nodestatus, nodextr, nin, nsample, nnode, g_compat.use_casewise,
+                                    g_compat.n_real, scale, zp, out)))
+        ok(fn, ctx, rfxp_sync(ctx));
 }
 
 void gpu_proximity_upper_triangle_fp16(const integer_t* nodestatus, const integer_t* nodextr, const integer_t* nin,
@@ -204,8 +217,9 @@ void gpu_proximity_rfgap_upper_triangle_fp16(const integer_t* nin_tree, const in
     const char* fn = "rf::cuda::gpu_proximity_rfgap_upper_triangle_fp16";
     rfxp_ctx* ctx = compat_ctx(fn);
     if (!ctx) return;
-    ok(fn, ctx, rfxp_rfgap_tree_upper(ctx, nin_tree, nodextr_tree, nsample, g_compat.n_real,
-                                      (uint16_t*)prox_upper_fp16));
+    if (ok(fn, ctx, rfxp_rfgap_tree_upper(ctx, nin_tree, nodextr_tree, nsample, g_compat.n_real,
+                                          (uint16_t*)prox_upper_fp16)))
+        ok(fn, ctx, rfxp_sync(ctx));
 }
 
 // ---- quantization utilities (cuda/rf_quantization_kernels.cu:24-406) ------

@@ -171,6 +171,14 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->tr_out.release();
     ctx->dn_prox.release();
     ctx->dn_out.release();
+    for (auto* b : {&ctx->sa_i, &ctx->sa_j, &ctx->sa_col, &ctx->sa_sv}) b->release();
+    ctx->sa_v.release();
+    ctx->sa_val.release();
+    ctx->sa_cnt.release();
+    ctx->sa_rowptr.release();
+    ctx->sa_deg.release();
+    for (auto* b : {&ctx->sa_stage, &ctx->sa_x, &ctx->sa_y, &ctx->sa_z, &ctx->sa_part, &ctx->sa_g, &ctx->sa_w, &ctx->sa_wv})
+        b->release();
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();
     delete ctx;

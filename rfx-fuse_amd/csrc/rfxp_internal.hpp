@@ -122,6 +122,15 @@ struct rfxp_ctx {
     DevBuf<double> dn_prox, dn_out;
     DevBuf<int32_t> dn_nout;
 
+    // symmetric accumulator of the low-rank class (rfxp_symacc_*)
+    int64_t sa_N = 0, sa_nnz = 0;
+    bool sa_csr_ok = false;
+    DevBuf<int32_t> sa_i, sa_j, sa_col, sa_sv;  // COO rows / cols, CSR columns, RF-GAP counts
+    DevBuf<float> sa_v, sa_val;                  // COO / CSR values
+    DevBuf<int64_t> sa_cnt, sa_rowptr;
+    DevBuf<unsigned long long> sa_deg;
+    DevBuf<double> sa_stage, sa_x, sa_y, sa_z, sa_part, sa_g, sa_w, sa_wv;
+
     // timing
     bool timing = false;
     std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> pending;
@@ -146,6 +155,10 @@ int check_launch(rfxp_ctx* ctx, const char* what);
 // (current), taken once per device (rfxp_noalloc.hip).
 void noalloc_setup(int device);
 bool is_device_pointer(const void* p);
+// Failure reporting of the reference-signature layer (rfxp_compat.hip): one
+// stderr line, readable through rfx_compat_last_error().
+void compat_report(const char* fn, rfxp_ctx* ctx, int rc);
+void compat_report_msg(const char* fn, const char* msg);
 
 }  // namespace rfxp
 

@@ -82,6 +82,20 @@ def load(path: str = LIB_PATH):
     L.rfxp_pair_proximity.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, vp, i64, vp]
     L.rfxp_outlier_raw.argtypes = [vp, vp, i64, i64, i64, i64, vp, C.c_float, C.c_float, vp]
     L.rfxp_outlier_normalize.argtypes = [vp, i64, vp, vp, vp, vp]
+    L.rfxp_symacc_reset.argtypes = [vp, i64]
+    L.rfxp_symacc_nnz.argtypes = [vp]
+    L.rfxp_symacc_nnz.restype = i64
+    L.rfxp_symacc_add_upper.argtypes = [vp, C.c_int, vp, C.c_float, C.c_float]
+    L.rfxp_symacc_add_dense.argtypes = [vp, vp]
+    L.rfxp_symacc_apply.argtypes = [vp, vp, i32, vp]
+    L.rfxp_symacc_factor.argtypes = [vp, i32, i32, C.c_uint64, vp, vp]
+    L.rfxp_factor_reconstruct.argtypes = [vp, vp, vp, i64, i32, vp, vp]
+    L.rfxp_factor_mds.argtypes = [vp, vp, i64, i32, i32, vp, i32, vp, vp]
+    L.rfxp_factor_quantized_bytes.argtypes = [C.c_int, i64]
+    L.rfxp_factor_quantized_bytes.restype = i64
+    L.rfxp_factor_quantize.argtypes = [vp, C.c_int, vp, i64, vp, vp]
+    L.rfxp_factor_dequantize.argtypes = [vp, C.c_int, vp, i64, vp, vp]
+    L.rfxp_host_symeig.argtypes = [i32, vp, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
     L.rfxp_lowrank_subspace.argtypes = [vp, vp, i32, i32, vp, vp]
     L.rfxp_tree_pairs.argtypes = [vp, vp, vp, vp, i32, i32, C.c_int, C.POINTER(C.POINTER(i64)),
@@ -317,6 +331,81 @@ class Context:
         self._check(self._L.rfxp_outlier_raw(self.h, qleaf.data_ptr(), si, st, q, exclude_base, ex,
                                              numerator, isolated, raw.data_ptr()))
         return raw
+
+    # ---- accumulated symmetric matrix and its factor (low-rank class engine)
+
+    def symacc_reset(self, n: int):
+        self._check(self._L.rfxp_symacc_reset(self.h, n))
+
+    def symacc_nnz(self) -> int:
+        return self._L.rfxp_symacc_nnz(self.h)
+
+    def symacc_add_upper(self, fmt: int, tri, scale: float = 1.0, zp: float = 0.0):
+        """tri: a device tensor or a host numpy array (packed triangle)."""
+        ptr = tri.data_ptr() if hasattr(tri, "data_ptr") else tri.ctypes.data
+        self._check(self._L.rfxp_symacc_add_upper(self.h, fmt, ptr, scale, zp))
+
+    def symacc_add_dense(self, full):
+        ptr = full.data_ptr() if hasattr(full, "data_ptr") else full.ctypes.data
+        self._check(self._L.rfxp_symacc_add_dense(self.h, ptr))
+
+    def symacc_apply(self, X):
+        import torch
+
+        assert X.dtype == torch.float64 and X.is_cuda and X.is_contiguous()
+        Y = torch.empty_like(X)
+        self._check(self._L.rfxp_symacc_apply(self.h, X.data_ptr(), X.shape[1], Y.data_ptr()))
+        return Y
+
+    def symacc_factor(self, n: int, rank: int, iters: int, seed: int = 1):
+        """(A device (rank, n) tensor holding the column-major N x rank factor, Ritz values)."""
+        import numpy as np
+        import torch
+
+        A = torch.empty((rank, n), dtype=torch.float64, device="cuda:0")
+        ev = np.empty(rank)
+        self._check(self._L.rfxp_symacc_factor(self.h, rank, iters, seed, A.data_ptr(), ev.ctypes.data))
+        return A, ev
+
+    def factor_reconstruct(self, A_cm, n: int, rank: int, oob_counts=None):
+        """A_cm: device (rank, n) float64 (column-major N x rank); returns the
+        device (n, n) tensor holding the column-major reconstruction."""
+        import numpy as np
+        import torch
+
+        out = torch.empty((n, n), dtype=torch.float64, device="cuda:0")
+        cnt = None if oob_counts is None else np.ascontiguousarray(oob_counts, dtype=np.int32)
+        self._check(self._L.rfxp_factor_reconstruct(self.h, A_cm.data_ptr(), A_cm.data_ptr(), n, rank,
+                                                    None if cnt is None else cnt.ctypes.data, out.data_ptr()))
+        return out
+
+    def factor_mds(self, A_cm, n: int, rank: int, k: int, oob_counts=None, iters: int = 100):
+        import numpy as np
+
+        cnt = None if oob_counts is None else np.ascontiguousarray(oob_counts, dtype=np.int32)
+        coords = np.empty((n, k))
+        ev = np.empty(k)
+        self._check(self._L.rfxp_factor_mds(self.h, A_cm.data_ptr(), n, rank, k,
+                                            None if cnt is None else cnt.ctypes.data, iters, coords.ctypes.data,
+                                            ev.ctypes.data))
+        return coords, ev
+
+    def factor_quantize(self, level: int, A, scale_zp=None):
+        import torch
+
+        nb = self._L.rfxp_factor_quantized_bytes(level, A.numel())
+        q = torch.empty(max(nb, 1), dtype=torch.uint8, device=A.device)
+        self._check(self._L.rfxp_factor_quantize(self.h, level, A.data_ptr(), A.numel(),
+                                                 None if scale_zp is None else scale_zp.data_ptr(), q.data_ptr()))
+        return q
+
+    def factor_dequantize(self, level: int, q, count: int, scale_zp=None):
+        import torch
+
+        A = torch.empty(count, dtype=torch.float64, device=q.device)
+        self._check(self._L.rfxp_factor_dequantize(self.h, level, q.data_ptr(), count,
+                                                   None if scale_zp is None else scale_zp.data_ptr(), A.data_ptr()))
+        return A
 
     def lowrank_pv(self, V):
         """Y = P V for the reference set (P = A A^T / T): V float32 device

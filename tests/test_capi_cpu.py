@@ -202,3 +202,32 @@ def test_outlier_normalize_host_matches_oracle():
         assert np.array_equal(got, O.outlier_normalize(raw, c))
     got, med, mad = R.outlier_normalize(np.array([5, 1, 3, 2, 4], np.float32))
     assert med[0] == 3 and mad[0] == 1
+
+
+@pytest.mark.parametrize("n,seed", [(1, 0), (7, 1), (40, 2), (130, 3)])
+def test_host_symeig_matches_numpy(n, seed):
+    """The host eigensolver of the factor and MDS paths (cyclic Jacobi)
+    against numpy.linalg.eigh, including repeated eigenvalues."""
+    import ctypes as C
+
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((n, n))
+    a = a + a.T
+    if n >= 7:  # a repeated eigenvalue and a zero one
+        q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+        lam = rng.standard_normal(n)
+        lam[1] = lam[0]
+        lam[2] = 0.0
+        a = (q * lam) @ q.T
+        a = 0.5 * (a + a.T)
+    L = R.load()
+    L.rfxp_host_symeig.argtypes = [C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]
+    A = np.ascontiguousarray(a)
+    w = np.empty(n)
+    v = np.empty((n, n))
+    assert L.rfxp_host_symeig(n, A.ctypes.data, w.ctypes.data, v.ctypes.data) == 0
+    want = np.sort(np.linalg.eigvalsh(a))[::-1]
+    scale = max(1.0, np.abs(want).max())
+    assert np.allclose(w, want, rtol=0, atol=1e-12 * scale)
+    assert np.allclose(v.T @ v, np.eye(n), atol=1e-12)
+    assert np.allclose(a @ v, v * w, atol=1e-11 * scale)

@@ -1,0 +1,356 @@
+"""GPU checks of the engine behind the LowRankProximityMatrix surface
+(rfxp_symacc_*, rfxp_factor_*): the accumulated matrix against the dense
+sum of the same contributions, the factor against numpy's eigendecomposition
+(numpy.linalg.eigh is the library routine the factor reduces to), the
+reconstruction and MDS against their dense numpy definitions, and the factor
+storage formats against the reference converters' formulas."""
+import numpy as np
+import pytest
+
+import oracle as O
+import rfxprox as R
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def sym_from_upper(vals, n):
+    d = np.zeros((n, n))
+    d[np.triu_indices(n)] = vals
+    return d + np.triu(d, 1).T
+
+
+def i8_values(q, scale, zp):
+    # int8_to_fp32 then FP16 (cuda/rf_proximity_lowrank.cu:199-211)
+    v = (q.astype(np.float32) - np.float32(zp)) * np.float32(scale)
+    return v.astype(np.float16).astype(np.float64)
+
+
+def nf4_values(packed, ne):
+    nib = np.stack([packed & 15, packed >> 4], axis=1).ravel()[:ne].astype(np.int64)
+    v = np.where(nib <= 7, nib.astype(np.float32) / np.float32(7), -(nib - 8).astype(np.float32) / np.float32(7))
+    return v.astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def positive_part(M, r):
+    w, V = np.linalg.eigh(M)
+    idx = np.argsort(w)[::-1][:r]
+    w, V = w[idx], V[:, idx]
+    w = np.maximum(w, 0.0)
+    return (V * w) @ V.T, w
+
+
+def random_forest_trees(rng, n, t, nnode=9):
+    out = []
+    for _ in range(t):
+        ns = np.where(rng.random(nnode) < 0.75, -1, 1).astype(np.int32)
+        nx = rng.integers(0, nnode, n).astype(np.int32)
+        nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+        out.append((ns, nx, nin))
+    return out
+
+
+def test_symacc_apply_matches_dense_sum(gpu_ctx):
+    rng = np.random.default_rng(41)
+    n = 257
+    ne = n * (n + 1) // 2
+    gpu_ctx.symacc_reset(n)
+    M = np.zeros((n, n))
+    nnz = 0
+    for k, (ns, nx, nin) in enumerate(random_forest_trees(rng, n, 3)):
+        tri = O.tree_upper(O.FMT_F16, ns, nx, nin)
+        gpu_ctx.symacc_add_upper(O.FMT_F16, tri if k % 2 else dev(tri))  # host and device inputs
+        v = tri.view(np.float16).astype(np.float64)
+        M += sym_from_upper(v, n)
+        nnz += int((v != 0).sum())
+    q8 = rng.integers(-128, 128, ne).astype(np.int8)
+    q8[rng.random(ne) < 0.5] = 3                      # (3 - 3) * s = 0: not stored
+    gpu_ctx.symacc_add_upper(O.FMT_I8, dev(q8), 0.01, 3.0)
+    v = i8_values(q8, 0.01, 3.0)
+    M += sym_from_upper(v, n)
+    nnz += int((v != 0).sum())
+    p4 = rng.integers(0, 256, (ne + 1) // 2).astype(np.uint8)
+    gpu_ctx.symacc_add_upper(O.FMT_NF4, p4)
+    v = nf4_values(p4, ne)
+    M += sym_from_upper(v, n)
+    nnz += int((v != 0).sum())
+    f32 = rng.standard_normal(ne).astype(np.float32)
+    f32[rng.random(ne) < 0.3] = 0
+    gpu_ctx.symacc_add_upper(O.FMT_F32, dev(f32))
+    M += sym_from_upper(f32.astype(np.float64), n)
+    nnz += int((f32 != 0).sum())
+    full = rng.standard_normal((n, n))                 # not symmetric: only i <= j is read
+    gpu_ctx.symacc_add_dense(full)
+    v = full[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64)
+    M += sym_from_upper(v, n)
+    nnz += int((v != 0).sum())
+    assert gpu_ctx.symacc_nnz() == nnz
+    X = rng.standard_normal((n, 70))
+    got = gpu_ctx.symacc_apply(dev(X)).cpu().numpy()
+    want = M @ X
+    assert np.abs(got - want).max() <= 1e-12 * np.abs(M).sum(axis=1).max() * np.abs(X).max()
+
+
+def test_symacc_factor_full_rank_is_positive_part(gpu_ctx):
+    rng = np.random.default_rng(42)
+    n = 60
+    S = rng.standard_normal((n, n))
+    gpu_ctx.symacc_reset(n)
+    gpu_ctx.symacc_add_dense(S)
+    M = sym_from_upper(S[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64), n)
+    A, ev = gpu_ctx.symacc_factor(n, n, 3)
+    A = A.cpu().numpy().T                              # N x r
+    want, w = positive_part(M, n)
+    assert np.linalg.norm(A @ A.T - want) <= 1e-9 * np.linalg.norm(want)
+    assert np.allclose(np.maximum(ev, 0), w, atol=1e-9 * np.abs(w).max())
+
+
+def test_symacc_factor_planted_spectrum(gpu_ctx):
+    """Top-6 positive part of a matrix with planted eigenvalues (negative
+    ones of larger magnitude included) within 1e-4 relative Frobenius."""
+    rng = np.random.default_rng(43)
+    n, r = 400, 6
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    lam = np.concatenate([[40, 30, 22, 16, 12, 9], [-35, -30, -25], 1.5 * rng.standard_normal(n - 9)])
+    S = (Q * lam) @ Q.T
+    gpu_ctx.symacc_reset(n)
+    gpu_ctx.symacc_add_dense(S)
+    M = sym_from_upper(S[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64), n)
+    A, ev = gpu_ctx.symacc_factor(n, r, 30)
+    A = A.cpu().numpy().T
+    want, w = positive_part(M, r)
+    assert np.linalg.norm(A @ A.T - want) <= 1e-4 * np.linalg.norm(want)
+    assert np.allclose(ev, w, rtol=1e-6)
+
+
+def test_symacc_factor_near_optimal_on_forest_triangles(gpu_ctx):
+    """The reference fixture's 40 trees as per-tree FP16 triangles (the live
+    caller's input, cuda/rf_growtree.cu:5294-5308): rank 10 = sqrt(120)
+    from 30 products is within 1% of the best rank-10 positive part in
+    Frobenius error, and the Ritz values are the leading eigenvalues."""
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "cpu_prox_small.npz"))
+    ns, nx, nin = g["nodestatus"].astype(np.int32), g["nodextr"].astype(np.int32), g["nin"].astype(np.int32)
+    t, n = nx.shape
+    gpu_ctx.symacc_reset(n)
+    M = np.zeros((n, n))
+    for k in range(t):
+        tri = O.tree_upper(O.FMT_F16, ns[k], nx[k], nin[k])
+        gpu_ctx.symacc_add_upper(O.FMT_F16, dev(tri))
+        M += sym_from_upper(tri.view(np.float16).astype(np.float64), n)
+    r = 10
+    A, ev = gpu_ctx.symacc_factor(n, r, 30)
+    A = A.cpu().numpy().T
+    best, w = positive_part(M, r)
+    assert np.linalg.norm(A @ A.T - M) <= 1.01 * np.linalg.norm(best - M)
+    assert abs(ev[0] - w[0]) <= 1e-8 * w[0]
+
+
+def test_reconstruct_matches_dense_definition(gpu_ctx):
+    rng = np.random.default_rng(44)
+    n, r = 150, 7
+    A = rng.standard_normal((n, r))
+    Acm = dev(np.ascontiguousarray(A.T))
+    P = A @ A.T
+    got = gpu_ctx.factor_reconstruct(Acm, n, r).cpu().numpy().T   # column-major -> (row, col)
+    want = P.copy()
+    np.fill_diagonal(want, 1.0)
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+    s = rng.integers(0, 5, n).astype(np.int32)                       # some zero counts
+    w = np.where(s > 0, 1.0 / np.maximum(s, 1), 1.0)
+    got = gpu_ctx.factor_reconstruct(Acm, n, r, oob_counts=s).cpu().numpy().T
+    lo = np.minimum.outer(np.arange(n), np.arange(n))
+    hi = np.maximum.outer(np.arange(n), np.arange(n))
+    want = 0.5 * (P * w[lo] + P * w[hi])
+    want[np.diag_indices(n)] = w
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+def dense_mds(P, k):
+    n = P.shape[0]
+    m = np.diag(P).max()
+    m = 1.0 if m < 1e-10 else m
+    D2 = (1.0 - P / m) ** 2
+    J = np.eye(n) - 1.0 / n
+    C = -0.5 * J @ D2 @ J
+    w, V = np.linalg.eigh(C)
+    idx = np.argsort(w)[::-1][:k]
+    return V[:, idx] * np.sqrt(np.abs(w[idx])), w[idx]
+
+
+@pytest.mark.parametrize("rfgap", [False, True])
+def test_mds_matches_dense_classical_mds(gpu_ctx, rfgap):
+    rng = np.random.default_rng(45 + rfgap)
+    n, r, k = 180, 5, 3
+    A = rng.standard_normal((n, r)) * np.array([3.0, 2.0, 1.2, 0.5, 0.2])
+    P = A @ A.T
+    s = None
+    if rfgap:
+        s = rng.integers(0, 6, n).astype(np.int32)
+        w = np.where(s > 0, 1.0 / np.maximum(s, 1), 1.0)
+        P = 0.5 * (w[:, None] * P + P * w[None, :])
+    coords, ev = gpu_ctx.factor_mds(dev(np.ascontiguousarray(A.T)), n, r, k, oob_counts=s, iters=300)
+    want, wv = dense_mds(P, k)
+    assert np.allclose(ev, wv, rtol=1e-8)
+    check_mds_consistent({"coords": coords}, P, k)
+    for c in range(k):   # distinct eigenvalues here: the columns themselves, up to sign
+        sg = np.sign(np.dot(coords[:, c], want[:, c]))
+        assert np.allclose(sg * coords[:, c], want[:, c], rtol=0, atol=1e-6 * np.abs(want[:, c]).max())
+
+
+def test_factor_storage_formats(gpu_ctx):
+    import torch
+
+    rng = np.random.default_rng(46)
+    a = rng.standard_normal(1001) * 0.7
+    A = dev(a)
+    q = gpu_ctx.factor_quantize(O.FMT_F16, A)
+    assert np.array_equal(q.cpu().numpy()[:2002].view(np.float16), a.astype(np.float32).astype(np.float16))
+    back = gpu_ctx.factor_dequantize(O.FMT_F16, q, a.size).cpu().numpy()
+    assert np.array_equal(back, a.astype(np.float32).astype(np.float16).astype(np.float64))
+    sz = torch.tensor([0.013, 5.0, 0.013, 5.0], dtype=torch.float32, device="cuda:0")
+    q = gpu_ctx.factor_quantize(O.FMT_I8, A, sz).cpu().numpy()[:a.size].view(np.int8)
+    want = np.clip(a.astype(np.float32) / np.float32(0.013) + np.float32(5.0), -128, 127).astype(np.int8)
+    assert np.array_equal(q, want)
+    back = gpu_ctx.factor_dequantize(O.FMT_I8, dev(q.view(np.uint8)), a.size, sz).cpu().numpy()
+    assert np.array_equal(back, ((want.astype(np.float32) - np.float32(5.0)) * np.float32(0.013)).astype(np.float64))
+    q = gpu_ctx.factor_quantize(O.FMT_NF4, A).cpu().numpy()[:(a.size + 1) // 2]
+    nib = np.stack([q & 15, q >> 4], axis=1).ravel()[:a.size]
+    # fp32_to_nf4 masked to its low nibble (cuda/rf_proximity_lowrank.cu:355-385)
+    assert all(nib[e] == (O.q_nf4(float(np.float32(a[e]))) & 15) for e in range(a.size))
+    assert (q[-1] >> 4) == 0                           # odd count: the last high nibble stays 0
+    back = gpu_ctx.factor_dequantize(O.FMT_NF4, dev(q), a.size).cpu().numpy()
+    ni = nib.astype(np.int64)
+    want = np.where(ni <= 7, ni.astype(np.float32) / np.float32(7), -(ni - 8).astype(np.float32) / np.float32(7))
+    assert np.array_equal(back, want.astype(np.float32).astype(np.float64))
+
+
+# ---- the class, called as RFX-Fuse calls it (tests/compat/lowrank_driver) ------
+
+LRDRIVER = __import__("os").path.join(__import__("os").path.dirname(__file__), "compat", "lowrank_driver")
+
+
+def run_lowrank_driver(tmp_path, mode, level):
+    import os
+    import subprocess
+
+    from test_gpu_compat import fixture, write_driver_input
+
+    assert os.path.exists(LRDRIVER), "tests/compat/lowrank_driver not built (make -C rfx-fuse_amd driver)"
+    ns, nx, nin, g = fixture()
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    write_driver_input(inp, ns, nx, nin, g["nout"], 0)
+    r = subprocess.run(["timeout", "-k", "10", "120", LRDRIVER, str(inp), str(outp), mode, str(level)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    raw = np.fromfile(outp, np.uint8)
+    n = nx.shape[1]
+    off = 0
+
+    def take(count, dt):
+        nonlocal off
+        nb = count * np.dtype(dt).itemsize
+        a = raw[off:off + nb].view(dt)
+        off += nb
+        return a
+
+    rank, isq, lev = (int(x) for x in take(3, np.int32))
+    A = take(n * rank, np.float64).reshape((rank, n)).T
+    B = take(n * rank, np.float64).reshape((rank, n)).T
+    nc = int(take(1, np.int64)[0])
+    coords = take(nc, np.float64).reshape((-1, 3))
+    rec = int(take(1, np.int32)[0])
+    P = take(n * n, np.float64).reshape((n, n)).T if rec else None
+    mem, inc, est, empty = take(4, np.uint64), take(2, np.int32), take(4, np.int32), take(2, np.int32)
+    assert off == raw.size
+    return dict(ns=ns, nx=nx, nin=nin, g=g, n=n, rank=rank, isq=isq, lev=lev, A=A, B=B, coords=coords, P=P,
+                mem=mem, inc=inc, est=est, empty=empty)
+
+
+def forest_sum(ns, nx, nin):
+    t, n = nx.shape
+    M = np.zeros((n, n))
+    for k in range(t):
+        M += sym_from_upper(O.tree_upper(O.FMT_F16, ns[k], nx[k], nin[k]).view(np.float16).astype(np.float64), n)
+    return M
+
+
+def mds_operator(P):
+    n = P.shape[0]
+    m = np.diag(P).max()
+    m = 1.0 if m < 1e-10 else m
+    J = np.eye(n) - 1.0 / n
+    return -0.5 * J @ ((1.0 - P / m) ** 2) @ J
+
+
+def check_mds_consistent(d, P, k=3):
+    """Column c of the coordinates is an eigenvector of the MDS operator
+    for its c-th largest eigenvalue, scaled to norm sqrt(lambda_c); this
+    holds whatever basis a repeated eigenvalue gets."""
+    C = mds_operator(P)
+    w = np.sort(np.linalg.eigvalsh(C))[::-1][:k]
+    X = d["coords"]
+    lam = (X * X).sum(axis=0)
+    assert np.allclose(lam, np.abs(w), rtol=1e-7)
+    scale = np.abs(C).sum(axis=1).max()
+    for c in range(k):
+        assert np.linalg.norm(C @ X[:, c] - w[c] * X[:, c]) <= 1e-6 * scale * np.linalg.norm(X[:, c])
+    G = X.T @ X
+    assert np.abs(G - np.diag(np.diag(G))).max() <= 1e-8 * lam.max()
+
+
+@pytest.mark.parametrize("level", [0, 1, 2, 3])
+def test_class_growtree_sequence(tmp_path, level):
+    d = run_lowrank_driver(tmp_path, "growtree", level)
+    n, r, A = d["n"], d["rank"], d["A"]
+    assert r == 10 == int(np.sqrt(n))                        # estimate_optimal_rank(120, 1000)
+    assert np.array_equal(A, d["B"])                         # B = A
+    assert d["isq"] == int(level != 0) and d["lev"] == level  # current level from the constructor
+    M = forest_sum(d["ns"], d["nx"], d["nin"])
+    best, _ = positive_part(M, r)
+    err = np.linalg.norm(A @ A.T - M)
+    if level == 0:                                           # FP64 factors
+        assert err <= 1.01 * np.linalg.norm(best - M)
+    elif level == 1:                                         # stored as FP16, returned dequantised
+        assert np.array_equal(A, A.astype(np.float32).astype(np.float16).astype(np.float64))
+        assert err <= 1.02 * np.linalg.norm(best - M)
+    elif level == 2:                                         # INT8 grid: at most 256 values
+        assert len(np.unique(A)) <= 256
+    else:                                                    # NF4: values q/7 and -q/7
+        grid = np.concatenate([np.arange(8) / 7.0, -np.arange(8) / 7.0]).astype(np.float32).astype(np.float64)
+        assert np.isin(A, grid).all()
+    Pw = A @ A.T
+    want = Pw.copy()
+    np.fill_diagonal(want, 1.0)
+    assert d["P"] is not None and np.allclose(d["P"], want, rtol=1e-13, atol=1e-13)
+    check_mds_consistent(d, Pw)
+    assert list(d["mem"]) == [2 * n * r * 2, 2 * n * r * 2, 2 * n * r * 1, 0]
+    assert list(d["inc"]) == [1, 0]
+    assert list(d["est"]) == [10, 5, 7, 100]
+    assert d["empty"][1] == 1 and d["empty"][0] == 10        # no factors before any contribution
+
+
+def test_class_rfgap_sequence(tmp_path):
+    d = run_lowrank_driver(tmp_path, "rfgap", 0)
+    n, r, A = d["n"], d["rank"], d["A"]
+    assert r == 8
+    g = d["g"]
+    rg = O.rfgap(d["nin"], d["nx"])
+    M = sym_from_upper(rg[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64), n)
+    best, _ = positive_part(M, r)
+    assert np.linalg.norm(A @ A.T - M) <= 1.01 * np.linalg.norm(best - M)
+    s = g["nout"].astype(np.int64)
+    w = np.where(s > 0, 1.0 / np.maximum(s, 1), 1.0)
+    Pw = A @ A.T
+    lo = np.minimum.outer(np.arange(n), np.arange(n))
+    hi = np.maximum.outer(np.arange(n), np.arange(n))
+    want = 0.5 * (Pw * w[lo] + Pw * w[hi])
+    want[np.diag_indices(n)] = w
+    assert np.allclose(d["P"], want, rtol=1e-13, atol=1e-15)
+    check_mds_consistent(d, 0.5 * (w[:, None] * Pw + Pw * w[None, :]))
