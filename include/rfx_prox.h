@@ -157,6 +157,41 @@ int rfxp_upper_noalloc(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int
  * bad arguments); nout_given: a caller nout is passed. */
 int64_t rfxp_upper_noalloc_workspace(int64_t N, int32_t T, int32_t nleaf, int nout_given);
 
+/* ---- leaf assignments (producer of the forest input) ---------------------- */
+
+#define RFXP_LEAVES_PREDICT 0 /* predict_leaf_assignments (src/rf_random_forest.cpp:4789-4852) */
+#define RFXP_LEAVES_TRAIN 1   /* training assignment (src/rf_random_forest.cpp:1581-1609) */
+
+/* Walks every sample through every tree (device arrays in RandomForest's
+ * layout, include/rf_random_forest.hpp: nodestatus / bestvar / xbestsplit
+ * [t*maxnode + k], treemap [t*maxnode*2 + 2k (+1)], catgoleft
+ * [t*maxnode*maxcat + k*maxcat + c], cat [mdim] or NULL for all-numeric
+ * features; X [n*mdim + v] float) and writes the node reached to
+ * leaf_out[t*N + n] (int32, tree-major: rfxp_set_forest's stride_i = 1,
+ * stride_t = N).
+ *   RFXP_LEAVES_PREDICT: predict_leaf_assignments' walk (cat == 1 numeric,
+ *     categories (int)(x + 0.5), a bad split variable or category leaves
+ *     the walk where it is, at most maxnode steps);
+ *   RFXP_LEAVES_TRAIN: with nin [t*N + n] (bootstrap counts), OOB samples
+ *     (nin == 0) by cpu_testreebag's walk (src/rf_testreebag.cpp:13-122:
+ *     split nodes only, cat <= 2 numeric, categories (int)x, invalid codes
+ *     right, the node if terminal or status 2 else 0) and in-bag samples
+ *     by find_terminal_node (src/rf_random_forest.cpp:3724-3774: node 0 on
+ *     a bad split variable or category); oob_words (optional, T x oob_ld
+ *     words) gets the OOB bits in rfxp_set_forest's layout.
+ * A child index outside [0, maxnode) ends a walk (predict and testreebag
+ * at the parent, find_terminal_node at 0); a category code at or above
+ * maxcat is invalid.  The reference keeps the node as int16; here it is
+ * int32.  terminal_only != 0 writes -1 where the node reached is not
+ * terminal (nodestatus != -1): those samples take no part in the proximity
+ * (src/rf_proximity.cpp:126-135), so the output feeds rfxp_set_forest with
+ * nleaf = maxnode directly. */
+int rfxp_forest_leaves(rfxp_ctx* ctx, int mode, const int32_t* nodestatus, const int32_t* bestvar,
+                       const float* xbestsplit, const int32_t* treemap, const int32_t* catgoleft, const int32_t* cat,
+                       int32_t T, int32_t maxnode, int32_t maxcat, int32_t mdim, const float* X, int64_t N,
+                       const int32_t* nin, int terminal_only, int32_t* leaf_out, uint32_t* oob_words,
+                       int64_t oob_ld);
+
 /* ---- top-K similarity retrieval ----------------------------------------- */
 
 /* Indexes a reference set (N samples x T trees of leaf labels, same layout

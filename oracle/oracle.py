@@ -90,6 +90,8 @@ def lib():
         L.orc_outlier_raw.argtypes = [_i32, C.c_int64, C.c_int32, C.c_int32, _i32, C.c_int64, C.c_void_p,
                                       C.c_float, C.c_float, _f32, C.c_int]
         L.orc_outlier_normalize.argtypes = [_f32, C.c_int64, C.c_void_p, _f32]
+        L.orc_forest_leaves.argtypes = [C.c_int, _i32, _i32, _f32, _i32, C.c_void_p, C.c_void_p, C.c_int32,
+                                        C.c_int32, C.c_int32, C.c_int32, _f32, C.c_int64, C.c_void_p, _i32]
         _lib = L
     return _lib
 
@@ -361,4 +363,28 @@ def outlier_normalize(raw, classes=None):
     out = np.empty_like(raw)
     cl = None if classes is None else _c(classes, np.int32)
     lib().orc_outlier_normalize(raw, len(raw), cl.ctypes.data if cl is not None else None, out)
+    return out
+
+
+# ---- leaf assignments on a forest ---------------------------------------------
+
+def forest_leaves(mode, forest, X, nin=None):
+    """forest: dict of nodestatus, bestvar, xbestsplit (T x maxnode), treemap
+    (T x maxnode x 2), catgoleft (T x maxnode x maxcat) or None, cat (mdim)
+    or None.  Returns leaf (T x N) int32."""
+    ns = _c(forest["nodestatus"], np.int32)
+    t, maxnode = ns.shape
+    X = _c(X, np.float32)
+    n, mdim = X.shape
+    cg = forest.get("catgoleft")
+    maxcat = 1 if cg is None else cg.shape[2]
+    cg = None if cg is None else _c(cg, np.int32)
+    cat = forest.get("cat")
+    cat = None if cat is None else _c(cat, np.int32)
+    ni = None if nin is None else _c(nin, np.int32)
+    out = np.empty((t, n), np.int32)
+    lib().orc_forest_leaves(mode, ns.ravel(), _c(forest["bestvar"], np.int32).ravel(),
+                            _c(forest["xbestsplit"], np.float32).ravel(), _c(forest["treemap"], np.int32).ravel(),
+                            None if cg is None else cg.ctypes.data, None if cat is None else cat.ctypes.data, t,
+                            maxnode, maxcat, mdim, X.ravel(), n, None if ni is None else ni.ctypes.data, out.ravel())
     return out

@@ -8,6 +8,7 @@
 //   rf::cpu_proximity        include/rf_proximity.hpp:10-14
 //   rf::cpu_proximity_rfgap  include/rf_proximity.hpp:34-38
 //   rf::cpu_finishprox       include/rf_finishprox.hpp:9
+//   rf::cpu_testreebag       include/rf_testreebag.hpp:9-15
 //   rf::g_config             include/rf_config.hpp:156 (fields use_casewise,
 //                            use_sparse, n_threads_cpu)
 #include <cstdint>
@@ -16,6 +17,7 @@
 #include "rf_config.hpp"
 #include "rf_finishprox.hpp"
 #include "rf_proximity.hpp"
+#include "rf_testreebag.hpp"
 
 extern "C" {
 
@@ -48,6 +50,15 @@ void ref_cpu_proximity_rfgap(int32_t ntree, int32_t nsample, const int32_t* nin_
         ndx[t].assign(nodextr_flat + (size_t)t * nsample, nodextr_flat + (size_t)(t + 1) * nsample);
     }
     rf::cpu_proximity_rfgap(ntree, nsample, nin, ndx, prox);
+}
+
+// One tree: nodextr of the OOB samples (0 for the others), x row-major N x mdim.
+void ref_cpu_testreebag(const float* x, const float* xbestsplit, const int32_t* nin, const int32_t* treemap,
+                        const int32_t* bestvar, const int32_t* cat, const int32_t* nodestatus, const int32_t* catgoleft,
+                        int32_t nsample, int32_t mdim, int32_t nnode, int32_t maxcat, int32_t* nodextr) {
+    std::vector<int32_t> nodeclass(nnode > 0 ? nnode : 1, 0), jtr(nsample > 0 ? nsample : 1);
+    rf::cpu_testreebag(x, xbestsplit, nin, treemap, bestvar, nodeclass.data(), cat, nodestatus, catgoleft, nsample,
+                       mdim, nnode, maxcat, jtr.data(), nodextr);
 }
 
 }  // extern "C"

@@ -775,3 +775,120 @@ void orc_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, 
     free(d);
     free(keys);
 }
+
+/* ------------------------------------------------------------------------ */
+/* f1: leaf assignments on a forest (tree walks)                             */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    const int32_t *ns, *bv, *tm, *cg, *cat;
+    const float* sp;
+    int32_t maxnode, maxcat, mdim;
+} orc_tree;
+
+/* (int)(f + 0.5) with f + 0.5 in double; values whose truncation leaves
+ * int32 give -1 (an invalid category) */
+static int32_t orc_round_cat(float f) {
+    const double d = (double)f + 0.5;
+    if (!(d > -2147483649.0 && d < 2147483648.0)) return -1;
+    return (int32_t)d;
+}
+static int32_t orc_trunc_cat(float f) {
+    if (!(f > -2147483649.0f && f < 2147483648.0f)) return -1;
+    return (int32_t)f;
+}
+static int orc_node_ok(const orc_tree* t, int32_t k) { return k >= 0 && k < t->maxnode; }
+
+/* predict_leaf_assignments, src/rf_random_forest.cpp:4800-4845 */
+static int32_t orc_walk_predict(const orc_tree* t, const float* x) {
+    int32_t cur = 0;
+    for (int32_t k = 0; k < t->maxnode; ++k) {
+        if (t->ns[cur] == -1) break;
+        const int32_t v = t->bv[cur];
+        int32_t nxt = cur;
+        if (v >= 0 && v < t->mdim) {
+            const float f = x[v];
+            const int32_t c = t->cat ? t->cat[v] : 1;
+            if (c == 1) {
+                nxt = f <= t->sp[cur] ? t->tm[2 * cur] : t->tm[2 * cur + 1];
+            } else {
+                const int32_t j = orc_round_cat(f);
+                if (j >= 0 && j < c && j < t->maxcat)
+                    nxt = t->cg[cur * t->maxcat + j] == 1 ? t->tm[2 * cur] : t->tm[2 * cur + 1];
+            }
+        }
+        if (!orc_node_ok(t, nxt)) break; /* a child outside the tree ends the walk */
+        cur = nxt;
+    }
+    return cur;
+}
+
+/* RandomForest::find_terminal_node, src/rf_random_forest.cpp:3724-3774 */
+static int32_t orc_walk_inbag(const orc_tree* t, const float* x) {
+    int32_t cur = 0;
+    for (int32_t k = 0; k < t->maxnode; ++k) {
+        if (t->ns[cur] == -1) return cur;
+        const int32_t v = t->bv[cur];
+        if (!(v >= 0 && v < t->mdim)) return 0;
+        const float f = x[v];
+        const int32_t c = t->cat ? t->cat[v] : 1;
+        int32_t nxt;
+        if (c == 1) {
+            nxt = f <= t->sp[cur] ? t->tm[2 * cur] : t->tm[2 * cur + 1];
+        } else {
+            const int32_t j = orc_round_cat(f);
+            if (!(j >= 0 && j < c && j < t->maxcat)) return 0;
+            nxt = t->cg[cur * t->maxcat + j] == 1 ? t->tm[2 * cur] : t->tm[2 * cur + 1];
+        }
+        if (!orc_node_ok(t, nxt)) return 0;
+        cur = nxt;
+    }
+    return 0;
+}
+
+/* cpu_testreebag's walk of an OOB sample, src/rf_testreebag.cpp:43-119 */
+static int32_t orc_walk_oob(const orc_tree* t, const float* x) {
+    int32_t kt = 0, count = 0;
+    while (t->ns[kt] == 1 && count < 1000) {
+        count++;
+        const int32_t mvar = t->bv[kt];
+        if (!(mvar >= 0 && mvar < t->mdim)) break; /* (the reference reads outside x here) */
+        int32_t nxt;
+        if (!t->cat || t->cat[mvar] <= 2) {
+            nxt = x[mvar] <= t->sp[kt] ? t->tm[2 * kt] : t->tm[2 * kt + 1];
+        } else {
+            const int32_t cv = orc_trunc_cat(x[mvar]);
+            if (cv >= 0 && cv < t->cat[mvar] && cv < t->maxcat)
+                nxt = t->cg[cv + kt * t->maxcat] == 1 ? t->tm[2 * kt] : t->tm[2 * kt + 1];
+            else nxt = t->tm[2 * kt + 1];
+        }
+        if (!orc_node_ok(t, nxt)) break;
+        kt = nxt;
+        if (t->ns[kt] != 1) break;
+    }
+    return (t->ns[kt] == -1 || t->ns[kt] == 2) ? kt : 0;
+}
+
+void orc_forest_leaves(int mode, const int32_t* nodestatus, const int32_t* bestvar, const float* xbestsplit,
+                       const int32_t* treemap, const int32_t* catgoleft, const int32_t* cat, int32_t T, int32_t maxnode,
+                       int32_t maxcat, int32_t mdim, const float* X, int64_t N, const int32_t* nin, int32_t* leaf_out) {
+#pragma omp parallel for schedule(static)
+    for (int32_t tr = 0; tr < T; ++tr) {
+        orc_tree t;
+        t.ns = nodestatus + (int64_t)tr * maxnode;
+        t.bv = bestvar + (int64_t)tr * maxnode;
+        t.sp = xbestsplit + (int64_t)tr * maxnode;
+        t.tm = treemap + (int64_t)tr * maxnode * 2;
+        t.cg = catgoleft ? catgoleft + (int64_t)tr * maxnode * maxcat : NULL;
+        t.cat = cat;
+        t.maxnode = maxnode;
+        t.maxcat = maxcat;
+        t.mdim = mdim;
+        for (int64_t n = 0; n < N; ++n) {
+            const float* x = X + n * mdim;
+            int32_t leaf;
+            if (mode == 0) leaf = orc_walk_predict(&t, x);
+            else leaf = nin[(int64_t)tr * N + n] == 0 ? orc_walk_oob(&t, x) : orc_walk_inbag(&t, x);
+            leaf_out[(int64_t)tr * N + n] = leaf;
+        }
+    }
+}

@@ -182,6 +182,24 @@ void orc_outlier_raw(const int32_t* ref_leaf, int64_t N, int32_t T, int32_t nlea
  * 1e-10), score = (raw - median) / MAD.  classes may be NULL. */
 void orc_outlier_normalize(const float* raw, int64_t N, const int32_t* classes, float* scores);
 
+/* ---- leaf assignments on a forest ------------------------------------------ */
+
+/* Per tree t (arrays of RandomForest, include/rf_random_forest.hpp: nodestatus
+ * / bestvar / xbestsplit [t*maxnode + k], treemap [t*maxnode*2 + 2k (+1)],
+ * catgoleft [t*maxnode*maxcat + k*maxcat + c], cat [mdim] or NULL = all
+ * numeric) and sample n (X[n*mdim + v]), the node leaf_out[t*N + n]:
+ *   mode 0: predict_leaf_assignments' walk (src/rf_random_forest.cpp:4800-4845);
+ *   mode 1: training assignment (:1581-1609): OOB samples (nin[t*N+n] == 0)
+ *           by cpu_testreebag's walk (src/rf_testreebag.cpp:43-119), in-bag
+ *           samples by find_terminal_node (src/rf_random_forest.cpp:3724-3774).
+ * A child index outside [0, maxnode) ends a walk (predict: at the parent;
+ * find_terminal_node: node 0; testreebag: at the parent); testreebag with a
+ * split variable outside [0, mdim) stops at that node; a category code at
+ * or above maxcat counts as invalid (cat <= maxcat in a well-formed forest). */
+void orc_forest_leaves(int mode, const int32_t* nodestatus, const int32_t* bestvar, const float* xbestsplit,
+                       const int32_t* treemap, const int32_t* catgoleft, const int32_t* cat, int32_t T, int32_t maxnode,
+                       int32_t maxcat, int32_t mdim, const float* X, int64_t N, const int32_t* nin, int32_t* leaf_out);
+
 #ifdef __cplusplus
 }
 #endif

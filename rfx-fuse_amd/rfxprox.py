@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(HERE, "lib", "librfxprox.so")
 REPO = os.path.dirname(HERE)
 HEADER = os.path.join(REPO, "include", "rfx_prox.h")
 
+LEAVES_PREDICT, LEAVES_TRAIN = 0, 1
 FMT_F32, FMT_F16, FMT_I8, FMT_NF4, FMT_U8, FMT_U16 = range(6)
 FMT_NAMES = {"f32": FMT_F32, "f16": FMT_F16, "i8": FMT_I8, "nf4": FMT_NF4, "u8": FMT_U8,
              "u16": FMT_U16}
@@ -82,6 +83,8 @@ def load(path: str = LIB_PATH):
     L.rfxp_pair_proximity.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, vp, i64, vp]
     L.rfxp_outlier_raw.argtypes = [vp, vp, i64, i64, i64, i64, vp, C.c_float, C.c_float, vp]
     L.rfxp_outlier_normalize.argtypes = [vp, i64, vp, vp, vp, vp]
+    L.rfxp_forest_leaves.argtypes = [vp, C.c_int, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i64, vp, C.c_int,
+                                     vp, vp, i64]
     L.rfxp_symacc_reset.argtypes = [vp, i64]
     L.rfxp_symacc_nnz.argtypes = [vp]
     L.rfxp_symacc_nnz.restype = i64
@@ -331,6 +334,29 @@ class Context:
         self._check(self._L.rfxp_outlier_raw(self.h, qleaf.data_ptr(), si, st, q, exclude_base, ex,
                                              numerator, isolated, raw.data_ptr()))
         return raw
+
+    def forest_leaves(self, mode: int, forest: dict, X, nin=None, terminal_only: bool = False, oob: bool = False):
+        """forest: dict of device tensors nodestatus, bestvar (int32), xbestsplit
+        (float32) (T, maxnode), treemap (T, maxnode, 2), optional catgoleft
+        (T, maxnode, maxcat) and cat (mdim,); X (N, mdim) float32 device.
+        Returns leaf (T, N) int32 and, with oob=True (training mode), the
+        OOB words (T, ceil(N/32)) int32."""
+        import torch
+
+        ns = forest["nodestatus"]
+        t, maxnode = ns.shape
+        n, mdim = X.shape
+        cg, cat = forest.get("catgoleft"), forest.get("cat")
+        maxcat = 1 if cg is None else cg.shape[2]
+        leaf = torch.empty((t, n), dtype=torch.int32, device=X.device)
+        words = torch.empty((t, (n + 31) // 32), dtype=torch.int32, device=X.device) if oob else None
+        self._check(self._L.rfxp_forest_leaves(
+            self.h, mode, ns.data_ptr(), forest["bestvar"].data_ptr(), forest["xbestsplit"].data_ptr(),
+            forest["treemap"].data_ptr(), None if cg is None else cg.data_ptr(),
+            None if cat is None else cat.data_ptr(), t, maxnode, maxcat, mdim, X.data_ptr(), n,
+            None if nin is None else nin.data_ptr(), int(terminal_only), leaf.data_ptr(),
+            None if words is None else words.data_ptr(), 0 if words is None else words.shape[1]))
+        return (leaf, words) if oob else leaf
 
     # ---- accumulated symmetric matrix and its factor (low-rank class engine)
 

@@ -231,3 +231,40 @@ def test_host_symeig_matches_numpy(n, seed):
     assert np.allclose(w, want, rtol=0, atol=1e-12 * scale)
     assert np.allclose(v.T @ v, np.eye(n), atol=1e-12)
     assert np.allclose(a @ v, v * w, atol=1e-11 * scale)
+
+
+def test_library_exports_lowrank_class_with_reference_signatures():
+    """include/rf_proximity_lowrank.hpp:27-433 and rf_lowrank_helpers.hpp:13-34:
+    every public member and helper, with the reference's parameter types."""
+    out = subprocess.run(["nm", "-DC", "--defined-only", R.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    C_ = "rf::cuda::LowRankProximityMatrix::"
+    want = [
+        C_ + "LowRankProximityMatrix(int, int, rf::cuda::QuantizationLevel, int, int)",
+        C_ + "~LowRankProximityMatrix()",
+        C_ + "initialize()",
+        C_ + "add_tree_contribution(double const*, int, bool)",
+        C_ + "add_tree_contribution_incremental(double const*, int)",
+        C_ + "add_tree_contribution_incremental_upper_triangle(void const*, int, rf::cuda::QuantizationLevel, "
+             "float, float)",
+        C_ + "add_tree_contribution_incremental_upper_triangle_fp16(__half const*, int)",
+        C_ + "finalize_accumulation(int, bool)",
+        C_ + "get_accumulated_proximity(double*, int)",
+        C_ + "reconstruct_full_matrix(double*, int, rf::cuda::QuantizationLevel)",
+        C_ + "quantize_factors(rf::cuda::QuantizationLevel)",
+        C_ + "dequantize_factors()",
+        C_ + "get_factors(double**, double**, int*)",
+        C_ + "compute_distances_from_factors(double*, int)",
+        C_ + "set_oob_counts_for_rfgap(int const*)",
+        C_ + "compute_mds_from_factors(int)",
+        C_ + "auto_adjust_rank(double)",
+        C_ + "get_memory_usage() const",
+        C_ + "get_memory_usage(rf::cuda::QuantizationLevel) const",
+        C_ + "should_use_incremental(int, unsigned long)",
+        "rf::cuda::estimate_optimal_rank(int, int)",
+        "rf::cuda::get_lowrank_factors_host(void*, double**, double**, int*, int)",
+        "rf::cuda::compute_mds_from_factors_host(void*, int)",
+        "rf::cuda::reconstruct_proximity_matrix_host(void*, double**, int)",
+    ]
+    for w in want:
+        assert w in out, w

@@ -6,6 +6,7 @@ checker of the HIP path:
   * against brute force and closed forms for what the reference leaves open
     (quantizers, top-K ordering, low rank)."""
 import hashlib
+import ctypes
 import os
 
 import numpy as np
@@ -546,3 +547,140 @@ def test_outlier_normalize_reference_median_rule():
     cls = np.array([1, 0, 1, 0, 1, 0], np.int32)                            # medians 20 / 2, MADs 10 / 1
     got = O.outlier_normalize(raw, cls)
     assert np.array_equal(got, np.array([-1, -1, 0, 0, 1, 1], np.float32))
+
+
+# ---- leaf assignments on a forest ---------------------------------------------
+
+def random_forest_arrays(rng, t, maxnode, cat, maxcat):
+    mdim = len(cat)
+    ns = -np.ones((t, maxnode), np.int32)
+    bv = np.zeros((t, maxnode), np.int32)
+    sp = np.zeros((t, maxnode), np.float32)
+    tm = np.zeros((t, maxnode, 2), np.int32)
+    cg = rng.integers(0, 2, (t, maxnode, maxcat)).astype(np.int32)
+    for k in range(t):
+        nodes, queue = 1, [0]
+        while queue:
+            v = queue.pop(0)
+            bv[k, v] = rng.integers(0, mdim)
+            sp[k, v] = np.float32(rng.standard_normal() * 0.8)
+            if nodes + 2 <= maxnode and rng.random() < 0.8:
+                ns[k, v] = 2 if rng.random() < 0.05 else 1
+                tm[k, v] = (nodes, nodes + 1)
+                queue += [nodes, nodes + 1]
+                nodes += 2
+    return dict(nodestatus=ns, bestvar=bv, xbestsplit=sp, treemap=tm, catgoleft=cg, cat=np.asarray(cat, np.int32))
+
+
+def random_features(rng, n, cat):
+    X = rng.standard_normal((n, len(cat))).astype(np.float32)
+    for v, c in enumerate(cat):
+        if c > 1:   # category codes with fractions and out-of-range values
+            X[:, v] = (rng.integers(-1, c + 2, n) + rng.choice([0.0, 0.3, 0.5, 0.7, -0.2], n)).astype(np.float32)
+    return X
+
+
+def test_forest_leaves_oob_walk_equals_compiled_testreebag():
+    Rf = compiled_reference()
+    rng = np.random.default_rng(61)
+    cat, maxcat, t, n, maxnode = [1, 1, 3, 5, 2, 1], 5, 12, 400, 41
+    f = random_forest_arrays(rng, t, maxnode, cat, maxcat)
+    X = random_features(rng, n, cat)
+    nin = (rng.random((t, n)) < 0.6).astype(np.int32) * rng.integers(1, 3, (t, n)).astype(np.int32)
+    got = O.forest_leaves(1, f, X, nin)
+    Rf.ref_cpu_testreebag.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_int32] * 4 + [ctypes.c_void_p]
+    for k in range(t):
+        nodextr = np.empty(n, np.int32)
+        Rf.ref_cpu_testreebag(X.ctypes.data, np.ascontiguousarray(f["xbestsplit"][k]).ctypes.data,
+                              np.ascontiguousarray(nin[k]).ctypes.data,
+                              np.ascontiguousarray(f["treemap"][k]).ctypes.data,
+                              np.ascontiguousarray(f["bestvar"][k]).ctypes.data, f["cat"].ctypes.data,
+                              np.ascontiguousarray(f["nodestatus"][k]).ctypes.data,
+                              np.ascontiguousarray(f["catgoleft"][k]).ctypes.data, n, len(cat), maxnode, maxcat,
+                              nodextr.ctypes.data)
+        oob = nin[k] == 0
+        assert np.array_equal(got[k][oob], nodextr[oob]), k
+        assert (f["nodestatus"][k][got[k][oob]] != 1).all()
+
+
+def sklearn_forest(rng, t, n, mdim):
+    from sklearn.tree import DecisionTreeRegressor
+
+    X = rng.standard_normal((n, mdim)).astype(np.float32)
+    y = np.sin(X[:, 0]) + X[:, 1] * X[:, 2] + 0.1 * rng.standard_normal(n)
+    trees = [DecisionTreeRegressor(max_depth=7, random_state=k).fit(X[rng.integers(0, n, n)], y)
+             for k in range(t)]
+    maxnode = max(tr.tree_.node_count for tr in trees)
+    ns = -np.ones((t, maxnode), np.int32)
+    bv = np.zeros((t, maxnode), np.int32)
+    sp = np.zeros((t, maxnode), np.float32)
+    tm = np.zeros((t, maxnode, 2), np.int32)
+    for k, tr in enumerate(trees):
+        s = tr.tree_
+        m = s.node_count
+        split = s.children_left >= 0
+        ns[k, :m] = np.where(split, 1, -1)
+        bv[k, :m] = np.where(split, s.feature, 0)
+        thr = s.threshold.astype(np.float32)          # largest float32 <= the double threshold:
+        thr = np.where(thr.astype(np.float64) > s.threshold, np.nextafter(thr, np.float32(-np.inf)), thr)
+        sp[k, :m] = np.where(split, thr, 0)           # x <= thr32 iff x <= thr for float32 x
+        tm[k, :m, 0] = np.where(split, s.children_left, 0)
+        tm[k, :m, 1] = np.where(split, s.children_right, 0)
+    return trees, dict(nodestatus=ns, bestvar=bv, xbestsplit=sp, treemap=tm, catgoleft=None, cat=None), X
+
+
+def test_forest_leaves_numeric_walks_equal_sklearn_apply():
+    """On numeric trees all three walks reach the leaf sklearn's apply()
+    reports (its own traversal, x <= threshold goes left)."""
+    rng = np.random.default_rng(62)
+    trees, f, X = sklearn_forest(rng, 6, 700, 5)
+    Xq = rng.standard_normal((300, 5)).astype(np.float32)
+    want = np.stack([tr.apply(Xq) for tr in trees]).astype(np.int32)
+    assert np.array_equal(O.forest_leaves(0, f, Xq), want)
+    for nin in (np.ones((6, 300), np.int32), np.zeros((6, 300), np.int32)):
+        assert np.array_equal(O.forest_leaves(1, f, Xq, nin), want)
+
+
+def test_forest_leaves_categorical_rules():
+    """One categorical split at the root: predict and find_terminal_node use
+    (int)(x + 0.5), testreebag uses (int)x and sends invalid codes right;
+    find_terminal_node returns 0 for an invalid code, predict stays at 0."""
+    cat = np.array([4], np.int32)
+    ns = np.array([[1, -1, -1]], np.int32)
+    f = dict(nodestatus=ns, bestvar=np.zeros((1, 3), np.int32), xbestsplit=np.zeros((1, 3), np.float32),
+             treemap=np.array([[[1, 2], [0, 0], [0, 0]]], np.int32),
+             catgoleft=np.array([[[1, 0, 1, 0], [0] * 4, [0] * 4]], np.int32), cat=cat)
+    x = np.array([[0.0], [0.4], [0.6], [1.49], [2.5], [3.6], [-0.6], [-0.4], [4.2]], np.float32)
+    rnd = [0, 0, 1, 1, 3, 4, 0, 0, 4]           # (int)(x + 0.5), truncation toward 0
+    trc = [0, 0, 0, 1, 2, 3, 0, 0, 4]           # (int)x
+    pred = O.forest_leaves(0, f, x)[0]
+    inbag = O.forest_leaves(1, f, x, np.ones((1, len(x)), np.int32))[0]
+    oob = O.forest_leaves(1, f, x, np.zeros((1, len(x)), np.int32))[0]
+    go = lambda c: 1 if f["catgoleft"][0, 0, c] == 1 else 2  # noqa: E731
+    assert list(pred) == [go(c) if 0 <= c < 4 else 0 for c in rnd]
+    assert list(inbag) == [go(c) if 0 <= c < 4 else 0 for c in rnd]
+    assert list(oob) == [go(c) if 0 <= c < 4 else 2 for c in trc]
+
+
+def test_forest_leaves_feed_the_reference_proximity():
+    """Training leaves as nodextr, with non-terminal nodes excluded, give the
+    compiled reference's cpu_proximity + cpu_finishprox through the
+    triangle restatement: the producer composes with the proximity path."""
+    Rf = compiled_reference()
+    rng = np.random.default_rng(63)
+    trees, f, X = sklearn_forest(rng, 8, 300, 5)
+    t, maxnode = f["nodestatus"].shape
+    n = X.shape[0]
+    nin = np.stack([np.bincount(rng.integers(0, n, n), minlength=n) for _ in range(t)]).astype(np.int32)
+    leaf = O.forest_leaves(1, f, X, nin)
+    Rf.ref_set_config(0, 0, 2)
+    pr = np.zeros((n, n), order="F")
+    for k in range(t):
+        Rf.ref_cpu_proximity(np.ascontiguousarray(f["nodestatus"][k]), np.ascontiguousarray(leaf[k]), nin[k], n,
+                             maxnode, pr.reshape(-1, order="F"))
+    nout = (nin == 0).sum(axis=0).astype(np.int32)
+    ps = np.zeros((n, n), order="F")
+    Rf.ref_cpu_finishprox(n, nout, pr.reshape(-1, order="F"), ps.reshape(-1, order="F"))
+    term = np.where(np.take_along_axis(f["nodestatus"], leaf, axis=1) == -1, leaf, -1).astype(np.int32)
+    got = O.upper_rows(term, (nin == 0).astype(np.uint8), maxnode, O.FMT_F32)
+    assert np.array_equal(got, ps[np.triu_indices(n)].astype(np.float32))
