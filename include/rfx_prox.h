@@ -354,6 +354,16 @@ int rfxp_factor_dequantize(rfxp_ctx* ctx, int level, const void* q, int64_t coun
  * by cyclic Jacobi rotations; the b x b eigensolver of the calls above. */
 int rfxp_host_symeig(int32_t n, const double* a, double* w, double* v);
 
+/* Y = P V for the OOB-normalised proximity of the current forest
+ * (rfxp_set_forest): P = 1/4 (D^-1 U + U D^-1) + I, U the OOB co-occurrence
+ * counts of rfxp_upper (U_ii = 0), D^-1 = diag(nout > 0 ? 1/nout : 1) --
+ * the matrix of rf::cpu_finishprox (src/rf_finishprox.cpp:12-74) -- as
+ * bucket SpMMs (U = B A^T + A B^T - 2 B B^T, A the one-hot leaf matrix, B
+ * its OOB entries), never forming P.  V, Y: device N x r row-major fp32,
+ * 1 <= r <= 32, not aliased; sums in double.  Reads the leaf matrix and OOB
+ * words given to rfxp_set_forest, which must still be valid. */
+int rfxp_lowrank_oob_pv(rfxp_ctx* ctx, const float* V, int32_t r, float* Y);
+
 /* ---- per-tree and dense small-N operations -------------------------------
  * A tree is (nodestatus[nnode], nodextr[N], nin[N]): sample n lies in node
  * nodextr[n], which takes part when nodestatus of it is -1 (terminal);

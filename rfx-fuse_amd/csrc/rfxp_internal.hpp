@@ -96,6 +96,10 @@ struct rfxp_ctx {
     DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits
     DevBuf<int32_t> flags;     // device status words
     ForestBufs fb;             // the forest index of rfxp_set_forest (pointers into the buffers above)
+    const int32_t* fo_leaf = nullptr;   // the caller's leaf matrix and OOB words given to rfxp_set_forest
+    int64_t fo_si = 0, fo_st = 0;       // (rfxp_lowrank_oob_pv reads them)
+    const uint32_t* fo_oob = nullptr;
+    int64_t fo_old = 0;
 
     // reference set for top-K (rfxp_set_reference)
     bool ref_ready = false;

@@ -394,3 +394,98 @@ extern "C" int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, 
     std::copy(G.begin(), G.end(), B);
     return RFXP_OK;
 }
+
+// ---------------------------------------------------------------------------
+// OOB-normalised proximity applied through the forest's buckets
+// ---------------------------------------------------------------------------
+// P = 1/4 (D^-1 U + U D^-1) + I with U_ij = #{t : same leaf, oob_i != oob_j}
+// and D^-1 = diag(r), r = nout > 0 ? 1/nout : 1: the matrix
+// cpu_finishprox produces from the OOB co-occurrence counts
+// (src/rf_finishprox.cpp:12-74; 1/4 (r_i + r_j) U_ij is its
+// 0.5 (U/2 r_i + U/2 r_j), and the diagonal is 1).  U X is a bucket SpMM on
+// the forest index of rfxp_set_forest (bucket b = 2 leaf + oob):
+//     W_t[b] = sum over the members j of bucket b of X_j,
+//     (U X)_i = sum_t W_t[b(i, t) xor 1]   (the bucket of the other OOB bit),
+// which is B A^T + A B^T - 2 B B^T applied to X, A the one-hot leaf matrix
+// and B its OOB entries.  X = [V, r o V] gives both products in one pass.
+
+namespace rfxp {
+
+// W[(t*nb + b)*c2 + c] = sum over bucket b of tree t of X[j*c2 + c]
+__global__ __launch_bounds__(256) void k_oob_w(const int32_t* off, const uint32_t* mem, int64_t N, int32_t T,
+                                               int32_t nb, const float* X, int32_t c2, float* W) {
+    const int64_t wb = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wb >= (int64_t)T * nb) return;
+    const int32_t t = (int32_t)(wb / nb), b = (int32_t)(wb % nb);
+    const int32_t c = threadIdx.x & 63;
+    const int32_t* ot = off + (int64_t)t * (nb + 1);
+    const uint32_t* m = mem + (int64_t)t * N;
+    const int32_t s = ot[b], e = ot[b + 1];
+    double acc = 0.0;
+    if (c < c2)
+        for (int32_t k = s; k < e; ++k) acc += (double)X[(int64_t)((m[k] & MEM_ID) - 1u) * c2 + c];
+    if (c < c2) W[wb * c2 + c] = (float)acc;
+}
+
+// Y[i*r + c] = 1/4 (r_i Z_i,c + Z_i,r+c) + V_i,c with Z = U [V, r o V]
+// formed per sample from the other bucket's W row in every tree.
+__global__ __launch_bounds__(256) void k_oob_y(const int32_t* leaf, int64_t si, int64_t st, const uint32_t* oob,
+                                               int64_t old, int64_t N, int32_t T, int32_t L, int32_t nb,
+                                               const float* W, const float* V, const double* rinv, int32_t r,
+                                               float* Y) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= N) return;
+    const int32_t c = threadIdx.x & 63;
+    const int32_t c2 = 2 * r;
+    double acc = 0.0;
+    for (int32_t t = 0; t < T; ++t) {
+        const int32_t l = leaf[i * si + (int64_t)t * st];
+        if (l < 0 || l >= L) continue;
+        const uint32_t o = (oob[(int64_t)t * old + (i >> 5)] >> (i & 31)) & 1u;
+        const int32_t ob = 2 * l + (int32_t)(o ^ 1u);
+        if (c < c2) acc += (double)W[((int64_t)t * nb + ob) * c2 + c];
+    }
+    // lanes r..2r-1 hold U (r o V); lane c < r combines with lane c + r
+    const double other = __shfl_down(acc, r, 64);
+    if (c < r) Y[i * r + c] = (float)(0.25 * (rinv[i] * acc + other) + (double)V[i * r + c]);
+}
+
+__global__ void k_oob_x2(const float* V, const double* rinv, int64_t N, int32_t r, float* X2) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= N * r) return;
+    const int64_t i = e / r;
+    const int32_t c = (int32_t)(e % r);
+    const float v = V[e];
+    X2[i * 2 * r + c] = v;
+    X2[i * 2 * r + r + c] = (float)(rinv[i] * (double)v);
+}
+
+}  // namespace rfxp
+
+extern "C" int rfxp_lowrank_oob_pv(rfxp_ctx* ctx, const float* V, int32_t r, float* Y) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_lowrank_oob_pv: no forest set");
+    if (r < 1 || r > 32) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_lowrank_oob_pv: need 1 <= r <= 32");
+    if (!V || !Y || !is_device_pointer(V) || !is_device_pointer(Y) || V == Y)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_lowrank_oob_pv: V and Y distinct device pointers");
+    const int64_t N = ctx->N;
+    const int32_t T = ctx->T, L = ctx->L, nb = 2 * L;
+    if (N == 0) return RFXP_OK;
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    RFXP_HIP(ctx, ctx->lr_tmp.ensure((size_t)N * 2 * r));
+    RFXP_HIP(ctx, ctx->lr_w.ensure((size_t)T * nb * 2 * r));
+    const unsigned nx = (unsigned)((N * r + 255) / 256);
+    hipLaunchKernelGGL(k_oob_x2, dim3(nx), dim3(256), 0, ctx->stream, V, ctx->fb.rinv, N, r, ctx->lr_tmp.p);
+    const int64_t nw = (int64_t)T * nb;
+    {
+        LaunchTimer tm(ctx, "lr_oob_w");
+        hipLaunchKernelGGL(k_oob_w, dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, ctx->stream, ctx->fb.off, ctx->fb.mem,
+                           N, T, nb, ctx->lr_tmp.p, 2 * r, ctx->lr_w.p);
+    }
+    {
+        LaunchTimer tm(ctx, "lr_oob_y");
+        hipLaunchKernelGGL(k_oob_y, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, ctx->stream, ctx->fo_leaf, ctx->fo_si,
+                           ctx->fo_st, ctx->fo_oob, ctx->fo_old, N, T, L, nb, ctx->lr_w.p, V, ctx->fb.rinv, r, Y);
+    }
+    return check_launch(ctx, "k_oob launch");
+}

@@ -811,6 +811,11 @@ extern "C" int rfxp_set_forest(rfxp_ctx* ctx, const int32_t* leaf, int64_t strid
     ctx->ldr = z.ldr;
     ctx->lmax = z.lmax;
     if (int rc = pack_forest(ctx, v, nout, ctx->fb)) return rc;
+    ctx->fo_leaf = leaf;
+    ctx->fo_si = stride_i;
+    ctx->fo_st = stride_t;
+    ctx->fo_oob = oob_words;
+    ctx->fo_old = oob_ld;
     ctx->forest_ready = true;
     return RFXP_OK;
 }

@@ -100,6 +100,7 @@ def load(path: str = LIB_PATH):
     L.rfxp_factor_dequantize.argtypes = [vp, C.c_int, vp, i64, vp, vp]
     L.rfxp_host_symeig.argtypes = [i32, vp, vp, vp]
     L.rfxp_lowrank_pv.argtypes = [vp, vp, i32, vp]
+    L.rfxp_lowrank_oob_pv.argtypes = [vp, vp, i32, vp]
     L.rfxp_lowrank_subspace.argtypes = [vp, vp, i32, i32, vp, vp]
     L.rfxp_tree_pairs.argtypes = [vp, vp, vp, vp, i32, i32, C.c_int, C.POINTER(C.POINTER(i64)),
                                   C.POINTER(C.POINTER(C.c_double)), C.POINTER(i64)]
@@ -432,6 +433,15 @@ class Context:
         self._check(self._L.rfxp_factor_dequantize(self.h, level, q.data_ptr(), count,
                                                    None if scale_zp is None else scale_zp.data_ptr(), A.data_ptr()))
         return A
+
+    def lowrank_oob_pv(self, V):
+        """Y = P V for the OOB-normalised proximity of the current forest."""
+        import torch
+
+        assert V.dtype == torch.float32 and V.is_cuda and V.is_contiguous()
+        Y = torch.empty_like(V)
+        self._check(self._L.rfxp_lowrank_oob_pv(self.h, V.data_ptr(), V.shape[1], Y.data_ptr()))
+        return Y
 
     def lowrank_pv(self, V):
         """Y = P V for the reference set (P = A A^T / T): V float32 device

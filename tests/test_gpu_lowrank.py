@@ -105,3 +105,34 @@ def test_c4_shape_properties(gpu_ctx):
     b = (v.double() * Pu.double()).sum(0)
     scale = u.double().norm(dim=0) * Pv.double().norm(dim=0)
     assert ((a - b).abs() / scale).max().item() < 1e-5
+
+
+@pytest.mark.parametrize("n,t,nleaf,r,layout", [(1, 2, 1, 1, "tree"), (1500, 40, 12, 8, "tree"),
+                                                (4000, 25, 30, 32, "sample")])
+def test_oob_normalised_pv_matches_finishprox_matrix(gpu_ctx, n, t, nleaf, r, layout):
+    """Y = P V for the cpu_finishprox matrix P of the forest's OOB counts:
+    the dense P here rounds to the oracle's F32 triangle (pinned to the
+    compiled reference), and the SpMM matches P V within 1e-6."""
+    import torch
+
+    import rfxprox as R
+
+    rng = np.random.default_rng(n + t + r)
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    leaf[rng.random((t, n)) < 0.03] = -1
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    if n > 1:
+        oob[:, 1] = 0   # never OOB: r = 1
+    words = R.pack_oob_bits(dev(oob).to(torch.bool))
+    lf = dev(leaf if layout == "tree" else np.ascontiguousarray(leaf.T))  # kept alive: the SpMM reads it
+    gpu_ctx.set_forest(lf, words, n, t, nleaf, layout=layout)
+    U = np.zeros((n, n))
+    U[np.triu_indices(n)] = O.upper_counts_scatter(leaf, oob, nleaf)
+    U = U + np.triu(U, 1).T
+    nout = oob.sum(axis=0)
+    rv = np.where(nout > 0, 1.0 / np.maximum(nout, 1), 1.0)
+    P = 0.25 * (rv[:, None] * U + U * rv[None, :]) + np.eye(n)
+    assert np.array_equal(P[np.triu_indices(n)].astype(np.float32), O.upper_rows(leaf, oob, nleaf, O.FMT_F32))
+    V = rng.standard_normal((n, r)).astype(np.float32)
+    Y = gpu_ctx.lowrank_oob_pv(dev(V)).cpu().numpy()
+    assert rel_fro(Y.astype(np.float64), P @ V.astype(np.float64)) <= 1e-6
