@@ -310,6 +310,8 @@ def run_triangle(args):
         "output_GBps": nbytes / (ms_step / 1e3) / 1e9,
         "kernels_ms": {"tri_avg": tri_avg, "pack_per_step": pack_ms / args.steps,
                        **{f"{k}_per_step": v for k, v in pack_each.items()}},
+        # row segments the last step recounted with 16-bit counters (wrapped 8-bit counts)
+        "tri_recounts": ctx.upper_recounts(),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_launch": tri_bytes,
                      "traffic": traffic_from_profile(args.config) if n == cfg["n"] else None,

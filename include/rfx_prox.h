@@ -116,6 +116,11 @@ int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t row_begin,
 /* Size in bytes of the output of rfxp_upper for rows [row_begin, row_end). */
 int64_t rfxp_upper_nbytes(int fmt, int64_t N, int64_t row_begin, int64_t row_end);
 
+/* Number of row segments rfxp_upper recounted with 16-bit counters since
+ * rfxp_set_forest (their 8-bit counters wrapped; T > 255 only).  Host
+ * int64; synchronises the context stream. */
+int rfxp_upper_recounts(rfxp_ctx* ctx, int64_t* count);
+
 /* The per-sample nout actually used (device int32[N] copy into `nout`). */
 int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
 

@@ -679,6 +679,7 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
         const int64_t n1 = std::max<int64_t>(N, 1);
         fill_u32(ctx, fb.roff + n1 * fb.ldr, REC_PAD, 0u);
         fill_u32(ctx, (uint32_t*)(fb.rlen + n1 * fb.ldr), REC_PAD / 2, 0u);
+        fill_u32(ctx, (uint32_t*)fb.flags, 16, 0u);  // status words (recount counter)
         LaunchTimer tm(ctx, "rr_init");
         hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, fb.rrange);
     }

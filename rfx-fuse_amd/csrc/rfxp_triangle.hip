@@ -278,10 +278,15 @@ __device__ __forceinline__ void lds_add(uint32_t addr, uint32_t val) {
 // sits with the other dummy words right after the item's counters; units
 // between the counters and xlim fall on other threads' dummy words.  Every
 // lane of every step thus adds 1 to some byte (16-bit unit) of the
-// counter-and-dummy area, without a compare or select.
-template <int BITS>
+// counter-and-dummy area, without a compare or select.  base1 = lo + 1 -
+// shift; when it is not positive (an item that starts within the first
+// output chunk of the triangle, lo < shift) an empty lane's m - base1 is a
+// small padding unit, so those items (EMPTY_FIX) send m = 0 to xlim
+// explicitly.
+template <int BITS, bool EMPTY_FIX = false>
 __device__ __forceinline__ void count_hits(uint32_t m, uint32_t base1, uint32_t xlim) {
-    const uint32_t c = min(m - base1, xlim);
+    uint32_t c = min(m - base1, xlim);
+    if constexpr (EMPTY_FIX) c = m ? c : xlim;
     if constexpr (BITS == 8) lds_add(c & ~3u, 1u << ((c << 3) & 31u));
     else lds_add((c << 1) & ~3u, 1u << ((c << 4) & 31u));
 }
@@ -303,7 +308,7 @@ __device__ __forceinline__ uint32_t long_run_end(const TriArgs& a, int32_t t, ui
 // record groups (16 trees each) and keeps two groups' loads in flight; no
 // load is issued past its range.  Returns the wave's 64-lane counting steps
 // (uniform).
-template <int BITS>
+template <int BITS, bool EMPTY_FIX = false>
 __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64_t lo, int32_t shift, uint32_t xlim) {
     const uint32_t lane4 = (threadIdx.x & 63) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -325,7 +330,8 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
             const uint32_t end = len4 == 4u * REC_LONG ? long_run_end(a, t0 + u, off, off + len4) : off + len4;
             const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, end);
             for (uint32_t p4 = 256u; off + p4 < end; p4 += 256u) {
-                count_hits<BITS>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0), base1, xlim);
+                count_hits<BITS, EMPTY_FIX>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0), base1,
+                                            xlim);
                 ++steps;
             }
         }
@@ -338,14 +344,14 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
     for (int32_t g = g0;; g += 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) count_hits<BITS>(A.m[u], base1, xlim);
+        for (int u = 0; u < 16; ++u) count_hits<BITS, EMPTY_FIX>(A.m[u], base1, xlim);
         steps += 16;
         if (A.has_long) long_tail(16 * g);
         if (g + 2 < g1) load_group(a.mem, ro + 16 * (g + 2), rl + 16 * (g + 2), lane4, A);
         if (g + 1 >= g1) break;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) count_hits<BITS>(B.m[u], base1, xlim);
+        for (int u = 0; u < 16; ++u) count_hits<BITS, EMPTY_FIX>(B.m[u], base1, xlim);
         steps += 16;
         if (B.has_long) long_tail(16 * (g + 1));
         if (g + 3 < g1) load_group(a.mem, ro + 16 * (g + 3), rl + 16 * (g + 3), lane4, B);
@@ -492,11 +498,12 @@ __device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, d
     }
 }
 
-// Zeroes the item's counter words [0, nwords) (nwords a multiple of 4) and
-// the dummy words after them.
+// Zeroes the item's counter words [0, nwords) and the TRI_THREADS dummy
+// words after them (rounded up to whole 16-byte stores: at most 3 words past
+// the last dummy word, inside the 64-byte gap before the item scalars).
 __device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords) {
     uint4* c4 = (uint4*)cnt;
-    const int32_t n4 = (nwords >> 2) + TRI_THREADS / 4;
+    const int32_t n4 = (nwords + TRI_THREADS + 3) >> 2;
     for (int32_t w = threadIdx.x; w < n4; w += TRI_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
 }
 
@@ -544,7 +551,8 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     // item's columns but inside that range land in the unstored padding
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x);
+    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x)
+                                       : hit_phase<8, true>(a, i, lo, shift, cap + 4u * threadIdx.x);
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -671,7 +679,8 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     __syncthreads();
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x);
+    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x)
+                                       : hit_phase<8, true>(a, i, lo, shift, cap + 4u * threadIdx.x);
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -938,6 +947,17 @@ extern "C" int rfxp_upper(rfxp_ctx* ctx, int fmt, float scale, float zp, int64_t
     if (r0 == r1) return RFXP_OK;
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     return upper_launch(ctx, ctx->fb, ctx->N, ctx->T, fmt, scale, zp, r0, r1, out);
+}
+
+extern "C" int rfxp_upper_recounts(rfxp_ctx* ctx, int64_t* count) {
+    if (!ctx || !count) return RFXP_ERR_INVALID;
+    if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_upper_recounts: no forest set");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    int32_t v = 0;
+    RFXP_HIP(ctx, hipMemcpyAsync(&v, ctx->fb.flags, sizeof(v), hipMemcpyDeviceToHost, ctx->stream));
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *count = v;
+    return RFXP_OK;
 }
 
 extern "C" int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout) {

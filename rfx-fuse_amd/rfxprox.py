@@ -69,6 +69,7 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_nbytes.argtypes = [C.c_int, i64, i64, i64]
     L.rfxp_upper_nbytes.restype = i64
     L.rfxp_get_nout.argtypes = [vp, vp]
+    L.rfxp_upper_recounts.argtypes = [vp, C.POINTER(i64)]
     L.rfxp_upper_work_item.argtypes = [i64, i32, i64, i64, i64, C.POINTER(i64), C.POINTER(i64)]
     L.rfxp_upper_work_item.restype = i64
     L.rfxp_upper_launches.argtypes = [i64]
@@ -497,6 +498,12 @@ class Context:
                                                oob_words.shape[1], n, t, nleaf, nptr, fmt, scale, zp, r0, r1,
                                                out.data_ptr()))
         return out
+
+    def upper_recounts(self) -> int:
+        """Row segments recounted with 16-bit counters since set_forest."""
+        v = C.c_int64()
+        self._check(self._L.rfxp_upper_recounts(self.h, C.byref(v)))
+        return v.value
 
     def nout(self):
         import torch

@@ -139,6 +139,7 @@ def test_counts_beyond_255_use_wide_counters(gpu_ctx, fmt):
     got, _ = gpu_rows(gpu_ctx, fmt, 0, n, scale=np.float32(1 / 255.0))
     want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(1 / 255.0))
     check_equal(got, want, f"wide counters fmt {fmt}")
+    assert gpu_ctx.upper_recounts() > 0   # the wrapped segments were recounted
     del keep
 
 
@@ -290,6 +291,9 @@ def test_c2_shape_full_triangle_f32(gpu_ctx):
         out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
         gpu_ctx.upper(fmt, out, 0, n)
         torch.cuda.synchronize()
+        # T > 255 runs the byte-sum wrap check; counts here stay far below 256,
+        # so no row segment may be recounted (a spurious recount rewrites it)
+        assert gpu_ctx.upper_recounts() == 0, fmt
         got = out.cpu().numpy().view(O.FMT_DTYPE[fmt])
         want = idx.rows(fmt, 0, n)
         if fmt == O.FMT_F32:
