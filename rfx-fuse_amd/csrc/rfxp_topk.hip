@@ -68,7 +68,7 @@ struct TopkArgs {
 // candidate and running lists.
 __host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) { return (1u << shift) * 2u; }
 constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
-constexpr uint32_t TOPK_RED_WORDS = 64;                     // wave partials
+constexpr uint32_t TOPK_RED_WORDS = 96;                     // wave partials (48) + two max slots (2 x 16)
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
     return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
@@ -283,6 +283,61 @@ __device__ __forceinline__ void count_segment(const TopkArgs& a, int64_t q, int3
     }
 }
 
+// A wave's bucket runs of one segment, counted into the 16-bit LDS
+// counters.  Lane l holds the run (byte offset soff, byte length len4) of
+// the wave's l-th tree; n_trees (<= 64, uniform) lanes hold one.  The runs
+// are loaded sixteen at a time, two groups in flight.
+__device__ __forceinline__ void count_lane_runs(const TopkArgs& a, uint32_t soff, uint32_t len4, int32_t n_trees,
+                                                uint32_t lane4, uint32_t base1, uint32_t width, uint32_t dummy) {
+    const int32_t ng = (n_trees + 15) >> 4;
+    if (ng == 0) return;
+    uint32_t A[16], B[16];
+    auto load = [&](int32_t g, uint32_t (&m)[16]) {
+        bool lng = false;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
+            const uint32_t ln = (uint32_t)__builtin_amdgcn_readlane((int)len4, 16 * g + u);
+            lng |= ln > 256u;
+            m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, so + ln), lane4, so, 0);
+        }
+        return lng;
+    };
+    auto tails = [&](int32_t g) {
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t ln = (uint32_t)__builtin_amdgcn_readlane((int)len4, 16 * g + u);
+            if (ln <= 256u) continue;
+            const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
+            const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, so + ln);
+            for (uint32_t p4 = 256u; p4 < ln; p4 += 256u)
+                count16((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, so, 0), base1, width, dummy);
+        }
+    };
+    bool la = load(0, A);
+    bool lb = ng > 1 ? load(1, B) : false;
+    for (int32_t g = 0;; g += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
+        if (la) tails(g);
+        if (g + 2 < ng) la = load(g + 2, A);
+        if (g + 1 >= ng) break;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
+        if (lb) tails(g + 1);
+        if (g + 3 < ng) lb = load(g + 3, B);
+        if (g + 2 >= ng) break;
+    }
+}
+
+// Packed maximum of the two 16-bit halves of a and b.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+    const u16x2 m = __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b));
+    return __builtin_bit_cast(uint32_t, m);
+}
+
 template <int NW>  // 16-bit words per thread: S = 2 * NW * TOPK_THREADS
 __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk(TopkArgs a) {
     extern __shared__ uint32_t sm[];
@@ -304,29 +359,80 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const uint32_t K = (uint32_t)a.K;
     const int64_t ex = query_exclusion(a, q);
 
+    // The wave's trees [tw0, tw1), lane l holding tree tw0 + 64 r + l in
+    // round r.  Round 0's run offsets are kept in registers across segments:
+    // ob indexes the offset row entry of the lane tree's bucket in segment 0,
+    // and the entries of segments s, s + 1, s + 2 are o0, o1, o2, the last
+    // one loaded a segment ahead.  Later rounds (T > 1024) look their runs up
+    // per segment.
+    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
+    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
+    const int32_t lane = (int32_t)(threadIdx.x & 63u);
+    int64_t ob = -1;
+    uint32_t tb = 0u, o0 = 0u, o1 = 0u, o2 = 0u;
+    if (lane < tw1 - tw0) {
+        const int32_t t = tw0 + lane;
+        const int32_t l = a.qleaf[q * a.qsi + (int64_t)t * a.qst];
+        bool ok = l >= 0 && l < a.L;
+        if (ok && a.qoob) ok = ((a.qoob[(int64_t)t * a.qold + (q >> 5)] >> (q & 31)) & 1u) != 0u;
+        if (ok) {
+            ob = (int64_t)t * (a.nb + 1) + (int64_t)l * a.nseg;
+            tb = 4u * (uint32_t)t * (uint32_t)a.N;
+            o0 = (uint32_t)a.off[ob];
+            o1 = (uint32_t)a.off[ob + 1];
+            o2 = a.nseg >= 2 ? (uint32_t)a.off[ob + 2] : o1;
+        }
+    }
+    // counters start at zero; afterwards each thread zeroes its own words as
+    // it reads them
+    {
+        uint4* c4 = (uint4*)sm;
+        for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+
     uint32_t nrun = 0;  // entries in the running list (uniform)
     uint32_t kmin = 0;  // key of the running K-th entry once the list is full
     for (int32_t s = 0; s < a.nseg; ++s) {
         const uint32_t lo = (uint32_t)s << shift;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
         const uint32_t base1 = lo + 1u;
-        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, base1, width);
+        // this segment's run of the lane's tree; the entry two segments on is
+        // loaded now for the next one
+        const uint32_t soff = tb + 4u * o0;
+        const uint32_t len4 = 4u * (o1 - o0);
+        const uint32_t o3 = (ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[ob + s + 3] : o2;
+        count_lane_runs(a, soff, len4, min(tw1 - tw0, 64), lane4, base1, width, dummy);
+        for (int32_t r0 = tw0 + 64; r0 < tw1; r0 += 64) {
+            uint32_t so2, ln2;
+            query_bucket(a, q, r0 + lane < tw1 ? r0 + lane : a.T, s, so2, ln2);
+            count_lane_runs(a, so2, ln2, min(tw1 - r0, 64), lane4, base1, width, dummy);
+        }
+        o0 = o1;
+        o1 = o2;
+        o2 = o3;
+        __syncthreads();  // every count is in LDS
         // counters -> keys, held in registers from here on: count + 1, or
-        // 0 where the reference may not be chosen (past the end, or excluded)
+        // 0 where the reference may not be chosen (past the end, or excluded);
+        // the counter words are zeroed for the next segment
         const uint32_t u0 = threadIdx.x * 2u * NW;
         uint32_t key[NW];
-        if constexpr (NW >= 4) {
 #pragma unroll
-            for (int k = 0; k < NW; k += 4) {
+        for (int k = 0; k < NW; k += 4) {
+            if constexpr (NW >= 4) {
                 const uint4 x = *(const uint4*)(kw + k);
                 key[k] = x.x;
                 key[k + 1] = x.y;
                 key[k + 2] = x.z;
                 key[k + 3] = x.w;
-            }
-        } else {
+                *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
+            } else {
 #pragma unroll
-            for (int k = 0; k < NW; ++k) key[k] = kw[k];
+                for (int kk = 0; kk < NW; ++kk) {
+                    key[kk] = kw[kk];
+                    kw[kk] = 0u;
+                }
+            }
         }
         // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
         // excluded unit `exu` (offsets against constants keep no per-unit
@@ -335,25 +441,49 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
         const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
         uint32_t mloc = 0;
+        if (rem >= 2 * NW && exu < 0) {
+            // every unit valid: key = count + 1 in both halves (counts stay
+            // below 65535, so no half carries into the other)
+            uint32_t m2 = 0u;
 #pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            const uint32_t w = key[k];
-            const bool va = 2 * k < rem && 2 * k != exu;
-            const bool vb = 2 * k + 1 < rem && 2 * k + 1 != exu;
-            const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
-            const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
-            key[k] = ka | (kb << 16);
-            mloc = max(mloc, max(ka, kb));
+            for (int k = 0; k < NW; ++k) {
+                key[k] += 0x00010001u;
+                m2 = max_u16x2(m2, key[k]);
+            }
+            mloc = max(m2 & 0xffffu, m2 >> 16);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                const uint32_t w = key[k];
+                const bool va = 2 * k < rem && 2 * k != exu;
+                const bool vb = 2 * k + 1 < rem && 2 * k + 1 != exu;
+                const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
+                const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
+                key[k] = ka | (kb << 16);
+                mloc = max(mloc, max(ka, kb));
+            }
         }
+        // the segment's largest key; the barrier also orders every zeroing
+        // before the next segment's counts.  Two alternating slots, so a
+        // slot is rewritten only after everyone read it.
+        uint32_t M;
+        {
+            uint32_t* const slot = red + 48 + 16 * (s & 1);
+            const uint32_t wm = wave_max(mloc);
+            if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = wm;
+            __syncthreads();
+            M = wave_max((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
+        }
+        const uint32_t lowest0 = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+        if (M < lowest0) continue;
         // only keys above the running threshold can enter the list.  cstar:
         // keys > cstar all enter, keys == cstar in index order up to K; it is
         // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
         // keys reach `lowest`.  Each round counts four levels at once.
-        const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-        uint32_t c0 = lowest, w01, w23, M = mloc;
+        const uint32_t lowest = lowest0;
+        uint32_t c0 = lowest, w01, w23, m1 = 0u;
         level_counts<NW>(key, c0, w01, w23);
-        block_levels(w01, w23, M, red);  // also orders the key reads before the next segment's clear
-        if (M < lowest) continue;
+        block_levels(w01, w23, m1, red);
         uint32_t cstar = lowest;
         if ((w01 & 0xffffu) > K) {
             for (;;) {
