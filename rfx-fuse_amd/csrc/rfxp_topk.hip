@@ -40,7 +40,9 @@ namespace rfxp {
 constexpr int TOPK_THREADS = 1024;
 constexpr int TOPK_WAVES = TOPK_THREADS / 64;
 constexpr int TOPK_MAX_K = 64;
-constexpr int TOPK_MAX_SHIFT = 15;  // 32768 16-bit counters: 64 KB, two workgroups per CU
+constexpr int TOPK_MAX_SHIFT16 = 15;  // 32768 16-bit counters: 64 KB, two workgroups per CU
+constexpr int TOPK_SHIFT8 = 16;       // 65536 8-bit counters: 64 KB (top-K with T <= TOPK_MAX_T8)
+constexpr int TOPK_MAX_T8 = 2048;     // at most 128 trees, 128 counting steps, per wave and segment
 constexpr int TOPK_MIN_SHIFT = 11;  // at least 2 counters per thread
 
 struct TopkArgs {
@@ -63,12 +65,15 @@ struct TopkArgs {
     uint16_t* cnt_out;
 };
 
-// LDS layout: counters (S/2 words) | dummy words (1024) | per-segment
-// bucket records of up to 1024 trees (offset, length) | reduction scratch |
-// candidate and running lists.
-__host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) { return (1u << shift) * 2u; }
+// LDS layout: counters (64 KB at most: 2^shift 16-bit counters, or 2^16
+// 8-bit ones) | dummy words (1024) | per-segment bucket records of up to
+// 1024 trees (offset, length) | reduction scratch | candidate and running
+// lists.
+__host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) {
+    return shift >= TOPK_SHIFT8 ? (1u << shift) : (1u << shift) * 2u;
+}
 constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
-constexpr uint32_t TOPK_RED_WORDS = 96;                     // wave partials (48) + two max slots (2 x 16)
+constexpr uint32_t TOPK_RED_WORDS = 144;                    // wave partials (48) + two segment slots (2 x 48)
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
     return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
@@ -106,6 +111,21 @@ __device__ __forceinline__ void count16(uint32_t m, uint32_t base1, uint32_t wid
     const uint32_t c = m - base1;
     const bool h = c < width;
     lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
+}
+
+// Counting step of a query run with BITS-bit counters (8 or 16): m = j + 1
+// of a member (0: an empty lane), counter unit c = j - lo.  Units at or past
+// xlim -- empty lanes, and members outside the units being counted -- are
+// clamped to xlim, the unit of byte 0 of this thread's dummy word, which
+// sits after the counters with the other threads' dummy words; units between
+// the counters and xlim fall on those.  (A run holds only members of its
+// segment, lo <= j < lo + 65536, so a member never lands on a counter past
+// the segment's references.)
+template <int BITS>
+__device__ __forceinline__ void count_bits(uint32_t m, uint32_t base1, uint32_t xlim) {
+    const uint32_t c = min(m - base1, xlim);
+    if constexpr (BITS == 8) lds_add16(c & ~3u, 1u << ((c << 3) & 31u));
+    else lds_add16((c << 1) & ~3u, 1u << ((c << 4) & 31u));
 }
 
 // 16 bucket loads of record group g (records rec_off/rec_len in LDS); a
@@ -283,14 +303,19 @@ __device__ __forceinline__ void count_segment(const TopkArgs& a, int64_t q, int3
     }
 }
 
-// A wave's bucket runs of one segment, counted into the 16-bit LDS
-// counters.  Lane l holds the run (byte offset soff, byte length len4) of
-// the wave's l-th tree; n_trees (<= 64, uniform) lanes hold one.  The runs
-// are loaded sixteen at a time, two groups in flight.
-__device__ __forceinline__ void count_lane_runs(const TopkArgs& a, uint32_t soff, uint32_t len4, int32_t n_trees,
-                                                uint32_t lane4, uint32_t base1, uint32_t width, uint32_t dummy) {
+// A wave's bucket runs of one segment, counted into the LDS counters
+// (BITS 8 or 16).  Lane l holds the run (byte offset soff, byte length len4)
+// of the wave's l-th tree; n_trees (<= 64, uniform) lanes hold one.  The
+// runs are loaded sixteen at a time, two groups in flight.  Returns the
+// wave's 64-lane counting steps (uniform): every lane of a step adds 1 to
+// one counter or dummy byte.
+template <int BITS>
+__device__ __forceinline__ uint32_t count_lane_runs(const TopkArgs& a, uint32_t soff, uint32_t len4,
+                                                    int32_t n_trees, uint32_t lane4, uint32_t base1, uint32_t dummy) {
+    const uint32_t xlim = BITS == 8 ? dummy : dummy >> 1;
     const int32_t ng = (n_trees + 15) >> 4;
-    if (ng == 0) return;
+    if (ng == 0) return 0u;
+    uint32_t steps = 16u * (uint32_t)ng;
     uint32_t A[16], B[16];
     auto load = [&](int32_t g, uint32_t (&m)[16]) {
         bool lng = false;
@@ -309,8 +334,10 @@ __device__ __forceinline__ void count_lane_runs(const TopkArgs& a, uint32_t soff
             if (ln <= 256u) continue;
             const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
             const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, so + ln);
-            for (uint32_t p4 = 256u; p4 < ln; p4 += 256u)
-                count16((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, so, 0), base1, width, dummy);
+            for (uint32_t p4 = 256u; p4 < ln; p4 += 256u) {
+                count_bits<BITS>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, so, 0), base1, xlim);
+                ++steps;
+            }
         }
     };
     bool la = load(0, A);
@@ -318,17 +345,18 @@ __device__ __forceinline__ void count_lane_runs(const TopkArgs& a, uint32_t soff
     for (int32_t g = 0;; g += 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
+        for (int u = 0; u < 16; ++u) count_bits<BITS>(A[u], base1, xlim);
         if (la) tails(g);
         if (g + 2 < ng) la = load(g + 2, A);
         if (g + 1 >= ng) break;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
+        for (int u = 0; u < 16; ++u) count_bits<BITS>(B[u], base1, xlim);
         if (lb) tails(g + 1);
         if (g + 3 < ng) lb = load(g + 3, B);
         if (g + 2 >= ng) break;
     }
+    return steps;
 }
 
 // Packed maximum of the two 16-bit halves of a and b.
@@ -338,51 +366,247 @@ __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, m);
 }
 
-template <int NW>  // 16-bit words per thread: S = 2 * NW * TOPK_THREADS
-__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk(TopkArgs a) {
-    extern __shared__ uint32_t sm[];
-    const int32_t shift = a.shift;
-    const uint32_t S = 1u << shift;
-    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
-    uint32_t* const rec_len = rec_off + TOPK_THREADS;
-    uint32_t* const red = rec_len + TOPK_THREADS;
-    uint32_t* const cand_k = red + TOPK_RED_WORDS;  // candidates of a segment
-    uint32_t* const cand_i = cand_k + TOPK_MAX_K;
-    uint32_t* const run_k = cand_i + TOPK_MAX_K;    // running top-K (sorted)
-    uint32_t* const run_i = run_k + TOPK_MAX_K;
-    uint32_t* const nrun_p = run_i + TOPK_MAX_K;
-    uint32_t* const kw = sm + threadIdx.x * NW;     // this thread's counter / key words
-    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
-    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
-    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t q = a.q0 + blockIdx.x;
-    const uint32_t K = (uint32_t)a.K;
-    const int64_t ex = query_exclusion(a, q);
+// LDS pointers of a top-K workgroup.
+struct TopkLds {
+    uint32_t* red;     // reduction scratch (TOPK_RED_WORDS)
+    uint32_t* cand_k;  // candidates of a segment
+    uint32_t* cand_i;
+    uint32_t* run_k;   // running top-K (sorted)
+    uint32_t* run_i;
+    uint32_t* nrun_p;
+};
 
-    // The wave's trees [tw0, tw1), lane l holding tree tw0 + 64 r + l in
-    // round r.  Round 0's run offsets are kept in registers across segments:
-    // ob indexes the offset row entry of the lane tree's bucket in segment 0,
-    // and the entries of segments s, s + 1, s + 2 are o0, o1, o2, the last
-    // one loaded a segment ahead.  Later rounds (T > 1024) look their runs up
-    // per segment.
-    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
-    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
-    const int32_t lane = (int32_t)(threadIdx.x & 63u);
-    int64_t ob = -1;
-    uint32_t tb = 0u, o0 = 0u, o1 = 0u, o2 = 0u;
+__device__ __forceinline__ TopkLds topk_lds(uint32_t* sm, int32_t shift) {
+    TopkLds L;
+    L.red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + TOPK_REC_WORDS;
+    L.cand_k = L.red + TOPK_RED_WORDS;
+    L.cand_i = L.cand_k + TOPK_MAX_K;
+    L.run_k = L.cand_i + TOPK_MAX_K;
+    L.run_i = L.run_k + TOPK_MAX_K;
+    L.nrun_p = L.run_i + TOPK_MAX_K;
+    return L;
+}
+
+// Keys of a thread's 2 NW units u0 .. u0 + 2 NW - 1 (relative to the
+// segment start) from their 16-bit counts, two per word: count + 1, or 0
+// where the reference may not be chosen (at or past `rem`, or the excluded
+// unit `exu`).  Returns the thread's largest key.
+template <int NW>
+__device__ __forceinline__ uint32_t keys_of_counts(uint32_t (&key)[NW], int32_t rem, int32_t exu) {
+    uint32_t mloc = 0;
+    if (rem >= 2 * NW && exu < 0) {
+        // every unit valid: key = count + 1 in both halves (counts stay
+        // below 65535, so no half carries into the other)
+        uint32_t m2 = 0u;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            key[k] += 0x00010001u;
+            m2 = max_u16x2(m2, key[k]);
+        }
+        mloc = max(m2 & 0xffffu, m2 >> 16);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            const uint32_t w = key[k];
+            const bool va = 2 * k < rem && 2 * k != exu;
+            const bool vb = 2 * k + 1 < rem && 2 * k + 1 != exu;
+            const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
+            const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
+            key[k] = ka | (kb << 16);
+            mloc = max(mloc, max(ka, kb));
+        }
+    }
+    return mloc;
+}
+
+// Block maximum of v through 16 words of `slot`; one barrier.  A slot may be
+// reused only after a later barrier.
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* slot) {
+    const uint32_t wm = wave_max(v);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = wm;
+    __syncthreads();
+    return wave_max((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
+}
+
+// Merges the keys of one segment (thread x: units lo + u0 .. of key[NW],
+// u0 = 2 NW x) into the running list; M is the block's largest key, at
+// least `lowest` (the smallest key that can still enter).  Every thread
+// calls it; it ends with nrun / kmin updated and a barrier.
+template <int NW>
+__device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&key)[NW], uint32_t M,
+                                            uint32_t lowest, uint32_t lo, uint32_t u0, const TopkLds& L,
+                                            uint32_t& nrun, uint32_t& kmin) {
+    const uint32_t K = (uint32_t)a.K;
+    uint32_t* const red = L.red;
+    uint32_t* const cand_k = L.cand_k;
+    uint32_t* const cand_i = L.cand_i;
+    uint32_t* const run_k = L.run_k;
+    uint32_t* const run_i = L.run_i;
+    uint32_t* const nrun_p = L.nrun_p;
+    // only keys above the running threshold can enter the list.  cstar:
+    // keys > cstar all enter, keys == cstar in index order up to K; it is
+    // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
+    // keys reach `lowest`.  Each round counts four levels at once.
+    uint32_t c0 = lowest, w01, w23, m1 = 0u;
+    level_counts<NW>(key, c0, w01, w23);
+    block_levels(w01, w23, m1, red);
+    uint32_t cstar = lowest;
+    if ((w01 & 0xffffu) > K) {
+        for (;;) {
+            const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
+            const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
+            if (d < 3u || c0 + 3u >= M) {
+                cstar = c0 + d;
+                break;
+            }
+            c0 += 3u;
+            uint32_t m2 = 0;
+            level_counts<NW>(key, c0, w01, w23);
+            block_levels(w01, w23, m2, red);
+        }
+    }
+    const uint32_t ngt = count_ge<NW>(key, cstar + 1u);
+    const uint32_t neq = count_ge<NW>(key, cstar) - ngt;
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
+    const uint32_t G = tot & 0xffffu, E = tot >> 16;
+    const uint32_t take = min(E, K - G);
+    uint32_t rg = pre & 0xffffu, re = pre >> 16;
+    if (ngt + neq) {
+        const uint32_t j0 = lo + u0;
+#pragma unroll
+        for (int k = 0; k < 2 * NW; ++k) {
+            const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            const uint32_t j = j0 + (uint32_t)k;
+            if (kk > cstar) {
+                cand_k[rg] = kk;
+                cand_i[rg] = j;
+                ++rg;
+            } else if (kk == cstar) {
+                if (re < take) {
+                    cand_k[G + re] = kk;
+                    cand_i[G + re] = j;
+                }
+                ++re;
+            }
+        }
+    }
+    __syncthreads();
+    // merge by rank (first wave): running entries precede candidates of
+    // equal key, since they have lower indices
+    const uint32_t nc = G + take;
+    if (threadIdx.x < 64) {
+        const uint32_t ntot = nrun + nc;
+        uint32_t mk[4], mi[4], rk[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t e = threadIdx.x + 64u * r;
+            mk[r] = 0u;
+            mi[r] = 0xffffffffu;
+            if (e < nrun) {
+                mk[r] = run_k[e];
+                mi[r] = run_i[e];
+            } else if (e < ntot) {
+                mk[r] = cand_k[e - nrun];
+                mi[r] = cand_i[e - nrun];
+            }
+            uint32_t rank = 0;
+            for (uint32_t f = 0; f < ntot; ++f) {
+                const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
+                const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
+                rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
+            }
+            rk[r] = e < ntot ? rank : 0xffffffffu;
+        }
+        // one wave: its reads of the old list precede these writes
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (rk[r] < K) {
+                run_k[rk[r]] = mk[r];
+                run_i[rk[r]] = mi[r];
+            }
+        }
+        if (threadIdx.x == 0) *nrun_p = min(ntot, K);
+    }
+    __syncthreads();
+    nrun = *nrun_p;
+    kmin = nrun ? run_k[nrun - 1] : 0u;
+    __syncthreads();
+}
+
+// Per-lane bucket runs of a query.  The wave's trees are [tw0, tw1); lane l
+// holds tree tw0 + l.  The lane's offset-row entries of segments s, s + 1,
+// s + 2 are kept in o0, o1, o2, the last one loaded a segment ahead, so a
+// segment's runs need no dependent load.  Trees past the first 64 of a
+// wave (T > 1024) are looked up per segment.
+struct LaneRuns {
+    int64_t ob;   // offset-row index of the lane tree's bucket in segment 0 (-1: none)
+    uint32_t tb;  // byte offset of the lane tree's members in mem
+    uint32_t o0, o1, o2;
+};
+
+__device__ __forceinline__ LaneRuns lane_runs_init(const TopkArgs& a, int64_t q, int32_t tw0, int32_t tw1,
+                                                   int32_t lane) {
+    LaneRuns r{-1, 0u, 0u, 0u, 0u};
     if (lane < tw1 - tw0) {
         const int32_t t = tw0 + lane;
         const int32_t l = a.qleaf[q * a.qsi + (int64_t)t * a.qst];
         bool ok = l >= 0 && l < a.L;
         if (ok && a.qoob) ok = ((a.qoob[(int64_t)t * a.qold + (q >> 5)] >> (q & 31)) & 1u) != 0u;
         if (ok) {
-            ob = (int64_t)t * (a.nb + 1) + (int64_t)l * a.nseg;
-            tb = 4u * (uint32_t)t * (uint32_t)a.N;
-            o0 = (uint32_t)a.off[ob];
-            o1 = (uint32_t)a.off[ob + 1];
-            o2 = a.nseg >= 2 ? (uint32_t)a.off[ob + 2] : o1;
+            r.ob = (int64_t)t * (a.nb + 1) + (int64_t)l * a.nseg;
+            r.tb = 4u * (uint32_t)t * (uint32_t)a.N;
+            r.o0 = (uint32_t)a.off[r.ob];
+            r.o1 = (uint32_t)a.off[r.ob + 1];
+            r.o2 = a.nseg >= 2 ? (uint32_t)a.off[r.ob + 2] : r.o1;
         }
     }
+    return r;
+}
+
+// Counts the query's runs of segment s into the BITS-bit counters (member j
+// at unit j + 1 - base1; the counters end where the dummy words begin);
+// returns the wave's counting steps.
+template <int BITS>
+__device__ __forceinline__ uint32_t count_query_segment(const TopkArgs& a, int64_t q, int32_t s, uint32_t soff,
+                                                        uint32_t len4, int32_t tw0, int32_t tw1, int32_t lane,
+                                                        uint32_t lane4, uint32_t base1, uint32_t dummy) {
+    uint32_t steps = count_lane_runs<BITS>(a, soff, len4, min(tw1 - tw0, 64), lane4, base1, dummy);
+    for (int32_t r0 = tw0 + 64; r0 < tw1; r0 += 64) {
+        uint32_t so2, ln2;
+        query_bucket(a, q, r0 + lane < tw1 ? r0 + lane : a.T, s, so2, ln2);
+        steps += count_lane_runs<BITS>(a, so2, ln2, min(tw1 - r0, 64), lane4, base1, dummy);
+    }
+    return steps;
+}
+
+__device__ __forceinline__ void topk_write(const TopkArgs& a, int64_t q, const TopkLds& L, uint32_t nrun) {
+    if (threadIdx.x < (uint32_t)a.K) {
+        const bool have = threadIdx.x < nrun;
+        a.idx_out[q * a.K + threadIdx.x] = have ? (int32_t)L.run_i[threadIdx.x] : -1;
+        a.cnt_out[q * a.K + threadIdx.x] = have ? (uint16_t)(L.run_k[threadIdx.x] - 1u) : (uint16_t)0;
+    }
+}
+
+// 16-bit counters, S = 2^shift = 2 NW * TOPK_THREADS references per segment
+// (reference sets of up to 32768 samples, or more than TOPK_MAX_T8 trees).
+template <int NW>
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk(TopkArgs a) {
+    extern __shared__ uint32_t sm[];
+    const int32_t shift = a.shift;
+    const uint32_t S = 1u << shift;
+    const TopkLds L = topk_lds(sm, shift);
+    uint32_t* const kw = sm + threadIdx.x * NW;  // this thread's counter / key words
+    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
+    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t lane = (int32_t)(threadIdx.x & 63u);
+    const int64_t q = a.q0 + blockIdx.x;
+    const uint32_t K = (uint32_t)a.K;
+    const int64_t ex = query_exclusion(a, q);
+    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
+    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
+    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
     // counters start at zero; afterwards each thread zeroes its own words as
     // it reads them
     {
@@ -396,182 +620,205 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     for (int32_t s = 0; s < a.nseg; ++s) {
         const uint32_t lo = (uint32_t)s << shift;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
-        const uint32_t base1 = lo + 1u;
-        // this segment's run of the lane's tree; the entry two segments on is
-        // loaded now for the next one
-        const uint32_t soff = tb + 4u * o0;
-        const uint32_t len4 = 4u * (o1 - o0);
-        const uint32_t o3 = (ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[ob + s + 3] : o2;
-        count_lane_runs(a, soff, len4, min(tw1 - tw0, 64), lane4, base1, width, dummy);
-        for (int32_t r0 = tw0 + 64; r0 < tw1; r0 += 64) {
-            uint32_t so2, ln2;
-            query_bucket(a, q, r0 + lane < tw1 ? r0 + lane : a.T, s, so2, ln2);
-            count_lane_runs(a, so2, ln2, min(tw1 - r0, 64), lane4, base1, width, dummy);
-        }
-        o0 = o1;
-        o1 = o2;
-        o2 = o3;
+        const uint32_t soff = lr.tb + 4u * lr.o0;
+        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+        count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
+        lr.o0 = lr.o1;
+        lr.o1 = lr.o2;
+        lr.o2 = o3;
         __syncthreads();  // every count is in LDS
-        // counters -> keys, held in registers from here on: count + 1, or
-        // 0 where the reference may not be chosen (past the end, or excluded);
-        // the counter words are zeroed for the next segment
+        // counters -> keys, held in registers from here on; the counter
+        // words are zeroed for the next segment
         const uint32_t u0 = threadIdx.x * 2u * NW;
         uint32_t key[NW];
+        if constexpr (NW >= 4) {
 #pragma unroll
-        for (int k = 0; k < NW; k += 4) {
-            if constexpr (NW >= 4) {
+            for (int k = 0; k < NW; k += 4) {
                 const uint4 x = *(const uint4*)(kw + k);
                 key[k] = x.x;
                 key[k + 1] = x.y;
                 key[k + 2] = x.z;
                 key[k + 3] = x.w;
                 *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < NW; ++kk) {
-                    key[kk] = kw[kk];
-                    kw[kk] = 0u;
-                }
             }
-        }
-        // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
-        // excluded unit `exu` (offsets against constants keep no per-unit
-        // index live across the segment loop)
-        const int32_t rem = (int32_t)width - (int32_t)u0;
-        const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
-        const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
-        uint32_t mloc = 0;
-        if (rem >= 2 * NW && exu < 0) {
-            // every unit valid: key = count + 1 in both halves (counts stay
-            // below 65535, so no half carries into the other)
-            uint32_t m2 = 0u;
-#pragma unroll
-            for (int k = 0; k < NW; ++k) {
-                key[k] += 0x00010001u;
-                m2 = max_u16x2(m2, key[k]);
-            }
-            mloc = max(m2 & 0xffffu, m2 >> 16);
         } else {
 #pragma unroll
             for (int k = 0; k < NW; ++k) {
-                const uint32_t w = key[k];
-                const bool va = 2 * k < rem && 2 * k != exu;
-                const bool vb = 2 * k + 1 < rem && 2 * k + 1 != exu;
-                const uint32_t ka = va ? (w & 0xffffu) + 1u : 0u;
-                const uint32_t kb = vb ? (w >> 16) + 1u : 0u;
-                key[k] = ka | (kb << 16);
-                mloc = max(mloc, max(ka, kb));
+                key[k] = kw[k];
+                kw[k] = 0u;
             }
         }
+        // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
+        // excluded unit `exu`
+        const int32_t rem = (int32_t)width - (int32_t)u0;
+        const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
+        const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
+        const uint32_t mloc = keys_of_counts<NW>(key, rem, exu);
         // the segment's largest key; the barrier also orders every zeroing
-        // before the next segment's counts.  Two alternating slots, so a
-        // slot is rewritten only after everyone read it.
-        uint32_t M;
+        // before the next segment's counts (two alternating slots)
+        const uint32_t M = block_max(mloc, L.red + 48 + 16 * (s & 1));
+        const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+        if (M < lowest) continue;
+        select_into<NW>(a, key, M, lowest, lo, u0, L, nrun, kmin);
+    }
+    topk_write(a, q, L, nrun);
+}
+
+// 8-bit counters, 65536 references per segment (reference sets above 32768
+// samples, T <= TOPK_MAX_T8): half as many bucket runs per query as 16-bit
+// counters allow in the same 64 KB of LDS.  Thread x reads the counter bytes
+// of units 32x .. 32x + 31 of each half h (units h * 32768 + ...), so each
+// half is selected exactly like a 16-bit segment of 32768 references, in
+// index order.  CHECK (T > 255): a count of 256 or more wraps its byte; every
+// lane of every counting step adds 1 to one counter or dummy byte, so the
+// counts are exact iff all those bytes sum to 64 x the counting steps.  A
+// segment that fails the check is recounted with 16-bit counters, half by
+// half.
+template <bool CHECK>
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk8(TopkArgs a) {
+    extern __shared__ uint32_t sm[];
+    constexpr uint32_t S = 1u << TOPK_SHIFT8;
+    constexpr uint32_t H = S / 2;
+    const TopkLds L = topk_lds(sm, TOPK_SHIFT8);
+    uint32_t* const dw = sm + (topk_dummy_off(TOPK_SHIFT8) >> 2) + threadIdx.x;  // this thread's dummy word
+    const uint32_t dummy = topk_dummy_off(TOPK_SHIFT8) + threadIdx.x * 4u;
+    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t lane = (int32_t)(threadIdx.x & 63u);
+    const int64_t q = a.q0 + blockIdx.x;
+    const uint32_t K = (uint32_t)a.K;
+    const int64_t ex = query_exclusion(a, q);
+    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
+    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
+    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
+    {
+        uint4* c4 = (uint4*)sm;
+        for (uint32_t w = threadIdx.x; w < S / 16u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+        *dw = 0u;
+    }
+    __syncthreads();
+
+    const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each half
+    uint32_t nrun = 0;
+    uint32_t kmin = 0;
+    for (int32_t s = 0; s < a.nseg; ++s) {
+        const uint32_t lo = (uint32_t)s << TOPK_SHIFT8;
+        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        const uint32_t soff = lr.tb + 4u * lr.o0;
+        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+        const uint32_t steps =
+            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
+        lr.o0 = lr.o1;
+        lr.o1 = lr.o2;
+        lr.o2 = o3;
+        __syncthreads();  // every count is in LDS
+        // the thread's counter bytes of both halves (units 32x .. 32x + 31 of
+        // each, 8 words): per-half largest count (every unit, valid or not:
+        // an upper bound) and, for the check, the byte sum with the dummy word
+        uint4* const pw[2] = {(uint4*)(sm + 8u * threadIdx.x), (uint4*)(sm + H / 4u + 8u * threadIdx.x)};
+        uint32_t mh[2];
+        int32_t bal = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 x = pw[h][0], y = pw[h][1];
+            const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+            uint32_t m2 = 0u;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                m2 = max_u16x2(m2, w8[k] & 0x00ff00ffu);
+                m2 = max_u16x2(m2, (w8[k] >> 8) & 0x00ff00ffu);
+                if constexpr (CHECK) bal = (int32_t)__builtin_amdgcn_sad_u8(w8[k], 0u, (uint32_t)bal);
+            }
+            mh[h] = max(m2 & 0xffffu, m2 >> 16);
+        }
+        if constexpr (CHECK) {
+            bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
+            if (lane == 0) bal -= 64 * (int32_t)steps;
+        }
+        // block reduction of (max half 0, max half 1, byte balance)
+        uint32_t M0, M1;
+        bool exact = true;
         {
-            uint32_t* const slot = red + 48 + 16 * (s & 1);
-            const uint32_t wm = wave_max(mloc);
-            if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = wm;
+            uint32_t* const slot = L.red + 48 + 48 * (s & 1);
+            const uint32_t w0 = wave_max(mh[0]), w1 = wave_max(mh[1]);
+            const uint32_t wb = CHECK ? wave_sum((uint32_t)bal) : 0u;
+            if (lane == 0) {
+                slot[3 * (threadIdx.x >> 6)] = w0;
+                slot[3 * (threadIdx.x >> 6) + 1] = w1;
+                slot[3 * (threadIdx.x >> 6) + 2] = wb;
+            }
             __syncthreads();
-            M = wave_max((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
+            const bool have = (uint32_t)lane < (uint32_t)TOPK_WAVES;
+            M0 = wave_max(have ? slot[3 * lane] : 0u) + 1u;
+            M1 = wave_max(have ? slot[3 * lane + 1] : 0u) + 1u;
+            if constexpr (CHECK) exact = wave_sum(have ? slot[3 * lane + 2] : 0u) == 0u;
         }
-        const uint32_t lowest0 = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-        if (M < lowest0) continue;
-        // only keys above the running threshold can enter the list.  cstar:
-        // keys > cstar all enter, keys == cstar in index order up to K; it is
-        // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
-        // keys reach `lowest`.  Each round counts four levels at once.
-        const uint32_t lowest = lowest0;
-        uint32_t c0 = lowest, w01, w23, m1 = 0u;
-        level_counts<NW>(key, c0, w01, w23);
-        block_levels(w01, w23, m1, red);
-        uint32_t cstar = lowest;
-        if ((w01 & 0xffffu) > K) {
-            for (;;) {
-                const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
-                const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
-                if (d < 3u || c0 + 3u >= M) {
-                    cstar = c0 + d;
-                    break;
-                }
-                c0 += 3u;
-                uint32_t m2 = 0;
-                level_counts<NW>(key, c0, w01, w23);
-                block_levels(w01, w23, m2, red);
-            }
-        }
-        const uint32_t ngt = count_ge<NW>(key, cstar + 1u);
-        const uint32_t neq = count_ge<NW>(key, cstar) - ngt;
-        uint32_t tot;
-        const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
-        const uint32_t G = tot & 0xffffu, E = tot >> 16;
-        const uint32_t take = min(E, K - G);
-        uint32_t rg = pre & 0xffffu, re = pre >> 16;
-        if (ngt + neq) {
-            const uint32_t j0 = lo + u0;
+        if (exact) {
+            // keys of each half from its counter bytes; a half whose largest
+            // key cannot enter the list is skipped
+#pragma unroll 1
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+                if ((h == 0 ? M0 : M1) < lowest) continue;
+                const uint32_t loh = lo + (uint32_t)h * H;
+                const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (H / 4u) + 8u * threadIdx.x);
+                const uint4 x = ph[0], y = ph[1];
+                const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+                uint32_t key[16];
 #pragma unroll
-            for (int k = 0; k < 2 * NW; ++k) {
-                const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                const uint32_t j = j0 + (uint32_t)k;
-                if (kk > cstar) {
-                    cand_k[rg] = kk;
-                    cand_i[rg] = j;
-                    ++rg;
-                } else if (kk == cstar) {
-                    if (re < take) {
-                        cand_k[G + re] = kk;
-                        cand_i[G + re] = j;
-                    }
-                    ++re;
-                }
+                for (int k = 0; k < 16; ++k)
+                    key[k] = __builtin_amdgcn_perm(0u, w8[k >> 1], (k & 1) ? 0x0c030c02u : 0x0c010c00u);
+                const int32_t rem = (int32_t)width - (int32_t)(h * H) - (int32_t)u0;
+                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                keys_of_counts<16>(key, rem, exu);
+                select_into<16>(a, key, h == 0 ? M0 : M1, lowest, loh, u0, L, nrun, kmin);
             }
-        }
-        __syncthreads();
-        // merge by rank (first wave): running entries precede candidates of
-        // equal key, since they have lower indices
-        const uint32_t nc = G + take;
-        if (threadIdx.x < 64) {
-            const uint32_t ntot = nrun + nc;
-            uint32_t mk[4], mi[4], rk[4];
+            pw[0][0] = make_uint4(0u, 0u, 0u, 0u);
+            pw[0][1] = make_uint4(0u, 0u, 0u, 0u);
+            pw[1][0] = make_uint4(0u, 0u, 0u, 0u);
+            pw[1][1] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (CHECK) *dw = 0u;
+        } else {
+            // some count wrapped: recount the segment with 16-bit counters,
+            // half by half, zeroing each half's words as they are read
+            pw[0][0] = make_uint4(0u, 0u, 0u, 0u);
+            pw[0][1] = make_uint4(0u, 0u, 0u, 0u);
+            pw[1][0] = make_uint4(0u, 0u, 0u, 0u);
+            pw[1][1] = make_uint4(0u, 0u, 0u, 0u);
+            __syncthreads();
+            uint32_t* const kw = sm + 16u * threadIdx.x;
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t loh = lo + (uint32_t)h * H;
+                const uint32_t wh = (uint32_t)min(max((int32_t)width - (int32_t)(h * H), 0), (int32_t)H);
+                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy);
+                __syncthreads();
+                uint32_t key[16];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t e = threadIdx.x + 64u * r;
-                mk[r] = 0u;
-                mi[r] = 0xffffffffu;
-                if (e < nrun) {
-                    mk[r] = run_k[e];
-                    mi[r] = run_i[e];
-                } else if (e < ntot) {
-                    mk[r] = cand_k[e - nrun];
-                    mi[r] = cand_i[e - nrun];
+                for (int k = 0; k < 16; k += 4) {
+                    const uint4 x = *(const uint4*)(kw + k);
+                    key[k] = x.x;
+                    key[k + 1] = x.y;
+                    key[k + 2] = x.z;
+                    key[k + 3] = x.w;
+                    *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
                 }
-                uint32_t rank = 0;
-                for (uint32_t f = 0; f < ntot; ++f) {
-                    const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
-                    const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
-                    rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
-                }
-                rk[r] = e < ntot ? rank : 0xffffffffu;
+                const int32_t rem = (int32_t)wh - (int32_t)u0;
+                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                const uint32_t mloc = keys_of_counts<16>(key, rem, exu);
+                const uint32_t M = block_max(mloc, L.red + 48 + 16 * h);
+                const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+                if (M >= lowest) select_into<16>(a, key, M, lowest, loh, u0, L, nrun, kmin);
+                __syncthreads();  // the block_max slot is read before its next use
             }
-            // one wave: its reads of the old list precede these writes
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (rk[r] < K) {
-                    run_k[rk[r]] = mk[r];
-                    run_i[rk[r]] = mi[r];
-                }
-            }
-            if (threadIdx.x == 0) *nrun_p = min(ntot, K);
+            *dw = 0u;
         }
-        __syncthreads();
-        nrun = *nrun_p;
-        kmin = nrun ? run_k[nrun - 1] : 0u;
-        __syncthreads();
+        __syncthreads();  // every counter word is zero again before the next segment's counts
     }
-    if (threadIdx.x < K) {
-        const bool have = threadIdx.x < nrun;
-        a.idx_out[q * K + threadIdx.x] = have ? (int32_t)run_i[threadIdx.x] : -1;
-        a.cnt_out[q * K + threadIdx.x] = have ? (uint16_t)(run_k[threadIdx.x] - 1u) : (uint16_t)0;
-    }
+    topk_write(a, q, L, nrun);
 }
 
 // Outlier scores, full and anchor modes of RandomForest::compute_outlier_scores
@@ -604,12 +851,18 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t q = a.q0 + blockIdx.x;
     const int64_t ex = query_exclusion(a, q);
     const float fT = (float)a.T;
+    // 16-bit counters for at most 32768 references per counting pass: a
+    // segment of 65536 references is counted in two passes over its runs
+    const uint32_t C = min(S, 1u << TOPK_MAX_SHIFT16);
 
     double acc = 0.0;
-    for (int32_t s = 0; s < a.nseg; ++s) {
-        const uint32_t lo = (uint32_t)s << shift;
-        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
-        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
+    for (int32_t sp = 0; sp < a.nseg * (int32_t)(S / C); ++sp) {
+        const int32_t s = sp / (int32_t)(S / C);
+        const int64_t lo64 = ((int64_t)s << shift) + (int64_t)(sp % (int32_t)(S / C)) * C;
+        if (lo64 >= a.N) continue;  // uniform: every thread skips the pass
+        const uint32_t lo = (uint32_t)lo64;
+        const uint32_t width = (uint32_t)min((int64_t)C, a.N - lo64);
+        count_segment(a, q, s, C, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
         const uint32_t u0 = threadIdx.x * 2u * NW;
         const int32_t rem = (int32_t)width - (int32_t)u0;
         const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
@@ -716,18 +969,23 @@ __global__ __launch_bounds__(256) void k_topk_scores(ScoreArgs a) {
 // Queries per launch: gridDim.x * blockDim.x must stay below 2^32.
 constexpr int64_t TOPK_MAX_GRID = 1LL << 21;
 
-template <int NW>
-static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
+template <typename Kern>
+static hipError_t launch_topk_kernel(rfxp_ctx* ctx, Kern kern, TopkArgs a, int64_t Q) {
     const size_t lds = topk_lds_bytes(a.shift);
-    hipError_t e = hipFuncSetAttribute((const void*)k_topk<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
         a.q0 = q0;
         const unsigned nq = (unsigned)std::min(TOPK_MAX_GRID, Q - q0);
-        hipLaunchKernelGGL(k_topk<NW>, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a);
+        hipLaunchKernelGGL(kern, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+template <int NW>
+static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
+    return launch_topk_kernel(ctx, k_topk<NW>, a, Q);
 }
 
 template <int NW>
@@ -787,8 +1045,11 @@ extern "C" int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t st
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_reference: leaf must be a device pointer");
     if (N * (int64_t)T + MEM_PAD > (1LL << 30) - 1)
         return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_reference: N*T must stay below 2^30");
+    // segments of 2^shift references: 8-bit counters (65536 per segment)
+    // when the counts of a wave's trees fit their check, else 16-bit ones
+    const int32_t max_shift = T <= TOPK_MAX_T8 ? TOPK_SHIFT8 : TOPK_MAX_SHIFT16;
     int32_t shift = TOPK_MIN_SHIFT;
-    while (shift < TOPK_MAX_SHIFT && (1LL << shift) < N) ++shift;
+    while (shift < max_shift && (1LL << shift) < N) ++shift;
     const int64_t nseg = (N + (1LL << shift) - 1) >> shift;
     if ((int64_t)nleaf * nseg > (1LL << 29))
         return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_reference: nleaf * segments too large");
@@ -841,7 +1102,11 @@ extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
             case 12: e = launch_topk<2>(ctx, a, Q); break;
             case 13: e = launch_topk<4>(ctx, a, Q); break;
             case 14: e = launch_topk<8>(ctx, a, Q); break;
-            default: e = launch_topk<16>(ctx, a, Q); break;
+            case 15: e = launch_topk<16>(ctx, a, Q); break;
+            default:
+                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false>, a, Q)
+                               : launch_topk_kernel(ctx, k_topk8<true>, a, Q);
+                break;
         }
     }
     if (e != hipSuccess) return hip_error(ctx, e, "k_topk launch");
