@@ -73,7 +73,7 @@ __host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) {
     return shift >= TOPK_SHIFT8 ? (1u << shift) : (1u << shift) * 2u;
 }
 constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
-constexpr uint32_t TOPK_RED_WORDS = 144;                    // wave partials (48) + two segment slots (2 x 48)
+constexpr uint32_t TOPK_RED_WORDS = 160;  // wave partials (48), two segment slots (2 x 48), a selection slot (16)
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
     return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
@@ -324,7 +324,10 @@ __device__ __forceinline__ uint32_t count_lane_runs(const TopkArgs& a, uint32_t 
             const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
             const uint32_t ln = (uint32_t)__builtin_amdgcn_readlane((int)len4, 16 * g + u);
             lng |= ln > 256u;
-            m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, so + ln), lane4, so, 0);
+            // non-temporal (cache policy nt): a run is read once per query;
+            // streaming the runs keeps the offset rows, reread every segment,
+            // in L2
+            m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, so + ln), lane4, so, 2);
         }
         return lng;
     };
@@ -446,12 +449,33 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
     // only keys above the running threshold can enter the list.  cstar:
     // keys > cstar all enter, keys == cstar in index order up to K; it is
     // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
-    // keys reach `lowest`.  Each round counts four levels at once.
-    uint32_t c0 = lowest, w01, w23, m1 = 0u;
-    level_counts<NW>(key, c0, w01, w23);
-    block_levels(w01, w23, m1, red);
-    uint32_t cstar = lowest;
-    if ((w01 & 0xffffu) > K) {
+    // keys reach `lowest`.  One pass counts keys >= lowest and > lowest:
+    // when at most K keys reach `lowest` (the usual case once the list is
+    // full) that settles it; otherwise a search over key levels, four
+    // levels per round.
+    uint32_t n01 = 0;  // this thread: #(keys >= lowest) | #(keys > lowest) << 16
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+        const uint32_t va = key[k] & 0xffffu, vb = key[k] >> 16;
+        n01 += (va >= lowest ? 1u : 0u) + (va > lowest ? 0x10000u : 0u);
+        n01 += (vb >= lowest ? 1u : 0u) + (vb > lowest ? 0x10000u : 0u);
+    }
+    uint32_t tot01;
+    {
+        uint32_t* const slot = red + 144;
+        const uint32_t ws = wave_sum(n01);
+        if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = ws;
+        __syncthreads();
+        tot01 = wave_sum((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
+    }
+    uint32_t cstar = lowest, ngt, neq;
+    if ((tot01 & 0xffffu) <= K) {
+        ngt = n01 >> 16;
+        neq = (n01 & 0xffffu) - ngt;
+    } else {
+        uint32_t c0 = lowest, w01, w23, m1 = 0u;
+        level_counts<NW>(key, c0, w01, w23);
+        block_levels(w01, w23, m1, red);
         for (;;) {
             const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
             const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
@@ -464,9 +488,9 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
             level_counts<NW>(key, c0, w01, w23);
             block_levels(w01, w23, m2, red);
         }
+        ngt = count_ge<NW>(key, cstar + 1u);
+        neq = count_ge<NW>(key, cstar) - ngt;
     }
-    const uint32_t ngt = count_ge<NW>(key, cstar + 1u);
-    const uint32_t neq = count_ge<NW>(key, cstar) - ngt;
     uint32_t tot;
     const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
     const uint32_t G = tot & 0xffffu, E = tot >> 16;
@@ -492,41 +516,34 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
         }
     }
     __syncthreads();
-    // merge by rank (first wave): running entries precede candidates of
-    // equal key, since they have lower indices
+    // merge by rank (first wave; nrun, nc <= K <= 64, lane e holds running
+    // entry e and candidate e).  The running list is sorted; candidates have
+    // higher indices than every running entry, so a running entry keeps its
+    // place among running entries and precedes candidates of equal key.
     const uint32_t nc = G + take;
     if (threadIdx.x < 64) {
-        const uint32_t ntot = nrun + nc;
-        uint32_t mk[4], mi[4], rk[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t e = threadIdx.x + 64u * r;
-            mk[r] = 0u;
-            mi[r] = 0xffffffffu;
-            if (e < nrun) {
-                mk[r] = run_k[e];
-                mi[r] = run_i[e];
-            } else if (e < ntot) {
-                mk[r] = cand_k[e - nrun];
-                mi[r] = cand_i[e - nrun];
-            }
-            uint32_t rank = 0;
-            for (uint32_t f = 0; f < ntot; ++f) {
-                const uint32_t fk = f < nrun ? run_k[f] : cand_k[f - nrun];
-                const uint32_t fi = f < nrun ? run_i[f] : cand_i[f - nrun];
-                rank += better(fk, fi, mk[r], mi[r]) ? 1u : 0u;
-            }
-            rk[r] = e < ntot ? rank : 0xffffffffu;
+        const uint32_t e = threadIdx.x;
+        const bool has_r = e < nrun, has_c = e < nc;
+        const uint32_t rk = has_r ? run_k[e] : 0u, ri = has_r ? run_i[e] : 0u;
+        const uint32_t ck = has_c ? cand_k[e] : 0u, ci = has_c ? cand_i[e] : 0xffffffffu;
+        uint32_t rank_r = e, rank_c = 0u;
+        for (uint32_t c = 0; c < nc; ++c) {
+            const uint32_t fk = cand_k[c], fi = cand_i[c];
+            rank_r += fk > rk ? 1u : 0u;
+            rank_c += better(fk, fi, ck, ci) ? 1u : 0u;
         }
+        if (has_c)
+            for (uint32_t f = 0; f < nrun; ++f) rank_c += run_k[f] >= ck ? 1u : 0u;
         // one wave: its reads of the old list precede these writes
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (rk[r] < K) {
-                run_k[rk[r]] = mk[r];
-                run_i[rk[r]] = mi[r];
-            }
+        if (has_r && rank_r < K) {
+            run_k[rank_r] = rk;
+            run_i[rank_r] = ri;
         }
-        if (threadIdx.x == 0) *nrun_p = min(ntot, K);
+        if (has_c && rank_c < K) {
+            run_k[rank_c] = ck;
+            run_i[rank_c] = ci;
+        }
+        if (threadIdx.x == 0) *nrun_p = min(nrun + nc, K);
     }
     __syncthreads();
     nrun = *nrun_p;
