@@ -242,7 +242,9 @@ void QuantizationUtils::compute_int8_scaling(const float* data, size_t count, fl
 }
 
 // Block min / max of (float)data, one pair per block; then one block folds
-// all block results (every block, in index order).
+// all block results (every block, in index order).  Internal linkage: these
+// helpers are not part of the exported rf::cuda interface.
+namespace {
 __global__ __launch_bounds__(256) void k_q_minmax(const dp_t* data, size_t count, float* mins, float* maxs) {
     __shared__ float smn[256], smx[256];
     float mn = 1e30f, mx = -1e30f;
@@ -285,6 +287,7 @@ __global__ void k_q_scale(const float* mins, const float* maxs, int nblk, size_t
     *d_scale = scale;
     *d_zp = -mn / scale;
 }
+}  // namespace
 
 void QuantizationUtils::compute_int8_scaling_gpu(const dp_t* data_gpu, size_t count, float* d_scale,
                                                  float* d_zero_point) {
