@@ -495,12 +495,12 @@ def run_c4(args):
     Q, B = ctx.lowrank_subspace(V, cfg["iters"])
     torch.cuda.synchronize()
     sub_ms = (time.perf_counter() - t0) * 1e3
-    # compulsory HBM bytes of one P V: the leaf labels read twice (A^T V
-    # and A W), the member lists once, V and Y once, W written once and
-    # gathered once per (tree, leaf); the per-(sample, tree) row gathers of V
+    # compulsory HBM bytes of one P V: the member lists once (A^T V, k_lr_w),
+    # the leaf labels once (A W, k_lr_y), V and Y once, W written once and
+    # read once per (tree, leaf); the per-(sample, tree) row gathers of V
     # and W (2 N T r 4 B) are served from L2 / Infinity Cache and reported
     # separately as the gather rate
-    alg = 2 * n * t * 4 + n * t * 4 + 2 * n * r * 4 + 2 * t * nleaf * r * 4
+    alg = n * t * 4 + n * t * 4 + 2 * n * r * 4 + 2 * t * nleaf * r * 4
     gather = 2 * n * t * r * 4
     achieved = alg / (ms_step / 1e3) / 1e9
     rec = {
