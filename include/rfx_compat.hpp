@@ -145,6 +145,13 @@ void gpu_proximity_upper_triangle(const integer_t* nodestatus, const integer_t* 
 void gpu_proximity_rfgap_upper_triangle_fp16(const integer_t* nin_tree, const integer_t* nodextr_tree,
                                              integer_t nsample, __half* prox_upper_fp16);
 
+// The reference's include guards: whichever of this header and the
+// reference's rf_proximity_lowrank.hpp / rf_lowrank_helpers.hpp comes first
+// provides the declarations.  Code that creates the object must see this
+// declaration (its private layout is the library's), so such code includes
+// this header first, or the reference header is reduced to an include of it.
+#ifndef RF_PROXIMITY_LOWRANK_HPP
+#define RF_PROXIMITY_LOWRANK_HPP
 // include/rf_proximity_lowrank.hpp:27-433: the low-rank proximity object.
 // Public interface as the reference's; the private state is this build's.
 // Contributions (per-tree packed triangles in FP16 / INT8 / NF4, FP32 read
@@ -206,6 +213,10 @@ class LowRankProximityMatrix {
 
 // include/rf_proximity_lowrank.hpp:433: min(max_rank, floor(sqrt(nsample))), at least 1
 integer_t estimate_optimal_rank(integer_t nsample, integer_t max_rank = 1000);
+#endif  // RF_PROXIMITY_LOWRANK_HPP
+
+#ifndef RF_LOWRANK_HELPERS_HPP
+#define RF_LOWRANK_HELPERS_HPP
 
 // include/rf_lowrank_helpers.hpp:13-34 (lowrank_proximity_ptr is a
 // LowRankProximityMatrix*): host copies of the factors (new[], the caller
@@ -218,6 +229,7 @@ inline std::vector<double> compute_mds_3d_from_factors_host(void* lowrank_proxim
     return compute_mds_from_factors_host(lowrank_proximity_ptr, 3);
 }
 bool reconstruct_proximity_matrix_host(void* lowrank_proximity_ptr, dp_t** output_prox, integer_t nsamples);
+#endif  // RF_LOWRANK_HELPERS_HPP
 
 }  // namespace cuda
 }  // namespace rf
