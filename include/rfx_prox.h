@@ -138,6 +138,21 @@ int64_t rfxp_upper_work_item(int64_t N, int32_t S, int64_t row_begin, int64_t ro
                              int64_t* row, int64_t* col);
 int64_t rfxp_upper_launches(int64_t n_items);
 
+/* The "both OOB" proximity (R randomForest's oob.prox), which the reference
+ * does not implement -- its rule is OOB x in-bag normalised by nout
+ * (src/rf_proximity.cpp:179-230, src/rf_finishprox.cpp:47-73) -- and which
+ * the mid-size benchmark configuration's description names.  For i != j
+ *   num_ij = #{t : i and j both OOB in t, leaf_i(t) == leaf_j(t), label valid}
+ *   den_ij = #{t : i and j both OOB in t}
+ *   P_ij   = den_ij > 0 ? (float)num_ij / (float)den_ij : 0,   P_ii = 1,
+ * rows [row_begin, row_end) of the packed triangle into `out` (device) as
+ * RFXP_FMT_F32 (P) or RFXP_FMT_U16 (num, 0 on the diagonal).  Leaf matrix
+ * and OOB words (device) in rfxp_set_forest's layout; no forest index is
+ * used.  Work O(N^2 T / 2): a dense tiled kernel, for the sizes a dense
+ * N x N result is asked for. */
+int rfxp_both_oob(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_i, int64_t stride_t,
+                  const uint32_t* oob_words, int64_t oob_ld, int64_t N, int32_t T, int32_t nleaf, int fmt,
+                  int64_t row_begin, int64_t row_end, void* out);
 /* ---- allocation-free one-shot triangle ------------------------------------ */
 
 /* Maximum device workspace of rfxp_upper_noalloc, per GPU (64 MiB). */

@@ -67,6 +67,9 @@ def lib():
                                      C.c_int, C.c_float, C.c_float, C.c_int64, C.c_int64,
                                      C.c_void_p, C.c_int]
         L.orc_upper_rows.restype = C.c_int
+        L.orc_both_oob_rows.argtypes = [_i32, _u8, C.c_int64, C.c_int32, C.c_int32, C.c_int, C.c_int64,
+                                        C.c_int64, C.c_void_p, C.c_int]
+        L.orc_both_oob_rows.restype = C.c_int
         L.orc_index_build.argtypes = [_i32, _u8, C.c_int64, C.c_int32, C.c_int32, C.c_void_p, C.c_int]
         L.orc_index_build.restype = C.c_void_p
         L.orc_index_rows.argtypes = [C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_int64, C.c_int64,
@@ -176,6 +179,19 @@ def out_nbytes(fmt, n_entries):
     if fmt == FMT_NF4:
         return (n_entries + 1) // 2
     return n_entries * np.dtype(FMT_DTYPE[fmt]).itemsize
+
+
+def both_oob_rows(leaf_tn, oob_tn, nleaf, fmt=FMT_F32, r0=0, r1=None, threads=0):
+    """Rows [r0, r1) of the "both OOB" proximity triangle (orc_both_oob_rows):
+    F32 P = num / den, or U16 num."""
+    t, n = leaf_tn.shape
+    r1 = n if r1 is None else r1
+    e0, e1 = tri_idx(n, r0, r0), tri_idx(n, r1, r1)
+    out = np.zeros(e1 - e0, dtype=np.float32 if fmt == FMT_F32 else np.uint16)
+    rc = lib().orc_both_oob_rows(_c(leaf_tn, np.int32).ravel(), _c(oob_tn, np.uint8).ravel(), n, t, nleaf, fmt,
+                                 r0, r1, out.ctypes.data, threads)
+    assert rc == 0
+    return out
 
 
 def upper_rows(leaf_tn, oob_tn, nleaf, fmt=FMT_U16, scale=1.0, zp=0.0, r0=0, r1=None,

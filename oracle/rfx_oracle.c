@@ -402,6 +402,31 @@ int orc_upper_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T
     return rc;
 }
 
+int orc_both_oob_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int fmt,
+                      int64_t r0, int64_t r1, void* out, int threads) {
+    if (r0 < 0 || r1 > N || r0 > r1 || (fmt != 0 && fmt != 5)) return -1;
+    const int64_t e0 = tri_idx(N, r0, r0);
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int64_t i = r0; i < r1; ++i) {
+        for (int64_t j = i; j < N; ++j) {
+            uint32_t num = 0, den = 0;
+            if (j != i) {
+                for (int32_t t = 0; t < T; ++t) {
+                    if (!oob[(int64_t)t * N + i] || !oob[(int64_t)t * N + j]) continue;
+                    ++den;
+                    const int32_t a = leaf[(int64_t)t * N + i], b = leaf[(int64_t)t * N + j];
+                    if (a == b && a >= 0 && a < nleaf) ++num;
+                }
+            }
+            const int64_t e = tri_idx(N, i, j) - e0;
+            if (fmt == 5) ((uint16_t*)out)[e] = (uint16_t)num;
+            else ((float*)out)[e] = (j == i) ? 1.0f : (den > 0 ? (float)num / (float)den : 0.0f);
+        }
+    }
+    return 0;
+}
+
 void orc_upper_from_counts(const uint16_t* U, const int32_t* nout, int64_t N, int fmt, float scale,
                            float zp, void* out) {
     if (fmt == 3) memset(out, 0, (size_t)((N * (N + 1) / 2 + 1) / 2));

@@ -89,6 +89,16 @@ int orc_upper_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T
                    const int32_t* nout, int fmt, float scale, float zp, int64_t r0, int64_t r1,
                    void* out, int threads);
 
+/* The "both OOB" proximity (R randomForest's oob.prox; BASELINE config 1's
+ * prose), which the reference does not implement: for i != j
+ *   num_ij = #{t : oob_i(t), oob_j(t), leaf_i(t) == leaf_j(t), label valid}
+ *   den_ij = #{t : oob_i(t), oob_j(t)}
+ *   P_ij   = den_ij > 0 ? (float)num_ij / (float)den_ij : 0,   P_ii = 1.
+ * Rows [r0, r1) of the packed triangle in fmt 0 (F32, P) or 5 (U16, num;
+ * 0 on the diagonal).  A brute force over pairs and trees. */
+int orc_both_oob_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int fmt,
+                      int64_t r0, int64_t r1, void* out, int threads);
+
 /* The same, split so the per-tree buckets are built once and rows are
  * produced in several calls (the CPU baseline times them separately).
  * leaf/oob must outlive the index. */

@@ -76,6 +76,7 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_launches.restype = i64
     L.rfxp_upper_noalloc.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, C.c_int, C.c_float, C.c_float,
                                      i64, i64, vp]
+    L.rfxp_both_oob.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, C.c_int, i64, i64, vp]
     L.rfxp_upper_noalloc_workspace.argtypes = [i64, i32, i32, C.c_int]
     L.rfxp_upper_noalloc_workspace.restype = i64
     L.rfxp_set_reference.argtypes = [vp, vp, i64, i64, i64, i32, i32]
@@ -477,6 +478,23 @@ class Context:
             raise ValueError(f"output buffer has {have} bytes, rows need {need}")
         self._check(self._L.rfxp_upper(self.h, fmt, scale, zp, r0, r1, out.data_ptr()))
         return out
+
+    def both_oob(self, leaf, oob_words, n: int, t: int, nleaf: int, fmt: int = 0, r0: int = 0,
+                 r1: int | None = None, layout: str = "tree"):
+        """rfxp_both_oob: rows [r0, r1) of the both-OOB proximity triangle,
+        F32 (num / den) or U16 (num), as a new device tensor."""
+        import torch
+
+        assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
+        assert oob_words.dtype == torch.int32 and oob_words.is_cuda and oob_words.is_contiguous()
+        si, st = (1, n) if layout == "tree" else (t, 1)
+        r1 = n if r1 is None else r1
+        # a bad range is left for the library to reject
+        ne = upper_nbytes(FMT_U16, n, r0, r1) // 2 if 0 <= r0 <= r1 <= n else 1
+        out = torch.empty(max(ne, 1), dtype=torch.float32 if fmt == FMT_F32 else torch.int16, device=leaf.device)
+        self._check(self._L.rfxp_both_oob(self.h, leaf.data_ptr(), si, st, oob_words.data_ptr(), oob_words.shape[1],
+                                          n, t, nleaf, fmt, r0, r1, out.data_ptr()))
+        return out[:ne]
 
     def upper_noalloc(self, leaf, oob_words, n: int, t: int, nleaf: int, fmt: int, out, r0: int = 0,
                       r1: int | None = None, scale: float = 1.0, zp: float = 0.0, layout: str = "tree",

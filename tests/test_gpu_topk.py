@@ -39,6 +39,41 @@ def test_all_trees_topk_matches_oracle(gpu_ctx, n, t, nleaf, q, k):
     assert np.array_equal(got_i, want_i)
 
 
+def test_eight_bit_segments_with_wrapped_counts(gpu_ctx):
+    """Reference sets above 32768 samples with T <= 2048 are counted with 8-bit
+    counters in segments of 65536; T = 300 > 255 turns on the byte-sum check.
+    Copies of the queries planted in both halves of a segment, on the two
+    sides of a segment boundary and in the short last segment reach counts
+    of 300 (and 280 for a near copy), which wrap 8 bits and force the 16-bit
+    recount; with and without the exclusion of one planted copy.  Outlier
+    sums over the same segments too."""
+    rng = np.random.default_rng(31)
+    n, t, nleaf, q, k = 140_000, 300, 40, 6, 20
+    ref = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    qs = rng.integers(0, nleaf, size=(q, t), dtype=np.int32)
+    for pos in (1000, 40000, 100000, 139999):
+        ref[:, pos] = qs[0]
+    for pos in (65535, 65536):
+        ref[:, pos] = qs[1]
+    near = qs[3].copy()
+    near[:20] = (near[:20] + 1) % nleaf          # 280 of 300 trees match
+    ref[:, 70000] = near
+    ref[:, 131071] = qs[4]
+    got_i, got_c = run_topk(gpu_ctx, ref, nleaf, qs, k)
+    want_i, want_c = O.topk_all(ref, qs, k)
+    assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
+    assert got_c[0, :4].tolist() == [t] * 4 and got_c[3, 0] == 280
+    # exclude_base 40000: query 0 may not return its copy at 40000
+    idx, cnt = gpu_ctx.topk(dev(qs), k, exclude_base=40000)
+    want_i, want_c = O.topk_all(ref, qs, k, exclude=np.arange(40000, 40000 + q, dtype=np.int32))
+    assert np.array_equal(cnt.cpu().numpy().view(np.uint16), want_c)
+    assert np.array_equal(idx.cpu().numpy(), want_i)
+    raw = gpu_ctx.outlier_raw(dev(qs), exclude_base=40000, numerator=float(n - 1), isolated=n * 1e10)
+    want = O.outlier_raw(ref, nleaf, qs, exclude=np.arange(40000, 40000 + q, dtype=np.int32),
+                         numerator=float(n - 1), isolated=n * 1e10)
+    assert np.allclose(raw.cpu().numpy(), want, rtol=1e-6, atol=0)
+
+
 def test_invalid_labels_never_match(gpu_ctx):
     rng = np.random.default_rng(5)
     n, t, nleaf, q, k = 3000, 20, 11, 10, 30

@@ -684,3 +684,47 @@ def test_forest_leaves_feed_the_reference_proximity():
     term = np.where(np.take_along_axis(f["nodestatus"], leaf, axis=1) == -1, leaf, -1).astype(np.int32)
     got = O.upper_rows(term, (nin == 0).astype(np.uint8), maxnode, O.FMT_F32)
     assert np.array_equal(got, ps[np.triu_indices(n)].astype(np.float32))
+
+
+def both_oob_dense(leaf, oob, nleaf):
+    """Independent numpy evaluation of the both-OOB proximity: num and den as
+    (N, N) arrays from broadcast comparisons over the trees."""
+    valid = (leaf >= 0) & (leaf < nleaf)
+    o = oob.astype(bool)
+    both = o[:, :, None] & o[:, None, :]                       # (T, N, N)
+    same = (leaf[:, :, None] == leaf[:, None, :]) & valid[:, :, None] & valid[:, None, :]
+    return (both & same).sum(0), both.sum(0)
+
+
+@pytest.mark.parametrize("n,t,nleaf,r0,r1", [(1, 3, 2, 0, 1), (7, 33, 3, 0, 7), (60, 45, 5, 0, 60),
+                                             (61, 64, 4, 13, 50)])
+def test_both_oob_matches_independent_evaluation(n, t, nleaf, r0, r1):
+    rng = np.random.default_rng(n * 7 + t)
+    leaf = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    leaf[rng.random((t, n)) < 0.05] = -1
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    if n > 3:
+        oob[:, 2] = 0            # never OOB: den 0 with everyone
+        oob[:, 3] = 1            # always OOB
+    num, den = both_oob_dense(leaf, oob, nleaf)
+    iu = np.triu_indices(n)
+    keep = (iu[0] >= r0) & (iu[0] < r1)
+    i, j = iu[0][keep], iu[1][keep]
+    want_u16 = np.where(i == j, 0, num[i, j]).astype(np.uint16)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        p = np.where(den[i, j] > 0, num[i, j].astype(np.float32) / den[i, j].astype(np.float32), np.float32(0))
+    want_f32 = np.where(i == j, np.float32(1), p).astype(np.float32)
+    assert np.array_equal(O.both_oob_rows(leaf, oob, nleaf, O.FMT_U16, r0, r1), want_u16)
+    assert np.array_equal(O.both_oob_rows(leaf, oob, nleaf, O.FMT_F32, r0, r1), want_f32)
+
+
+def test_both_oob_hand_example():
+    """Three samples, four trees, worked by hand: samples 0 and 1 are both OOB
+    in trees 0, 1, 3 and share a leaf in trees 0 and 3 -> 2/3; sample 2 is OOB
+    only in tree 2, alone -> 0 with both."""
+    leaf = np.array([[0, 0, 1], [1, 0, 1], [0, 1, 0], [2, 2, 2]], np.int32)
+    oob = np.array([[1, 1, 0], [1, 1, 0], [0, 0, 1], [1, 1, 0]], np.uint8)
+    got = O.both_oob_rows(leaf, oob, 3, O.FMT_F32)
+    want = np.array([1.0, np.float32(2) / np.float32(3), 0.0, 1.0, 0.0, 1.0], np.float32)
+    assert np.array_equal(got, want)
+    assert np.array_equal(O.both_oob_rows(leaf, oob, 3, O.FMT_U16), np.array([0, 2, 0, 0, 0, 0], np.uint16))
