@@ -149,6 +149,7 @@ __global__ __launch_bounds__(256) void k_lr_y(const int32_t* leaf, int64_t si, i
     float acc[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+    const bool r8 = (r & 7) == 0;  // uniform
     int32_t t = 0;
     for (; t + 4 <= T; t += 4) {
         int32_t lv[4];
@@ -159,8 +160,19 @@ __global__ __launch_bounds__(256) void k_lr_y(const int32_t* leaf, int64_t si, i
         for (int u = 0; u < 4; ++u) {
             const bool ok = lv[u] >= 0 && lv[u] < L;
             const float* wr = W + ((int64_t)(t + u) * L + (ok ? lv[u] : 0)) * r;
+            if (r8) {
+                // whole 8-float slices, 16-byte aligned rows: two 16-byte loads
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+                if (ok && c0 < r) {
+                    a = *(const float4*)(wr + c0);
+                    b = *(const float4*)(wr + c0 + 4);
+                }
+                w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+                w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+            } else {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) w[u][c] = (ok && c0 + c < r) ? wr[c0 + c] : 0.f;
+                for (int c = 0; c < 8; ++c) w[u][c] = (ok && c0 + c < r) ? wr[c0 + c] : 0.f;
+            }
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
