@@ -58,7 +58,8 @@ def check_equal(got, want, what):
 
 @pytest.mark.parametrize("n,t,nleaf", [(1, 1, 1), (2, 3, 2), (37, 5, 3), (300, 64, 17),
                                        (2000, 100, 64), (4099, 257, 300),
-                                       (6000, 20, 5000)])   # 2L > 8192: the whole-tree packing path
+                                       (6000, 20, 5000),    # 2L > 8192: the whole-tree packing path
+                                       (3000, 300, 5000)])  # whole-tree path with the byte-sum check
 def test_counts_u16_match_oracle(gpu_ctx, n, t, nleaf):
     leaf, oob = make_forest(n * 31 + t, n, t, nleaf)
     keep = upload(gpu_ctx, leaf, oob, nleaf)
@@ -140,6 +141,54 @@ def test_counts_beyond_255_use_wide_counters(gpu_ctx, fmt):
     want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(1 / 255.0))
     check_equal(got, want, f"wide counters fmt {fmt}")
     assert gpu_ctx.upper_recounts() > 0   # the wrapped segments were recounted
+    del keep
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_U16, O.FMT_U8, O.FMT_F32])
+def test_many_trees_take_the_16bit_mode(gpu_ctx, fmt):
+    """T = 3200: a wave's share of trees is more counting steps than the 8-bit
+    byte-sum check covers, so every item is counted with 16-bit counters (the
+    launch's 16-bit mode); few leaves make counts in the hundreds."""
+    n, t, nleaf = 400, 3200, 3
+    leaf, oob = make_forest(41, n, t, nleaf, p_oob=0.45, p_invalid=0.01)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    want_u = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    assert want_u.max() > 600
+    got, guard = gpu_rows(gpu_ctx, fmt, 0, n, scale=np.float32(1 / 255.0))
+    check_equal(got, O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(1 / 255.0)), f"16-bit mode fmt {fmt}")
+    assert (guard == 0xA5).all()
+    del keep
+
+
+def test_split_rows_with_wrapped_8bit_counts(gpu_ctx):
+    """N = 80,000 is above one workgroup's column segment, so rows below
+    N - S are counted as two items.  T = 700 turns on the byte-sum check, and
+    samples 0..299 share sample 0's leaf in every tree: their pairs reach
+    counts near 325, which wrap 8 bits, inside both items of split rows.  Rows
+    on both sides of the split boundary and of the group are compared."""
+    import torch
+
+    n, t, nleaf = 80_000, 700, 400
+    leaf, oob = make_forest(43, n, t, nleaf, p_oob=0.368)
+    leaf[:, :300] = leaf[:, :1]
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    assert idx.rows(O.FMT_U16, 0, 1)[:300].max() > 255
+    split = n - 77_632       # S = 77,632 columns per item on gfx950 (two workgroups' LDS per CU)
+    for fmt in (O.FMT_U8, O.FMT_U16):
+        out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper(fmt, out, 0, n, scale=np.float32(1 / 255.0))
+        torch.cuda.synchronize()
+        for r0 in (0, 1, 150, 298, 299, 300, split - 2, split, 40_000, 79_990):
+            r1 = min(n, r0 + 3)
+            want = idx.rows(fmt, r0, r1, np.float32(1 / 255.0), np.float32(0.0))
+            e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
+            esz = np.dtype(O.FMT_DTYPE[fmt]).itemsize
+            got = out[e0 * esz:e1 * esz].cpu().numpy().view(O.FMT_DTYPE[fmt])
+            check_equal(got, want, f"fmt {fmt} rows {r0}:{r1}")
+        del out
+    assert gpu_ctx.upper_recounts() > 0
+    idx.close()
     del keep
 
 
