@@ -74,6 +74,20 @@ def test_eight_bit_segments_with_wrapped_counts(gpu_ctx):
     assert np.allclose(raw.cpu().numpy(), want, rtol=1e-6, atol=0)
 
 
+@pytest.mark.parametrize("n,t,nleaf", [(70_000, 1100, 30),    # 8-bit segments, more than 64 trees per wave
+                                       (40_000, 2100, 20)])   # above 2048 trees: 16-bit segments of 32768
+def test_many_trees(gpu_ctx, n, t, nleaf):
+    rng = np.random.default_rng(n + t)
+    ref = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    qs = rng.integers(0, nleaf, size=(5, t), dtype=np.int32)
+    ref[:, 33_000] = qs[0]       # counts of t wrap 8 bits
+    ref[:, 65_535 if n > 65_535 else 32_767] = qs[1]
+    got_i, got_c = run_topk(gpu_ctx, ref, nleaf, qs, 12)
+    want_i, want_c = O.topk_all(ref, qs, 12)
+    assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
+    assert got_c[0, 0] == t
+
+
 def test_invalid_labels_never_match(gpu_ctx):
     rng = np.random.default_rng(5)
     n, t, nleaf, q, k = 3000, 20, 11, 10, 30
