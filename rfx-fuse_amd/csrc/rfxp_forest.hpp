@@ -91,6 +91,7 @@ struct ForestSizes {
     int64_t ldr = 0;
     int32_t lmax = 0;
     bool part_path = false;  // per-part packing (forest mode, 2L <= 8192)
+    bool seg_path = false;   // per-segment packing (reference mode, L <= 16384)
     bool lds_path = false;   // whole-tree histogram in LDS
 };
 ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds);

@@ -279,6 +279,96 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 }
 
 // ---------------------------------------------------------------------------
+// Reference-set path (buckets b = leaf * nseg + segment, L <= SEG_MAX_L): the
+// samples of bucket (l, s) all lie in segment s, so one workgroup per
+// (tree, segment) sees every member of its L buckets.
+//   k_seg_hist    (tree, segment): LDS histogram over the leaves -> the
+//                 bucket counts cnt[t][l * nseg + s];
+//   k_seg_scan    (tree): exclusive scan of the counts into the offsets;
+//   k_seg_scatter (tree, segment): LDS cursors from the offsets; each
+//                 member goes straight to its slot in mem[t].
+// Every leaf label is read twice in all (once per pass), instead of once per
+// member window of the whole-tree path.  The segments of a tree run
+// together on one XCD: the buckets (l, s) and (l, s + 1) are neighbours in
+// mem[t], so the scattered member writes of a tree merge in that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int SEG_MAX_L = 16384;  // LDS counters per workgroup (64 KB)
+
+// (tree, segment) of a k_seg_* workgroup: consecutive dispatch slots of one
+// XCD walk the segments of a tree, trees x, x + 8, x + 16, ... on XCD x.
+__device__ __forceinline__ void seg_of_block(uint32_t bid, int32_t nseg, int32_t& t, int32_t& sg) {
+    const uint32_t xcd = bid & 7, slot = bid >> 3;
+    t = (int32_t)(xcd + 8 * (slot / (uint32_t)nseg));
+    sg = (int32_t)(slot % (uint32_t)nseg);
+}
+
+__global__ __launch_bounds__(PACK_THREADS) void k_seg_hist(LeafView v, uint32_t* cnt_all) {
+    extern __shared__ uint32_t sh[];
+    int32_t t, sg;
+    seg_of_block(blockIdx.x, v.nseg, t, sg);
+    if (t >= v.T) return;
+    for (int32_t l = threadIdx.x; l < v.L; l += PACK_THREADS) sh[l] = 0u;
+    __syncthreads();
+    const int64_t i0 = (int64_t)sg << v.seg_shift, i1 = min(v.N, i0 + ((int64_t)1 << v.seg_shift));
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    for (int64_t base = i0; base < i1; base += round) {
+        int32_t lv[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            lv[k] = i < i1 ? v.leaf[i * v.si + (int64_t)t * v.st] : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k)
+            if (lv[k] >= 0 && lv[k] < v.L) atomicAdd(&sh[lv[k]], 1u);
+    }
+    __syncthreads();
+    const int32_t nb = view_buckets(v);
+    uint32_t* cnt = cnt_all + (int64_t)t * (nb + 1);
+    for (int32_t l = threadIdx.x; l < v.L; l += PACK_THREADS) cnt[(int64_t)l * v.nseg + sg] = sh[l];
+    // the padding bucket of an odd L * nseg is empty
+    if (sg == 0 && threadIdx.x == 0 && nb > v.L * v.nseg) cnt[nb - 1] = 0u;
+}
+
+__global__ __launch_bounds__(PACK_THREADS) void k_seg_scan(int32_t nb, int32_t T, uint32_t* cnt_all,
+                                                           int32_t* goff_all) {
+    __shared__ uint32_t part[PACK_THREADS];
+    const int32_t t = blockIdx.x;
+    if (t >= T) return;
+    uint32_t* cnt = cnt_all + (int64_t)t * (nb + 1);
+    int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    scan_offsets(cnt, cnt, nb, part, goff);
+}
+
+__global__ __launch_bounds__(PACK_THREADS) void k_seg_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem) {
+    extern __shared__ uint32_t cur[];
+    int32_t t, sg;
+    seg_of_block(blockIdx.x, v.nseg, t, sg);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    for (int32_t l = threadIdx.x; l < v.L; l += PACK_THREADS) cur[l] = (uint32_t)goff[(int64_t)l * v.nseg + sg];
+    __syncthreads();
+    uint32_t* memt = mem + (int64_t)t * v.N;
+    const int64_t i0 = (int64_t)sg << v.seg_shift, i1 = min(v.N, i0 + ((int64_t)1 << v.seg_shift));
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    for (int64_t base = i0; base < i1; base += round) {
+        int32_t lv[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            lv[k] = i < i1 ? v.leaf[i * v.si + (int64_t)t * v.st] : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            if (lv[k] < 0 || lv[k] >= v.L) continue;
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            memt[atomicAdd(&cur[lv[k]], 1u)] = (uint32_t)(i + 1);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Forest path with per-part cursors (2L <= PART_MAX_NB): each tree's samples
 // are cut into PACK_PARTS contiguous parts.
 //   k_part_hist    (tree, part): LDS histogram of the part's buckets -> ph,
@@ -588,6 +678,7 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     z.ldr = ((int64_t)T + 15) / 16 * 16;
     z.lmax = (int32_t)(N / REC_LONG + 1);
     z.part_path = forest && nb <= PART_MAX_NB;
+    z.seg_path = !forest && v.L <= SEG_MAX_L;
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
     z.lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= max_lds;
     z.n[FB_OFF] = (size_t)T * (nb + 1);
@@ -597,6 +688,8 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
         z.n[FB_SCRATCH] = (size_t)T * PACK_PARTS * nb;
         z.n[FB_ROFFT] = (size_t)T * N;
         z.n[FB_RLENT] = (size_t)T * N;
+    } else if (z.seg_path) {
+        z.n[FB_SCRATCH] = (size_t)T * (nb + 1);
     } else {
         z.n[FB_KEY16] = nb < 0xffff ? (size_t)T * ldk : 0;
         z.n[FB_SCRATCH] = (size_t)T * 2 * (nb + 1);
@@ -657,6 +750,35 @@ size_t forest_elem_bytes(int k) {
 static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb);
 static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb);
 
+// Reference-set path (see k_seg_hist).
+static int pack_reference_segments(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
+    hipStream_t s = ctx->stream;
+    const int32_t nb = view_buckets(v);
+    const unsigned grid = (unsigned)(8 * cdiv(v.T, 8) * v.nseg);
+    const size_t lds = (size_t)v.L * 4;
+    if (lds > 32768) {
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_seg_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds));
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_seg_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds));
+    }
+    {
+        LaunchTimer tm(ctx, "pack_hist");
+        hipLaunchKernelGGL(k_seg_hist, dim3(grid), dim3(PACK_THREADS), lds, s, v, fb.scratch);
+    }
+    if (int rc = check_launch(ctx, "k_seg_hist")) return rc;
+    {
+        LaunchTimer tm(ctx, "pack_scan");
+        hipLaunchKernelGGL(k_seg_scan, dim3((unsigned)v.T), dim3(PACK_THREADS), 0, s, nb, v.T, fb.scratch, fb.off);
+    }
+    if (int rc = check_launch(ctx, "k_seg_scan")) return rc;
+    {
+        LaunchTimer tm(ctx, "pack_scatter");
+        hipLaunchKernelGGL(k_seg_scatter, dim3(grid), dim3(PACK_THREADS), lds, s, v, (const int32_t*)fb.off, fb.mem);
+    }
+    return check_launch(ctx, "k_seg_scatter");
+}
+
 // The table of long buckets (forest mode), once the offsets are known.
 static int pack_long_runs(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
     const int32_t nb = view_buckets(v);
@@ -690,6 +812,7 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
         if (int rc = pack_long_runs(ctx, v, fb)) return rc;
         return pack_nout(ctx, v, nout_in, fb);
     }
+    if (z.seg_path) return pack_reference_segments(ctx, v, fb);
     // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
     const unsigned grid = (unsigned)(cdiv(T, 128) * 128);
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
