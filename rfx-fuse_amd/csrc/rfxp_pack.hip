@@ -380,7 +380,10 @@ __global__ __launch_bounds__(PACK_THREADS) void k_seg_scatter(LeafView v, const 
 //                  to the tree-major arrays.  The parts of a tree run at
 //                  once on one XCD, eight trees per XCD: the 4-byte member
 //                  writes of those trees (8 x 4N bytes) merge in that XCD's
-//                  L2 before they reach HBM;
+//                  L2 before they reach HBM while that region fits the L2;
+//   k_part_scatter_sorted: the same, with the part's members sorted by
+//                  bucket in LDS first and written in bucket order (larger
+//                  forests, where the direct writes no longer merge);
 //   k_rec_transpose: tree-major records -> sample-major.
 // ---------------------------------------------------------------------------
 constexpr int PACK_PARTS = 8;
@@ -544,6 +547,127 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             ro[i] = o;
             rl[i] = (uint16_t)len;
         }
+    }
+}
+
+// k_part_scatter with the member writes in bucket order.  The part's members
+// are first counting-sorted by bucket in LDS, as 16-bit offsets from the
+// part's first sample; then thread k writes staged member k to its slot.
+// Consecutive lanes thus write consecutive slots of a bucket's part range,
+// and the parts of a tree, which run at once on one XCD, sweep mem[t] in the
+// same bucket order, so the lines they share fill up in L2 before they are
+// written back (random 4-byte stores leave most lines partial).  Parts of at
+// most PART_SORT_MAX samples.  The records are written as in k_part_scatter.
+//
+// LDS: lcur[nb] (the exclusive prefix of the part's bucket counts, used as
+// cursors, which leaves each bucket's inclusive end), off[nb + 1], ps0[nb],
+// wsum[16], stg[part size] (uint16).
+constexpr int64_t PART_SORT_MAX = 65536;
+constexpr int64_t PART_SORT_MIN_N = 32768;
+constexpr int32_t PART_SORT_MAX_NB = 4096;
+
+static size_t part_sorted_lds(int32_t nb, int64_t part) {
+    return (size_t)(3 * nb + 1 + 16) * 4 + (size_t)((part + 1) / 2) * 4;
+}
+
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted(
+    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
+    uint32_t* roffT, uint16_t* rlenT) {
+    extern __shared__ uint32_t sh[];
+    int32_t t;
+    int p;
+    part_of_block(blockIdx.x, t, p);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    uint32_t* lcur = sh;
+    uint32_t* off = sh + nb;
+    uint32_t* ps0 = off + nb + 1;
+    uint32_t* wsum = ps0 + nb;
+    uint16_t* stg = (uint16_t*)(wsum + 16);
+    const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
+    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    // the part's count in bucket b runs up to the next part's start there
+    // (the bucket's end for the last part)
+    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)goff + 1 : pp + nb;
+    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
+        off[b] = (uint32_t)goff[b];
+        if (b < nb) {
+            const uint32_t s = pp[b];
+            ps0[b] = s;
+            lcur[b] = pn[b] - s;
+        }
+    }
+    __syncthreads();
+    // exclusive scan of the counts: thread tid takes buckets [tid*E, tid*E + E)
+    {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int32_t E = (nb + PACK_THREADS - 1) / PACK_THREADS;
+        const int32_t b0 = min(nb, tid * E), b1 = min(nb, b0 + E);
+        uint32_t s = 0;
+        for (int32_t b = b0; b < b1; ++b) s += lcur[b];
+        uint32_t incl = s;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t run = incl - s;
+        for (int w = 0; w < wave; ++w) run += wsum[w];
+        for (int32_t b = b0; b < b1; ++b) {
+            const uint32_t c = lcur[b];
+            lcur[b] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    const int64_t N = v.N;
+    const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
+    uint32_t* ro = roffT + (int64_t)t * N;
+    uint16_t* rl = rlenT + (int64_t)t * N;
+    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const uint16_t* kt = key16 + (int64_t)t * ldk;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    for (int64_t base = i0; base < i1; base += round) {
+        uint32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0x10000u;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            const uint32_t b = key[k];
+            if (b == 0x10000u) continue;
+            uint32_t o = 0u, len = 0u;
+            if (b != 0xffffu) {
+                stg[atomicAdd(&lcur[b], 1u)] = (uint16_t)(i - i0);
+                // the run of (i, t), as in k_part_scatter
+                const uint32_t ob = b ^ 1u;
+                const uint32_t rs = ps0[ob], rem = off[ob + 1] - rs;
+                o = (tbase + rs) * 4u;
+                len = min(rem, REC_LONG) * 4u;
+            }
+            ro[i] = o;
+            rl[i] = (uint16_t)len;
+        }
+    }
+    __syncthreads();
+    // staged member k belongs to the first bucket b with lcur[b] > k
+    const uint32_t total = nb > 0 ? lcur[nb - 1] : 0u;
+    uint32_t* memt = mem + (int64_t)t * N;
+    const uint32_t id0 = (uint32_t)i0 + 1u;
+    for (uint32_t k = threadIdx.x; k < total; k += PACK_THREADS) {
+        int32_t lo = 0, hi = nb - 1;
+        while (lo < hi) {
+            const int32_t mid = (lo + hi) >> 1;
+            if (lcur[mid] > k) hi = mid;
+            else lo = mid + 1;
+        }
+        const uint32_t first = lo > 0 ? lcur[lo - 1] : 0u;
+        memt[ps0[lo] + (k - first)] = id0 + (uint32_t)stg[k];
     }
 }
 
@@ -867,13 +991,23 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     const int64_t ldk = cdiv(N, 8) * 8;
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
     const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
-    const size_t lds_h = (size_t)nb * 4, lds_s = (size_t)(3 * nb + 1) * 4;
+    const size_t lds_h = (size_t)nb * 4;
+    // Bucket-ordered member writes when the part's staging fits in LDS, for
+    // forests whose member regions outgrow the L2 (8 trees x 4N bytes in
+    // flight per XCD) and with at most PART_SORT_MAX_NB buckets: measured
+    // at T = 500, N = 50,000-400,000 and 2L <= 4,096 it is 1.1-2.6x faster
+    // than k_part_scatter; at 2L = 8,192 its tables leave one workgroup per
+    // CU and it is slower.
+    const int64_t part = cdiv(N, PACK_PARTS);
+    const bool sorted = N >= PART_SORT_MIN_N && nb <= PART_SORT_MAX_NB && part <= PART_SORT_MAX &&
+                        part_sorted_lds(nb, part) <= (size_t)ctx->max_lds;
+    const void* scatter = sorted ? (const void*)k_part_scatter_sorted : (const void*)k_part_scatter;
+    const size_t lds_s = sorted ? part_sorted_lds(nb, part) : (size_t)(3 * nb + 1) * 4;
     if (lds_h > 32768)
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds_h));
     if (lds_s > 32768)
-        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          (int)lds_s));
+        RFXP_HIP(ctx, hipFuncSetAttribute(scatter, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_s));
     {
         LaunchTimer tm(ctx, "pack_hist");
         hipLaunchKernelGGL(k_part_hist, dim3(grid), dim3(PACK_THREADS), lds_h, s, v, fb.scratch, fb.key16, ldk);
@@ -886,8 +1020,14 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
-        hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v, (const uint32_t*)fb.scratch,
-                           (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk, fb.mem, fb.roffT, fb.rlenT);
+        if (sorted)
+            hipLaunchKernelGGL(k_part_scatter_sorted, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
+                               fb.mem, fb.roffT, fb.rlenT);
+        else
+            hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
+                               fb.mem, fb.roffT, fb.rlenT);
     }
     if (int rc = check_launch(ctx, "k_part_scatter")) return rc;
     {
