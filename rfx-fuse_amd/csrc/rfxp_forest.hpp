@@ -69,6 +69,31 @@ __device__ __forceinline__ int32_t bucket_of(const LeafView& v, int64_t i, int32
     return 2 * l + (int32_t)((w >> (i & 31)) & 1u);
 }
 
+// bucket_of in two steps, so that a kernel can issue the loads of many
+// samples before it uses any of them (a branch on a loaded label between the
+// two loads would make every sample wait for its own label).  key_load reads
+// the label and, in forest mode, the OOB word of sample i (a valid index: the
+// caller clamps it); key_bucket turns them into the bucket id, -1 for an
+// invalid label.
+struct KeyLoad {
+    int32_t l;
+    uint32_t w;
+};
+
+__device__ __forceinline__ KeyLoad key_load(const LeafView& v, int64_t i, int32_t t) {
+    KeyLoad k;
+    k.l = v.leaf[i * v.si + (int64_t)t * v.st];
+    k.w = v.nseg > 0 ? 0u : v.oob[(int64_t)t * v.old + (i >> 5)];
+    return k;
+}
+
+__device__ __forceinline__ int32_t key_bucket(const LeafView& v, KeyLoad k, int64_t i) {
+    const uint32_t l = (uint32_t)k.l;
+    const uint32_t b = v.nseg > 0 ? l * (uint32_t)v.nseg + (uint32_t)(i >> v.seg_shift)
+                                  : 2u * l + ((k.w >> (i & 31)) & 1u);
+    return (k.l >= 0 && k.l < v.L) ? (int32_t)b : -1;
+}
+
 // Buckets per tree of a view (even: packing windows split at even buckets).
 __host__ __device__ inline int32_t view_buckets(const LeafView& v) {
     if (v.nseg == 0) return 2 * v.L;

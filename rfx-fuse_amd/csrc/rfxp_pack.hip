@@ -83,11 +83,17 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     uint16_t* kt = key16 ? key16 + (int64_t)t * ldk : nullptr;
     for (int64_t base = 0; base < N; base += round) {
+        KeyLoad ld[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            ld[k] = key_load(v, i < N ? i : 0, t);
+        }
         int32_t key[PACK_KR];
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
             const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < N ? bucket_of(v, i, t) : -1;
+            key[k] = i < N ? key_bucket(v, ld[k], i) : -1;
         }
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
@@ -127,34 +133,49 @@ __global__ __launch_bounds__(256) void k_records(LeafView v, const uint16_t* key
     for (int k = threadIdx.x; k < 64 * 4; k += 256) {
         const int r = k >> 2, c0 = (k & 3) * 16;
         const int32_t t = t0 + r;
+        // loads at clamped indices first, then the bucket ids, then the
+        // offset lookups (bucket 0's for empty records), then the records
+        const int32_t tc = t < T ? t : 0;
         int32_t key[16];
+        if (key16) {
+            uint32_t kk[16];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const int64_t i = i0 + c0 + c;
-            int32_t b = -1;
-            if (t < T && i < N) {
-                if (key16) {
-                    const uint16_t kk = key16[(int64_t)t * ldk + i];
-                    b = kk == 0xffffu ? -1 : (int32_t)kk;
-                } else {
-                    b = bucket_of(v, i, t);
-                }
+            for (int c = 0; c < 16; ++c) {
+                const int64_t i = i0 + c0 + c;
+                kk[c] = key16[(int64_t)tc * ldk + (i < N ? i : 0)];
             }
-            key[c] = b;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const int64_t i = i0 + c0 + c;
+                key[c] = (t < T && i < N && kk[c] != 0xffffu) ? (int32_t)kk[c] : -1;
+            }
+        } else {
+            KeyLoad ld[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const int64_t i = i0 + c0 + c;
+                ld[c] = key_load(v, i < N ? i : 0, tc);
+            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const int64_t i = i0 + c0 + c;
+                key[c] = (t < T && i < N) ? key_bucket(v, ld[c], i) : -1;
+            }
         }
-        const int32_t* off = goff_all + (int64_t)(t < T ? t : 0) * (nb + 1);
+        const int32_t* off = goff_all + (int64_t)tc * (nb + 1);
         const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+        uint32_t st[16], en[16];
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            uint32_t o = 0u, len = 0u;
-            if (key[c] >= 0) {
-                const int32_t ob = key[c] ^ 1;
-                const uint32_t s = (uint32_t)off[ob];
-                o = (tbase + s) * 4u;
-                len = min((uint32_t)off[ob + 1] - s, REC_LONG) * 4u;
-            }
-            to[r][c0 + c] = o;
-            tl[r][c0 + c] = (uint16_t)len;
+            const int32_t ob = key[c] >= 0 ? key[c] ^ 1 : 0;
+            st[c] = (uint32_t)off[ob];
+            en[c] = (uint32_t)off[ob + 1];
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const bool ok = key[c] >= 0;
+            to[r][c0 + c] = ok ? (tbase + st[c]) * 4u : 0u;
+            tl[r][c0 + c] = ok ? (uint16_t)(min(en[c] - st[c], REC_LONG) * 4u) : (uint16_t)0;
         }
     }
     __syncthreads();
@@ -263,11 +284,17 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     } else {
         const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
         for (int64_t base = 0; base < N; base += round) {
+            KeyLoad ld[PACK_KR];
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                ld[k] = key_load(v, i < N ? i : 0, t);
+            }
             int32_t key[PACK_KR];
 #pragma unroll
             for (int k = 0; k < PACK_KR; ++k) {
                 const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-                key[k] = i < N ? bucket_of(v, i, t) : -1;
+                key[k] = i < N ? key_bucket(v, ld[k], i) : -1;
             }
 #pragma unroll
             for (int k = 0; k < PACK_KR; ++k) place(base + (int64_t)k * PACK_THREADS + threadIdx.x, key[k]);
@@ -416,11 +443,18 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     uint16_t* kt = key16 + (int64_t)t * ldk;
     for (int64_t base = i0; base < i1; base += round) {
+        // every load of the round first (indices past the part read sample i0)
+        KeyLoad ld[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            ld[k] = key_load(v, i < i1 ? i : i0, t);
+        }
         int32_t key[PACK_KR];
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
             const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < i1 ? bucket_of(v, i, t) : -2;
+            key[k] = i < i1 ? key_bucket(v, ld[k], i) : -2;
         }
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
@@ -678,18 +712,26 @@ __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, co
     __shared__ uint16_t tl[64][66];
     const int64_t i0 = (int64_t)blockIdx.x * 64;
     const int32_t t0 = blockIdx.y * 64;
-    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
+    // all 16 loads of a thread first, at clamped indices
+    uint32_t o[16];
+    uint16_t l[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int k = threadIdx.x + 256 * q;
         const int r = k >> 6, c = k & 63;  // r: tree, c: sample
         const int64_t i = i0 + c;
         const int32_t t = t0 + r;
-        uint32_t o = 0u;
-        uint16_t l = 0;
-        if (i < N && t < T) {
-            o = roffT[(int64_t)t * N + i];
-            l = rlenT[(int64_t)t * N + i];
-        }
-        to[r][c] = o;
-        tl[r][c] = l;
+        const int64_t e = (i < N && t < T) ? (int64_t)t * N + i : 0;
+        o[q] = roffT[e];
+        l[q] = rlenT[e];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int k = threadIdx.x + 256 * q;
+        const int r = k >> 6, c = k & 63;
+        const bool ok = i0 + c < N && t0 + r < T;
+        to[r][c] = ok ? o[q] : 0u;
+        tl[r][c] = ok ? l[q] : (uint16_t)0;
     }
     __syncthreads();
     for (int k = threadIdx.x; k < 64 * 64; k += 256) {
