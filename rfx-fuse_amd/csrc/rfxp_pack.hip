@@ -705,6 +705,138 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     }
 }
 
+// k_part_scatter_sorted with 4-byte staging entries (bucket << 16 | offset
+// in the part), so that staged member k finds its slot without a search:
+// slot = ps0[b] + (k - start of b's staged run).  To keep the LDS at two
+// workgroups per CU at part sizes like 12,500 with 4,096 buckets:
+//   - the local cursors are 16-bit halves of 32-bit words counting down from
+//     each bucket's end, so that they end at its start (counts stay below
+//     2^16: parts of at most PART_SORT4_MAX samples);
+//   - the records are written in a pass of their own over the part's keys,
+//     after which the staging area reuses the bucket-offset table's LDS
+//     (the second pass reads the keys again, from L2).
+// LDS: ps0[nb], wsum[16], lc[nb] (uint16, padded to a word), then off[nb + 1]
+// (records pass) overlaid by stg[part] (staging and writes).
+constexpr int64_t PART_SORT4_MAX = 65535;
+
+static size_t part_sorted4_lds(int32_t nb, int64_t part) {
+    const int64_t un = std::max<int64_t>(nb + 1, part);
+    return (size_t)(nb + 16 + (nb + 1) / 2 + un) * 4;
+}
+
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted4(
+    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
+    uint32_t* roffT, uint16_t* rlenT) {
+    extern __shared__ uint32_t sh[];
+    int32_t t;
+    int p;
+    part_of_block(blockIdx.x, t, p);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    uint32_t* ps0 = sh;
+    uint32_t* wsum = ps0 + nb;
+    uint16_t* lc = (uint16_t*)(wsum + 16);
+    uint32_t* lc32 = wsum + 16;
+    uint32_t* off = wsum + 16 + (nb + 1) / 2;
+    uint32_t* stg = off;
+    const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
+    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    // the part's count in bucket b runs up to the next part's start there
+    // (the bucket's end for the last part)
+    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)goff + 1 : pp + nb;
+    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
+        off[b] = (uint32_t)goff[b];
+        if (b < nb) {
+            const uint32_t s = pp[b];
+            ps0[b] = s;
+            lc[b] = (uint16_t)(pn[b] - s);
+        }
+    }
+    __syncthreads();
+    // inclusive scan of the counts: thread tid takes buckets [tid*E, tid*E + E)
+    {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int32_t E = (nb + PACK_THREADS - 1) / PACK_THREADS;
+        const int32_t b0 = min(nb, tid * E), b1 = min(nb, b0 + E);
+        uint32_t s = 0;
+        for (int32_t b = b0; b < b1; ++b) s += lc[b];
+        uint32_t incl = s;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t run = incl - s;
+        for (int w = 0; w < wave; ++w) run += wsum[w];
+        for (int32_t b = b0; b < b1; ++b) {
+            run += lc[b];
+            lc[b] = (uint16_t)run;
+        }
+    }
+    const int64_t N = v.N;
+    const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
+    const uint16_t* kt = key16 + (int64_t)t * ldk;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    // records pass
+    {
+        uint32_t* ro = roffT + (int64_t)t * N;
+        uint16_t* rl = rlenT + (int64_t)t * N;
+        const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+        for (int64_t base = i0; base < i1; base += round) {
+            uint32_t key[PACK_KR];
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                key[k] = (uint32_t)kt[i < i1 ? i : i0];
+            }
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                if (i >= i1) continue;
+                const uint32_t b = key[k];
+                // the run of (i, t), as in k_part_scatter
+                const uint32_t ob = (b ^ 1u) & 0xffffu;
+                const uint32_t rs = ps0[ob < (uint32_t)nb ? ob : 0u];
+                const uint32_t rem = off[ob < (uint32_t)nb ? ob + 1u : 0u] - rs;
+                const bool ok = b != 0xffffu;
+                ro[i] = ok ? (tbase + rs) * 4u : 0u;
+                rl[i] = ok ? (uint16_t)(min(rem, REC_LONG) * 4u) : (uint16_t)0;
+            }
+        }
+    }
+    __syncthreads();  // off is dead from here on: stg overlays it
+    for (int64_t base = i0; base < i1; base += round) {
+        uint32_t key[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const uint32_t b = key[k];
+            if (b == 0xffffu) continue;
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            const uint32_t sh16 = (b & 1u) * 16u;
+            const uint32_t old = atomicSub(&lc32[b >> 1], 1u << sh16);
+            stg[((old >> sh16) & 0xffffu) - 1u] = (b << 16) | (uint32_t)(i - i0);
+        }
+    }
+    __syncthreads();
+    // lc[b] is now the start of bucket b's staged run
+    uint32_t nval = 0;
+    for (int w = 0; w < PACK_THREADS / 64; ++w) nval += wsum[w];
+    uint32_t* memt = mem + (int64_t)t * N;
+    const uint32_t id0 = (uint32_t)i0 + 1u;
+    for (uint32_t k = threadIdx.x; k < nval; k += PACK_THREADS) {
+        const uint32_t e = stg[k];
+        const uint32_t b = e >> 16;
+        memt[ps0[b] + (k - (uint32_t)lc[b])] = id0 + (e & 0xffffu);
+    }
+}
+
 // [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
 __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint16_t* rlenT, int64_t N,
                                                       int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen) {
@@ -1024,6 +1156,24 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     return pack_nout(ctx, v, nout_in, fb);
 }
 
+// Member scatter of the per-part path (RFXP_PACK_PARTS_*).  Bucket-ordered
+// writes for forests whose member regions outgrow the L2 (8 trees x 4N bytes
+// in flight per XCD), when the part's staging fits in LDS: of the two sorted
+// kernels, the one with more workgroups per CU (at most two), the 4-byte
+// staging on a tie; the 2-byte one only up to PART_SORT_MAX_NB buckets (its
+// search gets slower with more).  Measured at T = 500 and N = 50,000-400,000
+// they are up to 2.6x faster than k_part_scatter; below N = 32,768 the
+// direct writes merge in L2.
+static int part_scatter_kind(int64_t N, int32_t nb, int max_lds) {
+    const int64_t part = cdiv(N, PACK_PARTS);
+    if (N < PART_SORT_MIN_N) return RFXP_PACK_PARTS_DIRECT;
+    auto wgs_per_cu = [&](size_t lds) { return lds * 2 <= (size_t)max_lds ? 2 : lds <= (size_t)max_lds ? 1 : 0; };
+    const int occ4 = part <= PART_SORT4_MAX ? wgs_per_cu(part_sorted4_lds(nb, part)) : 0;
+    const int occ2 = nb <= PART_SORT_MAX_NB && part <= PART_SORT_MAX ? wgs_per_cu(part_sorted_lds(nb, part)) : 0;
+    if (occ4 > 0 && occ4 >= occ2) return RFXP_PACK_PARTS_SORTED4;
+    return occ2 > 0 ? RFXP_PACK_PARTS_SORTED2 : RFXP_PACK_PARTS_DIRECT;
+}
+
 // Forest path for 2L <= PART_MAX_NB (see k_part_hist).
 static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
@@ -1034,17 +1184,15 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
     const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
     const size_t lds_h = (size_t)nb * 4;
-    // Bucket-ordered member writes when the part's staging fits in LDS, for
-    // forests whose member regions outgrow the L2 (8 trees x 4N bytes in
-    // flight per XCD) and with at most PART_SORT_MAX_NB buckets: measured
-    // at T = 500, N = 50,000-400,000 and 2L <= 4,096 it is 1.1-2.6x faster
-    // than k_part_scatter; at 2L = 8,192 its tables leave one workgroup per
-    // CU and it is slower.
     const int64_t part = cdiv(N, PACK_PARTS);
-    const bool sorted = N >= PART_SORT_MIN_N && nb <= PART_SORT_MAX_NB && part <= PART_SORT_MAX &&
-                        part_sorted_lds(nb, part) <= (size_t)ctx->max_lds;
-    const void* scatter = sorted ? (const void*)k_part_scatter_sorted : (const void*)k_part_scatter;
-    const size_t lds_s = sorted ? part_sorted_lds(nb, part) : (size_t)(3 * nb + 1) * 4;
+    const int kind = part_scatter_kind(N, nb, ctx->max_lds);
+    const bool sorted4 = kind == RFXP_PACK_PARTS_SORTED4, sorted = kind == RFXP_PACK_PARTS_SORTED2;
+    const void* scatter = sorted4  ? (const void*)k_part_scatter_sorted4
+                          : sorted ? (const void*)k_part_scatter_sorted
+                                   : (const void*)k_part_scatter;
+    const size_t lds_s = sorted4  ? part_sorted4_lds(nb, part)
+                         : sorted ? part_sorted_lds(nb, part)
+                                  : (size_t)(3 * nb + 1) * 4;
     if (lds_h > 32768)
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds_h));
@@ -1062,7 +1210,11 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
-        if (sorted)
+        if (sorted4)
+            hipLaunchKernelGGL(k_part_scatter_sorted4, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
+                               fb.mem, fb.roffT, fb.rlenT);
+        else if (sorted)
             hipLaunchKernelGGL(k_part_scatter_sorted, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
                                (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
                                fb.mem, fb.roffT, fb.rlenT);
@@ -1102,3 +1254,15 @@ static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, c
 }
 
 }  // namespace rfxp
+
+extern "C" int rfxp_pack_plan(int64_t N, int32_t T, int32_t nleaf, int32_t max_lds) {
+    using namespace rfxp;
+    if (N < 1 || N > MAX_FOREST_N || T < 1 || nleaf < 1 || nleaf > 0x3fffffff || max_lds < 1) return -1;
+    LeafView v{};
+    v.N = N;
+    v.T = T;
+    v.L = nleaf;
+    const ForestSizes z = forest_sizes(v, true, max_lds);
+    if (z.part_path) return part_scatter_kind(N, view_buckets(v), max_lds);
+    return z.lds_path ? RFXP_PACK_TREE_LDS : RFXP_PACK_TREE_GLOBAL;
+}

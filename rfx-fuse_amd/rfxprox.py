@@ -74,6 +74,8 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_work_item.restype = i64
     L.rfxp_upper_launches.argtypes = [i64]
     L.rfxp_upper_launches.restype = i64
+    L.rfxp_pack_plan.argtypes = [i64, i32, i32, i32]
+    L.rfxp_pack_plan.restype = C.c_int
     L.rfxp_upper_noalloc.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, vp, C.c_int, C.c_float, C.c_float,
                                      i64, i64, vp]
     L.rfxp_both_oob.argtypes = [vp, vp, i64, i64, vp, i64, i64, i32, i32, C.c_int, i64, i64, vp]
@@ -120,6 +122,19 @@ def upper_nbytes(fmt: int, n: int, r0: int = 0, r1: int | None = None) -> int:
     v = load().rfxp_upper_nbytes(fmt, n, r0, r1)
     if v < 0:
         raise ValueError("bad format or row range")
+    return v
+
+
+PACK_PARTS_DIRECT, PACK_PARTS_SORTED2, PACK_PARTS_SORTED4, PACK_TREE_LDS, PACK_TREE_GLOBAL = range(5)
+GFX950_MAX_LDS = 163840
+
+
+def pack_plan(n: int, t: int, nleaf: int, max_lds: int = GFX950_MAX_LDS) -> int:
+    """Packing path rfxp_set_forest takes for a forest of this shape
+    (PACK_* codes; host only)."""
+    v = load().rfxp_pack_plan(n, t, nleaf, max_lds)
+    if v < 0:
+        raise ValueError("bad arguments")
     return v
 
 

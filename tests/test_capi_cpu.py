@@ -268,3 +268,22 @@ def test_library_exports_lowrank_class_with_reference_signatures():
     ]
     for w in want:
         assert w in out, w
+
+
+@pytest.mark.parametrize("args,plan", [
+    ((100_000, 500, 2048), R.PACK_PARTS_SORTED4),   # C3: 74 KB of LDS, two workgroups per CU
+    ((20_000, 500, 4096), R.PACK_PARTS_DIRECT),     # C2: N below 32,768
+    ((200_000, 6, 256), R.PACK_PARTS_SORTED2),
+    ((400_000, 500, 2048), R.PACK_PARTS_SORTED2),   # 4-byte staging of 50,000 does not fit
+    ((600_000, 4, 16), R.PACK_PARTS_DIRECT),        # parts above 65,535 samples
+    ((100_000, 20, 8192), R.PACK_TREE_LDS),         # 16,384 buckets: whole-tree path
+    ((100_000, 20, 25_000), R.PACK_TREE_GLOBAL),
+])
+def test_pack_plan_paths(args, plan):
+    assert R.pack_plan(*args) == plan
+
+
+def test_pack_plan_rejects_bad_arguments():
+    for args in ((0, 5, 5), (10, 0, 5), (10, 5, 0), (10, 5, 5, 0)):
+        with pytest.raises(ValueError):
+            R.pack_plan(*args)

@@ -391,6 +391,31 @@ def test_buckets_beyond_16383_members(gpu_ctx, case):
     del keep
 
 
+@pytest.mark.parametrize("n,t,nleaf,plan", [
+    (20_000, 5, 300, R.PACK_PARTS_DIRECT),      # N below 32,768: direct writes
+    (600_000, 3, 16, R.PACK_PARTS_DIRECT),      # parts of 75,000 > 65,535 samples
+    (200_000, 6, 256, R.PACK_PARTS_SORTED2),    # 2-byte staging keeps two workgroups per CU
+    (50_000, 6, 64, R.PACK_PARTS_SORTED4),
+    (40_000, 6, 4096, R.PACK_PARTS_SORTED4),    # 8,192 buckets, one workgroup per CU
+])
+def test_member_scatter_variants(gpu_ctx, n, t, nleaf, plan):
+    """Each member-scatter kernel of the per-part packing path (the plan
+    query names the one this shape takes) gives the oracle's counts: row bands
+    at the start, middle and end of the triangle, raw U16 counts, 2% invalid
+    labels."""
+    assert R.pack_plan(n, t, nleaf) == plan
+    leaf, oob = make_forest(n + nleaf, n, t, nleaf, p_invalid=0.02)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for r0 in (0, n // 2 - 1, n - 3):
+        r1 = r0 + 3
+        got, guard = gpu_rows(gpu_ctx, O.FMT_U16, r0, r1)
+        check_equal(got, idx.rows(O.FMT_U16, r0, r1, 1.0, 0.0), f"plan {plan} rows {r0}:{r1}")
+        assert (guard == 0xA5).all()
+    idx.close()
+    del keep
+
+
 def test_row_bands_back_to_back_on_the_context_stream():
     """Two row bands queued on the context's own (non-blocking) stream with
     no synchronisation between them, the second band no larger than the
