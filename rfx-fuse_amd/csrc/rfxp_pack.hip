@@ -724,6 +724,7 @@ static size_t part_sorted4_lds(int32_t nb, int64_t part) {
     return (size_t)(nb + 16 + (nb + 1) / 2 + un) * 4;
 }
 
+template <bool KEEP>
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted4(
     LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
     uint32_t* roffT, uint16_t* rlenT) {
@@ -779,11 +780,49 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
-    // records pass
-    {
-        uint32_t* ro = roffT + (int64_t)t * N;
-        uint16_t* rl = rlenT + (int64_t)t * N;
-        const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    uint32_t* ro = roffT + (int64_t)t * N;
+    uint16_t* rl = rlenT + (int64_t)t * N;
+    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    // the record of sample i with key b (the run of (i, t), as in
+    // k_part_scatter), and its staging
+    auto record = [&](int64_t i, uint32_t b) {
+        const uint32_t ob = (b ^ 1u) & 0xffffu;
+        const uint32_t rs = ps0[ob < (uint32_t)nb ? ob : 0u];
+        const uint32_t rem = off[ob < (uint32_t)nb ? ob + 1u : 0u] - rs;
+        const bool ok = b != 0xffffu;
+        ro[i] = ok ? (tbase + rs) * 4u : 0u;
+        rl[i] = ok ? (uint16_t)(min(rem, REC_LONG) * 4u) : (uint16_t)0;
+    };
+    auto stage = [&](int64_t i, uint32_t b) {
+        const uint32_t sh16 = (b & 1u) * 16u;
+        const uint32_t old = atomicSub(&lc32[b >> 1], 1u << sh16);
+        stg[((old >> sh16) & 0xffffu) - 1u] = (b << 16) | (uint32_t)(i - i0);
+    };
+    if constexpr (KEEP) {
+        // the part (at most 2 rounds) in registers: its keys are read once
+        uint32_t key[2][PACK_KR];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x;
+                key[r][k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
+            }
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x;
+                if (i < i1) record(i, key[r][k]);
+            }
+        __syncthreads();  // off is dead from here on: stg overlays it
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k)
+                if (key[r][k] != 0xffffu) stage(i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x, key[r][k]);
+    } else {
+        // records pass, then the staging pass reading the keys again
         for (int64_t base = i0; base < i1; base += round) {
             uint32_t key[PACK_KR];
 #pragma unroll
@@ -794,34 +833,20 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
             for (int k = 0; k < PACK_KR; ++k) {
                 const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-                if (i >= i1) continue;
-                const uint32_t b = key[k];
-                // the run of (i, t), as in k_part_scatter
-                const uint32_t ob = (b ^ 1u) & 0xffffu;
-                const uint32_t rs = ps0[ob < (uint32_t)nb ? ob : 0u];
-                const uint32_t rem = off[ob < (uint32_t)nb ? ob + 1u : 0u] - rs;
-                const bool ok = b != 0xffffu;
-                ro[i] = ok ? (tbase + rs) * 4u : 0u;
-                rl[i] = ok ? (uint16_t)(min(rem, REC_LONG) * 4u) : (uint16_t)0;
+                if (i < i1) record(i, key[k]);
             }
         }
-    }
-    __syncthreads();  // off is dead from here on: stg overlays it
-    for (int64_t base = i0; base < i1; base += round) {
-        uint32_t key[PACK_KR];
+        __syncthreads();  // off is dead from here on: stg overlays it
+        for (int64_t base = i0; base < i1; base += round) {
+            uint32_t key[PACK_KR];
 #pragma unroll
-        for (int k = 0; k < PACK_KR; ++k) {
-            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
-        }
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
+            }
 #pragma unroll
-        for (int k = 0; k < PACK_KR; ++k) {
-            const uint32_t b = key[k];
-            if (b == 0xffffu) continue;
-            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            const uint32_t sh16 = (b & 1u) * 16u;
-            const uint32_t old = atomicSub(&lc32[b >> 1], 1u << sh16);
-            stg[((old >> sh16) & 0xffffu) - 1u] = (b << 16) | (uint32_t)(i - i0);
+            for (int k = 0; k < PACK_KR; ++k)
+                if (key[k] != 0xffffu) stage(base + (int64_t)k * PACK_THREADS + threadIdx.x, key[k]);
         }
     }
     __syncthreads();
@@ -937,9 +962,35 @@ __global__ __launch_bounds__(256) void k_nout_final(int64_t N, const int32_t* no
     }
 }
 
-__global__ void k_rr_init(unsigned long long* rr) {
-    rr[0] = 0x7ff0000000000000ull;
-    rr[1] = 0ull;
+// Everything the forest kernels accumulate into, or read as slack, cleared
+// in one launch: the record slack after the last row (empty records), the
+// status words, the per-tree long-bucket counts, the OOB-count accumulator
+// (acc, N words, or NULL) and the 1/nout range (min = +inf, max = 0, as
+// IEEE bits).
+struct ForestInit {
+    uint32_t* roff_slack;
+    uint32_t* rlen_slack;
+    uint32_t* flags;
+    uint32_t* lngn;
+    int32_t T;
+    uint32_t* acc;
+    int64_t N;
+    unsigned long long* rr;
+};
+
+__global__ __launch_bounds__(256) void k_forest_init(ForestInit a) {
+    const int64_t k0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if (a.acc)
+        for (int64_t k = k0; k < a.N; k += stride) a.acc[k] = 0u;
+    for (int64_t k = k0; k < a.T; k += stride) a.lngn[k] = 0u;
+    if (k0 < REC_PAD) a.roff_slack[k0] = 0u;
+    if (k0 < REC_PAD / 2) a.rlen_slack[k0] = 0u;
+    if (k0 < 16) a.flags[k0] = 0u;
+    if (k0 == 0) {
+        a.rr[0] = 0x7ff0000000000000ull;
+        a.rr[1] = 0ull;
+    }
 }
 
 // Buckets of REC_LONG or more members (forest mode): their start and end
@@ -1080,7 +1131,6 @@ static int pack_reference_segments(rfxp_ctx* ctx, const LeafView& v, const Fores
 // The table of long buckets (forest mode), once the offsets are known.
 static int pack_long_runs(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
     const int32_t nb = view_buckets(v);
-    fill_u32(ctx, (uint32_t*)fb.lngn, v.T, 0u);
     const int64_t n = (int64_t)v.T * nb;
     hipLaunchKernelGGL(k_long_runs, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, ctx->stream, (const int32_t*)fb.off,
                        nb, v.T, v.N, fb.lng, fb.lngn, fb.lmax);
@@ -1095,15 +1145,15 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     const bool forest = v.nseg == 0;
     const ForestSizes z = forest_sizes(v, nout_in == nullptr, ctx->max_lds);
     if (forest) {
-        // the record slack after the last row reads as empty records
         const int64_t n1 = std::max<int64_t>(N, 1);
-        fill_u32(ctx, fb.roff + n1 * fb.ldr, REC_PAD, 0u);
-        fill_u32(ctx, (uint32_t*)(fb.rlen + n1 * fb.ldr), REC_PAD / 2, 0u);
-        fill_u32(ctx, (uint32_t*)fb.flags, 16, 0u);  // status words (recount counter)
+        ForestInit fi{fb.roff + n1 * fb.ldr, (uint32_t*)(fb.rlen + n1 * fb.ldr), (uint32_t*)fb.flags,
+                      (uint32_t*)fb.lngn, T, nout_in ? nullptr : fb.scratch2, N, fb.rrange};
+        const int64_t work = std::max<int64_t>({N, (int64_t)T, (int64_t)REC_PAD});
         LaunchTimer tm(ctx, "rr_init");
-        hipLaunchKernelGGL(k_rr_init, dim3(1), dim3(1), 0, s, fb.rrange);
+        hipLaunchKernelGGL(k_forest_init, dim3((unsigned)std::min<int64_t>(cdiv(work, 256), 1024)), dim3(256), 0, s,
+                           fi);
     }
-    if (int rc = check_launch(ctx, "k_rr_init")) return rc;
+    if (int rc = check_launch(ctx, "k_forest_init")) return rc;
     if (N == 0) return RFXP_OK;
     if (z.part_path) {
         if (int rc = pack_forest_parts(ctx, v, fb)) return rc;
@@ -1187,7 +1237,8 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     const int64_t part = cdiv(N, PACK_PARTS);
     const int kind = part_scatter_kind(N, nb, ctx->max_lds);
     const bool sorted4 = kind == RFXP_PACK_PARTS_SORTED4, sorted = kind == RFXP_PACK_PARTS_SORTED2;
-    const void* scatter = sorted4  ? (const void*)k_part_scatter_sorted4
+    const void* scatter = sorted4  ? (part <= 2 * PACK_THREADS * PACK_KR ? (const void*)k_part_scatter_sorted4<true>
+                                                                         : (const void*)k_part_scatter_sorted4<false>)
                           : sorted ? (const void*)k_part_scatter_sorted
                                    : (const void*)k_part_scatter;
     const size_t lds_s = sorted4  ? part_sorted4_lds(nb, part)
@@ -1210,8 +1261,12 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
-        if (sorted4)
-            hipLaunchKernelGGL(k_part_scatter_sorted4, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+        if (sorted4 && part <= 2 * PACK_THREADS * PACK_KR)
+            hipLaunchKernelGGL(k_part_scatter_sorted4<true>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
+                               fb.mem, fb.roffT, fb.rlenT);
+        else if (sorted4)
+            hipLaunchKernelGGL(k_part_scatter_sorted4<false>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
                                (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
                                fb.mem, fb.roffT, fb.rlenT);
         else if (sorted)
@@ -1238,8 +1293,7 @@ static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, c
     const int64_t N = v.N;
     const int32_t T = v.T;
     if (!nout_in) {
-        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(N, 256), 65536)), dim3(256), 0, s,
-                           fb.scratch2, N, 0u);
+        // fb.scratch2 was cleared by k_forest_init
         const unsigned G = (unsigned)std::min<int32_t>(T, 16);
         LaunchTimer tm(ctx, "nout");
         hipLaunchKernelGGL(k_nout_part, dim3((unsigned)cdiv(N, 256), G), dim3(256), 0, s, v, fb.scratch2);
