@@ -56,29 +56,24 @@ __device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t*
     __syncthreads();
 }
 
-// Pass A, one 1024-thread workgroup per tree: bucket histogram (LDS when
-// 2L+1 counters fit, else the zeroed global scratch `gscr`), exclusive scan
-// into the global offsets, and the tree's bucket ids as uint16 (`key16`,
-// rows of ldk entries, pads 0xffff; written only when 2L < 0xffff, else
-// NULL).  Keys are held in registers, PACK_KR per thread per round, all
-// loads of a round issued before the first atomic.
-template <bool LDS_PATH>
+// Pass A, one 1024-thread workgroup per tree when its 2L + 1 counters fit
+// in LDS: bucket histogram, exclusive scan into the global offsets, and the
+// tree's bucket ids as uint16 (`key16`, rows of ldk entries, pads 0xffff;
+// written only when 2L < 0xffff, else NULL).  Keys are held in registers,
+// PACK_KR per thread per round, all loads of a round issued before the first
+// atomic.
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_hist(
-    LeafView v, int32_t* goff_all, uint32_t* gscr, uint16_t* key16, int64_t ldk) {
+    LeafView v, int32_t* goff_all, uint16_t* key16, int64_t ldk) {
     extern __shared__ uint32_t sh[];
     __shared__ uint32_t part[PACK_THREADS];
     const uint32_t bid = blockIdx.x;
     const int32_t t = (int32_t)((((bid >> 3) >> 4) << 3) + (bid & 7)) * 16 + (int32_t)((bid >> 3) & 15);
     if (t >= v.T) return;
     const int32_t nb = view_buckets(v);
-    uint32_t* cnt;
-    if constexpr (LDS_PATH) cnt = sh;
-    else cnt = gscr + (int64_t)t * 2 * (nb + 1);
+    uint32_t* cnt = sh;
     uint32_t* off0 = cnt + (nb + 1);
-    if constexpr (LDS_PATH) {
-        for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) cnt[b] = 0u;
-        __syncthreads();
-    }
+    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) cnt[b] = 0u;
+    __syncthreads();
     const int64_t N = v.N;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     uint16_t* kt = key16 ? key16 + (int64_t)t * ldk : nullptr;
@@ -103,14 +98,51 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         }
     }
     __syncthreads();
-    int32_t* goff = goff_all + (int64_t)t * (nb + 1);
-    if constexpr (LDS_PATH) {
-        scan_offsets(cnt, off0, nb, part, goff);
-    } else {
-        __threadfence_block();
-        scan_offsets((volatile uint32_t*)cnt, (volatile uint32_t*)off0, nb, part, goff);
-        __threadfence_block();
+    scan_offsets(cnt, off0, nb, part, goff_all + (int64_t)t * (nb + 1));
+}
+
+// Pass A for trees whose 2L + 1 counters do not fit in LDS: workgroup
+// (tree t, range r) counts the buckets [r * TREE_HR, (r + 1) * TREE_HR) of
+// tree t in LDS, reading all of the tree's labels (the ranges of a tree run
+// one after another on one XCD, so the later ones read them from L2), and
+// writes its range of cnt[t]; range 0 also writes the tree's 16-bit keys
+// (when key16 is not NULL).  k_seg_scan then turns the counts into offsets.
+constexpr int TREE_HR = 16384;  // buckets per range (64 KB of LDS)
+
+__global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tree_hist(
+    LeafView v, int32_t nrange, uint32_t* cnt_all, uint16_t* key16, int64_t ldk) {
+    extern __shared__ uint32_t sh[];
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid & 7, slot = bid >> 3;
+    const int64_t lin = (int64_t)xcd * (gridDim.x >> 3) + slot;
+    const int32_t t = (int32_t)(lin / nrange), r = (int32_t)(lin % nrange);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    const int32_t b0 = r * TREE_HR, nr = min(nb - b0, TREE_HR);
+    for (int32_t b = threadIdx.x; b < nr; b += PACK_THREADS) sh[b] = 0u;
+    __syncthreads();
+    const int64_t N = v.N;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    uint16_t* kt = (key16 && r == 0) ? key16 + (int64_t)t * ldk : nullptr;
+    for (int64_t base = 0; base < N; base += round) {
+        KeyLoad ld[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            ld[k] = key_load(v, i < N ? i : 0, t);
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            const int32_t b = i < N ? key_bucket(v, ld[k], i) : -1;
+            const uint32_t rb = (uint32_t)(b - b0);
+            if (b >= 0 && rb < (uint32_t)nr) atomicAdd(&sh[rb], 1u);
+            if (kt && i < ldk) kt[i] = b >= 0 ? (uint16_t)b : (uint16_t)0xffffu;
+        }
     }
+    __syncthreads();
+    uint32_t* cnt = cnt_all + (int64_t)t * (nb + 1) + b0;
+    for (int32_t b = threadIdx.x; b < nr; b += PACK_THREADS) cnt[b] = sh[b];
 }
 
 // Sample-major records, one 256-thread workgroup per 64 x 64 tile of
@@ -191,14 +223,18 @@ __global__ __launch_bounds__(256) void k_records(LeafView v, const uint16_t* key
 }
 
 // Pass B: workgroup (tree t, window w) owns the buckets whose offsets start
-// in [w*PACK_WIN, (w+1)*PACK_WIN) (bucket pairs kept together).  It reads
+// in [w*win, (w+1)*win) (bucket pairs kept together).  It reads
 // the tree's bucket ids again -- from key16, eight per 16-byte load, when
 // pass A wrote it, else from the leaves -- places its members in an LDS
 // copy of its slice of mem[t] through LDS cursors, and writes the slice
 // with coalesced stores.  Members beyond the LDS slice (a window grown by
 // one very large bucket) are written directly.
-constexpr int PACK_WIN = 12288;  // members per window (LDS slice; two workgroups per CU)
-constexpr int PACK_CUR = 4096;   // buckets per window with LDS cursors
+// The LDS holds win staged members and ncur cursors, win + ncur =
+// PACK_STAGE_WORDS (plus 8 bytes of statics: two workgroups per CU).  The
+// host splits it by the forest's members per bucket: a window of win members
+// spans about win * 2L / N buckets, and ncur leaves room for half as many
+// again (windows whose buckets do not fit use global cursors).
+constexpr int PACK_STAGE_WORDS = 20464;
 constexpr int SCAT_LOADS = 4;    // 16-byte key loads in flight per thread
 
 __device__ __forceinline__ int32_t first_bucket_at(const int32_t* off, int32_t nb, int64_t pos) {
@@ -213,7 +249,7 @@ __device__ __forceinline__ int32_t first_bucket_at(const int32_t* off, int32_t n
 }
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pack_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem,
-                                                              uint32_t* gcur_all, int32_t nwin,
+                                                              uint32_t* gcur_all, int32_t nwin, int32_t win,
                                                               const uint16_t* key16, int64_t ldk) {
     extern __shared__ uint32_t sh[];
     __shared__ int32_t s_b0, s_b1;
@@ -228,8 +264,8 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int32_t nb = view_buckets(v);
     const int32_t* off = goff_all + (int64_t)t * (nb + 1);
     if (threadIdx.x == 0) {
-        s_b0 = first_bucket_at(off, nb, (int64_t)w * PACK_WIN);
-        s_b1 = first_bucket_at(off, nb, (int64_t)(w + 1) * PACK_WIN);
+        s_b0 = first_bucket_at(off, nb, (int64_t)w * win);
+        s_b1 = first_bucket_at(off, nb, (int64_t)(w + 1) * win);
     }
     __syncthreads();
     const int32_t b0 = s_b0, b1 = s_b1;
@@ -238,9 +274,9 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const uint32_t end_pos = (uint32_t)off[b1];
     if (end_pos == base_pos) return;
     const int32_t nbk = b1 - b0;
-    const bool lds_cur = nbk <= PACK_CUR;
-    uint32_t* stage = sh;                 // PACK_WIN words
-    uint32_t* cur = sh + PACK_WIN;        // PACK_CUR words (relative cursors)
+    const bool lds_cur = nbk <= PACK_STAGE_WORDS - win;
+    uint32_t* stage = sh;                 // win words
+    uint32_t* cur = sh + win;             // the rest: relative cursors
     uint32_t* gcur = gcur_all + (int64_t)t * (nb + 1);
     if (lds_cur) {
         for (int32_t k = threadIdx.x; k < nbk; k += PACK_THREADS) cur[k] = (uint32_t)off[b0 + k] - base_pos;
@@ -255,7 +291,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         if (b < b0 || b >= b1) return;
         const uint32_t rel = lds_cur ? atomicAdd(&cur[b - b0], 1u) : atomicAdd(&gcur[b], 1u);
         const uint32_t m = (uint32_t)(i + 1);
-        if (rel < (uint32_t)PACK_WIN) stage[rel] = m;
+        if (rel < (uint32_t)win) stage[rel] = m;
         else memt[base_pos + rel] = m;
     };
     if (key16) {
@@ -301,7 +337,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         }
     }
     __syncthreads();
-    const uint32_t nst = min(end_pos - base_pos, (uint32_t)PACK_WIN);
+    const uint32_t nst = min(end_pos - base_pos, (uint32_t)win);
     for (uint32_t k = threadIdx.x; k < nst; k += PACK_THREADS) memt[base_pos + k] = stage[k];
 }
 
@@ -357,14 +393,67 @@ __global__ __launch_bounds__(PACK_THREADS) void k_seg_hist(LeafView v, uint32_t*
     if (sg == 0 && threadIdx.x == 0 && nb > v.L * v.nseg) cnt[nb - 1] = 0u;
 }
 
+// Exclusive scan of a tree's bucket counts in global memory, in place, into
+// cnt[0..nb] and goff[0..nb] (one workgroup per tree).  The counts are taken
+// SCAN_BATCH chunks of 1024 at a time, one per thread, so every load is
+// coalesced and a batch's loads are in flight together; each chunk is scanned
+// within its waves, the wave totals go through LDS, and a running carry
+// joins the chunks.
+constexpr int SCAN_BATCH = 8;
+
 __global__ __launch_bounds__(PACK_THREADS) void k_seg_scan(int32_t nb, int32_t T, uint32_t* cnt_all,
                                                            int32_t* goff_all) {
-    __shared__ uint32_t part[PACK_THREADS];
+    __shared__ uint32_t wsum[SCAN_BATCH][PACK_THREADS / 64];
     const int32_t t = blockIdx.x;
     if (t >= T) return;
     uint32_t* cnt = cnt_all + (int64_t)t * (nb + 1);
     int32_t* goff = goff_all + (int64_t)t * (nb + 1);
-    scan_offsets(cnt, cnt, nb, part, goff);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t carry = 0;
+    for (int32_t c0 = 0; c0 < nb; c0 += SCAN_BATCH * PACK_THREADS) {
+        uint32_t x[SCAN_BATCH], incl[SCAN_BATCH];
+#pragma unroll
+        for (int q = 0; q < SCAN_BATCH; ++q) {
+            const int32_t b = c0 + q * PACK_THREADS + tid;
+            x[q] = b < nb ? cnt[b] : 0u;
+        }
+#pragma unroll
+        for (int q = 0; q < SCAN_BATCH; ++q) {
+            uint32_t v = x[q];
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t o = (uint32_t)__shfl_up((int)v, d, 64);
+                if (lane >= d) v += o;
+            }
+            incl[q] = v;
+            if (lane == 63) wsum[q][wave] = v;
+        }
+        __syncthreads();
+        uint32_t run = carry;
+#pragma unroll
+        for (int q = 0; q < SCAN_BATCH; ++q) {
+            uint32_t before = 0, total = 0;
+#pragma unroll
+            for (int w = 0; w < PACK_THREADS / 64; ++w) {
+                const uint32_t y = wsum[q][w];
+                before += w < wave ? y : 0u;
+                total += y;
+            }
+            const int32_t b = c0 + q * PACK_THREADS + tid;
+            const uint32_t e = run + before + incl[q] - x[q];
+            if (b < nb) {
+                cnt[b] = e;
+                goff[b] = (int32_t)e;
+            }
+            run += total;
+        }
+        carry = run;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        cnt[nb] = carry;
+        goff[nb] = (int32_t)carry;
+    }
 }
 
 __global__ __launch_bounds__(PACK_THREADS) void k_seg_scatter(LeafView v, const int32_t* goff_all, uint32_t* mem) {
@@ -1041,7 +1130,7 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
         z.n[FB_SCRATCH] = (size_t)T * (nb + 1);
     } else {
         z.n[FB_KEY16] = nb < 0xffff ? (size_t)T * ldk : 0;
-        z.n[FB_SCRATCH] = (size_t)T * 2 * (nb + 1);
+        z.n[FB_SCRATCH] = (size_t)T * (nb + 1);  // counts, then the global cursors
     }
     if (forest) {
         z.n[FB_ROFF] = (size_t)n1 * z.ldr + REC_PAD;
@@ -1164,22 +1253,28 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     // trees -> workgroups in XCD-sized groups of 128 (8 XCDs x 16 trees)
     const unsigned grid = (unsigned)(cdiv(T, 128) * 128);
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
-    const int64_t nscr = (int64_t)T * 2 * (nb + 1);
     // compact bucket ids for the second pass when they fit 16 bits
     uint16_t* k16 = z.n[FB_KEY16] ? fb.key16 : nullptr;
     const int64_t ldk = cdiv(N, 8) * 8;
     if (z.lds_path) {
         if (lds_bytes > 32768)
-            RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_hist<true>,
+            RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_hist,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
         LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<true>, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, fb.off,
-                           (uint32_t*)nullptr, k16, ldk);
+        hipLaunchKernelGGL(k_pack_hist, dim3(grid), dim3(PACK_THREADS), lds_bytes, s, v, fb.off, k16, ldk);
     } else {
-        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(cdiv(nscr, 256), 65536)), dim3(256), 0, s,
-                           fb.scratch, nscr, 0u);
-        LaunchTimer tm(ctx, "pack_hist");
-        hipLaunchKernelGGL(k_pack_hist<false>, dim3(grid), dim3(PACK_THREADS), 0, s, v, fb.off, fb.scratch, k16, ldk);
+        const int32_t nrange = (int32_t)cdiv(nb, TREE_HR);
+        const size_t lds_r = (size_t)std::min<int32_t>(nb, TREE_HR) * 4;
+        RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_tree_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)lds_r));
+        {
+            LaunchTimer tm(ctx, "pack_hist");
+            hipLaunchKernelGGL(k_tree_hist, dim3((unsigned)(cdiv((int64_t)T * nrange, 8) * 8)), dim3(PACK_THREADS),
+                               lds_r, s, v, nrange, fb.scratch, k16, ldk);
+        }
+        if (int rc = check_launch(ctx, "k_tree_hist")) return rc;
+        LaunchTimer tm(ctx, "pack_scan");
+        hipLaunchKernelGGL(k_seg_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.scratch, fb.off);
     }
     if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
     if (forest) {
@@ -1189,16 +1284,18 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     }
     if (int rc = check_launch(ctx, "k_records")) return rc;
     {
-        // windows of PACK_WIN members, plus one for the slack a window can
-        // gain from keeping bucket pairs whole
-        const int32_t nwin = (int32_t)cdiv(N, PACK_WIN) + 1;
+        // windows of win members, plus one for the slack a window can gain
+        // from keeping bucket pairs whole; ncur = 1.5 * win * nb / N cursors
+        const int64_t w0 = (int64_t)PACK_STAGE_WORDS * 2 * N / (2 * N + 3 * (int64_t)nb);
+        const int32_t win = (int32_t)std::min<int64_t>(std::max<int64_t>(w0 & ~15LL, 4096), 16384);
+        const int32_t nwin = (int32_t)cdiv(N, win) + 1;
         const int64_t nwg = cdiv((int64_t)T * nwin, 8) * 8;
-        const size_t lds2 = (size_t)(PACK_WIN + PACK_CUR) * 4;
+        const size_t lds2 = (size_t)PACK_STAGE_WORDS * 4;
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_pack_scatter, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds2));
         LaunchTimer tm(ctx, "pack_scatter");
         hipLaunchKernelGGL(k_pack_scatter, dim3((unsigned)nwg), dim3(PACK_THREADS), lds2, s, v, fb.off, fb.mem,
-                           fb.scratch, nwin, (const uint16_t*)k16, ldk);
+                           fb.scratch, nwin, win, (const uint16_t*)k16, ldk);
     }
     if (int rc = check_launch(ctx, "k_pack_scatter")) return rc;
     if (!forest) return RFXP_OK;
