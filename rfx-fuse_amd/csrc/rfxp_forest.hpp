@@ -118,6 +118,7 @@ struct ForestSizes {
     bool part_path = false;  // per-part packing (forest mode, 2L <= 8192)
     bool seg_path = false;   // per-segment packing (reference mode, L <= 16384)
     bool lds_path = false;   // whole-tree histogram in LDS
+    bool tree_rec = false;   // whole-tree records through k_tree_records + k_rec_transpose
 };
 ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds);
 size_t forest_elem_bytes(int k);

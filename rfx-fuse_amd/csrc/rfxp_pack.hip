@@ -222,6 +222,83 @@ __global__ __launch_bounds__(256) void k_records(LeafView v, const uint16_t* key
     }
 }
 
+// Tree-major records for the whole-tree path: workgroup (tree t, chunk c of
+// TREE_REC_CHUNK samples) writes the records of its samples in sample order
+// (the run of (i, t) is the whole bucket with the other OOB bit), so every
+// store is coalesced; k_rec_transpose then makes them sample-major.  The
+// tree's bucket offsets (2L + 1 words) are looked up in LDS when they fit
+// (IN_LDS), else in global memory, where they stay in L2: the chunks of a
+// tree run one after another on one XCD.  (k_records looks the offsets up
+// for 64 trees per workgroup, which the L2 does not hold for large trees.)
+constexpr int TREE_REC_CHUNK = 32768;
+
+template <bool IN_LDS>
+__global__ __launch_bounds__(PACK_THREADS) void k_tree_records(LeafView v, const uint16_t* key16, int64_t ldk,
+                                                             const int32_t* goff_all, int32_t nchunk, uint32_t* roffT,
+                                                             uint16_t* rlenT) {
+    extern __shared__ uint32_t off_lds[];
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid & 7, slot = bid >> 3;
+    const int64_t lin = (int64_t)xcd * (gridDim.x >> 3) + slot;
+    const int32_t t = (int32_t)(lin / nchunk), c = (int32_t)(lin % nchunk);
+    if (t >= v.T) return;
+    const int32_t nb = view_buckets(v);
+    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    const uint32_t* off = IN_LDS ? off_lds : (const uint32_t*)goff;
+    if constexpr (IN_LDS) {
+        for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) off_lds[b] = (uint32_t)goff[b];
+        __syncthreads();
+    }
+    const int64_t N = v.N;
+    const int64_t i0 = (int64_t)c * TREE_REC_CHUNK, i1 = min(N, i0 + TREE_REC_CHUNK);
+    uint32_t* ro = roffT + (int64_t)t * N;
+    uint16_t* rl = rlenT + (int64_t)t * N;
+    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
+    for (int64_t base = i0; base < i1; base += round) {
+        int32_t key[PACK_KR];
+        if (key16) {
+            const uint16_t* kt = key16 + (int64_t)t * ldk;
+            uint32_t kk[PACK_KR];
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                kk[k] = kt[i < i1 ? i : i0];
+            }
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) key[k] = kk[k] == 0xffffu ? -1 : (int32_t)kk[k];
+        } else {
+            KeyLoad ld[PACK_KR];
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                ld[k] = key_load(v, i < i1 ? i : i0, t);
+            }
+#pragma unroll
+            for (int k = 0; k < PACK_KR; ++k) {
+                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+                key[k] = key_bucket(v, ld[k], i);
+            }
+        }
+        // every lookup of the round first (bucket 0's for empty records)
+        uint32_t st[PACK_KR], en[PACK_KR];
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const uint32_t ob = key[k] >= 0 ? (uint32_t)(key[k] ^ 1) : 0u;
+            st[k] = off[ob];
+            en[k] = off[ob + 1];
+        }
+#pragma unroll
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            if (i >= i1) continue;
+            const bool ok = key[k] >= 0;
+            ro[i] = ok ? (tbase + st[k]) * 4u : 0u;
+            rl[i] = ok ? (uint16_t)(min(en[k] - st[k], REC_LONG) * 4u) : (uint16_t)0;
+        }
+    }
+}
+
 // Pass B: workgroup (tree t, window w) owns the buckets whose offsets start
 // in [w*win, (w+1)*win) (bucket pairs kept together).  It reads
 // the tree's bucket ids again -- from key16, eight per 16-byte load, when
@@ -1234,6 +1311,12 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     } else {
         z.n[FB_KEY16] = nb < 0xffff ? (size_t)T * ldk : 0;
         z.n[FB_SCRATCH] = (size_t)T * (nb + 1);  // counts, then the global cursors
+        // tree-major records (k_tree_records) in forest mode
+        z.tree_rec = forest;
+        if (z.tree_rec) {
+            z.n[FB_ROFFT] = (size_t)T * N;
+            z.n[FB_RLENT] = (size_t)T * N;
+        }
     }
     if (forest) {
         z.n[FB_ROFF] = (size_t)n1 * z.ldr + REC_PAD;
@@ -1396,7 +1479,25 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
         hipLaunchKernelGGL(k_seg_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.scratch, fb.off);
     }
     if (int rc = check_launch(ctx, "k_pack_hist")) return rc;
-    if (forest) {
+    if (forest && z.tree_rec) {
+        const int32_t nchunk = (int32_t)cdiv(N, TREE_REC_CHUNK);
+        const size_t lds_t = (size_t)(nb + 1) * 4;
+        const bool in_lds = lds_t <= (size_t)ctx->max_lds;
+        if (in_lds && lds_t > 32768)
+            RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_tree_records<true>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_t));
+        LaunchTimer tm(ctx, "records");
+        const dim3 grid_r((unsigned)(cdiv((int64_t)T * nchunk, 8) * 8));
+        if (in_lds)
+            hipLaunchKernelGGL(k_tree_records<true>, grid_r, dim3(PACK_THREADS), lds_t, s, v, (const uint16_t*)k16, ldk,
+                               (const int32_t*)fb.off, nchunk, fb.roffT, fb.rlenT);
+        else
+            hipLaunchKernelGGL(k_tree_records<false>, grid_r, dim3(PACK_THREADS), 0, s, v, (const uint16_t*)k16, ldk,
+                               (const int32_t*)fb.off, nchunk, fb.roffT, fb.rlenT);
+        if (int rc = check_launch(ctx, "k_tree_records")) return rc;
+        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s,
+                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen);
+    } else if (forest) {
         LaunchTimer tm(ctx, "records");
         hipLaunchKernelGGL(k_records, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s, v,
                            (const uint16_t*)k16, ldk, (const int32_t*)fb.off, fb.ldr, fb.roff, fb.rlen);
