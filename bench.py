@@ -279,7 +279,7 @@ def run_triangle(args):
     wall = time.perf_counter() - wall0
     ms_step = ev0.elapsed_time(ev1) / args.steps
     tri_ms, tri_n = ctx.kernel_time("tri")
-    pack_names = ("rr_init", "pack_hist", "pack_scan", "pack_scatter", "records", "nout", "nout_final")
+    pack_names = ("rr_init", "pack_hist", "pack_scan", "pack_scatter", "records", "nout_final")
     pack_each = {k: ctx.kernel_time(k)[0] / args.steps for k in pack_names}
     pack_ms = sum(pack_each.values()) * args.steps
     tri_avg = tri_ms / max(tri_n, 1)

@@ -1,18 +1,19 @@
 // Forest index construction (see rfxp_forest.hpp for the layout).
 //
-// k_pack_hist (one workgroup per tree): bucket histogram, offsets and the
-// tree's 16-bit bucket keys.  k_records (forest mode; 64 x 64 tiles of
-// trees x samples): the sample-major records, looked up from the keys and
-// the tree's offsets and written through an LDS transpose.  k_pack_scatter
-// (one workgroup per tree and window of ~12k members): member lists built
-// in LDS and written out coalesced -- scattering 4-byte ids straight to HBM
-// costs a partial-line write each.  Trees are mapped to workgroups so that
-// related work lands on one XCD: 16 consecutive trees per XCD in the first
-// kernel, all windows of a tree in the third (they re-read the tree's keys
-// from L2).
+// Forests with 2L <= 8192 buckets per tree take the per-part path (see
+// k_part_hist below); larger ones the whole-tree path: k_pack_hist (one
+// workgroup per tree) or k_tree_hist + k_seg_scan (bucket histogram and
+// offsets, and the tree's 16-bit bucket keys), k_tree_records +
+// k_rec_transpose (the sample-major records), k_pack_scatter (one workgroup
+// per tree and window of members: member lists built in LDS and written out
+// coalesced -- scattering 4-byte ids straight to HBM costs a partial-line
+// write each).  Trees are mapped to workgroups so that related work lands on
+// one XCD, where the later workgroups of a tree read its data from L2.
 //
-// k_nout_part / k_nout_final: nout_i = sum over trees of OOB bits
-// (src/rf_bootstrap.cpp:67-70), its reciprocal, and the reciprocal's range.
+// nout_i = sum over trees of the OOB bits (src/rf_bootstrap.cpp:67-70) is
+// summed by k_rec_transpose; k_nout_final takes its reciprocal and the
+// reciprocal's range.  Reference sets (top-K, low rank) take the per-segment
+// path (k_seg_*).
 #include <algorithm>
 
 #include "rfxp_device.hpp"
@@ -145,91 +146,13 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     for (int32_t b = threadIdx.x; b < nr; b += PACK_THREADS) cnt[b] = sh[b];
 }
 
-// Sample-major records, one 256-thread workgroup per 64 x 64 tile of
-// (trees t0.., samples i0..): the bucket key of (i, t) from key16 (or from
-// the leaves when key16 is NULL), the start and length of the bucket with
-// the other OOB bit from the tree's offsets (L2-resident), then an LDS
-// transpose so that each sample's 64 records are written as one run.
-// Padding trees T..ldr-1 get empty records.
-__global__ __launch_bounds__(256) void k_records(LeafView v, const uint16_t* key16, int64_t ldk,
-                                                 const int32_t* goff_all, int64_t ldr, uint32_t* roff,
-                                                 uint16_t* rlen) {
-    __shared__ uint32_t to[64][65];
-    __shared__ uint16_t tl[64][66];
-    const int64_t N = v.N;
-    const int32_t T = v.T;
-    const int32_t nb = view_buckets(v);
-    const int64_t i0 = (int64_t)blockIdx.x * 64;
-    const int32_t t0 = blockIdx.y * 64;
-    // thread -> (tree row r, 16 consecutive samples) for the lookups
-    for (int k = threadIdx.x; k < 64 * 4; k += 256) {
-        const int r = k >> 2, c0 = (k & 3) * 16;
-        const int32_t t = t0 + r;
-        // loads at clamped indices first, then the bucket ids, then the
-        // offset lookups (bucket 0's for empty records), then the records
-        const int32_t tc = t < T ? t : 0;
-        int32_t key[16];
-        if (key16) {
-            uint32_t kk[16];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const int64_t i = i0 + c0 + c;
-                kk[c] = key16[(int64_t)tc * ldk + (i < N ? i : 0)];
-            }
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const int64_t i = i0 + c0 + c;
-                key[c] = (t < T && i < N && kk[c] != 0xffffu) ? (int32_t)kk[c] : -1;
-            }
-        } else {
-            KeyLoad ld[16];
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const int64_t i = i0 + c0 + c;
-                ld[c] = key_load(v, i < N ? i : 0, tc);
-            }
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const int64_t i = i0 + c0 + c;
-                key[c] = (t < T && i < N) ? key_bucket(v, ld[c], i) : -1;
-            }
-        }
-        const int32_t* off = goff_all + (int64_t)tc * (nb + 1);
-        const uint32_t tbase = (uint32_t)t * (uint32_t)N;
-        uint32_t st[16], en[16];
-#pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const int32_t ob = key[c] >= 0 ? key[c] ^ 1 : 0;
-            st[c] = (uint32_t)off[ob];
-            en[c] = (uint32_t)off[ob + 1];
-        }
-#pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const bool ok = key[c] >= 0;
-            to[r][c0 + c] = ok ? (tbase + st[c]) * 4u : 0u;
-            tl[r][c0 + c] = ok ? (uint16_t)(min(en[c] - st[c], REC_LONG) * 4u) : (uint16_t)0;
-        }
-    }
-    __syncthreads();
-    for (int k = threadIdx.x; k < 64 * 64; k += 256) {
-        const int r = k >> 6, c = k & 63;  // r: sample, c: tree
-        const int64_t i = i0 + r;
-        const int32_t t = t0 + c;
-        if (i < N && t < ldr) {
-            roff[i * ldr + t] = to[c][r];
-            rlen[i * ldr + t] = tl[c][r];
-        }
-    }
-}
-
 // Tree-major records for the whole-tree path: workgroup (tree t, chunk c of
 // TREE_REC_CHUNK samples) writes the records of its samples in sample order
 // (the run of (i, t) is the whole bucket with the other OOB bit), so every
 // store is coalesced; k_rec_transpose then makes them sample-major.  The
 // tree's bucket offsets (2L + 1 words) are looked up in LDS when they fit
 // (IN_LDS), else in global memory, where they stay in L2: the chunks of a
-// tree run one after another on one XCD.  (k_records looks the offsets up
-// for 64 trees per workgroup, which the L2 does not hold for large trees.)
+// tree run one after another on one XCD.
 constexpr int TREE_REC_CHUNK = 32768;
 
 template <bool IN_LDS>
@@ -744,7 +667,11 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // thread, so that every load and store of the part table is coalesced; a
 // workgroup-wide exclusive scan per chunk and a running carry give the
 // bucket starts, and each part's start in each bucket replaces its count.
-__global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, uint32_t* ph, int32_t* goff_all) {
+// It also lists the tree's buckets of REC_LONG or more members (start and
+// end byte offsets in mem, in lng[t][0 .. lngn[t]), lngn zeroed before).
+__global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, int64_t N, uint32_t* ph,
+                                                            int32_t* goff_all, uint2* lng, int32_t* lngn,
+                                                            int32_t lmax) {
     __shared__ uint32_t wsum[PACK_THREADS / 64];
     const int32_t t = blockIdx.x;
     if (t >= T) return;
@@ -779,6 +706,11 @@ __global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t 
         }
         __syncthreads();
         uint32_t run = carry + before + incl - s;
+        if (b < nb && s >= REC_LONG) {
+            const int32_t slot = atomicAdd(&lngn[t], 1);
+            const uint32_t base = (uint32_t)t * (uint32_t)N;
+            if (slot < lmax) lng[(int64_t)t * lmax + slot] = make_uint2(4u * (base + run), 4u * (base + run + s));
+        }
         if (b < nb) {
             goff[b] = (int32_t)run;
 #pragma unroll
@@ -1132,8 +1064,12 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 }
 
 // [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
+// With acc (forest mode, nout counted here), each tile also adds its trees'
+// OOB bits of its 64 samples to acc[i] (one atomic per sample and tile):
+// nout_i = sum over trees of the OOB bits (src/rf_bootstrap.cpp:67-70).
 __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, const uint16_t* rlenT, int64_t N,
-                                                      int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen) {
+                                                      int32_t T, int64_t ldr, uint32_t* roff, uint16_t* rlen,
+                                                      const uint32_t* oob, int64_t old, uint32_t* acc) {
     __shared__ uint32_t to[64][65];
     __shared__ uint16_t tl[64][66];
     const int64_t i0 = (int64_t)blockIdx.x * 64;
@@ -1170,35 +1106,32 @@ __global__ __launch_bounds__(256) void k_rec_transpose(const uint32_t* roffT, co
             rlen[i * ldr + t] = t < T ? tl[c][r] : (uint16_t)0;
         }
     }
+    if (acc) {
+        // thread (sample c, tree group g of 16): its OOB bits, then the four
+        // groups' sums through LDS
+        __shared__ uint32_t part[4][64];
+        const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
+        const int64_t i = i0 + c;
+        const int64_t ic = i < N ? i : 0;
+        uint32_t w[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int32_t t = t0 + 16 * g + k;
+            w[k] = t < T ? oob[(int64_t)t * old + (ic >> 5)] : 0u;
+        }
+        uint32_t n = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) n += (w[k] >> (ic & 31)) & 1u;
+        part[g][c] = n;
+        __syncthreads();
+        if (g == 0 && i < N) atomicAdd(&acc[i], part[0][c] + part[1][c] + part[2][c] + part[3][c]);
+    }
 }
 
 __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t val) {
     int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; k < n; k += stride) p[k] = val;
-}
-
-// Partial OOB counts: grid (ceil(N/256), G), block g sums trees
-// [g*T/G, (g+1)*T/G) for 256 samples.
-__global__ __launch_bounds__(256) void k_nout_part(LeafView v, uint32_t* acc) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= v.N) return;
-    const int32_t G = gridDim.y;
-    const int32_t t0 = (int32_t)((int64_t)v.T * blockIdx.y / G);
-    const int32_t t1 = (int32_t)((int64_t)v.T * (blockIdx.y + 1) / G);
-    const uint32_t* w = v.oob + (i >> 5);
-    const uint32_t sh = (uint32_t)(i & 31);
-    uint32_t s = 0;
-    int32_t t = t0;
-    for (; t + 8 <= t1; t += 8) {
-        uint32_t x[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) x[k] = w[(int64_t)(t + k) * v.old];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s += (x[k] >> sh) & 1u;
-    }
-    for (; t < t1; ++t) s += (w[(int64_t)t * v.old] >> sh) & 1u;
-    atomicAdd(&acc[i], s);
 }
 
 __global__ __launch_bounds__(256) void k_nout_final(int64_t N, const int32_t* nout_in, const uint32_t* acc,
@@ -1371,7 +1304,7 @@ size_t forest_elem_bytes(int k) {
     }
 }
 
-static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb);
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb);
 static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb);
 
 // Reference-set path (see k_seg_hist).
@@ -1447,8 +1380,7 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
     if (int rc = check_launch(ctx, "k_forest_init")) return rc;
     if (N == 0) return RFXP_OK;
     if (z.part_path) {
-        if (int rc = pack_forest_parts(ctx, v, fb)) return rc;
-        if (int rc = pack_long_runs(ctx, v, fb)) return rc;
+        if (int rc = pack_forest_parts(ctx, v, nout_in, fb)) return rc;  // long runs listed by k_part_scan
         return pack_nout(ctx, v, nout_in, fb);
     }
     if (z.seg_path) return pack_reference_segments(ctx, v, fb);
@@ -1496,13 +1428,10 @@ int pack_forest(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const 
                                (const int32_t*)fb.off, nchunk, fb.roffT, fb.rlenT);
         if (int rc = check_launch(ctx, "k_tree_records")) return rc;
         hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s,
-                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen);
-    } else if (forest) {
-        LaunchTimer tm(ctx, "records");
-        hipLaunchKernelGGL(k_records, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s, v,
-                           (const uint16_t*)k16, ldk, (const int32_t*)fb.off, fb.ldr, fb.roff, fb.rlen);
+                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen, v.oob, v.old,
+                           nout_in ? nullptr : fb.scratch2);
     }
-    if (int rc = check_launch(ctx, "k_records")) return rc;
+    if (int rc = check_launch(ctx, "k_rec_transpose")) return rc;
     {
         // windows of win members, plus one for the slack a window can gain
         // from keeping bucket pairs whole; ncur = 1.5 * win * nb / N cursors
@@ -1542,7 +1471,7 @@ static int part_scatter_kind(int64_t N, int32_t nb, int max_lds) {
 }
 
 // Forest path for 2L <= PART_MAX_NB (see k_part_hist).
-static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs& fb) {
+static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
     const int32_t T = v.T;
@@ -1573,7 +1502,8 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     if (int rc = check_launch(ctx, "k_part_hist")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scan");
-        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.scratch, fb.off);
+        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, N, fb.scratch, fb.off,
+                           fb.lng, fb.lngn, fb.lmax);
     }
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
@@ -1599,7 +1529,8 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
     {
         LaunchTimer tm(ctx, "records");
         hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s,
-                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen);
+                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen, v.oob, v.old,
+                           nout_in ? nullptr : fb.scratch2);
     }
     return check_launch(ctx, "k_rec_transpose");
 }
@@ -1608,14 +1539,7 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const ForestBufs&
 static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
-    const int32_t T = v.T;
-    if (!nout_in) {
-        // fb.scratch2 was cleared by k_forest_init
-        const unsigned G = (unsigned)std::min<int32_t>(T, 16);
-        LaunchTimer tm(ctx, "nout");
-        hipLaunchKernelGGL(k_nout_part, dim3((unsigned)cdiv(N, 256), G), dim3(256), 0, s, v, fb.scratch2);
-    }
-    if (int rc = check_launch(ctx, "k_nout_part")) return rc;
+    // without nout_in, k_rec_transpose has summed the OOB bits into fb.scratch2
     {
         LaunchTimer tm(ctx, "nout_final");
         hipLaunchKernelGGL(k_nout_final, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, s, N, nout_in,
