@@ -7,6 +7,7 @@ import pytest
 
 import oracle as O
 import rfxprox as R
+from closed_forms import pair_total
 
 pytestmark = pytest.mark.gpu
 
@@ -320,6 +321,35 @@ def test_c3_shape_sampled_rows(gpu_ctx):
     diag = torch.tensor([O.tri_idx(n, i, i) for i in range(0, n, 997)], device="cuda:0")
     assert bool((out[diag] == dcode).all())
     idx.close()
+
+
+@pytest.mark.parametrize("n,t,nleaf", [
+    (100_000, 500, 2048),   # C3: per-part packing, sorted member scatter
+    (100_000, 200, 25_000),  # whole-tree packing: range histograms, offsets read from L2
+])
+def test_whole_triangle_invariants(gpu_ctx, n, t, nleaf):
+    """Raw U16 counts over the whole triangle (5e9 entries at N = 100k):
+    their sum equals the closed form from the leaf histograms (pair_total),
+    every count lies in [0, T], and the diagonal is 0."""
+    import torch
+
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(20261205 + nleaf)
+    leaf = torch.randint(0, nleaf, (t, n), generator=g, device="cuda:0", dtype=torch.int32)
+    oob = torch.rand((t, n), generator=g, device="cuda:0") < 0.368
+    words = R.pack_oob_bits(oob)
+    gpu_ctx.set_forest(leaf, words, n, t, nleaf)
+    out = torch.empty(R.upper_nbytes(O.FMT_U16, n), dtype=torch.uint8, device="cuda:0")
+    gpu_ctx.upper(O.FMT_U16, out, 0, n)
+    torch.cuda.synchronize()
+    u = out.view(torch.int16)  # counts <= 500 read the same as int16
+    got_total = int(u.sum(dtype=torch.int64).item())
+    want_total = pair_total(leaf.cpu().numpy(), oob.to(torch.uint8).cpu().numpy(), nleaf)
+    assert got_total == want_total, (got_total, want_total)
+    assert int(u.max().item()) <= t and int(u.min().item()) >= 0
+    diag = torch.tensor([O.tri_idx(n, i, i) for i in range(0, n, 613)], device="cuda:0")
+    assert bool((u[diag] == 0).all())
+    del out, u
 
 
 def test_c2_shape_full_triangle_f32(gpu_ctx):

@@ -728,3 +728,17 @@ def test_both_oob_hand_example():
     want = np.array([1.0, np.float32(2) / np.float32(3), 0.0, 1.0, 0.0, 1.0], np.float32)
     assert np.array_equal(got, want)
     assert np.array_equal(O.both_oob_rows(leaf, oob, 3, O.FMT_U16), np.array([0, 2, 0, 0, 0, 0], np.uint16))
+
+
+def test_pair_total_closed_form_matches_the_oracle_triangle():
+    """The closed form behind the full-size triangle check (sum of U over
+    i < j = sum over trees and leaves of #OOB x #in-bag) against the
+    oracle's U16 triangle, with invalid labels mixed in."""
+    from closed_forms import pair_total
+
+    rng = np.random.default_rng(91)
+    n, t, nleaf = 300, 40, 7
+    leaf = rng.integers(-1, nleaf + 1, size=(t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    tri = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    assert int(tri.astype(np.int64).sum()) == pair_total(leaf, oob, nleaf)
