@@ -140,20 +140,20 @@ int64_t rfxp_upper_launches(int64_t n_items);
 
 /* How rfxp_set_forest packs a forest of N samples, T trees and nleaf leaves
  * per tree on a device whose workgroups may use max_lds bytes of LDS
- * (163840 on gfx950), host-only.  With 2 * nleaf <= 8192 buckets per tree
- * the samples of each tree are cut into 8 parts, and each part's members go
- * to their buckets directly (PARTS_DIRECT: small forests, whose scattered
- * writes merge in L2) or after a counting sort by bucket in LDS (SORTED2,
- * SORTED4: 2- or 4-byte staging entries, whichever keeps more workgroups
- * per CU).  More buckets take the whole-tree path, with the bucket
- * histogram in LDS or in global memory.  Returns one of these codes, -1 for
- * bad arguments.  Lets callers and tests see which kernels a forest takes;
- * no reference counterpart. */
+ * (163840 on gfx950), host-only.  Large forests with B = 2 * nleaf <= 8192
+ * buckets per tree, N >= 32768 and N >= 16 * B have the samples of each
+ * tree cut into 8 parts, and each part's members go to their buckets
+ * directly (PARTS_DIRECT: parts too large for the staging below) or after a
+ * counting sort by bucket in LDS (SORTED2, SORTED4: 2- or 4-byte staging
+ * entries, whichever keeps more workgroups per CU).  Other forests take the
+ * whole-tree path, with the bucket histogram in one LDS array or in LDS
+ * ranges.  Returns one of these codes, -1 for bad arguments.  Lets callers
+ * and tests see which kernels a forest takes; no reference counterpart. */
 #define RFXP_PACK_PARTS_DIRECT 0
 #define RFXP_PACK_PARTS_SORTED2 1
 #define RFXP_PACK_PARTS_SORTED4 2
 #define RFXP_PACK_TREE_LDS 3
-#define RFXP_PACK_TREE_GLOBAL 4
+#define RFXP_PACK_TREE_RANGES 4
 int rfxp_pack_plan(int64_t N, int32_t T, int32_t nleaf, int32_t max_lds);
 
 /* The "both OOB" proximity (R randomForest's oob.prox), which the reference

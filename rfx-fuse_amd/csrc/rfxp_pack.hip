@@ -588,8 +588,9 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 }
 
 // ---------------------------------------------------------------------------
-// Forest path with per-part cursors (2L <= PART_MAX_NB): each tree's samples
-// are cut into PACK_PARTS contiguous parts.
+// Forest path with per-part cursors (2L <= PART_MAX_NB, N >= PART_MIN_N and
+// N >= 16 * 2L, see forest_sizes): each tree's samples are cut into
+// PACK_PARTS contiguous parts.
 //   k_part_hist    (tree, part): LDS histogram of the part's buckets -> ph,
 //                  and the part's 16-bit keys;
 //   k_part_scan    (tree): bucket starts (off) and, per part, the start of
@@ -607,6 +608,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // ---------------------------------------------------------------------------
 constexpr int PACK_PARTS = 8;
 constexpr int PART_MAX_NB = 8192;
+constexpr int64_t PART_MIN_N = 32768;
 
 __device__ __forceinline__ int64_t part_begin(int64_t N, int p) {
     const int64_t chunk = (N + PACK_PARTS - 1) / PACK_PARTS;
@@ -1228,7 +1230,15 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     const int64_t ldk = cdiv(N, 8) * 8;
     z.ldr = ((int64_t)T + 15) / 16 * 16;
     z.lmax = (int32_t)(N / REC_LONG + 1);
-    z.part_path = forest && nb <= PART_MAX_NB;
+    // Per-part packing pays off for large forests with many members per
+    // bucket and part: below N = 32,768 or 16 members per bucket (parts of
+    // fewer than 2 members per bucket) its per-part tables cost more than
+    // the whole-tree path's repeated key reads, and the runs it shortens
+    // fit a line either way.  Step (packing + triangle, T = 500) measured
+    // both ways: N = 20,000 with 1,000-4,096 leaves 0.68 -> 0.55 ms whole
+    // tree; N = 100,000 / 2,048 leaves 3.18 (per part) against 3.31 ms;
+    // N = 200,000 / 2,048 leaves 12.5 against 17.1 ms.
+    z.part_path = forest && nb <= PART_MAX_NB && N >= PART_MIN_N && N >= 16 * (int64_t)nb;
     z.seg_path = !forest && v.L <= SEG_MAX_L;
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
     z.lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= max_lds;
@@ -1559,5 +1569,5 @@ extern "C" int rfxp_pack_plan(int64_t N, int32_t T, int32_t nleaf, int32_t max_l
     v.L = nleaf;
     const ForestSizes z = forest_sizes(v, true, max_lds);
     if (z.part_path) return part_scatter_kind(N, view_buckets(v), max_lds);
-    return z.lds_path ? RFXP_PACK_TREE_LDS : RFXP_PACK_TREE_GLOBAL;
+    return z.lds_path ? RFXP_PACK_TREE_LDS : RFXP_PACK_TREE_RANGES;
 }

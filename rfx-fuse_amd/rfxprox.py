@@ -125,7 +125,7 @@ def upper_nbytes(fmt: int, n: int, r0: int = 0, r1: int | None = None) -> int:
     return v
 
 
-PACK_PARTS_DIRECT, PACK_PARTS_SORTED2, PACK_PARTS_SORTED4, PACK_TREE_LDS, PACK_TREE_GLOBAL = range(5)
+PACK_PARTS_DIRECT, PACK_PARTS_SORTED2, PACK_PARTS_SORTED4, PACK_TREE_LDS, PACK_TREE_RANGES = range(5)
 GFX950_MAX_LDS = 163840
 
 

@@ -272,12 +272,13 @@ def test_library_exports_lowrank_class_with_reference_signatures():
 
 @pytest.mark.parametrize("args,plan", [
     ((100_000, 500, 2048), R.PACK_PARTS_SORTED4),   # C3: 74 KB of LDS, two workgroups per CU
-    ((20_000, 500, 4096), R.PACK_PARTS_DIRECT),     # C2: N below 32,768
+    ((20_000, 500, 4096), R.PACK_TREE_LDS),         # C2: N below 32,768 -> whole tree
+    ((70_000, 500, 4096), R.PACK_TREE_LDS),         # N < 16 x 2L
     ((200_000, 6, 256), R.PACK_PARTS_SORTED2),
     ((400_000, 500, 2048), R.PACK_PARTS_SORTED2),   # 4-byte staging of 50,000 does not fit
     ((600_000, 4, 16), R.PACK_PARTS_DIRECT),        # parts above 65,535 samples
     ((100_000, 20, 8192), R.PACK_TREE_LDS),         # 16,384 buckets: whole-tree path
-    ((100_000, 20, 25_000), R.PACK_TREE_GLOBAL),
+    ((100_000, 20, 25_000), R.PACK_TREE_RANGES),
 ])
 def test_pack_plan_paths(args, plan):
     assert R.pack_plan(*args) == plan

@@ -422,12 +422,11 @@ def test_buckets_beyond_16383_members(gpu_ctx, case):
 
 
 @pytest.mark.parametrize("n,t,nleaf,plan", [
-    (20_000, 5, 300, R.PACK_PARTS_DIRECT),      # N below 32,768: direct writes
     (600_000, 3, 16, R.PACK_PARTS_DIRECT),      # parts of 75,000 > 65,535 samples
     (200_000, 6, 256, R.PACK_PARTS_SORTED2),    # 2-byte staging keeps two workgroups per CU
     (50_000, 6, 64, R.PACK_PARTS_SORTED4),       # keys of a part held in registers
     (200_000, 4, 2048, R.PACK_PARTS_SORTED4),    # parts of 25,000: keys read twice
-    (40_000, 6, 4096, R.PACK_PARTS_SORTED4),    # 8,192 buckets, one workgroup per CU
+    (140_000, 6, 4096, R.PACK_PARTS_SORTED4),   # 8,192 buckets, one workgroup per CU
 ])
 def test_member_scatter_variants(gpu_ctx, n, t, nleaf, plan):
     """Each member-scatter kernel of the per-part packing path (the plan
