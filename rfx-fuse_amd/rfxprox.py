@@ -214,6 +214,8 @@ class Context:
         if getattr(self, "h", None):
             self._L.rfxp_ctx_destroy(self.h)
             self.h = None
+        self._forest_inputs = None
+        self._reference_leaf = None
 
     def __del__(self):
         try:
@@ -269,6 +271,8 @@ class Context:
             nptr = nout.data_ptr()
         self._check(self._L.rfxp_set_forest(self.h, leaf.data_ptr(), si, st, oob_words.data_ptr(),
                                             oob_words.shape[1], n, t, nleaf, nptr))
+        # rfxp_lowrank_oob_pv reads these later: keep them alive with the forest
+        self._forest_inputs = (leaf, oob_words)
         self.n = n
         self.t = t
 
@@ -280,6 +284,8 @@ class Context:
         assert leaf.dtype == torch.int32 and leaf.is_cuda and leaf.is_contiguous()
         si, st = (1, n) if layout == "tree" else (t, 1)
         self._check(self._L.rfxp_set_reference(self.h, leaf.data_ptr(), si, st, n, t, nleaf))
+        # rfxp_lowrank_pv reads the leaf matrix later: keep it alive with the set
+        self._reference_leaf = leaf
         self.ref_n = n
 
     def topk(self, qleaf, k: int, layout: str = "sample", oob_words=None, exclude_base: int = -1,

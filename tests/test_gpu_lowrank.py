@@ -46,6 +46,27 @@ def test_pv_matches_oracle(gpu_ctx, n, t, nleaf, r):
     assert rel_fro(Y.astype(np.float64), want) < 1e-5
 
 
+def test_pv_repeat_runs_differ_only_by_rounding(gpu_ctx):
+    """k_lr_w adds the partial sums of a leaf split over several pieces with
+    float atomics, whose order varies between runs: P V is not bit-for-bit
+    repeatable for such forests, but repeated runs agree to fp32 rounding
+    (1e-6 relative Frobenius, far inside the 1e-5 contract) and each stays
+    within that contract of the double-precision oracle.  The leaf matrix is
+    handed over as a temporary: the binding keeps it alive for the later
+    P V calls (rfxp_lowrank_pv reads it), even when V takes a block of the
+    same size."""
+    rng = np.random.default_rng(77)
+    n, t, nleaf, r = 60_000, 16, 6, 16   # Zipf(1.1) over 6 leaves: leaves of ~25,000 members split
+    leaf = zipf_leaves(rng, n, t, nleaf)
+    V = rng.standard_normal((n, r)).astype(np.float32)
+    gpu_ctx.set_reference(dev(leaf), n, t, nleaf)
+    runs = [gpu_ctx.lowrank_pv(dev(V)).cpu().numpy().astype(np.float64) for _ in range(4)]
+    want = O.lowrank_pv(leaf, nleaf, V.astype(np.float64))
+    for Y in runs:
+        assert rel_fro(Y, want) < 1e-5
+        assert rel_fro(Y, runs[0]) < 1e-6
+
+
 def numpy_subspace(leaf, nleaf, V0, iters):
     def orth(X):
         Q, R = np.linalg.qr(X)
@@ -133,6 +154,31 @@ def test_oob_normalised_pv_matches_finishprox_matrix(gpu_ctx, n, t, nleaf, r, la
     rv = np.where(nout > 0, 1.0 / np.maximum(nout, 1), 1.0)
     P = 0.25 * (rv[:, None] * U + U * rv[None, :]) + np.eye(n)
     assert np.array_equal(P[np.triu_indices(n)].astype(np.float32), O.upper_rows(leaf, oob, nleaf, O.FMT_F32))
+    V = rng.standard_normal((n, r)).astype(np.float32)
+    Y = gpu_ctx.lowrank_oob_pv(dev(V)).cpu().numpy()
+    assert rel_fro(Y.astype(np.float64), P @ V.astype(np.float64)) <= 1e-6
+
+
+def test_oob_normalised_pv_with_temporary_forest_inputs(gpu_ctx):
+    """The forest's leaf matrix and OOB words handed over as temporaries: the
+    binding keeps them alive for rfxp_lowrank_oob_pv, which reads them after
+    rfxp_set_forest returns, even when V takes a freed block of the same size
+    (leaf: 8 x 4000 int32; V: 4000 x 8 float32)."""
+    import torch
+
+    import rfxprox as R
+
+    rng = np.random.default_rng(5)
+    n, t, nleaf, r = 4000, 8, 9, 8
+    leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
+    oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
+    gpu_ctx.set_forest(dev(leaf), R.pack_oob_bits(dev(oob).to(torch.bool)), n, t, nleaf)
+    U = np.zeros((n, n))
+    U[np.triu_indices(n)] = O.upper_counts_scatter(leaf, oob, nleaf)
+    U = U + np.triu(U, 1).T
+    nout = oob.sum(axis=0)
+    rv = np.where(nout > 0, 1.0 / np.maximum(nout, 1), 1.0)
+    P = 0.25 * (rv[:, None] * U + U * rv[None, :]) + np.eye(n)
     V = rng.standard_normal((n, r)).astype(np.float32)
     Y = gpu_ctx.lowrank_oob_pv(dev(V)).cpu().numpy()
     assert rel_fro(Y.astype(np.float64), P @ V.astype(np.float64)) <= 1e-6
