@@ -12,11 +12,13 @@
 //                         (4*(t*N + start)) of the run of i: the bucket of
 //                         i's leaf with the other OOB bit holds exactly the
 //                         samples that pair with i in tree t
-//                         (src/rf_proximity.cpp:179-230).  Members are placed
-//                         part by part (contiguous sample ranges, ascending),
-//                         so the run starts where the members from i's own
-//                         part begin: every member j > i is in the run, and
-//                         of the members j < i only those of i's part
+//                         (src/rf_proximity.cpp:179-230).  On the per-part
+//                         packing path members are placed part by part
+//                         (contiguous sample ranges, ascending), so the run
+//                         starts where the members from i's own part begin:
+//                         every member j > i is in the run, and of the
+//                         members j < i only those of i's part.  On the
+//                         whole-tree path the run is the whole bucket
 //   rlen [N][ldr] uint16  the run's length in bytes, 4*min(len, REC_LONG);
 //                         4*REC_LONG means "REC_LONG or more members: the run
 //                         ends where its bucket ends", found in lng below; 0
@@ -60,21 +62,13 @@ struct LeafView {
     int32_t seg_shift;
 };
 
-// Bucket id of sample i in tree t, -1 when its label is not a valid leaf.
-__device__ __forceinline__ int32_t bucket_of(const LeafView& v, int64_t i, int32_t t) {
-    int32_t l = v.leaf[i * v.si + (int64_t)t * v.st];
-    if (l < 0 || l >= v.L) return -1;
-    if (v.nseg > 0) return l * v.nseg + (int32_t)(i >> v.seg_shift);
-    uint32_t w = v.oob[(int64_t)t * v.old + (i >> 5)];
-    return 2 * l + (int32_t)((w >> (i & 31)) & 1u);
-}
-
-// bucket_of in two steps, so that a kernel can issue the loads of many
-// samples before it uses any of them (a branch on a loaded label between the
-// two loads would make every sample wait for its own label).  key_load reads
-// the label and, in forest mode, the OOB word of sample i (a valid index: the
-// caller clamps it); key_bucket turns them into the bucket id, -1 for an
-// invalid label.
+// Bucket id of sample i in tree t, in two steps, so that a kernel can issue
+// the loads of many samples before it uses any of them (a branch on a loaded
+// label between the two loads would make every sample wait for its own
+// label).  key_load reads the label and, in forest mode, the OOB word of
+// sample i (a valid index: the caller clamps it); key_bucket turns them into
+// the bucket id (forest: 2 * leaf + OOB bit; reference set: leaf * nseg +
+// segment), -1 for an invalid label.
 struct KeyLoad {
     int32_t l;
     uint32_t w;

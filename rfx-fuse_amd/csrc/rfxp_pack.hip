@@ -26,8 +26,7 @@ constexpr int PACK_KR = 8;  // keys per thread per round
 
 // Exclusive scan of cnt[0..nb) (one workgroup) into off0[0..nb] and the
 // global offsets table; cnt becomes the running cursor.
-template <class P>
-__device__ void scan_offsets(P cnt, P off0, int32_t nb, uint32_t* part, int32_t* goff) {
+__device__ void scan_offsets(uint32_t* cnt, uint32_t* off0, int32_t nb, uint32_t* part, int32_t* goff) {
     const int tid = threadIdx.x;
     const int32_t chunk = (nb + PACK_THREADS - 1) / PACK_THREADS;
     const int32_t b0 = tid * chunk;
