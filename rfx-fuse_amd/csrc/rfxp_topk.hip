@@ -42,6 +42,8 @@ constexpr int TOPK_WAVES = TOPK_THREADS / 64;
 constexpr int TOPK_MAX_K = 64;
 constexpr int TOPK_MAX_SHIFT16 = 15;  // 32768 16-bit counters: 64 KB, two workgroups per CU
 constexpr int TOPK_SHIFT8 = 16;       // 65536 8-bit counters: 64 KB (top-K with T <= TOPK_MAX_T8)
+constexpr int TOPK_MAX_SHIFT8 = 17;   // 131072 8-bit counters: 128 KB, one workgroup per CU
+constexpr uint32_t TOPK_BLOCK = 32768;  // references selected at once (32 units per thread)
 constexpr int TOPK_MAX_T8 = 2048;     // at most 128 trees, 128 counting steps, per wave and segment
 constexpr int TOPK_MIN_SHIFT = 11;  // at least 2 counters per thread
 
@@ -65,15 +67,17 @@ struct TopkArgs {
     uint16_t* cnt_out;
 };
 
-// LDS layout: counters (64 KB at most: 2^shift 16-bit counters, or 2^16
-// 8-bit ones) | dummy words (1024) | per-segment bucket records of up to
+// LDS layout: counters (2^shift 16-bit counters, shift <= 15, or 2^shift
+// 8-bit ones, shift 16 or 17) | dummy words (1024) | per-segment bucket records of up to
 // 1024 trees (offset, length) | reduction scratch | candidate and running
 // lists.
 __host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) {
     return shift >= TOPK_SHIFT8 ? (1u << shift) : (1u << shift) * 2u;
 }
 constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
-constexpr uint32_t TOPK_RED_WORDS = 160;  // wave partials (48), two segment slots (2 x 48), a selection slot (16)
+// wave partials (48), two segment slots (2 x 80: five words per wave), a
+// selection slot (16)
+constexpr uint32_t TOPK_RED_WORDS = 224;
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
     return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
@@ -119,8 +123,8 @@ __device__ __forceinline__ void count16(uint32_t m, uint32_t base1, uint32_t wid
 // clamped to xlim, the unit of byte 0 of this thread's dummy word, which
 // sits after the counters with the other threads' dummy words; units between
 // the counters and xlim fall on those.  (A run holds only members of its
-// segment, lo <= j < lo + 65536, so a member never lands on a counter past
-// the segment's references.)
+// segment, lo <= j < lo + 2^shift, so a member never lands on a counter
+// past the segment's references.)
 template <int BITS>
 __device__ __forceinline__ void count_bits(uint32_t m, uint32_t base1, uint32_t xlim) {
     const uint32_t c = min(m - base1, xlim);
@@ -371,22 +375,22 @@ __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
 
 // LDS pointers of a top-K workgroup.
 struct TopkLds {
+    uint32_t* wsc;     // this wave's 128 words of the record area (run lists)
     uint32_t* red;     // reduction scratch (TOPK_RED_WORDS)
     uint32_t* cand_k;  // candidates of a segment
     uint32_t* cand_i;
     uint32_t* run_k;   // running top-K (sorted)
     uint32_t* run_i;
-    uint32_t* nrun_p;
 };
 
 __device__ __forceinline__ TopkLds topk_lds(uint32_t* sm, int32_t shift) {
     TopkLds L;
+    L.wsc = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + (threadIdx.x >> 6) * (TOPK_REC_WORDS / TOPK_WAVES);
     L.red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + TOPK_REC_WORDS;
     L.cand_k = L.red + TOPK_RED_WORDS;
     L.cand_i = L.cand_k + TOPK_MAX_K;
     L.run_k = L.cand_i + TOPK_MAX_K;
     L.run_i = L.run_k + TOPK_MAX_K;
-    L.nrun_p = L.run_i + TOPK_MAX_K;
     return L;
 }
 
@@ -431,12 +435,29 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* slot) {
     return wave_max((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
 }
 
+// Exclusive prefix over the lanes of a wave of n < 64, bit by bit from
+// ballots (mbcnt counts the set lanes below this one).
+__device__ __forceinline__ uint32_t wave_excl_prefix6(uint32_t n) {
+    uint32_t pre = 0;
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+        const uint64_t m = __ballot((n >> b) & 1u);
+        pre += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+    }
+    return pre;
+}
+
 // Merges the keys of one segment (thread x: units lo + u0 .. of key[NW],
-// u0 = 2 NW x) into the running list; M is the block's largest key, at
-// least `lowest` (the smallest key that can still enter).  Every thread
-// calls it; it ends with nrun / kmin updated and a barrier.
+// u0 = 2 NW x) into the running list; M is the block's largest key (or an
+// upper bound of it), at least `lowest` (the smallest key that can still
+// enter); tmax is this thread's largest key.  Keys are read only in waves
+// where some tmax reaches `lowest`: a wave without such a key skips every
+// pass over them.  Every thread calls it; it ends with nrun / kmin updated.
+// The LDS it writes (reduction slots, candidate and running lists) is next
+// written after the first barrier of the next call, which every thread
+// reaches only after its reads here, so it needs no closing barrier.
 template <int NW>
-__device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&key)[NW], uint32_t M,
+__device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&key)[NW], uint32_t tmax, uint32_t M,
                                             uint32_t lowest, uint32_t lo, uint32_t u0, const TopkLds& L,
                                             uint32_t& nrun, uint32_t& kmin) {
     const uint32_t K = (uint32_t)a.K;
@@ -445,37 +466,60 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
     uint32_t* const cand_i = L.cand_i;
     uint32_t* const run_k = L.run_k;
     uint32_t* const run_i = L.run_i;
-    uint32_t* const nrun_p = L.nrun_p;
+    const bool wlive = __ballot(tmax >= lowest) != 0ull;  // uniform
+    const uint32_t j0 = lo + u0;
     // only keys above the running threshold can enter the list.  cstar:
     // keys > cstar all enter, keys == cstar in index order up to K; it is
     // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
     // keys reach `lowest`.  One pass counts keys >= lowest and > lowest:
     // when at most K keys reach `lowest` (the usual case once the list is
-    // full) that settles it; otherwise a search over key levels, four
-    // levels per round.
+    // full) every one of them enters; otherwise a search over key levels,
+    // four levels per round.
     uint32_t n01 = 0;  // this thread: #(keys >= lowest) | #(keys > lowest) << 16
+    if (wlive) {
 #pragma unroll
-    for (int k = 0; k < NW; ++k) {
-        const uint32_t va = key[k] & 0xffffu, vb = key[k] >> 16;
-        n01 += (va >= lowest ? 1u : 0u) + (va > lowest ? 0x10000u : 0u);
-        n01 += (vb >= lowest ? 1u : 0u) + (vb > lowest ? 0x10000u : 0u);
+        for (int k = 0; k < NW; ++k) {
+            const uint32_t va = key[k] & 0xffffu, vb = key[k] >> 16;
+            n01 += (va >= lowest ? 1u : 0u) + (va > lowest ? 0x10000u : 0u);
+            n01 += (vb >= lowest ? 1u : 0u) + (vb > lowest ? 0x10000u : 0u);
+        }
     }
-    uint32_t tot01;
+    uint32_t tot01, wpre01;  // block total, and the total of the waves before this one
     {
-        uint32_t* const slot = red + 144;
+        uint32_t* const slot = red + TOPK_RED_WORDS - 16;
         const uint32_t ws = wave_sum(n01);
         if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = ws;
         __syncthreads();
-        tot01 = wave_sum((threadIdx.x & 63u) < (uint32_t)TOPK_WAVES ? slot[threadIdx.x & 63u] : 0u);
+        const uint32_t l = threadIdx.x & 63u;
+        const uint32_t x = l < (uint32_t)TOPK_WAVES ? slot[l] : 0u;
+        tot01 = wave_sum(x);
+        wpre01 = wave_sum(l < (threadIdx.x >> 6) ? x : 0u);
     }
-    uint32_t cstar = lowest, ngt, neq;
+    uint32_t nc;  // candidates (uniform)
     if ((tot01 & 0xffffu) <= K) {
-        ngt = n01 >> 16;
-        neq = (n01 & 0xffffu) - ngt;
+        // every key >= lowest enters, in slots of thread order (the merge
+        // ranks candidates by key and index, whatever their order)
+        nc = tot01 & 0xffffu;
+        if (wlive) {
+            const uint32_t n = n01 & 0xffffu;
+            uint32_t r = (wpre01 & 0xffffu) + wave_excl_prefix6(n);
+            if (n) {
+#pragma unroll
+                for (int k = 0; k < 2 * NW; ++k) {
+                    const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                    if (kk >= lowest) {
+                        cand_k[r] = kk;
+                        cand_i[r] = j0 + (uint32_t)k;
+                        ++r;
+                    }
+                }
+            }
+        }
     } else {
-        uint32_t c0 = lowest, w01, w23, m1 = 0u;
-        level_counts<NW>(key, c0, w01, w23);
+        uint32_t c0 = lowest, w01 = 0u, w23 = 0u, m1 = 0u;
+        if (wlive) level_counts<NW>(key, c0, w01, w23);
         block_levels(w01, w23, m1, red);
+        uint32_t cstar;
         for (;;) {
             const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
             const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
@@ -485,42 +529,46 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
             }
             c0 += 3u;
             uint32_t m2 = 0;
-            level_counts<NW>(key, c0, w01, w23);
+            w01 = w23 = 0u;
+            if (wlive) level_counts<NW>(key, c0, w01, w23);
             block_levels(w01, w23, m2, red);
         }
-        ngt = count_ge<NW>(key, cstar + 1u);
-        neq = count_ge<NW>(key, cstar) - ngt;
-    }
-    uint32_t tot;
-    const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
-    const uint32_t G = tot & 0xffffu, E = tot >> 16;
-    const uint32_t take = min(E, K - G);
-    uint32_t rg = pre & 0xffffu, re = pre >> 16;
-    if (ngt + neq) {
-        const uint32_t j0 = lo + u0;
+        uint32_t ngt = 0u, neq = 0u;
+        if (wlive) {
+            ngt = count_ge<NW>(key, cstar + 1u);
+            neq = count_ge<NW>(key, cstar) - ngt;
+        }
+        uint32_t tot;
+        const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
+        const uint32_t G = tot & 0xffffu, E = tot >> 16;
+        const uint32_t take = min(E, K - G);
+        nc = G + take;
+        uint32_t rg = pre & 0xffffu, re = pre >> 16;
+        if (ngt + neq) {
 #pragma unroll
-        for (int k = 0; k < 2 * NW; ++k) {
-            const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-            const uint32_t j = j0 + (uint32_t)k;
-            if (kk > cstar) {
-                cand_k[rg] = kk;
-                cand_i[rg] = j;
-                ++rg;
-            } else if (kk == cstar) {
-                if (re < take) {
-                    cand_k[G + re] = kk;
-                    cand_i[G + re] = j;
+            for (int k = 0; k < 2 * NW; ++k) {
+                const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                const uint32_t j = j0 + (uint32_t)k;
+                if (kk > cstar) {
+                    cand_k[rg] = kk;
+                    cand_i[rg] = j;
+                    ++rg;
+                } else if (kk == cstar) {
+                    if (re < take) {
+                        cand_k[G + re] = kk;
+                        cand_i[G + re] = j;
+                    }
+                    ++re;
                 }
-                ++re;
             }
         }
     }
     __syncthreads();
     // merge by rank (first wave; nrun, nc <= K <= 64, lane e holds running
-    // entry e and candidate e).  The running list is sorted; candidates have
-    // higher indices than every running entry, so a running entry keeps its
-    // place among running entries and precedes candidates of equal key.
-    const uint32_t nc = G + take;
+    // entry e and candidate e, and reads the others' with readlane).  The
+    // running list is sorted; candidates have higher indices than every
+    // running entry, so a running entry keeps its place among running
+    // entries and precedes candidates of equal key.
     if (threadIdx.x < 64) {
         const uint32_t e = threadIdx.x;
         const bool has_r = e < nrun, has_c = e < nc;
@@ -528,12 +576,13 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
         const uint32_t ck = has_c ? cand_k[e] : 0u, ci = has_c ? cand_i[e] : 0xffffffffu;
         uint32_t rank_r = e, rank_c = 0u;
         for (uint32_t c = 0; c < nc; ++c) {
-            const uint32_t fk = cand_k[c], fi = cand_i[c];
+            const uint32_t fk = (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)c);
+            const uint32_t fi = (uint32_t)__builtin_amdgcn_readlane((int)ci, (int)c);
             rank_r += fk > rk ? 1u : 0u;
             rank_c += better(fk, fi, ck, ci) ? 1u : 0u;
         }
-        if (has_c)
-            for (uint32_t f = 0; f < nrun; ++f) rank_c += run_k[f] >= ck ? 1u : 0u;
+        for (uint32_t f = 0; f < nrun; ++f)
+            rank_c += (uint32_t)__builtin_amdgcn_readlane((int)rk, (int)f) >= ck ? 1u : 0u;
         // one wave: its reads of the old list precede these writes
         if (has_r && rank_r < K) {
             run_k[rank_r] = rk;
@@ -543,12 +592,10 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
             run_k[rank_c] = ck;
             run_i[rank_c] = ci;
         }
-        if (threadIdx.x == 0) *nrun_p = min(nrun + nc, K);
     }
     __syncthreads();
-    nrun = *nrun_p;
+    nrun = min(nrun + nc, K);
     kmin = nrun ? run_k[nrun - 1] : 0u;
-    __syncthreads();
 }
 
 // Per-lane bucket runs of a query.  The wave's trees are [tw0, tw1); lane l
@@ -581,18 +628,56 @@ __device__ __forceinline__ LaneRuns lane_runs_init(const TopkArgs& a, int64_t q,
     return r;
 }
 
+// A wave's runs (lanes < nt, as in count_lane_runs), counted with the first
+// 64 members of every run in one pass and the rest of each longer run
+// appended to the same lane list: runs a little above 64 members, common
+// when a segment holds many references per leaf, then cost one more load in
+// the pipeline rather than a tail loop.  wsc: the wave's 128 words of LDS
+// scratch.
+template <int BITS>
+__device__ __forceinline__ uint32_t count_runs_split(const TopkArgs& a, uint32_t soff, uint32_t len4, int32_t nt,
+                                                     int32_t lane, uint32_t lane4, uint32_t base1, uint32_t dummy,
+                                                     uint32_t* wsc) {
+    const uint64_t lm = __ballot(len4 > 256u);
+    if (lm == 0u) return count_lane_runs<BITS>(a, soff, len4, nt, lane4, base1, dummy);
+    const int32_t n2 = (int32_t)__popcll(lm);
+    // entry p of the long runs: the rest of the run, (soff + 256, len4 - 256)
+    const uint32_t p = __builtin_amdgcn_mbcnt_hi((uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u));
+    if (len4 > 256u) {
+        wsc[p] = soff + 256u;
+        wsc[64 + p] = len4 - 256u;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t len1 = min(len4, 256u);
+    if (nt + n2 <= 64) {
+        // lane nt + e takes long-run entry e
+        const int32_t e = lane - nt;
+        const bool rest = e >= 0 && e < n2;
+        const uint32_t so = rest ? wsc[e] : soff;
+        const uint32_t ln = rest ? wsc[64 + e] : len1;
+        return count_lane_runs<BITS>(a, so, ln, nt + n2, lane4, base1, dummy);
+    }
+    uint32_t steps = count_lane_runs<BITS>(a, soff, len1, nt, lane4, base1, dummy);
+    const bool have = lane < n2;
+    steps += count_lane_runs<BITS>(a, have ? wsc[lane] : 0u, have ? wsc[64 + lane] : 0u, n2, lane4, base1, dummy);
+    return steps;
+}
+
 // Counts the query's runs of segment s into the BITS-bit counters (member j
 // at unit j + 1 - base1; the counters end where the dummy words begin);
 // returns the wave's counting steps.
 template <int BITS>
 __device__ __forceinline__ uint32_t count_query_segment(const TopkArgs& a, int64_t q, int32_t s, uint32_t soff,
                                                         uint32_t len4, int32_t tw0, int32_t tw1, int32_t lane,
-                                                        uint32_t lane4, uint32_t base1, uint32_t dummy) {
-    uint32_t steps = count_lane_runs<BITS>(a, soff, len4, min(tw1 - tw0, 64), lane4, base1, dummy);
+                                                        uint32_t lane4, uint32_t base1, uint32_t dummy,
+                                                        uint32_t* wsc) {
+    uint32_t steps = count_runs_split<BITS>(a, soff, len4, min(tw1 - tw0, 64), lane, lane4, base1, dummy, wsc);
     for (int32_t r0 = tw0 + 64; r0 < tw1; r0 += 64) {
         uint32_t so2, ln2;
         query_bucket(a, q, r0 + lane < tw1 ? r0 + lane : a.T, s, so2, ln2);
-        steps += count_lane_runs<BITS>(a, so2, ln2, min(tw1 - r0, 64), lane4, base1, dummy);
+        steps += count_runs_split<BITS>(a, so2, ln2, min(tw1 - r0, 64), lane, lane4, base1, dummy, wsc);
     }
     return steps;
 }
@@ -640,7 +725,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const uint32_t soff = lr.tb + 4u * lr.o0;
         const uint32_t len4 = 4u * (lr.o1 - lr.o0);
         const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
-        count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
+        count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
         lr.o0 = lr.o1;
         lr.o1 = lr.o2;
         lr.o2 = o3;
@@ -677,29 +762,38 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const uint32_t M = block_max(mloc, L.red + 48 + 16 * (s & 1));
         const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
         if (M < lowest) continue;
-        select_into<NW>(a, key, M, lowest, lo, u0, L, nrun, kmin);
+        select_into<NW>(a, key, mloc, M, lowest, lo, u0, L, nrun, kmin);
     }
     topk_write(a, q, L, nrun);
 }
 
-// 8-bit counters, 65536 references per segment (reference sets above 32768
-// samples, T <= TOPK_MAX_T8): half as many bucket runs per query as 16-bit
-// counters allow in the same 64 KB of LDS.  Thread x reads the counter bytes
-// of units 32x .. 32x + 31 of each half h (units h * 32768 + ...), so each
-// half is selected exactly like a 16-bit segment of 32768 references, in
-// index order.  CHECK (T > 255): a count of 256 or more wraps its byte; every
-// lane of every counting step adds 1 to one counter or dummy byte, so the
-// counts are exact iff all those bytes sum to 64 x the counting steps.  A
-// segment that fails the check is recounted with 16-bit counters, half by
-// half.
-template <bool CHECK>
-__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_topk8(TopkArgs a) {
+// 8-bit counters, NB blocks of TOPK_BLOCK = 32768 references per segment
+// (S = 65536 for reference sets of up to 65536 samples, two workgroups per
+// CU; S = 131072 above, one workgroup per CU), T <= TOPK_MAX_T8: a quarter
+// of the bucket runs per query that 16-bit counters allow in 64 KB of LDS,
+// and runs long enough to fill most of a 64-lane load.  Thread x reads the
+// counter bytes of units 32x .. 32x + 31 of each block h (units
+// h * 32768 + ...), so each block is selected exactly like a 16-bit segment
+// of 32768 references, in index order.  CHECK (T > 255): a count of 256 or
+// more wraps its byte; every lane of every counting step adds 1 to one
+// counter or dummy byte, so the counts are exact iff all those bytes sum to
+// 64 x the counting steps.  A segment that fails the check is recounted with
+// 16-bit counters, block by block.
+template <bool CHECK, int NB>
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16 / NB, 16 / NB))) void k_topk8(
+    TopkArgs a) {
+    static_assert(NB == 2 || NB == 4, "two or four blocks per segment");
     extern __shared__ uint32_t sm[];
-    constexpr uint32_t S = 1u << TOPK_SHIFT8;
-    constexpr uint32_t H = S / 2;
-    const TopkLds L = topk_lds(sm, TOPK_SHIFT8);
-    uint32_t* const dw = sm + (topk_dummy_off(TOPK_SHIFT8) >> 2) + threadIdx.x;  // this thread's dummy word
-    const uint32_t dummy = topk_dummy_off(TOPK_SHIFT8) + threadIdx.x * 4u;
+    constexpr int32_t SHIFT = NB == 2 ? TOPK_SHIFT8 : TOPK_SHIFT8 + 1;
+    constexpr uint32_t S = 1u << SHIFT;
+    constexpr uint32_t B = TOPK_BLOCK;
+    static_assert(S == NB * B, "segment = NB blocks");
+    const TopkLds L = topk_lds(sm, SHIFT);
+    uint32_t* const dw = sm + (topk_dummy_off(SHIFT) >> 2) + threadIdx.x;  // this thread's dummy word
+    const uint32_t dummy = topk_dummy_off(SHIFT) + threadIdx.x * 4u;
+    // the 16-bit recount of a block counts into bytes 0 .. 2B - 1; its
+    // out-of-block members go to the words 2B/4 + x (x < 1024) right after
+    const uint32_t dummy16 = 2u * B + threadIdx.x * 4u;
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int32_t lane = (int32_t)(threadIdx.x & 63u);
@@ -716,29 +810,30 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     }
     __syncthreads();
 
-    const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each half
+    const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each block
     uint32_t nrun = 0;
     uint32_t kmin = 0;
     for (int32_t s = 0; s < a.nseg; ++s) {
-        const uint32_t lo = (uint32_t)s << TOPK_SHIFT8;
+        const uint32_t lo = (uint32_t)s << SHIFT;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
         const uint32_t soff = lr.tb + 4u * lr.o0;
         const uint32_t len4 = 4u * (lr.o1 - lr.o0);
         const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
         const uint32_t steps =
-            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
+            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
         lr.o0 = lr.o1;
         lr.o1 = lr.o2;
         lr.o2 = o3;
         __syncthreads();  // every count is in LDS
-        // the thread's counter bytes of both halves (units 32x .. 32x + 31 of
-        // each, 8 words): per-half largest count (every unit, valid or not:
+        // the thread's counter bytes of every block (units 32x .. 32x + 31 of
+        // each, 8 words): per-block largest count (every unit, valid or not:
         // an upper bound) and, for the check, the byte sum with the dummy word
-        uint4* const pw[2] = {(uint4*)(sm + 8u * threadIdx.x), (uint4*)(sm + H / 4u + 8u * threadIdx.x)};
-        uint32_t mh[2];
+        uint4* pw[NB];
+        uint32_t mh[NB];
         int32_t bal = 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NB; ++h) {
+            pw[h] = (uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
             const uint4 x = pw[h][0], y = pw[h][1];
             const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
             uint32_t m2 = 0u;
@@ -754,63 +849,87 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
             if (lane == 0) bal -= 64 * (int32_t)steps;
         }
-        // block reduction of (max half 0, max half 1, byte balance)
-        uint32_t M0, M1;
+        // block reduction of (max of each block, byte balance): NB + 1 words
+        // per wave in one of two alternating slots
+        uint32_t M[NB];
         bool exact = true;
         {
-            uint32_t* const slot = L.red + 48 + 48 * (s & 1);
-            const uint32_t w0 = wave_max(mh[0]), w1 = wave_max(mh[1]);
+            constexpr uint32_t SW = NB + 1;
+            uint32_t* const slot = L.red + 48 + SW * TOPK_WAVES * (uint32_t)(s & 1);
+            uint32_t wm[NB];
+#pragma unroll
+            for (int h = 0; h < NB; ++h) wm[h] = wave_max(mh[h]);
             const uint32_t wb = CHECK ? wave_sum((uint32_t)bal) : 0u;
             if (lane == 0) {
-                slot[3 * (threadIdx.x >> 6)] = w0;
-                slot[3 * (threadIdx.x >> 6) + 1] = w1;
-                slot[3 * (threadIdx.x >> 6) + 2] = wb;
+#pragma unroll
+                for (int h = 0; h < NB; ++h) slot[SW * (threadIdx.x >> 6) + h] = wm[h];
+                slot[SW * (threadIdx.x >> 6) + NB] = wb;
             }
             __syncthreads();
             const bool have = (uint32_t)lane < (uint32_t)TOPK_WAVES;
-            M0 = wave_max(have ? slot[3 * lane] : 0u) + 1u;
-            M1 = wave_max(have ? slot[3 * lane + 1] : 0u) + 1u;
-            if constexpr (CHECK) exact = wave_sum(have ? slot[3 * lane + 2] : 0u) == 0u;
+#pragma unroll
+            for (int h = 0; h < NB; ++h) M[h] = wave_max(have ? slot[SW * lane + h] : 0u) + 1u;
+            if constexpr (CHECK) exact = wave_sum(have ? slot[SW * lane + NB] : 0u) == 0u;
         }
         if (exact) {
-            // keys of each half from its counter bytes; a half whose largest
-            // key cannot enter the list is skipped
+            // keys of each block from its counter bytes; a block past the
+            // references, or whose largest key cannot enter the list, is
+            // skipped
 #pragma unroll 1
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < NB; ++h) {
+                if ((uint32_t)h * B >= width) break;
                 const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-                if ((h == 0 ? M0 : M1) < lowest) continue;
-                const uint32_t loh = lo + (uint32_t)h * H;
-                const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (H / 4u) + 8u * threadIdx.x);
-                const uint4 x = ph[0], y = ph[1];
-                const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-                uint32_t key[16];
+                uint32_t Mh = M[0];
 #pragma unroll
-                for (int k = 0; k < 16; ++k)
-                    key[k] = __builtin_amdgcn_perm(0u, w8[k >> 1], (k & 1) ? 0x0c030c02u : 0x0c010c00u);
-                const int32_t rem = (int32_t)width - (int32_t)(h * H) - (int32_t)u0;
-                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
-                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
-                keys_of_counts<16>(key, rem, exu);
-                select_into<16>(a, key, h == 0 ? M0 : M1, lowest, loh, u0, L, nrun, kmin);
+                for (int g = 1; g < NB; ++g) Mh = h == g ? M[g] : Mh;
+                if (Mh < lowest) continue;
+                const uint32_t loh = lo + (uint32_t)h * B;
+                // keys only in waves where some thread's largest count can
+                // enter
+                uint32_t mt = mh[0];
+#pragma unroll
+                for (int g = 1; g < NB; ++g) mt = h == g ? mh[g] : mt;
+                uint32_t key[16];
+                uint32_t tmax = 0u;
+                if (__ballot(mt + 1u >= lowest) != 0ull) {
+                    const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
+                    const uint4 x = ph[0], y = ph[1];
+                    const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+                    for (int k = 0; k < 16; ++k)
+                        key[k] = __builtin_amdgcn_perm(0u, w8[k >> 1], (k & 1) ? 0x0c030c02u : 0x0c010c00u);
+                    const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
+                    const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                    const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                    tmax = keys_of_counts<16>(key, rem, exu);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) key[k] = 0u;
+                }
+                select_into<16>(a, key, tmax, Mh, lowest, loh, u0, L, nrun, kmin);
             }
-            pw[0][0] = make_uint4(0u, 0u, 0u, 0u);
-            pw[0][1] = make_uint4(0u, 0u, 0u, 0u);
-            pw[1][0] = make_uint4(0u, 0u, 0u, 0u);
-            pw[1][1] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+            }
             if constexpr (CHECK) *dw = 0u;
         } else {
             // some count wrapped: recount the segment with 16-bit counters,
-            // half by half, zeroing each half's words as they are read
-            pw[0][0] = make_uint4(0u, 0u, 0u, 0u);
-            pw[0][1] = make_uint4(0u, 0u, 0u, 0u);
-            pw[1][0] = make_uint4(0u, 0u, 0u, 0u);
-            pw[1][1] = make_uint4(0u, 0u, 0u, 0u);
+            // block by block, zeroing each block's words as they are read
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            *dw = 0u;
             __syncthreads();
             uint32_t* const kw = sm + 16u * threadIdx.x;
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t loh = lo + (uint32_t)h * H;
-                const uint32_t wh = (uint32_t)min(max((int32_t)width - (int32_t)(h * H), 0), (int32_t)H);
-                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy);
+            for (int h = 0; h < NB; ++h) {
+                if ((uint32_t)h * B >= width) break;
+                const uint32_t loh = lo + (uint32_t)h * B;
+                const uint32_t wh = min(width - (uint32_t)h * B, B);
+                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
                 __syncthreads();
                 uint32_t key[16];
 #pragma unroll
@@ -826,12 +945,13 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                 const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
                 const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
                 const uint32_t mloc = keys_of_counts<16>(key, rem, exu);
-                const uint32_t M = block_max(mloc, L.red + 48 + 16 * h);
+                const uint32_t Mh = block_max(mloc, L.red + 48 + 16 * h);
                 const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-                if (M >= lowest) select_into<16>(a, key, M, lowest, loh, u0, L, nrun, kmin);
+                if (Mh >= lowest) select_into<16>(a, key, mloc, Mh, lowest, loh, u0, L, nrun, kmin);
                 __syncthreads();  // the block_max slot is read before its next use
             }
-            *dw = 0u;
+            // the recount's out-of-block members: words 2B/4 .. 2B/4 + 1023
+            sm[(2u * B) / 4u + threadIdx.x] = 0u;
         }
         __syncthreads();  // every counter word is zero again before the next segment's counts
     }
@@ -852,24 +972,32 @@ struct OutlierArgs {
     float* raw_out;
 };
 
+__host__ __device__ constexpr int32_t outlier_layout_shift(int32_t shift) {
+    return shift < TOPK_SHIFT8 ? shift : TOPK_SHIFT8;
+}
+
 template <int NW>
 __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_outlier(TopkArgs a,
                                                                                                     OutlierArgs o) {
     extern __shared__ uint32_t sm[];
     const int32_t shift = a.shift;
     const uint32_t S = 1u << shift;
-    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
+    // counting passes use 16-bit counters for at most 32768 references: the
+    // LDS layout of a 64 KB counter area whatever the segment size
+    const int32_t ls = outlier_layout_shift(shift);
+    uint32_t* const rec_off = sm + (topk_dummy_off(ls) + TOPK_THREADS * 4) / 4;
     uint32_t* const rec_len = rec_off + TOPK_THREADS;
     double* const red = (double*)(rec_len + TOPK_THREADS);  // TOPK_WAVES doubles
     const uint32_t* const kw = sm + threadIdx.x * NW;
-    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
+    const uint32_t dummy = topk_dummy_off(ls) + threadIdx.x * 4u;
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t q = a.q0 + blockIdx.x;
     const int64_t ex = query_exclusion(a, q);
     const float fT = (float)a.T;
     // 16-bit counters for at most 32768 references per counting pass: a
-    // segment of 65536 references is counted in two passes over its runs
+    // segment of 65536 or 131072 references is counted in two or four
+    // passes over its runs
     const uint32_t C = min(S, 1u << TOPK_MAX_SHIFT16);
 
     double acc = 0.0;
@@ -1007,7 +1135,7 @@ static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
 
 template <int NW>
 static hipError_t launch_outlier(rfxp_ctx* ctx, TopkArgs a, const OutlierArgs& o, int64_t Q) {
-    const size_t lds = topk_lds_bytes(a.shift);
+    const size_t lds = topk_lds_bytes(outlier_layout_shift(a.shift));
     hipError_t e = hipFuncSetAttribute((const void*)k_outlier<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
@@ -1062,9 +1190,10 @@ extern "C" int rfxp_set_reference(rfxp_ctx* ctx, const int32_t* leaf, int64_t st
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_set_reference: leaf must be a device pointer");
     if (N * (int64_t)T + MEM_PAD > (1LL << 30) - 1)
         return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_set_reference: N*T must stay below 2^30");
-    // segments of 2^shift references: 8-bit counters (65536 per segment)
-    // when the counts of a wave's trees fit their check, else 16-bit ones
-    const int32_t max_shift = T <= TOPK_MAX_T8 ? TOPK_SHIFT8 : TOPK_MAX_SHIFT16;
+    // segments of 2^shift references: 8-bit counters (65536 or 131072 per
+    // segment) when the counts of a wave's trees fit their check, else
+    // 16-bit ones (at most 32768)
+    const int32_t max_shift = T <= TOPK_MAX_T8 ? TOPK_MAX_SHIFT8 : TOPK_MAX_SHIFT16;
     int32_t shift = TOPK_MIN_SHIFT;
     while (shift < max_shift && (1LL << shift) < N) ++shift;
     const int64_t nseg = (N + (1LL << shift) - 1) >> shift;
@@ -1120,9 +1249,13 @@ extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
             case 13: e = launch_topk<4>(ctx, a, Q); break;
             case 14: e = launch_topk<8>(ctx, a, Q); break;
             case 15: e = launch_topk<16>(ctx, a, Q); break;
+            case TOPK_SHIFT8:
+                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 2>, a, Q)
+                               : launch_topk_kernel(ctx, k_topk8<true, 2>, a, Q);
+                break;
             default:
-                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false>, a, Q)
-                               : launch_topk_kernel(ctx, k_topk8<true>, a, Q);
+                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 4>, a, Q)
+                               : launch_topk_kernel(ctx, k_topk8<true, 4>, a, Q);
                 break;
         }
     }

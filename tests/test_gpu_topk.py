@@ -40,25 +40,29 @@ def test_all_trees_topk_matches_oracle(gpu_ctx, n, t, nleaf, q, k):
 
 
 def test_eight_bit_segments_with_wrapped_counts(gpu_ctx):
-    """Reference sets above 32768 samples with T <= 2048 are counted with 8-bit
-    counters in segments of 65536; T = 300 > 255 turns on the byte-sum check.
-    Copies of the queries planted in both halves of a segment, on the two
-    sides of a segment boundary and in the short last segment reach counts
-    of 300 (and 280 for a near copy), which wrap 8 bits and force the 16-bit
-    recount; with and without the exclusion of one planted copy.  Outlier
-    sums over the same segments too."""
+    """Reference sets above 65536 samples with T <= 2048 are counted with 8-bit
+    counters in segments of 131072 (four blocks of 32768); T = 300 > 255
+    turns on the byte-sum check.  Copies of the queries planted in several
+    blocks of a segment, on the two sides of block boundaries and of the
+    segment boundary, and in the short last segment reach counts of 300 (and
+    280 for a near copy), which wrap 8 bits and force the 16-bit recount,
+    block by block; with and without the exclusion of one planted copy.  40
+    leaves make runs of thousands of members (loads past the first 128).
+    Outlier sums over the same segments too."""
     rng = np.random.default_rng(31)
     n, t, nleaf, q, k = 140_000, 300, 40, 6, 20
     ref = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
     qs = rng.integers(0, nleaf, size=(q, t), dtype=np.int32)
     for pos in (1000, 40000, 100000, 139999):
         ref[:, pos] = qs[0]
-    for pos in (65535, 65536):
+    for pos in (131071, 131072):
         ref[:, pos] = qs[1]
+    for pos in (32767, 98304):
+        ref[:, pos] = qs[2]
     near = qs[3].copy()
     near[:20] = (near[:20] + 1) % nleaf          # 280 of 300 trees match
     ref[:, 70000] = near
-    ref[:, 131071] = qs[4]
+    ref[:, 65535] = qs[4]
     got_i, got_c = run_topk(gpu_ctx, ref, nleaf, qs, k)
     want_i, want_c = O.topk_all(ref, qs, k)
     assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
@@ -74,7 +78,8 @@ def test_eight_bit_segments_with_wrapped_counts(gpu_ctx):
     assert np.allclose(raw.cpu().numpy(), want, rtol=1e-6, atol=0)
 
 
-@pytest.mark.parametrize("n,t,nleaf", [(70_000, 1100, 30),    # 8-bit segments, more than 64 trees per wave
+@pytest.mark.parametrize("n,t,nleaf", [(70_000, 1100, 30),    # 8-bit, 3 of 4 blocks used, > 64 trees per wave
+                                       (60_000, 400, 25),     # 8-bit segments of two blocks, counts wrap
                                        (40_000, 2100, 20)])   # above 2048 trees: 16-bit segments of 32768
 def test_many_trees(gpu_ctx, n, t, nleaf):
     rng = np.random.default_rng(n + t)
