@@ -966,48 +966,57 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
 // with c_j / T a float division and its square a float product, as the
 // reference computes them; the terms are summed in double (the reference
 // sums floats in hash-map order, which no order reproduces), then rounded
-// to float.  The counts come from count_segment, exactly as for top-K.
+// to float.  The counts come from the top-K counting, segment by segment.
 struct OutlierArgs {
     float numerator, isolated;
     float* raw_out;
 };
 
-__host__ __device__ constexpr int32_t outlier_layout_shift(int32_t shift) {
-    return shift < TOPK_SHIFT8 ? shift : TOPK_SHIFT8;
+// One term (c / T)^2, rounded as the reference rounds it.
+__device__ __forceinline__ double outlier_term(uint32_t c, float fT) {
+    const float p = (float)c / fT;
+    return (double)(p * p);
 }
 
+// Block sum of the threads' acc and the raw score of query q (thread 0);
+// red: TOPK_WAVES doubles.
+__device__ __forceinline__ void outlier_finish(double acc, double* red, const OutlierArgs& o, int64_t q) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < TOPK_WAVES; ++w) t += red[w];
+        const float sq = (float)t;
+        o.raw_out[q] = sq > 1e-10f ? o.numerator / sq : o.isolated;
+    }
+}
+
+// 16-bit counters, segments of S = 2^shift <= 32768 references (reference
+// sets of up to 32768 samples, or more than TOPK_MAX_T8 trees).
 template <int NW>
 __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_outlier(TopkArgs a,
                                                                                                     OutlierArgs o) {
     extern __shared__ uint32_t sm[];
     const int32_t shift = a.shift;
     const uint32_t S = 1u << shift;
-    // counting passes use 16-bit counters for at most 32768 references: the
-    // LDS layout of a 64 KB counter area whatever the segment size
-    const int32_t ls = outlier_layout_shift(shift);
-    uint32_t* const rec_off = sm + (topk_dummy_off(ls) + TOPK_THREADS * 4) / 4;
+    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
     uint32_t* const rec_len = rec_off + TOPK_THREADS;
     double* const red = (double*)(rec_len + TOPK_THREADS);  // TOPK_WAVES doubles
     const uint32_t* const kw = sm + threadIdx.x * NW;
-    const uint32_t dummy = topk_dummy_off(ls) + threadIdx.x * 4u;
+    const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t q = a.q0 + blockIdx.x;
     const int64_t ex = query_exclusion(a, q);
     const float fT = (float)a.T;
-    // 16-bit counters for at most 32768 references per counting pass: a
-    // segment of 65536 or 131072 references is counted in two or four
-    // passes over its runs
-    const uint32_t C = min(S, 1u << TOPK_MAX_SHIFT16);
 
     double acc = 0.0;
-    for (int32_t sp = 0; sp < a.nseg * (int32_t)(S / C); ++sp) {
-        const int32_t s = sp / (int32_t)(S / C);
-        const int64_t lo64 = ((int64_t)s << shift) + (int64_t)(sp % (int32_t)(S / C)) * C;
-        if (lo64 >= a.N) continue;  // uniform: every thread skips the pass
-        const uint32_t lo = (uint32_t)lo64;
-        const uint32_t width = (uint32_t)min((int64_t)C, a.N - lo64);
-        count_segment(a, q, s, C, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
+    for (int32_t s = 0; s < a.nseg; ++s) {
+        const uint32_t lo = (uint32_t)s << shift;
+        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
         const uint32_t u0 = threadIdx.x * 2u * NW;
         const int32_t rem = (int32_t)width - (int32_t)u0;
         const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
@@ -1018,24 +1027,161 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t c = (w >> (16 * h)) & 0xffffu;
-                if (c != 0u && 2 * k + h < rem && 2 * k + h != exu) {
-                    const float p = (float)c / fT;
-                    acc += (double)(p * p);
-                }
+                if (c != 0u && 2 * k + h < rem && 2 * k + h != exu) acc += outlier_term(c, fT);
             }
         }
         __syncthreads();  // counters read before the next segment clears them
     }
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d, 64);
-    if ((threadIdx.x & 63) == 0) red[wave] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (int w = 0; w < TOPK_WAVES; ++w) t += red[w];
-        const float sq = (float)t;
-        o.raw_out[q] = sq > 1e-10f ? o.numerator / sq : o.isolated;
+    outlier_finish(acc, red, o, q);
+}
+
+// 8-bit counters in the segments of k_topk8 (NB blocks of TOPK_BLOCK
+// references; reference sets above 32768 samples, T <= TOPK_MAX_T8): one
+// pass over the query's runs per segment.  Every thread then adds the terms
+// of its counter bytes from a table of the 256 possible ones (tab[c] =
+// (c / T)^2, tab[0] = 0, so units without members -- those past the
+// references included -- add nothing) and takes the excluded reference's
+// term back out.  A segment whose byte sum fails the check (T > 255) is
+// recounted with 16-bit counters, block by block, as in k_topk8.
+constexpr uint32_t OUTLIER_TAB_BYTES = 256 * 8;
+
+template <bool CHECK, int NB>
+__global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16 / NB, 16 / NB))) void k_outlier8(
+    TopkArgs a, OutlierArgs o) {
+    static_assert(NB == 2 || NB == 4, "two or four blocks per segment");
+    extern __shared__ uint32_t sm[];
+    constexpr int32_t SHIFT = NB == 2 ? TOPK_SHIFT8 : TOPK_SHIFT8 + 1;
+    constexpr uint32_t S = 1u << SHIFT;
+    constexpr uint32_t B = TOPK_BLOCK;
+    const TopkLds L = topk_lds(sm, SHIFT);
+    double* const tab = (double*)(sm + topk_lds_bytes(SHIFT) / 4u);
+    double* const red = (double*)L.red;  // TOPK_WAVES doubles at the end
+    uint32_t* const dw = sm + (topk_dummy_off(SHIFT) >> 2) + threadIdx.x;
+    const uint32_t dummy = topk_dummy_off(SHIFT) + threadIdx.x * 4u;
+    const uint32_t dummy16 = 2u * B + threadIdx.x * 4u;  // as in k_topk8
+    const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t lane = (int32_t)(threadIdx.x & 63u);
+    const int64_t q = a.q0 + blockIdx.x;
+    const int64_t ex = query_exclusion(a, q);
+    const float fT = (float)a.T;
+    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
+    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
+    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
+    if (threadIdx.x < 256) tab[threadIdx.x] = threadIdx.x ? outlier_term(threadIdx.x, fT) : 0.0;
+    {
+        uint4* c4 = (uint4*)sm;
+        for (uint32_t w = threadIdx.x; w < S / 16u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+        *dw = 0u;
     }
+    __syncthreads();
+
+    const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each block
+    double acc = 0.0;
+    for (int32_t s = 0; s < a.nseg; ++s) {
+        const uint32_t lo = (uint32_t)s << SHIFT;
+        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+        const uint32_t soff = lr.tb + 4u * lr.o0;
+        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+        const uint32_t steps =
+            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+        lr.o0 = lr.o1;
+        lr.o1 = lr.o2;
+        lr.o2 = o3;
+        __syncthreads();  // every count is in LDS
+        uint4* pw[NB];
+#pragma unroll
+        for (int h = 0; h < NB; ++h) pw[h] = (uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
+        bool exact = true;
+        if constexpr (CHECK) {
+            int32_t bal = 0;
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                const uint4 x = pw[h][0], y = pw[h][1];
+                bal = (int32_t)__builtin_amdgcn_sad_u8(x.x, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(x.y, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(x.z, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(x.w, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(y.x, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(y.y, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(y.z, 0u, (uint32_t)bal);
+                bal = (int32_t)__builtin_amdgcn_sad_u8(y.w, 0u, (uint32_t)bal);
+            }
+            bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
+            if (lane == 0) bal -= 64 * (int32_t)steps;
+            uint32_t* const slot = L.red + 48 + 16 * (uint32_t)(s & 1);
+            const uint32_t wb = wave_sum((uint32_t)bal);
+            if (lane == 0) slot[threadIdx.x >> 6] = wb;
+            __syncthreads();
+            exact = wave_sum((uint32_t)lane < (uint32_t)TOPK_WAVES ? slot[lane] : 0u) == 0u;
+        }
+        if (exact) {
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    const uint4 x = pw[h][v];
+                    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) acc += tab[(w4[k] >> (8 * b)) & 0xffu];
+                }
+            }
+            // the excluded reference, if in this segment: unit h * B + 32 x + r
+            const int64_t exd = ex - (int64_t)lo;
+            if (exd >= 0 && exd < (int64_t)width) {
+                const uint32_t eu = (uint32_t)exd;
+                if ((eu % B) / 32u == threadIdx.x) {
+                    const uint32_t r = eu % 32u;
+                    const uint32_t w = sm[(eu / B) * (B / 4u) + 8u * threadIdx.x + r / 4u];
+                    acc -= tab[(w >> (8u * (r % 4u))) & 0xffu];
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            if constexpr (CHECK) *dw = 0u;
+        } else {
+            // some count wrapped: recount the segment with 16-bit counters,
+            // block by block, zeroing each block's words as they are read
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            *dw = 0u;
+            __syncthreads();
+            uint32_t* const kw = sm + 16u * threadIdx.x;
+            for (int h = 0; h < NB; ++h) {
+                if ((uint32_t)h * B >= width) break;
+                const uint32_t loh = lo + (uint32_t)h * B;
+                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
+                __syncthreads();
+                const int32_t rem = (int32_t)min(width - (uint32_t)h * B, B) - (int32_t)u0;
+                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const uint32_t w = kw[k];
+                    kw[k] = 0u;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const uint32_t c = (w >> (16 * hh)) & 0xffffu;
+                        if (c != 0u && 2 * k + hh < rem && 2 * k + hh != exu) acc += outlier_term(c, fT);
+                    }
+                }
+                __syncthreads();  // every counter word is zero before the next block's counts
+            }
+            // the recount's out-of-block members: words 2B/4 .. 2B/4 + 1023
+            sm[(2u * B) / 4u + threadIdx.x] = 0u;
+        }
+        __syncthreads();  // every counter word is zero again before the next segment's counts
+    }
+    outlier_finish(acc, red, o, q);
 }
 
 // compute_proximity_from_leaves (src/rf_random_forest.cpp:4605-4642) for a
@@ -1133,18 +1279,30 @@ static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
     return launch_topk_kernel(ctx, k_topk<NW>, a, Q);
 }
 
-template <int NW>
-static hipError_t launch_outlier(rfxp_ctx* ctx, TopkArgs a, const OutlierArgs& o, int64_t Q) {
-    const size_t lds = topk_lds_bytes(outlier_layout_shift(a.shift));
-    hipError_t e = hipFuncSetAttribute((const void*)k_outlier<NW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+template <typename Kern>
+static hipError_t launch_outlier_kernel(rfxp_ctx* ctx, Kern kern, TopkArgs a, const OutlierArgs& o, int64_t Q,
+                                        size_t lds) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
         a.q0 = q0;
         const unsigned nq = (unsigned)std::min(TOPK_MAX_GRID, Q - q0);
-        hipLaunchKernelGGL(k_outlier<NW>, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a, o);
+        hipLaunchKernelGGL(kern, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a, o);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+template <int NW>
+static hipError_t launch_outlier(rfxp_ctx* ctx, TopkArgs a, const OutlierArgs& o, int64_t Q) {
+    return launch_outlier_kernel(ctx, k_outlier<NW>, a, o, Q, topk_lds_bytes(a.shift));
+}
+
+template <int NB>
+static hipError_t launch_outlier8(rfxp_ctx* ctx, TopkArgs a, const OutlierArgs& o, int64_t Q) {
+    const size_t lds = topk_lds_bytes(a.shift) + OUTLIER_TAB_BYTES;
+    return a.T <= 255 ? launch_outlier_kernel(ctx, k_outlier8<false, NB>, a, o, Q, lds)
+                      : launch_outlier_kernel(ctx, k_outlier8<true, NB>, a, o, Q, lds);
 }
 
 // Arguments of a query launch over the context's reference set.
@@ -1324,7 +1482,9 @@ extern "C" int rfxp_outlier_raw(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_
             case 12: e = launch_outlier<2>(ctx, a, o, Q); break;
             case 13: e = launch_outlier<4>(ctx, a, o, Q); break;
             case 14: e = launch_outlier<8>(ctx, a, o, Q); break;
-            default: e = launch_outlier<16>(ctx, a, o, Q); break;
+            case 15: e = launch_outlier<16>(ctx, a, o, Q); break;
+            case TOPK_SHIFT8: e = launch_outlier8<2>(ctx, a, o, Q); break;
+            default: e = launch_outlier8<4>(ctx, a, o, Q); break;
         }
     }
     if (e != hipSuccess) return hip_error(ctx, e, "k_outlier launch");

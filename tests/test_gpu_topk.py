@@ -91,6 +91,12 @@ def test_many_trees(gpu_ctx, n, t, nleaf):
     want_i, want_c = O.topk_all(ref, qs, 12)
     assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
     assert got_c[0, 0] == t
+    # outlier sums over the same segments (the wrapped ones recounted), one
+    # planted copy excluded
+    raw = gpu_ctx.outlier_raw(dev(qs), exclude_base=33_000, numerator=float(n - 1), isolated=n * 1e10)
+    want = O.outlier_raw(ref, nleaf, qs, exclude=np.arange(33_000, 33_005, dtype=np.int32),
+                         numerator=float(n - 1), isolated=n * 1e10)
+    assert np.allclose(raw.cpu().numpy(), want, rtol=1e-6, atol=0)
 
 
 def test_invalid_labels_never_match(gpu_ctx):
