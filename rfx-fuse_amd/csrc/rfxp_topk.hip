@@ -447,133 +447,95 @@ __device__ __forceinline__ uint32_t wave_excl_prefix6(uint32_t n) {
     return pre;
 }
 
-// Merges the keys of one segment (thread x: units lo + u0 .. of key[NW],
-// u0 = 2 NW x) into the running list; M is the block's largest key (or an
-// upper bound of it), at least `lowest` (the smallest key that can still
-// enter); tmax is this thread's largest key.  Keys are read only in waves
-// where some tmax reaches `lowest`: a wave without such a key skips every
-// pass over them.  Every thread calls it; it ends with nrun / kmin updated.
-// The LDS it writes (reduction slots, candidate and running lists) is next
-// written after the first barrier of the next call, which every thread
-// reaches only after its reads here, so it needs no closing barrier.
+// Block total of n (< 2^16 per thread) and the total of the waves before
+// this one, through 16 words of the selection slot; one barrier.
+__device__ __forceinline__ void block_count(uint32_t n, const TopkLds& L, uint32_t& tot, uint32_t& wpre) {
+    uint32_t* const slot = L.red + TOPK_RED_WORDS - 16;
+    const uint32_t ws = wave_sum(n);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = ws;
+    __syncthreads();
+    const uint32_t l = threadIdx.x & 63u;
+    const uint32_t x = l < (uint32_t)TOPK_WAVES ? slot[l] : 0u;
+    tot = wave_sum(x);
+    wpre = wave_sum(l < (threadIdx.x >> 6) ? x : 0u);
+}
+
+// More than K keys reach `lowest`: cstar is the largest c with
+// #(keys >= c) >= K, found by a search over key levels (four per round, M
+// bounding the largest key); keys > cstar become candidates, and keys ==
+// cstar in index order up to K.  Returns the candidate count; ends with a
+// barrier.  Keys are read only in waves with wlive set.
 template <int NW>
-__device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&key)[NW], uint32_t tmax, uint32_t M,
-                                            uint32_t lowest, uint32_t lo, uint32_t u0, const TopkLds& L,
-                                            uint32_t& nrun, uint32_t& kmin) {
+__device__ __forceinline__ uint32_t select_search(const TopkArgs& a, const uint32_t (&key)[NW], bool wlive,
+                                                  uint32_t M, uint32_t lowest, uint32_t j0, const TopkLds& L) {
     const uint32_t K = (uint32_t)a.K;
     uint32_t* const red = L.red;
-    uint32_t* const cand_k = L.cand_k;
-    uint32_t* const cand_i = L.cand_i;
-    uint32_t* const run_k = L.run_k;
-    uint32_t* const run_i = L.run_i;
-    const bool wlive = __ballot(tmax >= lowest) != 0ull;  // uniform
-    const uint32_t j0 = lo + u0;
-    // only keys above the running threshold can enter the list.  cstar:
-    // keys > cstar all enter, keys == cstar in index order up to K; it is
-    // the largest c with #(keys >= c) >= K, or `lowest` when fewer than K
-    // keys reach `lowest`.  One pass counts keys >= lowest and > lowest:
-    // when at most K keys reach `lowest` (the usual case once the list is
-    // full) every one of them enters; otherwise a search over key levels,
-    // four levels per round.
-    uint32_t n01 = 0;  // this thread: #(keys >= lowest) | #(keys > lowest) << 16
-    if (wlive) {
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            const uint32_t va = key[k] & 0xffffu, vb = key[k] >> 16;
-            n01 += (va >= lowest ? 1u : 0u) + (va > lowest ? 0x10000u : 0u);
-            n01 += (vb >= lowest ? 1u : 0u) + (vb > lowest ? 0x10000u : 0u);
+    uint32_t c0 = lowest, w01 = 0u, w23 = 0u, m1 = 0u;
+    if (wlive) level_counts<NW>(key, c0, w01, w23);
+    block_levels(w01, w23, m1, red);
+    uint32_t cstar;
+    for (;;) {
+        const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
+        const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
+        if (d < 3u || c0 + 3u >= M) {
+            cstar = c0 + d;
+            break;
         }
-    }
-    uint32_t tot01, wpre01;  // block total, and the total of the waves before this one
-    {
-        uint32_t* const slot = red + TOPK_RED_WORDS - 16;
-        const uint32_t ws = wave_sum(n01);
-        if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = ws;
-        __syncthreads();
-        const uint32_t l = threadIdx.x & 63u;
-        const uint32_t x = l < (uint32_t)TOPK_WAVES ? slot[l] : 0u;
-        tot01 = wave_sum(x);
-        wpre01 = wave_sum(l < (threadIdx.x >> 6) ? x : 0u);
-    }
-    uint32_t nc;  // candidates (uniform)
-    if ((tot01 & 0xffffu) <= K) {
-        // every key >= lowest enters, in slots of thread order (the merge
-        // ranks candidates by key and index, whatever their order)
-        nc = tot01 & 0xffffu;
-        if (wlive) {
-            const uint32_t n = n01 & 0xffffu;
-            uint32_t r = (wpre01 & 0xffffu) + wave_excl_prefix6(n);
-            if (n) {
-#pragma unroll
-                for (int k = 0; k < 2 * NW; ++k) {
-                    const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                    if (kk >= lowest) {
-                        cand_k[r] = kk;
-                        cand_i[r] = j0 + (uint32_t)k;
-                        ++r;
-                    }
-                }
-            }
-        }
-    } else {
-        uint32_t c0 = lowest, w01 = 0u, w23 = 0u, m1 = 0u;
+        c0 += 3u;
+        uint32_t m2 = 0;
+        w01 = w23 = 0u;
         if (wlive) level_counts<NW>(key, c0, w01, w23);
-        block_levels(w01, w23, m1, red);
-        uint32_t cstar;
-        for (;;) {
-            const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
-            const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
-            if (d < 3u || c0 + 3u >= M) {
-                cstar = c0 + d;
-                break;
-            }
-            c0 += 3u;
-            uint32_t m2 = 0;
-            w01 = w23 = 0u;
-            if (wlive) level_counts<NW>(key, c0, w01, w23);
-            block_levels(w01, w23, m2, red);
-        }
-        uint32_t ngt = 0u, neq = 0u;
-        if (wlive) {
-            ngt = count_ge<NW>(key, cstar + 1u);
-            neq = count_ge<NW>(key, cstar) - ngt;
-        }
-        uint32_t tot;
-        const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
-        const uint32_t G = tot & 0xffffu, E = tot >> 16;
-        const uint32_t take = min(E, K - G);
-        nc = G + take;
-        uint32_t rg = pre & 0xffffu, re = pre >> 16;
-        if (ngt + neq) {
+        block_levels(w01, w23, m2, red);
+    }
+    uint32_t ngt = 0u, neq = 0u;
+    if (wlive) {
+        ngt = count_ge<NW>(key, cstar + 1u);
+        neq = count_ge<NW>(key, cstar) - ngt;
+    }
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan(ngt | (neq << 16), red, &tot);
+    const uint32_t G = tot & 0xffffu, E = tot >> 16;
+    const uint32_t take = min(E, K - G);
+    uint32_t rg = pre & 0xffffu, re = pre >> 16;
+    if (ngt + neq) {
 #pragma unroll
-            for (int k = 0; k < 2 * NW; ++k) {
-                const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-                const uint32_t j = j0 + (uint32_t)k;
-                if (kk > cstar) {
-                    cand_k[rg] = kk;
-                    cand_i[rg] = j;
-                    ++rg;
-                } else if (kk == cstar) {
-                    if (re < take) {
-                        cand_k[G + re] = kk;
-                        cand_i[G + re] = j;
-                    }
-                    ++re;
+        for (int k = 0; k < 2 * NW; ++k) {
+            const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+            const uint32_t j = j0 + (uint32_t)k;
+            if (kk > cstar) {
+                L.cand_k[rg] = kk;
+                L.cand_i[rg] = j;
+                ++rg;
+            } else if (kk == cstar) {
+                if (re < take) {
+                    L.cand_k[G + re] = kk;
+                    L.cand_i[G + re] = j;
                 }
+                ++re;
             }
         }
     }
     __syncthreads();
-    // merge by rank (first wave; nrun, nc <= K <= 64, lane e holds running
-    // entry e and candidate e, and reads the others' with readlane).  The
-    // running list is sorted; candidates have higher indices than every
-    // running entry, so a running entry keeps its place among running
-    // entries and precedes candidates of equal key.
+    return G + take;
+}
+
+// Merges the nc candidates (in LDS, any order) into the running list by
+// rank (first wave; nrun, nc <= K <= 64, lane e holds running entry e and
+// candidate e, and reads the others' with readlane).  The running list is
+// sorted; candidates have higher indices than every running entry, so a
+// running entry keeps its place among running entries and precedes
+// candidates of equal key.  Ends with nrun / kmin updated.  The LDS a
+// selection writes (reduction slots, candidate and running lists) is next
+// written after the first barrier of the next selection, which every thread
+// reaches only after its reads here, so no closing barrier is needed.
+__device__ __forceinline__ void merge_candidates(const TopkArgs& a, uint32_t nc, const TopkLds& L, uint32_t& nrun,
+                                                 uint32_t& kmin) {
+    const uint32_t K = (uint32_t)a.K;
     if (threadIdx.x < 64) {
         const uint32_t e = threadIdx.x;
         const bool has_r = e < nrun, has_c = e < nc;
-        const uint32_t rk = has_r ? run_k[e] : 0u, ri = has_r ? run_i[e] : 0u;
-        const uint32_t ck = has_c ? cand_k[e] : 0u, ci = has_c ? cand_i[e] : 0xffffffffu;
+        const uint32_t rk = has_r ? L.run_k[e] : 0u, ri = has_r ? L.run_i[e] : 0u;
+        const uint32_t ck = has_c ? L.cand_k[e] : 0u, ci = has_c ? L.cand_i[e] : 0xffffffffu;
         uint32_t rank_r = e, rank_c = 0u;
         for (uint32_t c = 0; c < nc; ++c) {
             const uint32_t fk = (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)c);
@@ -585,17 +547,132 @@ __device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&
             rank_c += (uint32_t)__builtin_amdgcn_readlane((int)rk, (int)f) >= ck ? 1u : 0u;
         // one wave: its reads of the old list precede these writes
         if (has_r && rank_r < K) {
-            run_k[rank_r] = rk;
-            run_i[rank_r] = ri;
+            L.run_k[rank_r] = rk;
+            L.run_i[rank_r] = ri;
         }
         if (has_c && rank_c < K) {
-            run_k[rank_c] = ck;
-            run_i[rank_c] = ci;
+            L.run_k[rank_c] = ck;
+            L.run_i[rank_c] = ci;
         }
     }
     __syncthreads();
     nrun = min(nrun + nc, K);
-    kmin = nrun ? run_k[nrun - 1] : 0u;
+    kmin = nrun ? L.run_k[nrun - 1] : 0u;
+}
+
+// Merges the keys of one segment (thread x: units lo + u0 .. of key[NW],
+// u0 = 2 NW x) into the running list; M is the block's largest key (or an
+// upper bound of it), at least `lowest` (the smallest key that can still
+// enter); tmax is this thread's largest key.  Keys are read only in waves
+// where some tmax reaches `lowest`: a wave without such a key skips every
+// pass over them.  Usually (always once the list is full) at most K keys
+// reach `lowest` and they all enter, in slots of thread order; otherwise
+// select_search picks them.  Every thread calls it; it ends with nrun / kmin
+// updated.
+template <int NW>
+__device__ __forceinline__ void select_into(const TopkArgs& a, const uint32_t (&key)[NW], uint32_t tmax, uint32_t M,
+                                            uint32_t lowest, uint32_t lo, uint32_t u0, const TopkLds& L,
+                                            uint32_t& nrun, uint32_t& kmin) {
+    const uint32_t K = (uint32_t)a.K;
+    const bool wlive = __ballot(tmax >= lowest) != 0ull;  // uniform
+    const uint32_t j0 = lo + u0;
+    uint32_t n = 0;  // this thread's keys >= lowest
+    if (wlive) n = count_ge<NW>(key, lowest);
+    uint32_t tot, wpre;
+    block_count(n, L, tot, wpre);
+    uint32_t nc = tot;
+    if (tot <= K) {
+        if (wlive) {
+            uint32_t r = wpre + wave_excl_prefix6(n);
+            if (n) {
+#pragma unroll
+                for (int k = 0; k < 2 * NW; ++k) {
+                    const uint32_t kk = (key[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+                    if (kk >= lowest) {
+                        L.cand_k[r] = kk;
+                        L.cand_i[r] = j0 + (uint32_t)k;
+                        ++r;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    } else {
+        nc = select_search<NW>(a, key, wlive, M, lowest, j0, L);
+    }
+    merge_candidates(a, nc, L, nrun, kmin);
+}
+
+// Byte flags (bit 7 of each byte) of the bytes of w that are >= t (t <= 255).
+__device__ __forceinline__ uint32_t bytes_ge(uint32_t w, uint32_t t) {
+    const uint32_t hi = w & 0x80808080u, lo7 = w & 0x7f7f7f7fu;
+    return t <= 128u ? hi | ((lo7 + (128u - t) * 0x01010101u) & 0x80808080u)
+                     : hi & (lo7 + (256u - t) * 0x01010101u);
+}
+
+// select_into for the 8-bit counters of one block: thread x's 32 counts,
+// units lo + u0 + 4k + b in byte b of w8[k] (read only in waves with wlive
+// set), key = count + 1; units at or past rem, and unit exu, may not be
+// chosen.  The counts are tested against the threshold four at a time, and
+// only the flagged bytes are visited; when more than K keys reach `lowest`,
+// 16-bit keys are formed for select_search.
+__device__ __forceinline__ void select_bytes(const TopkArgs& a, const uint32_t (&w8)[8], bool wlive, int32_t rem,
+                                             int32_t exu, uint32_t M, uint32_t lowest, uint32_t lo, uint32_t u0,
+                                             const TopkLds& L, uint32_t& nrun, uint32_t& kmin) {
+    const uint32_t K = (uint32_t)a.K;
+    const uint32_t j0 = lo + u0;
+    uint32_t f8[8];
+    uint32_t n = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f8[k] = 0u;
+    if (wlive) {
+        // lowest <= M <= 256 here, so the count threshold is at most 255
+        const uint32_t t = lowest - 1u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f8[k] = bytes_ge(w8[k], t);
+        if (rem < 32 || exu >= 0) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (4 * k + b >= rem || 4 * k + b == exu) f8[k] &= ~(0x80u << (8 * b));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) n += (uint32_t)__popc(f8[k]);
+    }
+    uint32_t tot, wpre;
+    block_count(n, L, tot, wpre);
+    uint32_t nc = tot;
+    if (tot <= K) {
+        if (n) {
+            // lanes with n = 0 are inactive here and add no ballot bits
+            uint32_t r = wpre + wave_excl_prefix6(n);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                uint32_t f = f8[k];
+                while (f) {
+                    const uint32_t sh = (uint32_t)__builtin_ctz(f) - 7u;  // 8 * byte index
+                    L.cand_k[r] = ((w8[k] >> sh) & 0xffu) + 1u;
+                    L.cand_i[r] = j0 + 4u * (uint32_t)k + (sh >> 3);
+                    ++r;
+                    f &= f - 1u;
+                }
+            }
+        }
+        __syncthreads();
+    } else {
+        uint32_t key[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) key[k] = 0u;
+        if (wlive) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                key[k] = __builtin_amdgcn_perm(0u, w8[k >> 1], (k & 1) ? 0x0c030c02u : 0x0c010c00u);
+            keys_of_counts<16>(key, rem, exu);
+        }
+        nc = select_search<16>(a, key, wlive, M, lowest, j0, L);
+    }
+    merge_candidates(a, nc, L, nrun, kmin);
 }
 
 // Per-lane bucket runs of a query.  The wave's trees are [tw0, tw1); lane l
@@ -884,29 +961,26 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                 for (int g = 1; g < NB; ++g) Mh = h == g ? M[g] : Mh;
                 if (Mh < lowest) continue;
                 const uint32_t loh = lo + (uint32_t)h * B;
-                // keys only in waves where some thread's largest count can
-                // enter
+                // counts are read only in waves where some thread's largest
+                // count can enter
                 uint32_t mt = mh[0];
 #pragma unroll
                 for (int g = 1; g < NB; ++g) mt = h == g ? mh[g] : mt;
-                uint32_t key[16];
-                uint32_t tmax = 0u;
-                if (__ballot(mt + 1u >= lowest) != 0ull) {
+                const bool wl = __ballot(mt + 1u >= lowest) != 0ull;
+                uint32_t w8[8];
+                if (wl) {
                     const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
                     const uint4 x = ph[0], y = ph[1];
-                    const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-#pragma unroll
-                    for (int k = 0; k < 16; ++k)
-                        key[k] = __builtin_amdgcn_perm(0u, w8[k >> 1], (k & 1) ? 0x0c030c02u : 0x0c010c00u);
-                    const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
-                    const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
-                    const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
-                    tmax = keys_of_counts<16>(key, rem, exu);
+                    w8[0] = x.x, w8[1] = x.y, w8[2] = x.z, w8[3] = x.w;
+                    w8[4] = y.x, w8[5] = y.y, w8[6] = y.z, w8[7] = y.w;
                 } else {
 #pragma unroll
-                    for (int k = 0; k < 16; ++k) key[k] = 0u;
+                    for (int k = 0; k < 8; ++k) w8[k] = 0u;
                 }
-                select_into<16>(a, key, tmax, Mh, lowest, loh, u0, L, nrun, kmin);
+                const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
+                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                select_bytes(a, w8, wl, rem, exu, Mh, lowest, loh, u0, L, nrun, kmin);
             }
 #pragma unroll
             for (int h = 0; h < NB; ++h) {
