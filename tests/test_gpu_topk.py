@@ -121,11 +121,15 @@ def test_exclude_self(gpu_ctx):
     assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
 
 
-def test_oob_query_semantics(gpu_ctx):
+@pytest.mark.parametrize("n,t,nleaf,k,nsample", [(1500, 60, 8, 10, None),
+                                                 (70_000, 300, 40, 20, 25)])  # 8-bit, four blocks, wrap check
+def test_oob_query_semantics(gpu_ctx, n, t, nleaf, k, nsample):
+    """OOB queries of the training samples against their own forest: only
+    the trees where the query is out-of-bag, itself excluded, counts > 0;
+    every query (or a sample of them) against the oracle."""
     import torch
 
-    rng = np.random.default_rng(13)
-    n, t, nleaf, k = 1500, 60, 8, 10
+    rng = np.random.default_rng(13 + n)
     leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
     oob = (rng.random((t, n)) < 0.368).astype(np.uint8)
     oob[:, 7] = 0                                    # a sample never OOB: no results
@@ -134,7 +138,8 @@ def test_oob_query_semantics(gpu_ctx):
     idx, cnt = gpu_ctx.topk(dev(leaf), k, layout="tree", oob_words=words, exclude_base=0,
                             positive_only=True)
     idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy().view(np.uint16)
-    for q in range(n):
+    qs = range(n) if nsample is None else [7, 0, n - 1] + sorted(rng.choice(n, nsample, replace=False).tolist())
+    for q in qs:
         wi, wc, _ = O.topk_oob(leaf, oob, q, k)
         m = len(wi)
         assert np.array_equal(idx[q, :m], wi) and np.array_equal(cnt[q, :m], wc), q
