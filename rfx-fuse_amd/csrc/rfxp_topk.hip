@@ -61,6 +61,7 @@ struct TopkArgs {
     int64_t exclude_base;  // query q excludes reference exclude_base + q; < 0: none
     const int32_t* exclude_idx;  // or, when not NULL, reference exclude_idx[q] (< 0: none)
     int64_t q0;            // query of workgroup 0 of this launch
+    int64_t q1;            // end of this launch's queries (top-K kernels loop over them)
     int32_t K;
     int32_t floor_key;     // smallest selectable key: 1 (zeros allowed) or 2 (counts > 0)
     int32_t* idx_out;
@@ -461,31 +462,30 @@ __device__ __forceinline__ void block_count(uint32_t n, const TopkLds& L, uint32
 }
 
 // More than K keys reach `lowest`: cstar is the largest c with
-// #(keys >= c) >= K, found by a search over key levels (four per round, M
-// bounding the largest key); keys > cstar become candidates, and keys ==
-// cstar in index order up to K.  Returns the candidate count; ends with a
+// #(keys >= c) >= K, found by a search over key levels from the top (four
+// per round, M bounding the largest key, so that keys above the first
+// round's levels number fewer than K); keys > cstar become candidates, and
+// keys == cstar in index order up to K.  Returns the candidate count; ends with a
 // barrier.  Keys are read only in waves with wlive set.
 template <int NW>
 __device__ __forceinline__ uint32_t select_search(const TopkArgs& a, const uint32_t (&key)[NW], bool wlive,
                                                   uint32_t M, uint32_t lowest, uint32_t j0, const TopkLds& L) {
     const uint32_t K = (uint32_t)a.K;
     uint32_t* const red = L.red;
-    uint32_t c0 = lowest, w01 = 0u, w23 = 0u, m1 = 0u;
-    if (wlive) level_counts<NW>(key, c0, w01, w23);
-    block_levels(w01, w23, m1, red);
+    // levels c0 .. c0 + 3 per round, from the top (c0 = M - 3) down by four
+    // while fewer than K keys reach c0; at c0 == lowest at least K do
+    uint32_t c0 = M >= lowest + 3u ? M - 3u : lowest;
     uint32_t cstar;
     for (;;) {
-        const uint32_t f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
-        const uint32_t d = f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u;
-        if (d < 3u || c0 + 3u >= M) {
-            cstar = c0 + d;
+        uint32_t w01 = 0u, w23 = 0u, m1 = 0u;
+        if (wlive) level_counts<NW>(key, c0, w01, w23);
+        block_levels(w01, w23, m1, red);
+        const uint32_t f0 = w01 & 0xffffu, f1 = w01 >> 16, f2 = w23 & 0xffffu, f3 = w23 >> 16;
+        if (f0 >= K || c0 == lowest) {
+            cstar = c0 + (f3 >= K ? 3u : f2 >= K ? 2u : f1 >= K ? 1u : 0u);
             break;
         }
-        c0 += 3u;
-        uint32_t m2 = 0;
-        w01 = w23 = 0u;
-        if (wlive) level_counts<NW>(key, c0, w01, w23);
-        block_levels(w01, w23, m2, red);
+        c0 = c0 >= lowest + 4u ? c0 - 4u : lowest;
     }
     uint32_t ngt = 0u, neq = 0u;
     if (wlive) {
@@ -780,12 +780,9 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int32_t lane = (int32_t)(threadIdx.x & 63u);
-    const int64_t q = a.q0 + blockIdx.x;
     const uint32_t K = (uint32_t)a.K;
-    const int64_t ex = query_exclusion(a, q);
     const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
     const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
-    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
     // counters start at zero; afterwards each thread zeroes its own words as
     // it reads them
     {
@@ -794,54 +791,61 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     }
     __syncthreads();
 
-    uint32_t nrun = 0;  // entries in the running list (uniform)
-    uint32_t kmin = 0;  // key of the running K-th entry once the list is full
-    for (int32_t s = 0; s < a.nseg; ++s) {
-        const uint32_t lo = (uint32_t)s << shift;
-        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
-        const uint32_t soff = lr.tb + 4u * lr.o0;
-        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
-        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
-        count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
-        lr.o0 = lr.o1;
-        lr.o1 = lr.o2;
-        lr.o2 = o3;
-        __syncthreads();  // every count is in LDS
-        // counters -> keys, held in registers from here on; the counter
-        // words are zeroed for the next segment
-        const uint32_t u0 = threadIdx.x * 2u * NW;
-        uint32_t key[NW];
-        if constexpr (NW >= 4) {
-#pragma unroll
-            for (int k = 0; k < NW; k += 4) {
-                const uint4 x = *(const uint4*)(kw + k);
-                key[k] = x.x;
-                key[k + 1] = x.y;
-                key[k + 2] = x.z;
-                key[k + 3] = x.w;
-                *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
+    // queries q0 + blockIdx.x, + gridDim.x, ... below q1: about one workgroup
+    // per resident slot, so no workgroup starts or clears its counters per
+    // query (they are zero again after every segment)
+    for (int64_t q = a.q0 + blockIdx.x; q < a.q1; q += gridDim.x) {
+        const int64_t ex = query_exclusion(a, q);
+        LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
+        uint32_t nrun = 0;  // entries in the running list (uniform)
+        uint32_t kmin = 0;  // key of the running K-th entry once the list is full
+        for (int32_t s = 0; s < a.nseg; ++s) {
+            const uint32_t lo = (uint32_t)s << shift;
+            const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+            const uint32_t soff = lr.tb + 4u * lr.o0;
+            const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+            const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+            count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+            lr.o0 = lr.o1;
+            lr.o1 = lr.o2;
+            lr.o2 = o3;
+            __syncthreads();  // every count is in LDS
+            // counters -> keys, held in registers from here on; the counter
+            // words are zeroed for the next segment
+            const uint32_t u0 = threadIdx.x * 2u * NW;
+            uint32_t key[NW];
+            if constexpr (NW >= 4) {
+    #pragma unroll
+                for (int k = 0; k < NW; k += 4) {
+                    const uint4 x = *(const uint4*)(kw + k);
+                    key[k] = x.x;
+                    key[k + 1] = x.y;
+                    key[k + 2] = x.z;
+                    key[k + 3] = x.w;
+                    *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
+                }
+            } else {
+    #pragma unroll
+                for (int k = 0; k < NW; ++k) {
+                    key[k] = kw[k];
+                    kw[k] = 0u;
+                }
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < NW; ++k) {
-                key[k] = kw[k];
-                kw[k] = 0u;
-            }
+            // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
+            // excluded unit `exu`
+            const int32_t rem = (int32_t)width - (int32_t)u0;
+            const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
+            const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
+            const uint32_t mloc = keys_of_counts<NW>(key, rem, exu);
+            // the segment's largest key; the barrier also orders every zeroing
+            // before the next segment's counts (two alternating slots)
+            const uint32_t M = block_max(mloc, L.red + 48 + 16 * (s & 1));
+            const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+            if (M < lowest) continue;
+            select_into<NW>(a, key, mloc, M, lowest, lo, u0, L, nrun, kmin);
         }
-        // this thread's units u0 + h (h < 2 NW): valid below `rem`, and not the
-        // excluded unit `exu`
-        const int32_t rem = (int32_t)width - (int32_t)u0;
-        const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
-        const int32_t exu = exd >= 0 && exd < 2 * NW ? (int32_t)exd : -1;
-        const uint32_t mloc = keys_of_counts<NW>(key, rem, exu);
-        // the segment's largest key; the barrier also orders every zeroing
-        // before the next segment's counts (two alternating slots)
-        const uint32_t M = block_max(mloc, L.red + 48 + 16 * (s & 1));
-        const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-        if (M < lowest) continue;
-        select_into<NW>(a, key, mloc, M, lowest, lo, u0, L, nrun, kmin);
+        topk_write(a, q, L, nrun);
     }
-    topk_write(a, q, L, nrun);
 }
 
 // 8-bit counters, NB blocks of TOPK_BLOCK = 32768 references per segment
@@ -874,12 +878,9 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int32_t lane = (int32_t)(threadIdx.x & 63u);
-    const int64_t q = a.q0 + blockIdx.x;
     const uint32_t K = (uint32_t)a.K;
-    const int64_t ex = query_exclusion(a, q);
     const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
     const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
-    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
     {
         uint4* c4 = (uint4*)sm;
         for (uint32_t w = threadIdx.x; w < S / 16u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
@@ -887,149 +888,156 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
     }
     __syncthreads();
 
-    const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each block
-    uint32_t nrun = 0;
-    uint32_t kmin = 0;
-    for (int32_t s = 0; s < a.nseg; ++s) {
-        const uint32_t lo = (uint32_t)s << SHIFT;
-        const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
-        const uint32_t soff = lr.tb + 4u * lr.o0;
-        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
-        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
-        const uint32_t steps =
-            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
-        lr.o0 = lr.o1;
-        lr.o1 = lr.o2;
-        lr.o2 = o3;
-        __syncthreads();  // every count is in LDS
-        // the thread's counter bytes of every block (units 32x .. 32x + 31 of
-        // each, 8 words): per-block largest count (every unit, valid or not:
-        // an upper bound) and, for the check, the byte sum with the dummy word
-        uint4* pw[NB];
-        uint32_t mh[NB];
-        int32_t bal = 0;
-#pragma unroll
-        for (int h = 0; h < NB; ++h) {
-            pw[h] = (uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
-            const uint4 x = pw[h][0], y = pw[h][1];
-            const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-            uint32_t m2 = 0u;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                m2 = max_u16x2(m2, w8[k] & 0x00ff00ffu);
-                m2 = max_u16x2(m2, (w8[k] >> 8) & 0x00ff00ffu);
-                if constexpr (CHECK) bal = (int32_t)__builtin_amdgcn_sad_u8(w8[k], 0u, (uint32_t)bal);
-            }
-            mh[h] = max(m2 & 0xffffu, m2 >> 16);
-        }
-        if constexpr (CHECK) {
-            bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
-            if (lane == 0) bal -= 64 * (int32_t)steps;
-        }
-        // block reduction of (max of each block, byte balance): NB + 1 words
-        // per wave in one of two alternating slots
-        uint32_t M[NB];
-        bool exact = true;
-        {
-            constexpr uint32_t SW = NB + 1;
-            uint32_t* const slot = L.red + 48 + SW * TOPK_WAVES * (uint32_t)(s & 1);
-            uint32_t wm[NB];
-#pragma unroll
-            for (int h = 0; h < NB; ++h) wm[h] = wave_max(mh[h]);
-            const uint32_t wb = CHECK ? wave_sum((uint32_t)bal) : 0u;
-            if (lane == 0) {
-#pragma unroll
-                for (int h = 0; h < NB; ++h) slot[SW * (threadIdx.x >> 6) + h] = wm[h];
-                slot[SW * (threadIdx.x >> 6) + NB] = wb;
-            }
-            __syncthreads();
-            const bool have = (uint32_t)lane < (uint32_t)TOPK_WAVES;
-#pragma unroll
-            for (int h = 0; h < NB; ++h) M[h] = wave_max(have ? slot[SW * lane + h] : 0u) + 1u;
-            if constexpr (CHECK) exact = wave_sum(have ? slot[SW * lane + NB] : 0u) == 0u;
-        }
-        if (exact) {
-            // keys of each block from its counter bytes; a block past the
-            // references, or whose largest key cannot enter the list, is
-            // skipped
-#pragma unroll 1
+    // queries q0 + blockIdx.x, + gridDim.x, ... below q1: about one workgroup
+    // per resident slot, so no workgroup starts or clears its counters per
+    // query (they are zero again after every segment)
+    for (int64_t q = a.q0 + blockIdx.x; q < a.q1; q += gridDim.x) {
+        const int64_t ex = query_exclusion(a, q);
+        LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
+        const uint32_t u0 = threadIdx.x * 32u;  // first unit of this thread in each block
+        uint32_t nrun = 0;
+        uint32_t kmin = 0;
+        for (int32_t s = 0; s < a.nseg; ++s) {
+            const uint32_t lo = (uint32_t)s << SHIFT;
+            const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
+            const uint32_t soff = lr.tb + 4u * lr.o0;
+            const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+            const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+            const uint32_t steps =
+                count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+            lr.o0 = lr.o1;
+            lr.o1 = lr.o2;
+            lr.o2 = o3;
+            __syncthreads();  // every count is in LDS
+            // the thread's counter bytes of every block (units 32x .. 32x + 31 of
+            // each, 8 words): per-block largest count (every unit, valid or not:
+            // an upper bound) and, for the check, the byte sum with the dummy word
+            uint4* pw[NB];
+            uint32_t mh[NB];
+            int32_t bal = 0;
+    #pragma unroll
             for (int h = 0; h < NB; ++h) {
-                if ((uint32_t)h * B >= width) break;
-                const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-                uint32_t Mh = M[0];
-#pragma unroll
-                for (int g = 1; g < NB; ++g) Mh = h == g ? M[g] : Mh;
-                if (Mh < lowest) continue;
-                const uint32_t loh = lo + (uint32_t)h * B;
-                // counts are read only in waves where some thread's largest
-                // count can enter
-                uint32_t mt = mh[0];
-#pragma unroll
-                for (int g = 1; g < NB; ++g) mt = h == g ? mh[g] : mt;
-                const bool wl = __ballot(mt + 1u >= lowest) != 0ull;
-                uint32_t w8[8];
-                if (wl) {
-                    const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
-                    const uint4 x = ph[0], y = ph[1];
-                    w8[0] = x.x, w8[1] = x.y, w8[2] = x.z, w8[3] = x.w;
-                    w8[4] = y.x, w8[5] = y.y, w8[6] = y.z, w8[7] = y.w;
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) w8[k] = 0u;
+                pw[h] = (uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
+                const uint4 x = pw[h][0], y = pw[h][1];
+                const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+                uint32_t m2 = 0u;
+    #pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    m2 = max_u16x2(m2, w8[k] & 0x00ff00ffu);
+                    m2 = max_u16x2(m2, (w8[k] >> 8) & 0x00ff00ffu);
+                    if constexpr (CHECK) bal = (int32_t)__builtin_amdgcn_sad_u8(w8[k], 0u, (uint32_t)bal);
                 }
-                const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
-                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
-                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
-                select_bytes(a, w8, wl, rem, exu, Mh, lowest, loh, u0, L, nrun, kmin);
+                mh[h] = max(m2 & 0xffffu, m2 >> 16);
             }
-#pragma unroll
-            for (int h = 0; h < NB; ++h) {
-                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
-                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (CHECK) {
+                bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
+                if (lane == 0) bal -= 64 * (int32_t)steps;
             }
-            if constexpr (CHECK) *dw = 0u;
-        } else {
-            // some count wrapped: recount the segment with 16-bit counters,
-            // block by block, zeroing each block's words as they are read
-#pragma unroll
-            for (int h = 0; h < NB; ++h) {
-                pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
-                pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
-            }
-            *dw = 0u;
-            __syncthreads();
-            uint32_t* const kw = sm + 16u * threadIdx.x;
-            for (int h = 0; h < NB; ++h) {
-                if ((uint32_t)h * B >= width) break;
-                const uint32_t loh = lo + (uint32_t)h * B;
-                const uint32_t wh = min(width - (uint32_t)h * B, B);
-                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
+            // block reduction of (max of each block, byte balance): NB + 1 words
+            // per wave in one of two alternating slots
+            uint32_t M[NB];
+            bool exact = true;
+            {
+                constexpr uint32_t SW = NB + 1;
+                uint32_t* const slot = L.red + 48 + SW * TOPK_WAVES * (uint32_t)(s & 1);
+                uint32_t wm[NB];
+    #pragma unroll
+                for (int h = 0; h < NB; ++h) wm[h] = wave_max(mh[h]);
+                const uint32_t wb = CHECK ? wave_sum((uint32_t)bal) : 0u;
+                if (lane == 0) {
+    #pragma unroll
+                    for (int h = 0; h < NB; ++h) slot[SW * (threadIdx.x >> 6) + h] = wm[h];
+                    slot[SW * (threadIdx.x >> 6) + NB] = wb;
+                }
                 __syncthreads();
-                uint32_t key[16];
-#pragma unroll
-                for (int k = 0; k < 16; k += 4) {
-                    const uint4 x = *(const uint4*)(kw + k);
-                    key[k] = x.x;
-                    key[k + 1] = x.y;
-                    key[k + 2] = x.z;
-                    key[k + 3] = x.w;
-                    *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
-                }
-                const int32_t rem = (int32_t)wh - (int32_t)u0;
-                const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
-                const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
-                const uint32_t mloc = keys_of_counts<16>(key, rem, exu);
-                const uint32_t Mh = block_max(mloc, L.red + 48 + 16 * h);
-                const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
-                if (Mh >= lowest) select_into<16>(a, key, mloc, Mh, lowest, loh, u0, L, nrun, kmin);
-                __syncthreads();  // the block_max slot is read before its next use
+                const bool have = (uint32_t)lane < (uint32_t)TOPK_WAVES;
+    #pragma unroll
+                for (int h = 0; h < NB; ++h) M[h] = wave_max(have ? slot[SW * lane + h] : 0u) + 1u;
+                if constexpr (CHECK) exact = wave_sum(have ? slot[SW * lane + NB] : 0u) == 0u;
             }
-            // the recount's out-of-block members: words 2B/4 .. 2B/4 + 1023
-            sm[(2u * B) / 4u + threadIdx.x] = 0u;
+            if (exact) {
+                // keys of each block from its counter bytes; a block past the
+                // references, or whose largest key cannot enter the list, is
+                // skipped
+    #pragma unroll 1
+                for (int h = 0; h < NB; ++h) {
+                    if ((uint32_t)h * B >= width) break;
+                    const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+                    uint32_t Mh = M[0];
+    #pragma unroll
+                    for (int g = 1; g < NB; ++g) Mh = h == g ? M[g] : Mh;
+                    if (Mh < lowest) continue;
+                    const uint32_t loh = lo + (uint32_t)h * B;
+                    // counts are read only in waves where some thread's largest
+                    // count can enter
+                    uint32_t mt = mh[0];
+    #pragma unroll
+                    for (int g = 1; g < NB; ++g) mt = h == g ? mh[g] : mt;
+                    const bool wl = __ballot(mt + 1u >= lowest) != 0ull;
+                    uint32_t w8[8];
+                    if (wl) {
+                        const uint4* const ph = (const uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
+                        const uint4 x = ph[0], y = ph[1];
+                        w8[0] = x.x, w8[1] = x.y, w8[2] = x.z, w8[3] = x.w;
+                        w8[4] = y.x, w8[5] = y.y, w8[6] = y.z, w8[7] = y.w;
+                    } else {
+    #pragma unroll
+                        for (int k = 0; k < 8; ++k) w8[k] = 0u;
+                    }
+                    const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
+                    const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                    const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                    select_bytes(a, w8, wl, rem, exu, Mh, lowest, loh, u0, L, nrun, kmin);
+                }
+    #pragma unroll
+                for (int h = 0; h < NB; ++h) {
+                    pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                    pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+                }
+                if constexpr (CHECK) *dw = 0u;
+            } else {
+                // some count wrapped: recount the segment with 16-bit counters,
+                // block by block, zeroing each block's words as they are read
+    #pragma unroll
+                for (int h = 0; h < NB; ++h) {
+                    pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
+                    pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
+                }
+                *dw = 0u;
+                __syncthreads();
+                uint32_t* const kw = sm + 16u * threadIdx.x;
+                for (int h = 0; h < NB; ++h) {
+                    if ((uint32_t)h * B >= width) break;
+                    const uint32_t loh = lo + (uint32_t)h * B;
+                    const uint32_t wh = min(width - (uint32_t)h * B, B);
+                    count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
+                    __syncthreads();
+                    uint32_t key[16];
+    #pragma unroll
+                    for (int k = 0; k < 16; k += 4) {
+                        const uint4 x = *(const uint4*)(kw + k);
+                        key[k] = x.x;
+                        key[k + 1] = x.y;
+                        key[k + 2] = x.z;
+                        key[k + 3] = x.w;
+                        *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
+                    }
+                    const int32_t rem = (int32_t)wh - (int32_t)u0;
+                    const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
+                    const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
+                    const uint32_t mloc = keys_of_counts<16>(key, rem, exu);
+                    const uint32_t Mh = block_max(mloc, L.red + 48 + 16 * h);
+                    const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
+                    if (Mh >= lowest) select_into<16>(a, key, mloc, Mh, lowest, loh, u0, L, nrun, kmin);
+                    __syncthreads();  // the block_max slot is read before its next use
+                }
+                // the recount's out-of-block members: words 2B/4 .. 2B/4 + 1023
+                sm[(2u * B) / 4u + threadIdx.x] = 0u;
+            }
+            __syncthreads();  // every counter word is zero again before the next segment's counts
         }
-        __syncthreads();  // every counter word is zero again before the next segment's counts
+        topk_write(a, q, L, nrun);
     }
-    topk_write(a, q, L, nrun);
 }
 
 // Outlier scores, full and anchor modes of RandomForest::compute_outlier_scores
@@ -1334,23 +1342,24 @@ __global__ __launch_bounds__(256) void k_topk_scores(ScoreArgs a) {
 // Queries per launch: gridDim.x * blockDim.x must stay below 2^32.
 constexpr int64_t TOPK_MAX_GRID = 1LL << 21;
 
+// One launch over all Q queries with at most per_cu workgroups per CU (what
+// the kernel's LDS and waves let one CU hold): each workgroup loops over
+// queries blockIdx.x, + gridDim.x, ...
 template <typename Kern>
-static hipError_t launch_topk_kernel(rfxp_ctx* ctx, Kern kern, TopkArgs a, int64_t Q) {
+static hipError_t launch_topk_kernel(rfxp_ctx* ctx, Kern kern, TopkArgs a, int64_t Q, int per_cu) {
     const size_t lds = topk_lds_bytes(a.shift);
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    for (int64_t q0 = 0; q0 < Q; q0 += TOPK_MAX_GRID) {
-        a.q0 = q0;
-        const unsigned nq = (unsigned)std::min(TOPK_MAX_GRID, Q - q0);
-        hipLaunchKernelGGL(kern, dim3(nq), dim3(TOPK_THREADS), lds, ctx->stream, a);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
-    return hipSuccess;
+    const int64_t slots = (int64_t)std::max(ctx->n_cu, 1) * per_cu;
+    a.q0 = 0;
+    a.q1 = Q;
+    hipLaunchKernelGGL(kern, dim3((unsigned)std::min(slots, Q)), dim3(TOPK_THREADS), lds, ctx->stream, a);
+    return hipGetLastError();
 }
 
 template <int NW>
 static hipError_t launch_topk(rfxp_ctx* ctx, TopkArgs a, int64_t Q) {
-    return launch_topk_kernel(ctx, k_topk<NW>, a, Q);
+    return launch_topk_kernel(ctx, k_topk<NW>, a, Q, 2);
 }
 
 template <typename Kern>
@@ -1401,6 +1410,7 @@ static TopkArgs ref_args(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
     a.exclude_base = exclude_base;
     a.exclude_idx = exclude_idx;
     a.q0 = 0;
+    a.q1 = 0;
     a.K = 1;
     a.floor_key = 1;
     a.idx_out = nullptr;
@@ -1482,12 +1492,12 @@ extern "C" int rfxp_topk(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
             case 14: e = launch_topk<8>(ctx, a, Q); break;
             case 15: e = launch_topk<16>(ctx, a, Q); break;
             case TOPK_SHIFT8:
-                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 2>, a, Q)
-                               : launch_topk_kernel(ctx, k_topk8<true, 2>, a, Q);
+                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 2>, a, Q, 2)
+                               : launch_topk_kernel(ctx, k_topk8<true, 2>, a, Q, 2);
                 break;
             default:
-                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 4>, a, Q)
-                               : launch_topk_kernel(ctx, k_topk8<true, 4>, a, Q);
+                e = a.T <= 255 ? launch_topk_kernel(ctx, k_topk8<false, 4>, a, Q, 1)
+                               : launch_topk_kernel(ctx, k_topk8<true, 4>, a, Q, 1);
                 break;
         }
     }
