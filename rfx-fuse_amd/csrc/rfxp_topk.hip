@@ -17,15 +17,18 @@
 // query's bucket in tree t and segment s is then one contiguous run, found
 // from its leaf label with two offset loads.
 //
-// Kernel k_topk: one workgroup per query walks the segments in order.  Per
-// segment, 16-bit LDS counters (one per reference of the segment) take the
-// query's T buckets exactly as the triangle's hit phase does; then the
-// counters become keys (count + 1, 0 for references that may not be chosen)
-// and only keys above the running K-th best key are looked at: entries of a
-// later segment lose every tie against the running list, which holds lower
-// indices.  Selection is exact: a binary search over key levels for the
-// threshold, ordered compaction of the winners, and a rank merge with the
-// running list by one wave.
+// Kernels k_topk (16-bit counters) and k_topk8 (8-bit counters): a
+// workgroup takes one query at a time (about one workgroup per resident
+// slot, looping over the queries) and walks its segments in order.  Per
+// segment, LDS counters (one per reference of the segment) take the query's
+// T buckets exactly as the triangle's hit phase does; then the counts become
+// keys (count + 1, 0 for references that may not be chosen) and only keys
+// above the running K-th best key are looked at: entries of a later segment
+// lose every tie against the running list, which holds lower indices.
+// Selection is exact: the keys at or above the threshold when at most K
+// reach it, else a search over key levels for the K-th key, ordered
+// compaction of the winners, and a rank merge with the running list by one
+// wave.
 #include <algorithm>
 #include <cmath>
 #include <string>
