@@ -379,7 +379,6 @@ __device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
 
 // LDS pointers of a top-K workgroup.
 struct TopkLds {
-    uint32_t* wsc;     // this wave's 128 words of the record area (run lists)
     uint32_t* red;     // reduction scratch (TOPK_RED_WORDS)
     uint32_t* cand_k;  // candidates of a segment
     uint32_t* cand_i;
@@ -389,7 +388,6 @@ struct TopkLds {
 
 __device__ __forceinline__ TopkLds topk_lds(uint32_t* sm, int32_t shift) {
     TopkLds L;
-    L.wsc = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + (threadIdx.x >> 6) * (TOPK_REC_WORDS / TOPK_WAVES);
     L.red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + TOPK_REC_WORDS;
     L.cand_k = L.red + TOPK_RED_WORDS;
     L.cand_i = L.cand_k + TOPK_MAX_K;
@@ -708,40 +706,42 @@ __device__ __forceinline__ LaneRuns lane_runs_init(const TopkArgs& a, int64_t q,
     return r;
 }
 
-// A wave's runs (lanes < nt, as in count_lane_runs), counted with the first
-// 64 members of every run in one pass and the rest of each longer run
-// appended to the same lane list: runs a little above 64 members, common
-// when a segment holds many references per leaf, then cost one more load in
-// the pipeline rather than a tail loop.  wsc: the wave's 128 words of LDS
-// scratch.
+// A wave's runs (lanes < nt, as in count_lane_runs; lanes >= nt hold empty
+// runs) cut into chunks of at most 64 ids, all of them counted through the
+// load pipeline of count_lane_runs, 64 chunks per call: a run of thousands
+// of ids (a popular leaf) costs its chunks' loads, overlapped like any other
+// run's, rather than a chain of dependent loads.  Chunk g of the wave belongs
+// to the first lane whose inclusive chunk prefix exceeds g.
 template <int BITS>
-__device__ __forceinline__ uint32_t count_runs_split(const TopkArgs& a, uint32_t soff, uint32_t len4, int32_t nt,
-                                                     int32_t lane, uint32_t lane4, uint32_t base1, uint32_t dummy,
-                                                     uint32_t* wsc) {
-    const uint64_t lm = __ballot(len4 > 256u);
-    if (lm == 0u) return count_lane_runs<BITS>(a, soff, len4, nt, lane4, base1, dummy);
-    const int32_t n2 = (int32_t)__popcll(lm);
-    // entry p of the long runs: the rest of the run, (soff + 256, len4 - 256)
-    const uint32_t p = __builtin_amdgcn_mbcnt_hi((uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u));
-    if (len4 > 256u) {
-        wsc[p] = soff + 256u;
-        wsc[64 + p] = len4 - 256u;
+__device__ __forceinline__ uint32_t count_runs_chunked(const TopkArgs& a, uint32_t soff, uint32_t len4, int32_t nt,
+                                                       int32_t lane, uint32_t lane4, uint32_t base1, uint32_t dummy) {
+    if (__ballot(len4 > 256u) == 0ull) return count_lane_runs<BITS>(a, soff, len4, nt, lane4, base1, dummy);
+    const uint32_t c = (len4 + 255u) >> 8;  // chunks of this lane's run
+    uint32_t incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+        if (lane >= d) incl += o;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t len1 = min(len4, 256u);
-    if (nt + n2 <= 64) {
-        // lane nt + e takes long-run entry e
-        const int32_t e = lane - nt;
-        const bool rest = e >= 0 && e < n2;
-        const uint32_t so = rest ? wsc[e] : soff;
-        const uint32_t ln = rest ? wsc[64 + e] : len1;
-        return count_lane_runs<BITS>(a, so, ln, nt + n2, lane4, base1, dummy);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    uint32_t steps = 0;
+    for (uint32_t g0 = 0; g0 < total; g0 += 64u) {
+        const uint32_t g = g0 + (uint32_t)lane;
+        int32_t lo = 0, hi = 63;
+#pragma unroll
+        for (int it = 0; it < 6; ++it) {
+            const int32_t mid = (lo + hi) >> 1;
+            if ((uint32_t)__shfl((int)incl, mid, 64) > g) hi = mid;
+            else lo = mid + 1;
+        }
+        lo = min(lo, 63);
+        const uint32_t m = g - ((uint32_t)__shfl((int)incl, lo, 64) - (uint32_t)__shfl((int)c, lo, 64));
+        const uint32_t so_r = (uint32_t)__shfl((int)soff, lo, 64), ln_r = (uint32_t)__shfl((int)len4, lo, 64);
+        const bool ok = g < total;
+        const uint32_t so = ok ? so_r + 256u * m : 0u;
+        const uint32_t ln = ok ? min(ln_r - 256u * m, 256u) : 0u;
+        steps += count_lane_runs<BITS>(a, so, ln, (int32_t)min(total - g0, 64u), lane4, base1, dummy);
     }
-    uint32_t steps = count_lane_runs<BITS>(a, soff, len1, nt, lane4, base1, dummy);
-    const bool have = lane < n2;
-    steps += count_lane_runs<BITS>(a, have ? wsc[lane] : 0u, have ? wsc[64 + lane] : 0u, n2, lane4, base1, dummy);
     return steps;
 }
 
@@ -751,13 +751,12 @@ __device__ __forceinline__ uint32_t count_runs_split(const TopkArgs& a, uint32_t
 template <int BITS>
 __device__ __forceinline__ uint32_t count_query_segment(const TopkArgs& a, int64_t q, int32_t s, uint32_t soff,
                                                         uint32_t len4, int32_t tw0, int32_t tw1, int32_t lane,
-                                                        uint32_t lane4, uint32_t base1, uint32_t dummy,
-                                                        uint32_t* wsc) {
-    uint32_t steps = count_runs_split<BITS>(a, soff, len4, min(tw1 - tw0, 64), lane, lane4, base1, dummy, wsc);
+                                                        uint32_t lane4, uint32_t base1, uint32_t dummy) {
+    uint32_t steps = count_runs_chunked<BITS>(a, soff, len4, min(tw1 - tw0, 64), lane, lane4, base1, dummy);
     for (int32_t r0 = tw0 + 64; r0 < tw1; r0 += 64) {
         uint32_t so2, ln2;
         query_bucket(a, q, r0 + lane < tw1 ? r0 + lane : a.T, s, so2, ln2);
-        steps += count_runs_split<BITS>(a, so2, ln2, min(tw1 - r0, 64), lane, lane4, base1, dummy, wsc);
+        steps += count_runs_chunked<BITS>(a, so2, ln2, min(tw1 - r0, 64), lane, lane4, base1, dummy);
     }
     return steps;
 }
@@ -808,7 +807,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             const uint32_t soff = lr.tb + 4u * lr.o0;
             const uint32_t len4 = 4u * (lr.o1 - lr.o0);
             const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
-            count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+            count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
             lr.o0 = lr.o1;
             lr.o1 = lr.o2;
             lr.o2 = o3;
@@ -907,7 +906,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
             const uint32_t len4 = 4u * (lr.o1 - lr.o0);
             const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
             const uint32_t steps =
-                count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+                count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
             lr.o0 = lr.o1;
             lr.o1 = lr.o2;
             lr.o2 = o3;
@@ -1013,7 +1012,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                     if ((uint32_t)h * B >= width) break;
                     const uint32_t loh = lo + (uint32_t)h * B;
                     const uint32_t wh = min(width - (uint32_t)h * B, B);
-                    count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
+                    count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16);
                     __syncthreads();
                     uint32_t key[16];
     #pragma unroll
@@ -1170,7 +1169,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
         const uint32_t len4 = 4u * (lr.o1 - lr.o0);
         const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
         const uint32_t steps =
-            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy, L.wsc);
+            count_query_segment<8>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
         lr.o0 = lr.o1;
         lr.o1 = lr.o2;
         lr.o2 = o3;
@@ -1244,7 +1243,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
             for (int h = 0; h < NB; ++h) {
                 if ((uint32_t)h * B >= width) break;
                 const uint32_t loh = lo + (uint32_t)h * B;
-                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16, L.wsc);
+                count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16);
                 __syncthreads();
                 const int32_t rem = (int32_t)min(width - (uint32_t)h * B, B) - (int32_t)u0;
                 const int64_t exd = ex - (int64_t)loh - (int64_t)u0;
