@@ -52,7 +52,6 @@ constexpr int TOPK_MIN_SHIFT = 11;  // at least 2 counters per thread
 
 struct TopkArgs {
     const uint32_t* mem;  // reference members (j + 1), [T][N]
-    uint32_t mem_bytes;
     const int32_t* off;   // [T][nb + 1]
     int32_t nb;
     int64_t N;
@@ -72,19 +71,17 @@ struct TopkArgs {
 };
 
 // LDS layout: counters (2^shift 16-bit counters, shift <= 15, or 2^shift
-// 8-bit ones, shift 16 or 17) | dummy words (1024) | per-segment bucket records of up to
-// 1024 trees (offset, length) | reduction scratch | candidate and running
-// lists.
+// 8-bit ones, shift 16 or 17) | dummy words (1024) | reduction scratch |
+// candidate and running lists.
 __host__ __device__ constexpr uint32_t topk_dummy_off(int32_t shift) {
     return shift >= TOPK_SHIFT8 ? (1u << shift) : (1u << shift) * 2u;
 }
-constexpr uint32_t TOPK_REC_WORDS = 2 * TOPK_THREADS;
 // wave partials (48), two segment slots (2 x 80: five words per wave), a
 // selection slot (16)
 constexpr uint32_t TOPK_RED_WORDS = 224;
 constexpr uint32_t TOPK_LIST_WORDS = 4 * TOPK_MAX_K + 8;    // candidate / running lists
 __host__ __device__ constexpr uint32_t topk_lds_bytes(int32_t shift) {
-    return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_REC_WORDS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
+    return topk_dummy_off(shift) + (TOPK_THREADS + TOPK_RED_WORDS + TOPK_LIST_WORDS) * 4;
 }
 
 typedef __attribute__((address_space(3))) uint32_t lds_w;
@@ -114,13 +111,6 @@ __device__ __forceinline__ void query_bucket(const TopkArgs& a, int64_t q, int32
     len4 = 4u * (o1 - o0);
 }
 
-__device__ __forceinline__ void count16(uint32_t m, uint32_t base1, uint32_t width, uint32_t dummy) {
-    // m = j + 1 (0: no member); 16-bit counter unit c = j - lo
-    const uint32_t c = m - base1;
-    const bool h = c < width;
-    lds_add16(h ? ((c << 1) & ~3u) : dummy, 1u << ((c << 4) & 16u));
-}
-
 // Counting step of a query run with BITS-bit counters (8 or 16): m = j + 1
 // of a member (0: an empty lane), counter unit c = j - lo.  Units at or past
 // xlim -- empty lanes, and members outside the units being counted -- are
@@ -134,34 +124,6 @@ __device__ __forceinline__ void count_bits(uint32_t m, uint32_t base1, uint32_t 
     const uint32_t c = min(m - base1, xlim);
     if constexpr (BITS == 8) lds_add16(c & ~3u, 1u << ((c << 3) & 31u));
     else lds_add16((c << 1) & ~3u, 1u << ((c << 4) & 31u));
-}
-
-// 16 bucket loads of record group g (records rec_off/rec_len in LDS); a
-// group outside [.., g1) loads nothing.  Returns whether a bucket of the
-// group has more than 64 members.
-__device__ __forceinline__ bool load16(const TopkArgs& a, const uint32_t* rec_off, const uint32_t* rec_len, int32_t g,
-                                       bool ok, uint32_t lane4, uint32_t (&m)[16]) {
-    bool lng = false;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const uint32_t soff = ok ? __builtin_amdgcn_readfirstlane(rec_off[16 * g + u]) : 0u;
-        const uint32_t len4 = ok ? __builtin_amdgcn_readfirstlane(rec_len[16 * g + u]) : 0u;
-        lng |= len4 > 256u;
-        m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, soff + len4), lane4, soff, 0);
-    }
-    return lng;
-}
-
-__device__ __forceinline__ void tails16(const TopkArgs& a, const uint32_t* rec_off, const uint32_t* rec_len, int32_t g,
-                                        uint32_t lane4, uint32_t base1, uint32_t width, uint32_t dummy) {
-    for (int u = 0; u < 16; ++u) {
-        const uint32_t len4 = __builtin_amdgcn_readfirstlane(rec_len[16 * g + u]);
-        if (len4 <= 256u) continue;
-        const uint32_t soff = __builtin_amdgcn_readfirstlane(rec_off[16 * g + u]);
-        const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, soff + len4);
-        for (uint32_t p4 = 256u; p4 < len4; p4 += 256u)
-            count16((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, soff, 0), base1, width, dummy);
-    }
 }
 
 // Per-thread level counts of keys >= c0 + d for d = 0..3, two 16-bit fields
@@ -272,45 +234,6 @@ __device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, ui
     return ka > kb || (ka == kb && ia < ib);
 }
 
-// Clears the 16-bit LDS counters of a segment of S references and counts
-// into them, for query q, the members of the query's buckets of segment s
-// (counter unit j - lo for member j; base1 = lo + 1, width = references in
-// the segment).  Ends with a barrier: every count is in LDS.
-__device__ __forceinline__ void count_segment(const TopkArgs& a, int64_t q, int32_t s, uint32_t S, uint32_t* sm,
-                                              uint32_t* rec_off, uint32_t* rec_len, uint32_t dummy, uint32_t lane4,
-                                              int32_t wave, uint32_t base1, uint32_t width) {
-    uint4* c4 = (uint4*)sm;
-    for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
-    sm[dummy >> 2] = 0u;
-    for (int32_t tc = 0; tc < a.T; tc += TOPK_THREADS) {
-        // the query's bucket records of trees tc .. tc+1023, one per thread
-        uint32_t soff, len4;
-        query_bucket(a, q, tc + (int32_t)threadIdx.x, s, soff, len4);
-        rec_off[threadIdx.x] = soff;
-        rec_len[threadIdx.x] = len4;
-        __syncthreads();
-        const int32_t nt = min(a.T - tc, TOPK_THREADS);
-        const int32_t ng = (nt + 15) >> 4;
-        const int32_t g0 = (ng * wave) / TOPK_WAVES, g1 = (ng * (wave + 1)) / TOPK_WAVES;
-        // two groups in ping-pong: one is counted while the other loads
-        uint32_t A[16], B[16];
-        bool la = load16(a, rec_off, rec_len, g0, g0 < g1, lane4, A);
-        for (int32_t g = g0; g < g1; g += 2) {
-            const bool lb = load16(a, rec_off, rec_len, g + 1, g + 1 < g1, lane4, B);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) count16(A[u], base1, width, dummy);
-            if (la) tails16(a, rec_off, rec_len, g, lane4, base1, width, dummy);
-            la = load16(a, rec_off, rec_len, g + 2, g + 2 < g1, lane4, A);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) count16(B[u], base1, width, dummy);
-            if (lb) tails16(a, rec_off, rec_len, g + 1, lane4, base1, width, dummy);
-        }
-        __syncthreads();
-    }
-}
-
 // A wave's bucket runs of one segment, counted into the LDS counters
 // (BITS 8 or 16).  Lane l holds the run (byte offset soff, byte length len4)
 // of the wave's l-th tree; n_trees (<= 64, uniform) lanes hold one.  The
@@ -388,7 +311,7 @@ struct TopkLds {
 
 __device__ __forceinline__ TopkLds topk_lds(uint32_t* sm, int32_t shift) {
     TopkLds L;
-    L.red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4 + TOPK_REC_WORDS;
+    L.red = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
     L.cand_k = L.red + TOPK_RED_WORDS;
     L.cand_i = L.cand_k + TOPK_MAX_K;
     L.run_k = L.cand_i + TOPK_MAX_K;
@@ -1078,29 +1001,44 @@ __device__ __forceinline__ void outlier_finish(double acc, double* red, const Ou
 }
 
 // 16-bit counters, segments of S = 2^shift <= 32768 references (reference
-// sets of up to 32768 samples, or more than TOPK_MAX_T8 trees).
+// sets of up to 32768 samples, or more than TOPK_MAX_T8 trees), counted as
+// k_topk counts them.
 template <int NW>
 __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_outlier(TopkArgs a,
                                                                                                     OutlierArgs o) {
     extern __shared__ uint32_t sm[];
     const int32_t shift = a.shift;
     const uint32_t S = 1u << shift;
-    uint32_t* const rec_off = sm + (topk_dummy_off(shift) + TOPK_THREADS * 4) / 4;
-    uint32_t* const rec_len = rec_off + TOPK_THREADS;
-    double* const red = (double*)(rec_len + TOPK_THREADS);  // TOPK_WAVES doubles
-    const uint32_t* const kw = sm + threadIdx.x * NW;
+    const TopkLds L = topk_lds(sm, shift);
+    uint32_t* const kw = sm + threadIdx.x * NW;  // this thread's counter words
     const uint32_t dummy = topk_dummy_off(shift) + threadIdx.x * 4u;
     const uint32_t lane4 = (threadIdx.x & 63u) * 4u;
     const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t lane = (int32_t)(threadIdx.x & 63u);
     const int64_t q = a.q0 + blockIdx.x;
     const int64_t ex = query_exclusion(a, q);
     const float fT = (float)a.T;
+    const int32_t tw0 = (int32_t)(((int64_t)a.T * wave) / TOPK_WAVES);
+    const int32_t tw1 = (int32_t)(((int64_t)a.T * (wave + 1)) / TOPK_WAVES);
+    LaneRuns lr = lane_runs_init(a, q, tw0, tw1, lane);
+    {
+        uint4* c4 = (uint4*)sm;
+        for (uint32_t w = threadIdx.x; w < S / 8u; w += TOPK_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
 
     double acc = 0.0;
     for (int32_t s = 0; s < a.nseg; ++s) {
         const uint32_t lo = (uint32_t)s << shift;
         const uint32_t width = (uint32_t)min((int64_t)S, a.N - (int64_t)lo);
-        count_segment(a, q, s, S, sm, rec_off, rec_len, dummy, lane4, wave, lo + 1u, width);
+        const uint32_t soff = lr.tb + 4u * lr.o0;
+        const uint32_t len4 = 4u * (lr.o1 - lr.o0);
+        const uint32_t o3 = (lr.ob >= 0 && s + 3 <= a.nseg) ? (uint32_t)a.off[lr.ob + s + 3] : lr.o2;
+        count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, lo + 1u, dummy);
+        lr.o0 = lr.o1;
+        lr.o1 = lr.o2;
+        lr.o2 = o3;
+        __syncthreads();  // every count is in LDS
         const uint32_t u0 = threadIdx.x * 2u * NW;
         const int32_t rem = (int32_t)width - (int32_t)u0;
         const int64_t exd = ex - (int64_t)lo - (int64_t)u0;
@@ -1108,15 +1046,16 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
         for (int k = 0; k < NW; ++k) {
             const uint32_t w = kw[k];
+            kw[k] = 0u;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t c = (w >> (16 * h)) & 0xffffu;
                 if (c != 0u && 2 * k + h < rem && 2 * k + h != exu) acc += outlier_term(c, fT);
             }
         }
-        __syncthreads();  // counters read before the next segment clears them
+        __syncthreads();  // every counter word is zero again before the next segment's counts
     }
-    outlier_finish(acc, red, o, q);
+    outlier_finish(acc, (double*)L.red, o, q);
 }
 
 // 8-bit counters in the segments of k_topk8 (NB blocks of TOPK_BLOCK
@@ -1396,7 +1335,6 @@ static TopkArgs ref_args(rfxp_ctx* ctx, const int32_t* q_leaf, int64_t q_stride_
                          const int32_t* exclude_idx) {
     TopkArgs a;
     a.mem = ctx->ref_mem.p;
-    a.mem_bytes = (uint32_t)(((uint64_t)ctx->ref_T * (uint64_t)ctx->ref_N + MEM_PAD) * 4u);
     a.off = ctx->ref_off.p;
     a.nb = ctx->ref_nb;
     a.N = ctx->ref_N;
