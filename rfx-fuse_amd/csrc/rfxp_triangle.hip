@@ -321,7 +321,10 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
     const uint16_t* rl = a.rlen + i * a.ldr;
     const uint32_t base1 = (uint32_t)lo + 1u - (uint32_t)shift;
     uint32_t steps = 0;
-    // members past the first 64 of a run (rare for per-leaf buckets)
+    // members past the first 64 of a run (rare for per-leaf buckets), eight
+    // 64-member loads in flight at a time: loads past the run's end read 0
+    // (the buffer range ends there) and count into the dummy word, so every
+    // lane of each of the eight steps still adds 1 somewhere
     auto long_tail = [&](int32_t t0) {
         for (int u = 0; u < 16; ++u) {
             const uint32_t len4 = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
@@ -329,10 +332,14 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
             const uint32_t off = __builtin_amdgcn_readfirstlane(ro[t0 + u]);
             const uint32_t end = len4 == 4u * REC_LONG ? long_run_end(a, t0 + u, off, off + len4) : off + len4;
             const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, end);
-            for (uint32_t p4 = 256u; off + p4 < end; p4 += 256u) {
-                count_hits<BITS, EMPTY_FIX>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, off, 0), base1,
-                                            xlim);
-                ++steps;
+            for (uint32_t p4 = 256u; off + p4 < end; p4 += 8u * 256u) {
+                uint32_t m[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    m[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + 256u * k + lane4, off, 0);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) count_hits<BITS, EMPTY_FIX>(m[k], base1, xlim);
+                steps += 8;
             }
         }
     };
