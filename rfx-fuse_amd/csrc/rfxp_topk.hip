@@ -235,62 +235,45 @@ __device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, ui
 }
 
 // A wave's bucket runs of one segment, counted into the LDS counters
-// (BITS 8 or 16).  Lane l holds the run (byte offset soff, byte length len4)
-// of the wave's l-th tree; n_trees (<= 64, uniform) lanes hold one.  The
-// runs are loaded sixteen at a time, two groups in flight.  Returns the
-// wave's 64-lane counting steps (uniform): every lane of a step adds 1 to
-// one counter or dummy byte.
+// (BITS 8 or 16).  Lane l holds the run (byte offset soff, byte length len4
+// <= 256: at most 64 ids, count_runs_chunked cuts longer runs) of the wave's
+// l-th tree or chunk; n_trees (<= 64, uniform) lanes hold one.  The runs are
+// loaded sixteen at a time, two groups in flight.  Returns the wave's 64-lane
+// counting steps (uniform): every lane of a step adds 1 to one counter or
+// dummy byte.
 template <int BITS>
 __device__ __forceinline__ uint32_t count_lane_runs(const TopkArgs& a, uint32_t soff, uint32_t len4,
                                                     int32_t n_trees, uint32_t lane4, uint32_t base1, uint32_t dummy) {
     const uint32_t xlim = BITS == 8 ? dummy : dummy >> 1;
     const int32_t ng = (n_trees + 15) >> 4;
     if (ng == 0) return 0u;
-    uint32_t steps = 16u * (uint32_t)ng;
     uint32_t A[16], B[16];
     auto load = [&](int32_t g, uint32_t (&m)[16]) {
-        bool lng = false;
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
             const uint32_t ln = (uint32_t)__builtin_amdgcn_readlane((int)len4, 16 * g + u);
-            lng |= ln > 256u;
             // non-temporal (cache policy nt): a run is read once per query;
             // streaming the runs keeps the offset rows, reread every segment,
             // in L2
             m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(ref_rsrc(a.mem, so + ln), lane4, so, 2);
         }
-        return lng;
     };
-    auto tails = [&](int32_t g) {
-        for (int u = 0; u < 16; ++u) {
-            const uint32_t ln = (uint32_t)__builtin_amdgcn_readlane((int)len4, 16 * g + u);
-            if (ln <= 256u) continue;
-            const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, 16 * g + u);
-            const __amdgpu_buffer_rsrc_t rs = ref_rsrc(a.mem, so + ln);
-            for (uint32_t p4 = 256u; p4 < ln; p4 += 256u) {
-                count_bits<BITS>((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, p4 + lane4, so, 0), base1, xlim);
-                ++steps;
-            }
-        }
-    };
-    bool la = load(0, A);
-    bool lb = ng > 1 ? load(1, B) : false;
+    load(0, A);
+    if (ng > 1) load(1, B);
     for (int32_t g = 0;; g += 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 16; ++u) count_bits<BITS>(A[u], base1, xlim);
-        if (la) tails(g);
-        if (g + 2 < ng) la = load(g + 2, A);
+        if (g + 2 < ng) load(g + 2, A);
         if (g + 1 >= ng) break;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 16; ++u) count_bits<BITS>(B[u], base1, xlim);
-        if (lb) tails(g + 1);
-        if (g + 3 < ng) lb = load(g + 3, B);
+        if (g + 3 < ng) load(g + 3, B);
         if (g + 2 >= ng) break;
     }
-    return steps;
+    return 16u * (uint32_t)ng;
 }
 
 // Packed maximum of the two 16-bit halves of a and b.
