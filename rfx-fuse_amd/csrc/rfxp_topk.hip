@@ -765,7 +765,9 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // h * 32768 + ...), so each block is selected exactly like a 16-bit segment
 // of 32768 references, in index order.  CHECK (T > 255): a count of 256 or
 // more wraps its byte; every lane of every counting step adds 1 to one
-// counter or dummy byte, so the counts are exact iff all those bytes sum to
+// counter byte or to byte 0 of its thread's dummy word (empty lanes), so the
+// counts are exact iff the counter bytes plus the dummy words (plain counts,
+// read as integers so that many empty steps cannot look like a wrap) sum to
 // 64 x the counting steps.  A segment that fails the check is recounted with
 // 16-bit counters, block by block.
 template <bool CHECK, int NB>
@@ -838,7 +840,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                 mh[h] = max(m2 & 0xffffu, m2 >> 16);
             }
             if constexpr (CHECK) {
-                bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
+                bal += (int32_t)*dw;  // empty lanes only, all in byte 0: a plain count
                 if (lane == 0) bal -= 64 * (int32_t)steps;
             }
             // block reduction of (max of each block, byte balance): NB + 1 words
@@ -1114,7 +1116,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                 bal = (int32_t)__builtin_amdgcn_sad_u8(y.z, 0u, (uint32_t)bal);
                 bal = (int32_t)__builtin_amdgcn_sad_u8(y.w, 0u, (uint32_t)bal);
             }
-            bal = (int32_t)__builtin_amdgcn_sad_u8(*dw, 0u, (uint32_t)bal);
+            bal += (int32_t)*dw;  // empty lanes only, all in byte 0: a plain count
             if (lane == 0) bal -= 64 * (int32_t)steps;
             uint32_t* const slot = L.red + 48 + 16 * (uint32_t)(s & 1);
             const uint32_t wb = wave_sum((uint32_t)bal);
