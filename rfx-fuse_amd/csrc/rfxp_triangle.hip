@@ -134,6 +134,7 @@ struct TriArgs {
     float scale, zp;
     int32_t* flags;     // [0]: items redone with 16-bit counters
     int32_t mode;       // TRI_MODE_*
+    uint32_t dbytes;    // dummy area bytes (TRI_DUMMY_BYTES or TRI_DUMMY_SHARED_BYTES)
 };
 
 // Counter width / exactness check per launch:
@@ -147,10 +148,14 @@ enum { TRI_MODE_EXACT8 = 0, TRI_MODE_CHECK8 = 1, TRI_MODE_WIDE16 = 2 };
 // LDS layout of one workgroup (dynamic shared memory, at address 0):
 //   [0, cap)                 the item's counters, cap = 16 * chunks <= S + 32
 //                            (8-bit, or 16-bit when redoing)
-//   [cap, cap + 4096)        one dummy word per thread (see count_hits)
+//   [cap, cap + dbytes)      dummy words (see count_hits): one per thread
+//                            (dbytes 4096), or one per lane shared by the
+//                            waves (dbytes 256, 3,840 more columns), see
+//                            tri_dummy_bytes
 //   [misc_off, +64)          item scalars (geometry, row table, sums),
-//                            misc_off = round16(S + 64) + 4096
-constexpr int TRI_DUMMY_BYTES = TRI_THREADS * 4;
+//                            misc_off = round16(S + 64) + dbytes
+constexpr uint32_t TRI_DUMMY_BYTES = TRI_THREADS * 4;
+constexpr uint32_t TRI_DUMMY_SHARED_BYTES = 64 * 4;
 constexpr int TRI_MISC_WORDS = 16;
 enum {
     MISC_LUT_LO = 0, MISC_LUT_HI = 1, MISC_UC = 2, MISC_SUM = 3, MISC_SLOTS = 4,  // cleared per item
@@ -158,10 +163,23 @@ enum {
 };
 constexpr int TRI_MISC_ZEROED = 5;  // words cleared per item (the row table and the sums)
 
-__host__ __device__ constexpr uint32_t tri_misc_off(int32_t S) {
-    return (((uint32_t)S + 64u + 15u) & ~15u) + TRI_DUMMY_BYTES;
+__host__ __device__ constexpr uint32_t tri_misc_off(int32_t S, uint32_t dbytes) {
+    return (((uint32_t)S + 64u + 15u) & ~15u) + dbytes;
 }
-__host__ __device__ constexpr uint32_t tri_lds_bytes(int32_t S) { return tri_misc_off(S) + TRI_MISC_WORDS * 4; }
+__host__ __device__ constexpr uint32_t tri_lds_bytes(int32_t S, uint32_t dbytes) {
+    return tri_misc_off(S, dbytes) + TRI_MISC_WORDS * 4;
+}
+
+// This thread's dummy unit past the counters: 8-bit units (bytes), or 16-bit
+// ones.  With one dummy word per thread, byte 0 (half 0) of its own word;
+// with shared words, byte (wave & 3) (half (wave & 1)) of its lane's word,
+// so that four (eight) waves share a unit.
+__device__ __forceinline__ uint32_t dummy_unit8(uint32_t dbytes) {
+    return dbytes == TRI_DUMMY_BYTES ? 4u * threadIdx.x : 4u * (threadIdx.x & 63u) + ((threadIdx.x >> 6) & 3u);
+}
+__device__ __forceinline__ uint32_t dummy_unit16(uint32_t dbytes) {
+    return dbytes == TRI_DUMMY_BYTES ? 2u * threadIdx.x : 2u * (threadIdx.x & 63u) + ((threadIdx.x >> 6) & 1u);
+}
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int b) { return (w >> (8 * b)) & 0xffu; }
 
@@ -499,18 +517,18 @@ __device__ void redo_wide(const TriArgs& a, uint32_t* cnt, const ItemGeom& gm, d
         __syncthreads();
         for (int32_t w = threadIdx.x; w < (int32_t)cap16 / 2; w += TRI_THREADS) cnt[w] = 0u;
         __syncthreads();
-        hit_phase<16>(a, gm.i, gm.lo + d0, 0, cap16 + 2u * threadIdx.x);
+        hit_phase<16>(a, gm.i, gm.lo + d0, 0, cap16 + dummy_unit16(a.dbytes));
         __syncthreads();
         store_exact16<F>(a, cnt, gm.i, gm.lo + d0, w2, ri);
     }
 }
 
-// Zeroes the item's counter words [0, nwords) and the TRI_THREADS dummy
-// words after them (rounded up to whole 16-byte stores: at most 3 words past
-// the last dummy word, inside the 64-byte gap before the item scalars).
-__device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords) {
+// Zeroes the item's counter words [0, nwords) and the dwords dummy words
+// after them (rounded up to whole 16-byte stores: at most 3 words past the
+// last dummy word, inside the 64-byte gap before the item scalars).
+__device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords, int32_t dwords) {
     uint4* c4 = (uint4*)cnt;
-    const int32_t n4 = (nwords + TRI_THREADS + 3) >> 2;
+    const int32_t n4 = (nwords + dwords + 3) >> 2;
     for (int32_t w = threadIdx.x; w < n4; w += TRI_THREADS) c4[w] = make_uint4(0u, 0u, 0u, 0u);
 }
 
@@ -520,8 +538,9 @@ __device__ __forceinline__ void zero_counters(uint32_t* cnt, int32_t nwords) {
 // sum.  So the counters are exact iff
 //   sum of counter bytes + sum of dummy bytes == 64 * counting steps.
 // (A dummy byte that wraps only costs a recount.)
-__device__ __forceinline__ bool counts_exact(uint32_t* misc, uint32_t bsum, const uint32_t* cnt, uint32_t nwords) {
-    bsum = __builtin_amdgcn_sad_u8(cnt[nwords + threadIdx.x], 0u, bsum);
+__device__ __forceinline__ bool counts_exact(uint32_t* misc, uint32_t bsum, const uint32_t* cnt, uint32_t nwords,
+                                             uint32_t dwords) {
+    if (threadIdx.x < dwords) bsum = __builtin_amdgcn_sad_u8(cnt[nwords + threadIdx.x], 0u, bsum);
     // wave reduction, then one atomic per wave
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) bsum += (uint32_t)__shfl_xor((int)bsum, d, 64);
@@ -535,7 +554,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     extern __shared__ uint32_t cnt[];
     constexpr int esz = FmtInfo<F>::esz;
     constexpr int epc = 16 / esz;  // entries per 16-byte chunk
-    uint32_t* const misc = cnt + tri_misc_off(a.S) / 4;
+    uint32_t* const misc = cnt + tri_misc_off(a.S, a.dbytes) / 4;
 
     if (threadIdx.x == 0) item_to_lds<esz>(a, misc);
     __syncthreads();
@@ -550,7 +569,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
         redo_wide<F>(a, cnt, gm, ri);
         return;
     }
-    zero_counters(cnt, gm.nwords);
+    zero_counters(cnt, gm.nwords, (int32_t)(a.dbytes / 4u));
     if (threadIdx.x < TRI_MISC_ZEROED) misc[threadIdx.x] = 0u;
     if constexpr (F == I8 || F == U8) row_table<F>(a, ri, misc);
     __syncthreads();
@@ -558,8 +577,8 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     // item's columns but inside that range land in the unstored padding
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x)
-                                       : hit_phase<8, true>(a, i, lo, shift, cap + 4u * threadIdx.x);
+    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + dummy_unit8(a.dbytes))
+                                       : hit_phase<8, true>(a, i, lo, shift, cap + dummy_unit8(a.dbytes));
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -656,7 +675,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords)) redo_wide<F>(a, cnt, gm, ri);
+    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords, a.dbytes / 4u)) redo_wide<F>(a, cnt, gm, ri);
 }
 
 // NF4: two entries per byte.  Nibble position g(e) = e - e_base + (e_base & 1)
@@ -665,7 +684,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
 // merged with 32-bit atomics on its own nibble only.
 __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_tri_nf4(TriArgs a) {
     extern __shared__ uint32_t cnt[];
-    uint32_t* const misc = cnt + tri_misc_off(a.S) / 4;
+    uint32_t* const misc = cnt + tri_misc_off(a.S, a.dbytes) / 4;
 
     if (threadIdx.x == 0) item_to_lds<0>(a, misc);
     __syncthreads();
@@ -680,14 +699,14 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
         redo_wide<NF4>(a, cnt, gm, ri);
         return;
     }
-    zero_counters(cnt, gm.nwords);
+    zero_counters(cnt, gm.nwords, (int32_t)(a.dbytes / 4u));
     if (threadIdx.x < TRI_MISC_ZEROED) misc[threadIdx.x] = 0u;
     row_table<NF4>(a, ri, misc);
     __syncthreads();
     const bool check = a.mode == TRI_MODE_CHECK8;
     const uint32_t cap = (uint32_t)gm.nwords * 4u;
-    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + 4u * threadIdx.x)
-                                       : hit_phase<8, true>(a, i, lo, shift, cap + 4u * threadIdx.x);
+    const uint32_t steps = lo >= shift ? hit_phase<8>(a, i, lo, shift, cap + dummy_unit8(a.dbytes))
+                                       : hit_phase<8, true>(a, i, lo, shift, cap + dummy_unit8(a.dbytes));
     if (check && (threadIdx.x & 63) == 0) atomicAdd(&misc[MISC_SLOTS], steps);
     __syncthreads();
 
@@ -753,7 +772,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
     }
-    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords)) redo_wide<NF4>(a, cnt, gm, ri);
+    if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords, a.dbytes / 4u)) redo_wide<NF4>(a, cnt, gm, ri);
 }
 
 // ---------------------------------------------------------------------------
@@ -762,12 +781,22 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
 
 static int64_t ceil_div_i(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-static int tri_segment_cols(rfxp_ctx* ctx) {
+// Dummy area of a launch of T trees: one word per lane shared by the waves
+// when no dummy byte can reach 256 in a checked launch (T <= 255, which is
+// not checked, or four waves' counting steps within the CHECK8 limit of
+// 192), else one word per thread.
+static uint32_t tri_dummy_bytes(int32_t T) {
+    if (T <= 255) return TRI_DUMMY_SHARED_BYTES;
+    const int64_t groups = ceil_div_i((T + 15) / 16, TRI_WAVES);
+    return 4 * 16 * groups <= 192 ? TRI_DUMMY_SHARED_BYTES : TRI_DUMMY_BYTES;
+}
+
+static int tri_segment_cols(rfxp_ctx* ctx, uint32_t dbytes) {
     // Columns per item: one counter byte each (NF4: one per nibble entry),
     // plus the alignment slack, the dummy words and the item scalars
     // (tri_lds_bytes), two workgroups per CU (160 KB of LDS on gfx950).
     const int half = std::min(ctx->max_lds, 160 * 1024) / 2;
-    int S = half - TRI_DUMMY_BYTES - TRI_MISC_WORDS * 4 - 64 - 16;
+    int S = half - (int)dbytes - TRI_MISC_WORDS * 4 - 64 - 16;
     S = std::max(S, 4096) & ~63;
     return S;
 }
@@ -904,7 +933,8 @@ int upper_check_args(rfxp_ctx* ctx, const char* who, int64_t N, int fmt, float s
 int upper_launch(rfxp_ctx* ctx, const ForestBufs& fb, int64_t N, int32_t T, int fmt, float scale, float zp,
                  int64_t r0, int64_t r1, void* out) {
     if (r0 == r1) return RFXP_OK;
-    const int32_t S = tri_segment_cols(ctx);
+    const uint32_t dbytes = tri_dummy_bytes(T);
+    const int32_t S = tri_segment_cols(ctx, dbytes);
     TriArgs a;
     a.roff = fb.roff;
     a.rlen = fb.rlen;
@@ -927,8 +957,9 @@ int upper_launch(rfxp_ctx* ctx, const ForestBufs& fb, int64_t N, int32_t T, int 
     a.zp = zp;
     a.flags = fb.flags;
     a.mode = tri_mode(T);
+    a.dbytes = dbytes;
     const int64_t n_items = tri_slot_count(N, S, r0, r1);
-    const size_t lds = tri_lds_bytes(S);
+    const size_t lds = tri_lds_bytes(S, dbytes);
     hipError_t e;
     {
         LaunchTimer tm(ctx, "tri");

@@ -162,25 +162,27 @@ def test_many_trees_take_the_16bit_mode(gpu_ctx, fmt):
 
 
 def test_split_rows_with_wrapped_8bit_counts(gpu_ctx):
-    """N = 80,000 is above one workgroup's column segment, so rows below
+    """N = 90,000 is above one workgroup's column segment, so rows below
     N - S are counted as two items.  T = 700 turns on the byte-sum check, and
     samples 0..299 share sample 0's leaf in every tree: their pairs reach
     counts near 325, which wrap 8 bits, inside both items of split rows.  Rows
     on both sides of the split boundary and of the group are compared."""
     import torch
 
-    n, t, nleaf = 80_000, 700, 400
+    n, t, nleaf = 90_000, 700, 400
     leaf, oob = make_forest(43, n, t, nleaf, p_oob=0.368)
     leaf[:, :300] = leaf[:, :1]
     keep = upload(gpu_ctx, leaf, oob, nleaf)
     idx = O.RowIndex(leaf, oob, nleaf)
     assert idx.rows(O.FMT_U16, 0, 1)[:300].max() > 255
-    split = n - 77_632       # S = 77,632 columns per item on gfx950 (two workgroups' LDS per CU)
+    # S = 81,472 columns per item on gfx950 (two workgroups' LDS per CU, dummy
+    # words shared by the waves: T = 700 has at most 48 counting steps per wave)
+    split = n - 81_472
     for fmt in (O.FMT_U8, O.FMT_U16):
         out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
         gpu_ctx.upper(fmt, out, 0, n, scale=np.float32(1 / 255.0))
         torch.cuda.synchronize()
-        for r0 in (0, 1, 150, 298, 299, 300, split - 2, split, 40_000, 79_990):
+        for r0 in (0, 1, 150, 298, 299, 300, split - 2, split, 40_000, n - 10):
             r1 = min(n, r0 + 3)
             want = idx.rows(fmt, r0, r1, np.float32(1 / 255.0), np.float32(0.0))
             e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
