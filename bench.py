@@ -59,6 +59,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=16.0,
                     help="target CPU time of the bounded CPU-baseline sample")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only time the triangle's two traffic streams on synthetic data of its shape: "
+                         "random run gathers, the N(N+1)/2-byte streaming store, each alone and both in "
+                         "one kernel (rfx-fuse_amd/calib/rfxc_calib.hip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -128,6 +132,78 @@ def copy_calibration(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+
+
+def calibrate(args):
+    """Floor of the bucketed triangle's traffic on this GPU.  Synthetic
+    records of C3's shape (N rows, T random runs of 0..24 ids per row, ids
+    at uniform places of an id array), one workgroup per row as in k_tri:
+      gather  -- records, run loads and LDS counting, no output;
+      store   -- the N(N+1)/2-byte triangle streamed from LDS, no run loads;
+      both    -- both in one kernel, in k_tri's order.
+    The id array's size is swept to show where the runs are served from
+    (L2: a few MB; Infinity Cache: up to 256 MB; HBM beyond).  Times are HIP
+    events around single launches on one stream (median of 5)."""
+    import ctypes as C
+    import statistics
+
+    import torch
+
+    lib = C.CDLL(os.path.join(REPO, "rfx-fuse_amd", "lib", "librfxcalib.so"))
+    vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
+    lib.rfxc_setup.argtypes = [vp, i64, C.c_int, vp, vp, i64, i32, i64, C.c_uint32, vp]
+    lib.rfxc_run.argtypes = [C.c_int, C.c_int, vp, vp, vp, i64, i32, i64, vp, vp, vp]
+    cfg = CONFIGS["c3"]
+    n = args.n or cfg["n"]
+    t = cfg["t"]
+    ldr = (t + 15) // 16 * 16
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    roff = torch.empty(n * ldr, dtype=torch.int32, device=dev)
+    rlen = torch.empty(n * ldr, dtype=torch.int16, device=dev)
+    out = torch.empty(n * (n + 1) // 2, dtype=torch.uint8, device=dev)
+    sink = torch.empty(n, dtype=torch.int32, device=dev)
+    runs = n * t
+    res = {"workload": "calibration of the C3 triangle's traffic", "N": n, "T": t, "runs": runs,
+           "store_bytes": n * (n + 1) // 2, "cases": []}
+
+    def timed(mode, idb, mem):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ms = []
+        for k in range(7):
+            ev[0].record()
+            rc = lib.rfxc_run(mode, idb, mem.data_ptr(), roff.data_ptr(), rlen.data_ptr(), ldr, t, n,
+                              out.data_ptr(), sink.data_ptr(), stream)
+            ev[1].record()
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError(f"rfxc_run mode {mode} idb {idb}: hip error {rc}")
+            if k >= 2:
+                ms.append(ev[0].elapsed_time(ev[1]))
+        return statistics.median(ms)
+
+    # mode bits: 1 gather, 2 store, 4 records by one vector load per group
+    # (else by scalar loads)
+    for idb, mem_mb, modes in ((4, 200, (2, 1, 3, 5, 7)), (4, 2, (5, 7)), (4, 32, (5,)), (4, 1024, (5, 7)),
+                               (2, 100, (5, 7))):
+        mem_bytes = mem_mb << 20
+        mem = torch.empty(mem_bytes + 4096, dtype=torch.uint8, device=dev)
+        rc = lib.rfxc_setup(mem.data_ptr(), mem_bytes, idb, roff.data_ptr(), rlen.data_ptr(), n, t, ldr, 7, stream)
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError(f"rfxc_setup: hip error {rc}")
+        for mode in modes:
+            ms = timed(mode, idb, mem)
+            case = {"kind": {1: "gather", 2: "store", 3: "both"}[mode & 3], "id_bytes": idb, "id_array_MB": mem_mb,
+                    "records": "vector" if mode & 4 else "scalar", "ms": ms}
+            if mode & 1:
+                case["runs_per_s"] = runs / (ms / 1e3)
+            if mode & 2:
+                case["store_GBps"] = n * (n + 1) // 2 / (ms / 1e3) / 1e9
+            res["cases"].append(case)
+            print(json.dumps(case), flush=True)
+        del mem
+    print(json.dumps(res), flush=True)
 
 
 def make_inputs(cfg, n, device):
@@ -223,6 +299,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.calibrate:
+        calibrate(args)
         return
     if args.config == "c5":
         run_c5(args)

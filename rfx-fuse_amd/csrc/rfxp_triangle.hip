@@ -221,22 +221,25 @@ __device__ __forceinline__ uint32_t float_entry(uint32_t U, double ri, const dou
 // Nonzero when some byte of w is >= uc (or >= 0x80): kuc = (0x80 - uc) * 0x01010101.
 __device__ __forceinline__ uint32_t over_uc(uint32_t w, uint32_t kuc) { return ((w + kuc) | w) & 0x80808080u; }
 
-// Byte codes of the four counts of w for I8 / U8 / NF4, exact path: counts
-// below uc come from the row table, the others from the closed form.
-template <int F>
-__device__ __noinline__ uint32_t code_word_exact(uint32_t w, uint32_t lut_lo, uint32_t lut_hi, uint32_t uc,
-                                                 double ri, const double* rinv, int64_t j0, float scale,
-                                                 float zp) {
-    uint32_t o = 0;
+// Exact codes (I8 / U8 / NF4) for the counts >= uc of a chunk of NW words
+// of byte counters w, whose table codes are already in o: only those bytes
+// are recomputed from the closed form, each with its column's r_j (byte b
+// of the chunk is column j0 + b).  Inlined: the chunks that need it are
+// rare, and a call would make the kernel save registers around it.
+template <int F, int NW>
+__device__ __forceinline__ void fix_codes(uint32_t (&o)[NW], const uint32_t (&w)[NW], uint32_t uc, double ri,
+                                          const double* rinv, int64_t j0, float scale, float zp) {
+    uint32_t m = 0;  // bit b: byte b holds a count >= uc
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        uint32_t U = byte_of(w, b);
-        uint32_t c;
-        if (U < uc) c = (U < 4 ? lut_lo >> (8 * U) : lut_hi >> (8 * (U - 4))) & 0xffu;
-        else c = code_of<F>(pair_p(U, ri, rinv[j0 + b]), scale, zp);
-        o |= c << (8 * b);
+    for (int b = 0; b < 4 * NW; ++b) m |= (byte_of(w[b >> 2], b & 3) >= uc ? 1u : 0u) << b;
+    while (m) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1u;
+        uint32_t U = 0;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) U = (q == (b >> 2)) ? byte_of(w[q], b & 3) : U;
+        set_byte(o, b, code_of<F>(pair_p(U, ri, rinv[j0 + b]), scale, zp));
     }
-    return o;
 }
 
 // Hit phase: every member j of row i's opposite buckets with lo <= j < hi
@@ -589,28 +592,10 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
         const uint32_t lut_lo = misc[MISC_LUT_LO], lut_hi = misc[MISC_LUT_HI], uc = misc[MISC_UC];
         const uint32_t kuc = (0x80u - uc) * 0x01010101u;
         const uint32_t dcode = code_of<F>(1.0, a.scale, a.zp);
-        for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS) {
-            const uint4 w = c4[ck];
-            if (check) {
-                bsum = __builtin_amdgcn_sad_u8(w.x, 0u, bsum);
-                bsum = __builtin_amdgcn_sad_u8(w.y, 0u, bsum);
-                bsum = __builtin_amdgcn_sad_u8(w.z, 0u, bsum);
-                bsum = __builtin_amdgcn_sad_u8(w.w, 0u, bsum);
-            }
-            uint32_t o[4];
-            if ((over_uc(w.x, kuc) | over_uc(w.y, kuc) | over_uc(w.z, kuc) | over_uc(w.w, kuc)) == 0u) {
-                // every count below uc: table lookup, four bytes at a time
-                o[0] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.x);
-                o[1] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.y);
-                o[2] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.z);
-                o[3] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.w);
-            } else {
-                const int64_t jb = lo + (int64_t)ck * 16 - shift;  // column of byte 0
-                o[0] = code_word_exact<F>(w.x, lut_lo, lut_hi, uc, ri, a.rinv, jb + 0, a.scale, a.zp);
-                o[1] = code_word_exact<F>(w.y, lut_lo, lut_hi, uc, ri, a.rinv, jb + 4, a.scale, a.zp);
-                o[2] = code_word_exact<F>(w.z, lut_lo, lut_hi, uc, ri, a.rinv, jb + 8, a.scale, a.zp);
-                o[3] = code_word_exact<F>(w.w, lut_lo, lut_hi, uc, ri, a.rinv, jb + 12, a.scale, a.zp);
-            }
+        // Stores chunk ck's codes o: whole chunks with one 16-byte
+        // non-temporal store, the first and last chunk of the item byte by
+        // byte (only the item's own entries).
+        auto store_chunk = [&](int32_t ck, uint32_t (&o)[4]) {
             // the diagonal is column lo, byte `shift` of chunk 0
             if (has_diag && ck == 0) set_byte(o, shift, dcode);
             char* d = dst_al + (int64_t)ck * 16;
@@ -625,6 +610,45 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
                     if (e >= shift && e < shift + width) d[b] = (char)byte_of(o[b >> 2], b & 3);
                 }
             }
+        };
+        // Chunks whose 16 counts are all below uc are coded by the row table,
+        // four bytes at a time.  A chunk with a count >= uc needs its
+        // columns' r_j; it is only marked here (bit k of `defer`: chunk
+        // threadIdx.x + k * TRI_THREADS; nchunk <= S/16 + 2, so k < 32) and coded
+        // after the loop, so the loop stays free of calls and loads.
+        uint32_t defer = 0;
+        int32_t k = 0;
+        for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS, ++k) {
+            const uint4 w = c4[ck];
+            if (check) {
+                bsum = __builtin_amdgcn_sad_u8(w.x, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.y, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.z, 0u, bsum);
+                bsum = __builtin_amdgcn_sad_u8(w.w, 0u, bsum);
+            }
+            if ((over_uc(w.x, kuc) | over_uc(w.y, kuc) | over_uc(w.z, kuc) | over_uc(w.w, kuc)) != 0u) {
+                defer |= 1u << k;
+                continue;
+            }
+            uint32_t o[4];
+            o[0] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.x);
+            o[1] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.y);
+            o[2] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.z);
+            o[3] = __builtin_amdgcn_perm(lut_hi, lut_lo, w.w);
+            store_chunk(ck, o);
+        }
+        // the marked chunks: exact codes for the counts >= uc
+        while (defer) {
+            const int32_t ck = threadIdx.x + __builtin_ctz(defer) * TRI_THREADS;
+            defer &= defer - 1u;
+            const uint4 w = c4[ck];
+            const int64_t jb = lo + (int64_t)ck * 16 - shift;  // column of byte 0
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, wv[q]);
+            fix_codes<F>(o, wv, uc, ri, a.rinv, jb, a.scale, a.zp);
+            store_chunk(ck, o);
         }
     } else {
         // F32 / F16 / U16: epc entries per chunk = epc counters (bytes)
@@ -716,28 +740,10 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
     const uint32_t kuc = (0x80u - uc) * 0x01010101u;
     const bool has_diag = (lo == i);
     const uint4* c4 = (const uint4*)cnt;
-    for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS) {
-        // 32 counters -> 32 nibble codes -> 16 bytes
-        uint32_t cw[8];
-        const uint4 wa = c4[2 * ck], wb = c4[2 * ck + 1];
-        cw[0] = wa.x; cw[1] = wa.y; cw[2] = wa.z; cw[3] = wa.w;
-        cw[4] = wb.x; cw[5] = wb.y; cw[6] = wb.z; cw[7] = wb.w;
-        uint32_t over = 0u;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            if (check) bsum = __builtin_amdgcn_sad_u8(cw[q], 0u, bsum);
-            over |= over_uc(cw[q], kuc);
-        }
-        uint32_t codes[8];
-        if (over == 0u) {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) codes[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, cw[q]);
-        } else {
-            const int64_t jb = lo + (int64_t)ck * 32 - shift;
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                codes[q] = code_word_exact<NF4>(cw[q], lut_lo, lut_hi, uc, ri, a.rinv, jb + 4 * q, 0.f, 0.f);
-        }
+    // Packs the byte codes of chunk ck (32 entries) into 16 nibble bytes and
+    // stores them: whole chunks with one non-temporal store, boundary bytes
+    // shared with a neighbouring item merged on their own nibble.
+    auto store_chunk = [&](int32_t ck, uint32_t (&codes)[8]) {
         if (has_diag && ck == 0) set_byte(codes, shift, dcode);
         // pack byte codes c0..c3 of each word into two nibble-bytes
         uint32_t ob[4];
@@ -771,6 +777,43 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
                 }
             }
         }
+    };
+    // as in k_tri: chunks with a count >= uc are marked (bit k of defer)
+    // and coded exactly after the table-driven loop
+    uint32_t defer = 0;
+    int32_t k = 0;
+    for (int32_t ck = threadIdx.x; ck < nchunk; ck += TRI_THREADS, ++k) {
+        // 32 counters -> 32 nibble codes -> 16 bytes
+        uint32_t cw[8];
+        const uint4 wa = c4[2 * ck], wb = c4[2 * ck + 1];
+        cw[0] = wa.x; cw[1] = wa.y; cw[2] = wa.z; cw[3] = wa.w;
+        cw[4] = wb.x; cw[5] = wb.y; cw[6] = wb.z; cw[7] = wb.w;
+        uint32_t over = 0u;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (check) bsum = __builtin_amdgcn_sad_u8(cw[q], 0u, bsum);
+            over |= over_uc(cw[q], kuc);
+        }
+        if (over != 0u) {
+            defer |= 1u << k;
+            continue;
+        }
+        uint32_t codes[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) codes[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, cw[q]);
+        store_chunk(ck, codes);
+    }
+    while (defer) {
+        const int32_t ck = threadIdx.x + __builtin_ctz(defer) * TRI_THREADS;
+        defer &= defer - 1u;
+        const uint4 wa = c4[2 * ck], wb = c4[2 * ck + 1];
+        const uint32_t cw[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        const int64_t jb = lo + (int64_t)ck * 32 - shift;
+        uint32_t codes[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) codes[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, cw[q]);
+        fix_codes<NF4>(codes, cw, uc, ri, a.rinv, jb, 0.f, 0.f);
+        store_chunk(ck, codes);
     }
     if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords, a.dbytes / 4u)) redo_wide<NF4>(a, cnt, gm, ri);
 }
