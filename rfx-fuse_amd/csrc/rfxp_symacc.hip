@@ -373,10 +373,12 @@ __global__ void k_to_rowmajor(const double* A, int64_t N, int32_t r, double* Ar)
 // Reconstruction P = A B^T into the column-major N x N `out`
 // (cuda/rf_proximity_lowrank.cu:1274-1376): the dot products in column
 // order, the diagonal set to 1, and, with RF-GAP counts s (w = 1/s where
-// s > 0), the reference's row scaling of its row-major view followed by
-// (x + y)/2 symmetrisation, which for i != j gives
-// 0.5 * (P*w_lo + P*w_hi), lo = min(i, j), hi = max(i, j), and w_i on the
-// diagonal.
+// s > 0), each row scaled by its w and every off-diagonal pair averaged,
+// 0.5 * (P*w_lo + P*w_hi), lo = min(i, j), hi = max(i, j), with w_i on the
+// diagonal.  The reference's symmetrisation launch (:1356-1372) covers only
+// about N of the N^2 linear indices (row 0's pairs), leaving the rest with
+// one-sided scales; this kernel symmetrises every pair instead, as that
+// step intends.
 __global__ void k_reconstruct(const double* A, const double* B, int64_t N, int32_t r, const double* winv,
                               const int32_t* s, double* out) {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
