@@ -53,7 +53,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="one config only; by default C3 is the bench line and C2, C5, C4 are added "
+                         "to it as sub-records")
+    ap.add_argument("--no-sub", action="store_true", help="default run without the C2/C5/C4 sub-records")
     ap.add_argument("--n", type=int, default=None, help="override N (smaller smoke runs)")
     ap.add_argument("--q", type=int, default=None, help="override the query count (c5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -303,23 +306,44 @@ def main():
     if args.calibrate:
         calibrate(args)
         return
-    if args.config == "c5":
-        run_c5(args)
-        return
-    if args.config == "c4":
-        run_c4(args)
-        return
-    run_triangle(args)
+    name = args.config or "c3"
+    rec = RUNNERS[name](args, name)
+    if args.config is None and not args.no_sub:
+        rec["sub_records"] = sub_records(args)
+    print(json.dumps(rec), flush=True)
 
 
-def run_triangle(args):
+def sub_records(args):
+    """C2, C5 and C4 measured in the same process after the C3 line, at
+    their full sizes, with the same step counts.  A failure in one of them
+    is reported in its record and never stops the others or the C3 line."""
+    import copy
+    import gc
+
+    import torch
+
+    out = {}
+    for name in ("c2", "c5", "c4"):
+        sub = copy.copy(args)
+        sub.n = sub.q = None
+        try:
+            gc.collect()
+            torch.cuda.empty_cache()
+            out[name] = RUNNERS[name](sub, name)
+        except Exception as e:  # reported, not raised: the C3 line must still print
+            out[name] = {"config": CONFIGS[name]["workload"], "error": f"{type(e).__name__}: {e}"}
+    return out
+
+
+def run_triangle(args, name):
     """C3 (default) and C2: one step = rfxp_set_forest (bucket index over all
-    trees) + rfxp_upper (counting, normalisation, quantisation, stores)."""
+    trees) + rfxp_upper (counting, normalisation, quantisation, stores).
+    Returns the record."""
     import torch
 
     import rfxprox as R
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     n = args.n or cfg["n"]
     t = cfg["t"]
     dev = torch.device("cuda:0")
@@ -370,6 +394,9 @@ def run_triangle(args):
     ldr = (t + 15) // 16 * 16
     tri_bytes = nbytes + n * ldr * 6 + n * 8
     achieved = tri_bytes / (tri_avg / 1e3) / 1e9
+    # compulsory HBM bytes of the step: the output once, the int32 leaf
+    # matrix, the OOB bits and nout once each
+    compulsory = nbytes + n * t * 4 + n * t // 8 + n * 4
     rec = {
         "metric": f"pair-tree comparisons/sec at N={n // 1000}k,T={t} ({fmt} OOB proximity triangle)",
         "value": value,
@@ -393,8 +420,13 @@ def run_triangle(args):
         "tri_recounts": ctx.upper_recounts(),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_launch": tri_bytes,
-                     "traffic": traffic_from_profile(args.config) if n == cfg["n"] else None,
-                     "kernel_source_sha": kernel_source_sha()},
+                     "traffic": traffic_from_profile(name) if n == cfg["n"] else None,
+                     "kernel_source_sha": kernel_source_sha(),
+                     # the same against the config's compulsory bytes: the triangle
+                     # kernel alone, and the whole timed step (packing included)
+                     "compulsory_bytes": compulsory,
+                     "frac_compulsory_kernel": compulsory / (tri_avg / 1e3) / 1e9 / HBM_PEAK_GBS,
+                     "frac_compulsory_step": compulsory / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS},
         "wall_s": wall,
     }
     ctx.set_timing(False)
@@ -404,8 +436,8 @@ def run_triangle(args):
         rec["cpu_baseline"] = cpu_baseline(cfg, leaf_np, oob_np, n, fmt, scale, zp, args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
-    print(json.dumps(rec), flush=True)
     ctx.close()
+    return rec
 
 
 def cpu_baseline_topk(cfg, ref_tn, q_qt, k, target_s):
@@ -420,16 +452,20 @@ def cpu_baseline_topk(cfg, ref_tn, q_qt, k, target_s):
 
     model, ncpu, threads = host_cpu()
     t, n = ref_tn.shape
+    nq_all = q_qt.shape[0]
 
     def rate(nth, budget, seed_off):
-        n_q = nth
+        # queries [lo, lo + n_q) of the set: a first run of one query per
+        # thread sizes the timed run to the budget
+        lo = min(seed_off, max(0, nq_all - nth))
+        n_q = min(nth, nq_all - lo)
         t0 = time.perf_counter()
-        O.topk_all(ref_tn, q_qt[seed_off:seed_off + n_q], k, threads=nth)
+        O.topk_all(ref_tn, q_qt[lo:lo + n_q], k, threads=nth)
         dt = time.perf_counter() - t0
         if dt < budget:
-            n_q = min(q_qt.shape[0] - seed_off, max(n_q, int(n_q * budget / max(dt, 1e-3)) // nth * nth))
+            n_q = min(nq_all - lo, max(n_q, int(n_q * budget / max(dt, 1e-3)) // nth * nth))
             t0 = time.perf_counter()
-            O.topk_all(ref_tn, q_qt[seed_off:seed_off + n_q], k, threads=nth)
+            O.topk_all(ref_tn, q_qt[lo:lo + n_q], k, threads=nth)
             dt = time.perf_counter() - t0
         return n_q * n * t / dt, n_q, dt
 
@@ -451,11 +487,11 @@ def cpu_baseline_topk(cfg, ref_tn, q_qt, k, target_s):
     }
 
 
-def run_c5(args):
+def run_c5(args, name="c5"):
     """Top-K of K=20 references per query for Q queries against N references
     over T trees (all trees, zeros included, ties by lower index).  The
     reference index (rfxp_set_reference) is built once outside the timed
-    region; one step = rfxp_topk over all Q queries."""
+    region; one step = rfxp_topk over all Q queries.  Returns the record."""
     import numpy as np
     import torch
 
@@ -495,6 +531,9 @@ def run_c5(args):
     # buckets (N/nleaf per bucket on average, 4 B) + the query labels + outputs
     alg = q * t * (n / nleaf) * 4 + q * t * 4 + q * k * 6
     achieved = alg / (k_avg / 1e3) / 1e9
+    # compulsory HBM bytes: the reference leaf matrix and the queries once
+    # (int16 labels, as the survey counts them) and the outputs
+    compulsory = n * t * 2 + q * t * 2 + q * k * 6
     rec = {
         "metric": "pair-tree comparisons/sec (C5 top-K retrieval, Q x N x T)",
         "value": q * n * t / (ms_step / 1e3),
@@ -513,22 +552,24 @@ def run_c5(args):
         "index_build_ms": index_ms,
         "kernels_ms": {"topk_avg": k_avg},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_launch": alg, "traffic": None,
+                     "compulsory_bytes": compulsory,
+                     "frac_compulsory_step": compulsory / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS},
     }
     ctx.set_timing(False)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline_topk(cfg, ref.cpu().numpy(), qs.cpu().numpy(), k, args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
-    print(json.dumps(rec), flush=True)
     ctx.close()
+    return rec
 
 
-def run_c4(args):
+def run_c4(args, name="c4"):
     """One step = rfxp_lowrank_pv (Y = A (A^T V) / T) on an N x 32 block;
     also reported: the 5-iteration subspace run to a rank-32 factor.  The
     reference index (rfxp_set_reference) is built once outside the timed
-    region."""
+    region.  Returns the record."""
     import numpy as np
     import torch
 
@@ -601,7 +642,9 @@ def run_c4(args):
         "subspace_ms": sub_ms,
         "index_build_ms": index_ms,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_step": alg, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_step": alg, "traffic": None,
+                     "compulsory_bytes": alg,
+                     "frac_compulsory_step": alg / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS},
         "gather_GBps": gather / (ms_step / 1e3) / 1e9,
         "ritz_top": float(np.max(np.linalg.eigvalsh((B + B.T) / 2))),
     }
@@ -631,8 +674,11 @@ def run_c4(args):
                                "sample": f"{tt} of {t} trees at full N, scaled linearly; median of 3 runs"}
     else:
         rec["cpu_baseline"] = None
-    print(json.dumps(rec), flush=True)
     ctx.close()
+    return rec
+
+
+RUNNERS = {"c3": run_triangle, "c2": run_triangle, "c5": run_c5, "c4": run_c4}
 
 
 if __name__ == "__main__":
