@@ -94,11 +94,29 @@ def test_subspace_matches_numpy(gpu_ctx):
     assert rel_fro(Q @ (B @ (Q.T @ Vt)), Qw @ (Bw @ (Qw.T @ Vt))) < 1e-4
 
 
+def test_rank32_subspace_at_100k_matches_numpy(gpu_ctx):
+    """The rank-32, 5-iteration factor at N = 100,000 against numpy's
+    subspace iteration in double (same start block), within the 1e-4
+    relative Frobenius contract on Q B Q^T applied to a random block."""
+    rng = np.random.default_rng(8)
+    n, t, nleaf, r, iters = 100_000, 40, 48, 32, 5
+    leaf = zipf_leaves(rng, n, t, nleaf)
+    V0 = rng.standard_normal((n, r)).astype(np.float32)
+    gpu_ctx.set_reference(dev(leaf), n, t, nleaf)
+    Q, B = gpu_ctx.lowrank_subspace(dev(V0), iters)
+    Q = Q.cpu().numpy().astype(np.float64)
+    Qw, Bw = numpy_subspace(leaf, nleaf, V0, iters)
+    assert np.abs(Q.T @ Q - np.eye(r)).max() < 1e-5
+    Vt = rng.standard_normal((n, r))
+    assert rel_fro(Q @ (B @ (Q.T @ Vt)), Qw @ (Bw @ (Qw.T @ Vt))) < 1e-4
+
+
 def test_c4_shape_properties(gpu_ctx):
     """Config C4 shape (N=1M, T=500, 4096 leaves, Zipf(1.1) sizes, a label
     permutation per tree) through properties the size does not change:
-    P 1 = (1/T) sum_t |leaf_i(t)| exactly (in fp32 rounding), and P is
-    symmetric (u . P v = v . P u)."""
+    P 1 = (1/T) sum_t |leaf_i(t)| exactly (in fp32 rounding), P is
+    symmetric (u . P v = v . P u), and P V on sampled rows equals an
+    independent double evaluation within the 1e-5 contract."""
     import torch
 
     n, t, nleaf = 1_000_000, 500, 4096
@@ -126,6 +144,30 @@ def test_c4_shape_properties(gpu_ctx):
     b = (v.double() * Pu.double()).sum(0)
     scale = u.double().norm(dim=0) * Pv.double().norm(dim=0)
     assert ((a - b).abs() / scale).max().item() < 1e-5
+    # P V itself on 128 sampled rows against an exact double evaluation that
+    # shares nothing with the library's kernels: per tree, the double sums of
+    # V over the leaves the sampled rows sit in (torch index_add), averaged
+    # over the trees
+    r = 32
+    V = torch.randn((n, r), generator=g, device="cuda:0")
+    Y = gpu_ctx.lowrank_pv(V)
+    rows = torch.randint(0, n, (128,), generator=g, device="cuda:0")
+    V64 = V.double()
+    want = torch.zeros((rows.numel(), r), dtype=torch.float64, device="cuda:0")
+    slot_of = torch.full((nleaf,), -1, dtype=torch.int64, device="cuda:0")
+    for k in range(t):
+        lk = leaf[k].long()
+        labels, inv = torch.unique(lk[rows], return_inverse=True)
+        slot_of[labels] = torch.arange(labels.numel(), device="cuda:0")
+        slot = slot_of[lk]
+        sel = torch.nonzero(slot >= 0).squeeze(1)
+        W = torch.zeros((labels.numel(), r), dtype=torch.float64, device="cuda:0")
+        W.index_add_(0, slot[sel], V64[sel])
+        want += W[inv]
+        slot_of[labels] = -1
+    want /= t
+    got = Y[rows].double()
+    assert ((got - want).norm() / want.norm()).item() < 1e-5
 
 
 @pytest.mark.parametrize("n,t,nleaf,r,layout", [(1, 2, 1, 1, "tree"), (1500, 40, 12, 8, "tree"),

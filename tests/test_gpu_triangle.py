@@ -7,7 +7,8 @@ import pytest
 
 import oracle as O
 import rfxprox as R
-from closed_forms import pair_total
+from closed_forms import pair_total, row_pair_counts
+from tri_sums import symmetric_row_sums
 
 pytestmark = pytest.mark.gpu
 
@@ -119,6 +120,35 @@ def test_row_ranges(gpu_ctx, fmt, r0, r1, offset):
     del keep
 
 
+@pytest.mark.parametrize("planted", [True, False])
+def test_thousand_trees_check_with_per_thread_dummy_words(gpu_ctx, planted):
+    """T = 1,000: four groups of 16 trees per wave, more counting steps than
+    the shared dummy words allow, so the byte-sum check runs with one dummy
+    word per thread (the path forests of 769 to 3,072 trees take).  Planted:
+    samples 0..99 share sample 0's leaf in every tree, so their pairs reach
+    counts near 465, which wrap 8 bits and must be recounted; otherwise
+    counts stay near 2 and no item may be recounted."""
+    n, t = 3000, 1000
+    nleaf = 40 if planted else 200
+    leaf, oob = make_forest(97 + planted, n, t, nleaf, p_oob=0.368)
+    if planted:
+        leaf[:, :100] = leaf[:, :1]
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    want_u = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    assert (want_u.max() > 255) == planted
+    for fmt, scale in ((O.FMT_U16, 1.0), (O.FMT_U8, 1 / 255.0)):
+        scale = np.float32(scale)
+        got, guard = gpu_rows(gpu_ctx, fmt, 0, n, scale=scale)
+        want = want_u if fmt == O.FMT_U16 else O.upper_rows(leaf, oob, nleaf, fmt, scale=scale)
+        check_equal(got, want, f"T=1000 planted={planted} fmt {fmt}")
+        assert (guard == 0xA5).all()
+        if planted:
+            assert gpu_ctx.upper_recounts() > 0
+        else:
+            assert gpu_ctx.upper_recounts() == 0
+    del keep
+
+
 def test_sample_major_layout_and_given_nout(gpu_ctx):
     n, t, nleaf = 777, 33, 5
     leaf, oob = make_forest(5, n, t, nleaf, p_invalid=0.05)
@@ -166,7 +196,10 @@ def test_split_rows_with_wrapped_8bit_counts(gpu_ctx):
     N - S are counted as two items.  T = 700 turns on the byte-sum check, and
     samples 0..299 share sample 0's leaf in every tree: their pairs reach
     counts near 325, which wrap 8 bits, inside both items of split rows.  Rows
-    on both sides of the split boundary and of the group are compared."""
+    on both sides of the split boundary and of the group are compared, in
+    every integer format: U8 with the min-0/max-1 rule, raw U16 counts, I8
+    with a zero point, and U8 with codes that depend on the column (every
+    nonzero count takes the exact per-column path)."""
     import torch
 
     n, t, nleaf = 90_000, 700, 400
@@ -178,17 +211,20 @@ def test_split_rows_with_wrapped_8bit_counts(gpu_ctx):
     # S = 81,472 columns per item on gfx950 (two workgroups' LDS per CU, dummy
     # words shared by the waves: T = 700 has at most 48 counting steps per wave)
     split = n - 81_472
-    for fmt in (O.FMT_U8, O.FMT_U16):
+    cases = [(O.FMT_U8, 1 / 255.0, 0.0), (O.FMT_U16, 1.0, 0.0), (O.FMT_I8, 1 / 2000.0, -100.0),
+             (O.FMT_U8, 1 / 4000.0, 3.0)]
+    for fmt, scale, zp in cases:
+        scale, zp = np.float32(scale), np.float32(zp)
         out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
-        gpu_ctx.upper(fmt, out, 0, n, scale=np.float32(1 / 255.0))
+        gpu_ctx.upper(fmt, out, 0, n, scale=scale, zp=zp)
         torch.cuda.synchronize()
         for r0 in (0, 1, 150, 298, 299, 300, split - 2, split, 40_000, n - 10):
             r1 = min(n, r0 + 3)
-            want = idx.rows(fmt, r0, r1, np.float32(1 / 255.0), np.float32(0.0))
+            want = idx.rows(fmt, r0, r1, scale, zp)
             e0, e1 = O.tri_idx(n, r0, r0), O.tri_idx(n, r1, r1)
             esz = np.dtype(O.FMT_DTYPE[fmt]).itemsize
             got = out[e0 * esz:e1 * esz].cpu().numpy().view(O.FMT_DTYPE[fmt])
-            check_equal(got, want, f"fmt {fmt} rows {r0}:{r1}")
+            check_equal(got, want, f"fmt {fmt} scale {scale} zp {zp} rows {r0}:{r1}")
         del out
     assert gpu_ctx.upper_recounts() > 0
     idx.close()
@@ -332,7 +368,10 @@ def test_c3_shape_sampled_rows(gpu_ctx):
 def test_whole_triangle_invariants(gpu_ctx, n, t, nleaf):
     """Raw U16 counts over the whole triangle (5e9 entries at N = 100k):
     their sum equals the closed form from the leaf histograms (pair_total),
-    every count lies in [0, T], and the diagonal is 0."""
+    every sample's sum over its row and column equals the sizes of its
+    opposite buckets summed over the trees (row_pair_counts; a count in the
+    wrong column of the right row keeps the total but not these), every
+    count lies in [0, T], and the diagonal is 0."""
     import torch
 
     g = torch.Generator(device="cuda:0")
@@ -345,9 +384,14 @@ def test_whole_triangle_invariants(gpu_ctx, n, t, nleaf):
     gpu_ctx.upper(O.FMT_U16, out, 0, n)
     torch.cuda.synchronize()
     u = out.view(torch.int16)  # counts <= 500 read the same as int16
+    leaf_np, oob_np = leaf.cpu().numpy(), oob.to(torch.uint8).cpu().numpy()
     got_total = int(u.sum(dtype=torch.int64).item())
-    want_total = pair_total(leaf.cpu().numpy(), oob.to(torch.uint8).cpu().numpy(), nleaf)
+    want_total = pair_total(leaf_np, oob_np, nleaf)
     assert got_total == want_total, (got_total, want_total)
+    got_rows = symmetric_row_sums(u, n).cpu().numpy()
+    want_rows = row_pair_counts(leaf_np, oob_np, nleaf)
+    bad = np.nonzero(got_rows != want_rows)[0]
+    assert bad.size == 0, (bad.size, bad[:5], got_rows[bad[:5]], want_rows[bad[:5]])
     assert int(u.max().item()) <= t and int(u.min().item()) >= 0
     diag = torch.tensor([O.tri_idx(n, i, i) for i in range(0, n, 613)], device="cuda:0")
     assert bool((u[diag] == 0).all())

@@ -742,3 +742,45 @@ def test_pair_total_closed_form_matches_the_oracle_triangle():
     oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
     tri = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
     assert int(tri.astype(np.int64).sum()) == pair_total(leaf, oob, nleaf)
+
+
+def symmetric_row_sums_np(tri, n):
+    """Per sample, the sum of U over its row and column of the packed upper
+    triangle (the diagonal, 0 in U16, taken once from each side)."""
+    out = np.zeros(n, dtype=np.int64)
+    e = 0
+    for i in range(n):
+        row = tri[e:e + n - i].astype(np.int64)
+        out[i] += row.sum()
+        out[i:] += row
+        e += n - i
+    return out
+
+
+def test_row_pair_counts_closed_form_matches_the_oracle_triangle():
+    """The per-sample closed form behind the full-size row-sum check (sum of
+    U_ij over j != i = sum over trees of the size of i's opposite bucket)
+    against the oracle's U16 triangle, invalid labels included; a count
+    moved to another column of the same row keeps the total but breaks the
+    row sums, so the check catches what pair_total cannot."""
+    from closed_forms import row_pair_counts
+
+    rng = np.random.default_rng(92)
+    n, t, nleaf = 300, 40, 7
+    leaf = rng.integers(-1, nleaf + 1, size=(t, n)).astype(np.int32)
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    tri = O.upper_rows(leaf, oob, nleaf, O.FMT_U16)
+    want = row_pair_counts(leaf, oob, nleaf)
+    assert np.array_equal(symmetric_row_sums_np(tri, n), want)
+    # the torch version the full-size GPU tests use, run here on the CPU
+    import torch
+    from tri_sums import symmetric_row_sums
+
+    got = symmetric_row_sums(torch.from_numpy(tri.view(np.int16)), n, block=37).numpy()
+    assert np.array_equal(got, want)
+    # a planted mistake: one count moved within row 0 (columns 5 -> 9)
+    bad = tri.astype(np.int64).copy()
+    bad[5] -= 1
+    bad[9] += 1
+    assert int(bad.sum()) == int(tri.astype(np.int64).sum())
+    assert not np.array_equal(symmetric_row_sums_np(bad, n), want)

@@ -64,6 +64,34 @@ def test_noalloc_matches_set_forest_and_upper_on_two_calls(gpu_ctx):
         assert (got[-64:] == 0x5A).all(), "write past the output"
 
 
+def test_noalloc_with_a_caller_nout(gpu_ctx):
+    """A device nout (with zeros, so 1/nout falls back to 1) given to the
+    allocation-free call: the workspace then holds no OOB-count accumulator
+    and 1/nout comes from the caller's counts.  Bit-exact against
+    rfxp_set_forest(nout) + rfxp_upper, in fp32 (where 1/nout shows in every
+    entry) and uint8 codes of an unaligned row band."""
+    import torch
+
+    n, t, nleaf = 1500, 300, 12
+    leaf, oob = forest(31, n, t, nleaf)
+    lt, ow = device(leaf, oob)
+    nout = np.random.default_rng(32).integers(0, 5, size=n).astype(np.int32)
+    nout[::7] = 0
+    nt = torch.from_numpy(nout).to("cuda:0")
+    assert R.upper_noalloc_workspace(n, t, nleaf, nout_given=True) <= R.NOALLOC_MAX_BYTES
+    for fmt, r0, r1, scale in ((R.FMT_F32, 0, n, 1.0), (R.FMT_U8, 37, 1211, 1.0 / 4000.0)):
+        nb = R.upper_nbytes(fmt, n, r0, r1)
+        got = torch.full((nb + 64,), 0x5A, dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper_noalloc(lt, ow, n, t, nleaf, fmt, got[:nb], r0, r1, scale=scale, nout=nt)
+        gpu_ctx.set_forest(lt, ow, n, t, nleaf, nout=nt)
+        want = torch.full((nb + 64,), 0x5A, dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper(fmt, want[:nb], r0, r1, scale=scale)
+        torch.cuda.synchronize()
+        g, w = got.cpu().numpy(), want.cpu().numpy()
+        assert np.array_equal(g, w), f"fmt {fmt}: {int((g != w).sum())} bytes differ"
+        assert (g[-64:] == 0x5A).all(), "write past the output"
+
+
 def test_noalloc_leaves_the_context_forest_alone(gpu_ctx):
     import torch
 
