@@ -430,6 +430,17 @@ def run_triangle(args, name):
         "wall_s": wall,
     }
     ctx.set_timing(False)
+    if fmt == "u8":
+        # the reference quantizer rule on this forest's data, outside the
+        # timed region: min and max of the fp32 triangle (rfxp_upper_minmax)
+        # and the scale / zero point they give, against the ones used above
+        try:
+            mn, mx = ctx.upper_minmax()
+            dscale, dzp = R.quant_scale(mn, mx)
+            rec["quantizer"] = {"min": mn, "max": mx, "scale": dscale, "zp": dzp,
+                                "matches_the_scale_used": dscale == scale and dzp == zp}
+        except Exception as e:  # reported in the record, never fatal to the line
+            rec["quantizer"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu_baseline:
         leaf_np = leaf.cpu().numpy()
         oob_np = oob.to(torch.uint8).cpu().numpy()

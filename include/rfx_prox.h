@@ -124,6 +124,24 @@ int rfxp_upper_recounts(rfxp_ctx* ctx, int64_t* count);
 /* The per-sample nout actually used (device int32[N] copy into `nout`). */
 int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout);
 
+/* Minimum and maximum of the fp32 entries (float)P of rows
+ * [row_begin, row_end) of the triangle (diagonal 1 included), as rfxp_upper
+ * with RFXP_FMT_F32 writes them, into the host array minmax[2].  This is the
+ * data the reference's quantizer rule reads: compute_minmax_kernel and
+ * reduce_minmax_final_kernel over static_cast<float> of the proximity values
+ * (cuda/rf_quantization_kernels.cu:24-86); rfxp_quant_scale then gives the
+ * scale and zero point of compute_scale_from_minmax_kernel (:88-101), for
+ * the I8 / U8 formats of rfxp_upper.  The rows are evaluated in bands of at
+ * most 2^26 entries into a context workspace (256 MB), never all at once.
+ * Needs row_begin < row_end; synchronises the context stream. */
+int rfxp_upper_minmax(rfxp_ctx* ctx, int64_t row_begin, int64_t row_end, float* minmax);
+
+/* The reference's affine quantizer parameters from a min and max
+ * (cuda/rf_quantization_kernels.cu:88-101, float arithmetic):
+ * scale = (max - min) / 255, 1/127 when that is below 1e-10; zp = -min/scale.
+ * Host only. */
+void rfxp_quant_scale(float min_val, float max_val, float* scale, float* zero_point);
+
 /* Work decomposition of rfxp_upper, host-only (no device needed): row i of
  * the band [row_begin, row_end) is cut into segments of S columns starting
  * at i, i + S, ...; one workgroup slot per segment, rows taken in groups of

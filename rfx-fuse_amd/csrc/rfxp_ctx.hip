@@ -153,6 +153,8 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->rinv.release();
     ctx->rrange.release();
     ctx->flags.release();
+    ctx->mm_ws.release();
+    ctx->mm_part.release();
     ctx->ref_off.release();
     ctx->ref_mem.release();
     ctx->lr_start.release();

@@ -95,6 +95,8 @@ struct rfxp_ctx {
     DevBuf<double> rinv;       // N: nout > 0 ? 1/nout : 1
     DevBuf<unsigned long long> rrange;  // [min, max] of rinv as IEEE bits
     DevBuf<int32_t> flags;     // device status words
+    DevBuf<float> mm_ws;       // rfxp_upper_minmax: one band of fp32 entries
+    DevBuf<float> mm_part;     // rfxp_upper_minmax: block minima / maxima, then the running pair
     ForestBufs fb;             // the forest index of rfxp_set_forest (pointers into the buffers above)
     const int32_t* fo_leaf = nullptr;   // the caller's leaf matrix and OOB words given to rfxp_set_forest
     int64_t fo_si = 0, fo_st = 0;       // (rfxp_lowrank_oob_pv reads them)

@@ -1041,6 +1041,96 @@ extern "C" int rfxp_upper_recounts(rfxp_ctx* ctx, int64_t* count) {
     return RFXP_OK;
 }
 
+namespace rfxp {
+
+// Min and max of x[0, n): one (min, max) pair per block from a grid-stride
+// loop, into part[2 * blockIdx.x], part[2 * blockIdx.x + 1].
+__global__ __launch_bounds__(256) void k_minmax_f32(const float* x, int64_t n, float* part) {
+    __shared__ float smn[256], smx[256];
+    float mn = 3.0e38f, mx = -3.0e38f;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float v = x[i];
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    smn[threadIdx.x] = mn;
+    smx[threadIdx.x] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < (unsigned)s) {
+            smn[threadIdx.x] = fminf(smn[threadIdx.x], smn[threadIdx.x + s]);
+            smx[threadIdx.x] = fmaxf(smx[threadIdx.x], smx[threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part[2 * blockIdx.x] = smn[0];
+        part[2 * blockIdx.x + 1] = smx[0];
+    }
+}
+
+// Folds the nblk block pairs into run[0..1], starting from run's previous
+// contents unless first.
+__global__ void k_minmax_fold(const float* part, int32_t nblk, float* run, int32_t first) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float mn = first ? 3.0e38f : run[0], mx = first ? -3.0e38f : run[1];
+    for (int32_t b = 0; b < nblk; ++b) {
+        mn = fminf(mn, part[2 * b]);
+        mx = fmaxf(mx, part[2 * b + 1]);
+    }
+    run[0] = mn;
+    run[1] = mx;
+}
+
+// Entries per band of rfxp_upper_minmax.
+constexpr int64_t MINMAX_BAND = (int64_t)1 << 26;
+constexpr int32_t MINMAX_BLOCKS = 1024;
+
+}  // namespace rfxp
+
+extern "C" int rfxp_upper_minmax(rfxp_ctx* ctx, int64_t r0, int64_t r1, float* minmax) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_upper_minmax: no forest set");
+    const int64_t N = ctx->N;
+    if (!minmax || r0 < 0 || r1 > N || r0 >= r1)
+        return set_error(ctx, RFXP_ERR_INVALID, "rfxp_upper_minmax: need 0 <= row_begin < row_end <= N, minmax");
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    // a band holds whole rows: at least one row (N - r0 <= N entries)
+    const int64_t band = std::max<int64_t>(MINMAX_BAND, N);
+    RFXP_HIP(ctx, ctx->mm_ws.ensure((size_t)band));
+    RFXP_HIP(ctx, ctx->mm_part.ensure((size_t)2 * MINMAX_BLOCKS + 2));
+    float* run = ctx->mm_part.p + 2 * MINMAX_BLOCKS;
+    bool first = true;
+    for (int64_t a = r0; a < r1;) {
+        // rows [a, b): as many whole rows as the band holds (at least one)
+        int64_t b = a + 1;
+        while (b < r1 && tri_idx(N, b + 1, b + 1) - tri_idx(N, a, a) <= band) ++b;
+        const int64_t count = tri_idx(N, b, b) - tri_idx(N, a, a);
+        if (int rc = upper_launch(ctx, ctx->fb, N, ctx->T, F32, 1.0f, 0.0f, a, b, ctx->mm_ws.p)) return rc;
+        const int32_t nblk = (int32_t)std::min<int64_t>(MINMAX_BLOCKS, (count + 255) / 256);
+        hipLaunchKernelGGL(k_minmax_f32, dim3((unsigned)nblk), dim3(256), 0, ctx->stream, ctx->mm_ws.p, count,
+                           ctx->mm_part.p);
+        hipLaunchKernelGGL(k_minmax_fold, dim3(1), dim3(64), 0, ctx->stream, ctx->mm_part.p, nblk, run,
+                           (int32_t)first);
+        if (int rc = check_launch(ctx, "k_minmax launch")) return rc;
+        first = false;
+        a = b;
+    }
+    float host[2];
+    RFXP_HIP(ctx, hipMemcpyAsync(host, run, sizeof(host), hipMemcpyDeviceToHost, ctx->stream));
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    minmax[0] = host[0];
+    minmax[1] = host[1];
+    return RFXP_OK;
+}
+
+extern "C" void rfxp_quant_scale(float min_val, float max_val, float* scale, float* zero_point) {
+    float s = (max_val - min_val) / 255.0f;
+    if (s < 1e-10f) s = 1.0f / 127.0f;
+    if (scale) *scale = s;
+    if (zero_point) *zero_point = -min_val / s;
+}
+
 extern "C" int rfxp_get_nout(rfxp_ctx* ctx, int32_t* nout) {
     if (!ctx || !nout) return RFXP_ERR_INVALID;
     if (!ctx->forest_ready) return set_error(ctx, RFXP_ERR_STATE, "rfxp_get_nout: no forest set");

@@ -69,6 +69,9 @@ def load(path: str = LIB_PATH):
     L.rfxp_upper_nbytes.argtypes = [C.c_int, i64, i64, i64]
     L.rfxp_upper_nbytes.restype = i64
     L.rfxp_get_nout.argtypes = [vp, vp]
+    L.rfxp_upper_minmax.argtypes = [vp, i64, i64, vp]
+    L.rfxp_quant_scale.argtypes = [C.c_float, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]
+    L.rfxp_quant_scale.restype = None
     L.rfxp_upper_recounts.argtypes = [vp, C.POINTER(i64)]
     L.rfxp_upper_work_item.argtypes = [i64, i32, i64, i64, i64, C.POINTER(i64), C.POINTER(i64)]
     L.rfxp_upper_work_item.restype = i64
@@ -159,6 +162,14 @@ def upper_noalloc_workspace(n: int, t: int, nleaf: int, nout_given: bool = False
 
 
 NOALLOC_MAX_BYTES = 64 << 20
+
+
+def quant_scale(min_val: float, max_val: float):
+    """(scale, zero_point) of the reference's affine quantizer rule for a
+    min and max (rfxp_quant_scale, host only)."""
+    sc, zp = C.c_float(), C.c_float()
+    load().rfxp_quant_scale(min_val, max_val, C.byref(sc), C.byref(zp))
+    return sc.value, zp.value
 
 
 def outlier_normalize(raw, classes=None):
@@ -537,6 +548,16 @@ class Context:
                                                oob_words.shape[1], n, t, nleaf, nptr, fmt, scale, zp, r0, r1,
                                                out.data_ptr()))
         return out
+
+    def upper_minmax(self, r0: int = 0, r1: int | None = None):
+        """(min, max) of the fp32 entries of rows [r0, r1) of the triangle
+        (rfxp_upper_minmax): the data of the reference's quantizer rule."""
+        import numpy as np
+
+        r1 = self.n if r1 is None else r1
+        mm = np.zeros(2, dtype=np.float32)
+        self._check(self._L.rfxp_upper_minmax(self.h, r0, r1, mm.ctypes.data))
+        return float(mm[0]), float(mm[1])
 
     def upper_recounts(self) -> int:
         """Row segments recounted with 16-bit counters since set_forest."""

@@ -65,6 +65,9 @@ class _FakeContext:
     def upper_recounts(self):
         return 0
 
+    def upper_minmax(self, r0=0, r1=None):
+        return 0.0, 1.0
+
     def set_reference(self, leaf, n, t, nleaf, layout="tree"):
         self._maybe_fail("set_reference")
         self.n = n
@@ -136,6 +139,8 @@ def test_default_run_prints_one_line_with_sub_records(cpu_bench):
     for key in ("frac", "frac_compulsory_kernel", "frac_compulsory_step"):
         assert roof[key] > 0
     assert rec["cpu_baseline"]["kind"] == "port" and rec["cpu_baseline"]["value"] > 0
+    # the quantizer rule on the data: min 0 / max 1 give the parameters used
+    assert rec["quantizer"]["matches_the_scale_used"] is True
     subs = rec["sub_records"]
     assert set(subs) == {"c2", "c5", "c4"}
     for name, sub in subs.items():

@@ -288,3 +288,23 @@ def test_pack_plan_rejects_bad_arguments():
     for args in ((0, 5, 5), (10, 0, 5), (10, 5, 0), (10, 5, 5, 0)):
         with pytest.raises(ValueError):
             R.pack_plan(*args)
+
+
+def test_quant_scale_is_the_reference_rule():
+    """rfxp_quant_scale is compute_scale_from_minmax_kernel's float rule
+    (cuda/rf_quantization_kernels.cu:88-101): scale = (max - min)/255 in
+    float, 1/127 below 1e-10, zp = -min/scale.  Checked against numpy float32
+    arithmetic; for min 0, max 1 it gives the C3 parameters fl(1/255), -0."""
+    import numpy as np
+
+    f = np.float32
+    for mn, mx in ((0.0, 1.0), (0.0125, 1.0), (0.0, 7.5), (-0.25, 0.5), (0.3, 0.3), (1e-12, 2e-12)):
+        sc, zp = R.quant_scale(mn, mx)
+        want_sc = (f(mx) - f(mn)) / f(255.0)
+        if want_sc < f(1e-10):
+            want_sc = f(1.0) / f(127.0)
+        want_zp = -f(mn) / want_sc
+        assert f(sc) == want_sc and f(zp) == want_zp, (mn, mx, sc, zp)
+    sc, zp = R.quant_scale(0.0, 1.0)
+    assert f(sc) == f(1.0) / f(255.0) and zp == 0.0 and np.signbit(f(zp))
+    assert R.quant_scale(0.3, 0.3)[0] == float(f(1.0) / f(127.0))

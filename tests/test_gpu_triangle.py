@@ -149,6 +149,48 @@ def test_thousand_trees_check_with_per_thread_dummy_words(gpu_ctx, planted):
     del keep
 
 
+@pytest.mark.parametrize("case", ["every_pair_co_occurs", "entries_above_one", "zeros_and_diagonal"])
+def test_data_derived_quantizer_scale(gpu_ctx, case):
+    """rfxp_upper_minmax gives the min and max of the fp32 triangle, the
+    data the reference's quantizer rule reads (compute_minmax over (float)P),
+    for the whole triangle and for a row band; rfxp_quant_scale turns them
+    into scale and zero point, under which the U8 and I8 codes equal the
+    oracle's.  Cases: one leaf and T = 300, where every pair co-occurs
+    (min > 0); caller nout of 0..2, which puts entries above 1 (max > 1);
+    a sparse forest, where the rule gives the min 0 / max 1 parameters."""
+    nout = None
+    if case == "every_pair_co_occurs":
+        n, t, nleaf = 400, 300, 1
+        leaf, oob = make_forest(61, n, t, nleaf, p_oob=0.5)
+    elif case == "entries_above_one":
+        n, t, nleaf = 600, 40, 2
+        leaf, oob = make_forest(62, n, t, nleaf)
+        nout = np.random.default_rng(63).integers(0, 3, size=n).astype(np.int32)
+    else:
+        n, t, nleaf = 5000, 300, 2048
+        leaf, oob = make_forest(64, n, t, nleaf)
+    keep = upload(gpu_ctx, leaf, oob, nleaf, nout=nout)
+    tri = O.upper_rows(leaf, oob, nleaf, O.FMT_F32, nout_arr=nout)
+    mn, mx = gpu_ctx.upper_minmax()
+    assert (mn, mx) == (float(tri.min()), float(tri.max()))
+    r0 = n - 57
+    band = tri[O.tri_idx(n, r0, r0):]
+    assert gpu_ctx.upper_minmax(r0, n) == (float(band.min()), float(band.max()))
+    if case == "every_pair_co_occurs":
+        assert mn > 0
+    elif case == "entries_above_one":
+        assert mx > 1
+    else:
+        assert (mn, mx) == (0.0, 1.0)
+    scale, zp = R.quant_scale(mn, mx)
+    for fmt in (O.FMT_U8, O.FMT_I8):
+        got, guard = gpu_rows(gpu_ctx, fmt, 0, n, scale=np.float32(scale), zp=np.float32(zp))
+        want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(scale), zp=np.float32(zp), nout_arr=nout)
+        check_equal(got, want, f"{case} fmt {fmt} derived scale {scale} zp {zp}")
+        assert (guard == 0xA5).all()
+    del keep
+
+
 def test_sample_major_layout_and_given_nout(gpu_ctx):
     n, t, nleaf = 777, 33, 5
     leaf, oob = make_forest(5, n, t, nleaf, p_invalid=0.05)
