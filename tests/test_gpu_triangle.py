@@ -473,6 +473,45 @@ def test_c2_shape_full_triangle_f32(gpu_ctx):
     del keep
 
 
+def test_c2_data_grown_regression_forest(gpu_ctx):
+    """BASELINE config 2's data (N = 20,000, p = 50, y = sin(x0) + x1 x2 +
+    N(0, 0.1)) through a forest grown on it (sklearn CART, mtry 17, leaves of
+    at least 5 samples, seeded bootstrap; 100 of the config's 500 trees to
+    keep the growing short): ~2,000 leaves per tree of skewed sizes, labels
+    that are node ids (so most label values are internal nodes, never used),
+    OOB bits from each tree's bootstrap sample.  The whole fp32 triangle and
+    the raw counts equal the oracle's bit for bit."""
+    import torch
+
+    ens = pytest.importorskip("sklearn.ensemble")
+    rng = np.random.default_rng(20261201 + 2)
+    n, p, t = 20_000, 50, 100
+    X = rng.standard_normal((n, p)).astype(np.float32)
+    y = np.sin(X[:, 0]) + X[:, 1] * X[:, 2] + rng.normal(0.0, 0.1, n)
+    rf = ens.RandomForestRegressor(n_estimators=t, max_features=17, min_samples_leaf=5, bootstrap=True,
+                                   n_jobs=8, random_state=5).fit(X, y)
+    leaf = np.ascontiguousarray(rf.apply(X).T.astype(np.int32))    # (T, N) node ids
+    oob = np.ones((t, n), dtype=np.uint8)
+    for k, idx in enumerate(rf.estimators_samples_):
+        oob[k, idx] = 0
+    nleaf = int(leaf.max()) + 1
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    ridx = O.RowIndex(leaf, oob, nleaf)
+    for fmt in (O.FMT_F32, O.FMT_U16):
+        out = torch.empty(R.upper_nbytes(fmt, n), dtype=torch.uint8, device="cuda:0")
+        gpu_ctx.upper(fmt, out, 0, n)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(O.FMT_DTYPE[fmt])
+        want = ridx.rows(fmt, 0, n)
+        if fmt == O.FMT_F32:
+            check_equal(got.view(np.uint32), want.view(np.uint32), "grown C2 forest f32 triangle")
+        else:
+            check_equal(got, want, "grown C2 forest u16 triangle")
+        del out
+    ridx.close()
+    del keep
+
+
 @pytest.mark.parametrize("case", ["parts", "whole_tree"])
 def test_buckets_beyond_16383_members(gpu_ctx, case):
     """Buckets of 16,383 or more members take the read-to-the-mark path of
