@@ -1,0 +1,104 @@
+// Driver of the CPU emulation build (tests/emu): runs the library's C ABI
+// (include/rfx_prox.h) with its kernels executed by the emulator, on inputs
+// from a file, and writes the results for tests/test_emu_cpu.py to compare
+// with the oracle.
+//
+// usage: emu_driver in.bin out.bin
+// in:  int32 mode (1 rfxp_upper, 2 rfxp_upper_minmax, 3 rfxp_upper_noalloc),
+//      int64 N, int32 T, int32 nleaf, int32 fmt, float scale, float zp,
+//      int64 r0, int64 r1, int32 has_nout, int32 layout (0 tree-major, 1
+//      sample-major), then the int32 leaf matrix, the T x ceil(N/32) OOB
+//      words and, with has_nout, N int32 nout
+// out: int32 status, then for modes 1 and 3: int64 nbytes, the bytes, int32
+//      1 when the 64 guard bytes after the output are untouched, int64 the
+//      recount counter (mode 1); for mode 2: float min, float max
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "rfx_prox.h"
+
+template <class T>
+static void rd(FILE* f, T* p, size_t n) {
+    if (n && fread(p, sizeof(T), n, f) != n) {
+        fprintf(stderr, "short read\n");
+        exit(2);
+    }
+}
+
+int main(int argc, char** argv) {
+    if (argc != 3) return 2;
+    FILE* f = fopen(argv[1], "rb");
+    if (!f) return 2;
+    int32_t mode, T, nleaf, fmt, has_nout, layout;
+    int64_t N, r0, r1;
+    float scale, zp;
+    rd(f, &mode, 1);
+    rd(f, &N, 1);
+    rd(f, &T, 1);
+    rd(f, &nleaf, 1);
+    rd(f, &fmt, 1);
+    rd(f, &scale, 1);
+    rd(f, &zp, 1);
+    rd(f, &r0, 1);
+    rd(f, &r1, 1);
+    rd(f, &has_nout, 1);
+    rd(f, &layout, 1);
+    const int64_t ld = (N + 31) / 32;
+    std::vector<int32_t> leaf((size_t)N * T);
+    std::vector<uint32_t> oob((size_t)T * ld);
+    std::vector<int32_t> nout(has_nout ? (size_t)N : 0);
+    rd(f, leaf.data(), leaf.size());
+    rd(f, oob.data(), oob.size());
+    rd(f, nout.data(), nout.size());
+    fclose(f);
+    const int64_t si = layout ? T : 1, st = layout ? 1 : N;
+    FILE* o = fopen(argv[2], "wb");
+    rfxp_ctx* ctx = nullptr;
+    int rc = rfxp_ctx_create(0, &ctx);
+    auto fail = [&](int code) {
+        char msg[512] = {0};
+        if (ctx) rfxp_last_error(ctx, msg, sizeof msg);
+        fprintf(stderr, "status %d: %s\n", code, msg);
+        fwrite(&code, 4, 1, o);
+        fclose(o);
+        return 0;
+    };
+    if (rc) return fail(rc);
+    const int32_t* np = has_nout ? nout.data() : nullptr;
+    if (mode == 1 || mode == 3) {
+        const int64_t nb = rfxp_upper_nbytes(fmt, N, r0, r1);
+        std::vector<unsigned char> out((size_t)nb + 64, 0xA5);
+        if (mode == 1) {
+            if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
+            if ((rc = rfxp_upper(ctx, fmt, scale, zp, r0, r1, out.data()))) return fail(rc);
+        } else {
+            if ((rc = rfxp_upper_noalloc(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np, fmt, scale, zp, r0,
+                                         r1, out.data())))
+                return fail(rc);
+        }
+        rfxp_sync(ctx);
+        int32_t ok = 1;
+        for (int k = 0; k < 64; ++k) ok &= out[(size_t)nb + k] == 0xA5;
+        int64_t rec = -1;
+        if (mode == 1) rfxp_upper_recounts(ctx, &rec);
+        fwrite(&rc, 4, 1, o);
+        fwrite(&nb, 8, 1, o);
+        fwrite(out.data(), 1, (size_t)nb, o);
+        fwrite(&ok, 4, 1, o);
+        fwrite(&rec, 8, 1, o);
+    } else if (mode == 2) {
+        if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
+        float mm[2] = {0, 0};
+        if ((rc = rfxp_upper_minmax(ctx, r0, r1, mm))) return fail(rc);
+        fwrite(&rc, 4, 1, o);
+        fwrite(mm, 4, 2, o);
+    } else {
+        return fail(-1);
+    }
+    fclose(o);
+    rfxp_ctx_destroy(ctx);
+    return 0;
+}

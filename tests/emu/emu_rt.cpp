@@ -1,0 +1,411 @@
+// CPU emulation of the HIP execution model for the library's own kernels
+// (test infrastructure, see include/hip/hip_runtime.h here).
+//
+// A launch runs its workgroups one after the other.  Each GPU thread of a
+// workgroup is a coroutine with its own stack; the scheduler runs every
+// runnable thread until it blocks:
+//   - at __syncthreads (a workgroup barrier: released when every thread
+//     that has not returned is waiting there);
+//   - at a wave-wide builtin (released when every live lane of its 64-lane
+//     wave waits at the same builtin; the results are computed from all the
+//     lanes' inputs at once, as the SIMD does).
+// A wave whose live lanes wait at different builtins, or at a builtin and a
+// barrier, is a divergence the kernel language does not define: the
+// emulator aborts with the call site.  Dynamic LDS is a malloc'd block of
+// exactly the launch's size, so an AddressSanitizer build reports LDS
+// accesses past it; device memory is malloc'd too.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <sys/mman.h>
+#include <time.h>
+
+#include <chrono>
+#include <mutex>
+#include <vector>
+
+#if defined(__has_feature)
+#if __has_feature(address_sanitizer)
+#define EMU_ASAN 1
+#endif
+#endif
+#ifdef EMU_ASAN
+extern "C" void __sanitizer_start_switch_fiber(void** fake_stack_save, const void* bottom, size_t size);
+extern "C" void __sanitizer_finish_switch_fiber(void* fake_stack_save, const void** bottom_old, size_t* size_old);
+#endif
+
+extern "C" void emu_swap(void** save_sp, void* load_sp);
+
+namespace emu {
+
+namespace {
+
+constexpr size_t STACK_BYTES = 512 * 1024;
+constexpr int MAX_THREADS = 1024;
+
+enum State { RUN, BAR, WOP, DONE };
+
+struct Thread {
+    ThreadView v;
+    State st = RUN;
+    void* sp = nullptr;
+    char* stack = nullptr;
+    int op = 0;
+    uint64_t val = 0;
+    int64_t arg = 0, width = 64;
+    uint64_t res = 0;
+    void* fake = nullptr;
+};
+
+struct Launch {
+    Body body = nullptr;
+    void* closure = nullptr;
+    char* lds = nullptr;
+    size_t lds_bytes = 0;
+    int nthreads = 0;
+};
+
+std::vector<char*> g_stacks;
+Thread g_th[MAX_THREADS];
+Thread* g_cur = nullptr;
+Launch g_launch;
+void* g_sched_sp = nullptr;
+void* g_sched_fake = nullptr;
+const void* g_sched_bottom = nullptr;
+size_t g_sched_size = 0;
+hipError_t g_last = hipSuccess;
+std::mutex g_mu;  // one launch at a time
+
+[[noreturn]] void die(const char* what, const Thread* t) {
+    if (t)
+        fprintf(stderr, "[emu] %s (thread %u,%u,%u of block %u,%u,%u, lane %d, op %d)\n", what, t->v.tid.x,
+                t->v.tid.y, t->v.tid.z, t->v.bid.x, t->v.bid.y, t->v.bid.z, t->v.lane, t->op);
+    else
+        fprintf(stderr, "[emu] %s\n", what);
+    fflush(stderr);
+    abort();
+}
+
+char* stack_of(int i) {
+    while ((int)g_stacks.size() <= i) {
+        void* p = mmap(nullptr, STACK_BYTES, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+        if (p == MAP_FAILED) die("cannot map a coroutine stack", nullptr);
+        g_stacks.push_back((char*)p);
+    }
+    return g_stacks[i];
+}
+
+// switch from the running thread back to the scheduler
+void to_scheduler() {
+    Thread* t = g_cur;
+#ifdef EMU_ASAN
+    __sanitizer_start_switch_fiber(&t->fake, g_sched_bottom, g_sched_size);
+#endif
+    emu_swap(&t->sp, g_sched_sp);
+#ifdef EMU_ASAN
+    __sanitizer_finish_switch_fiber(t->fake, nullptr, nullptr);
+#endif
+}
+
+void entry() {
+#ifdef EMU_ASAN
+    __sanitizer_finish_switch_fiber(nullptr, &g_sched_bottom, &g_sched_size);
+#endif
+    g_launch.body(g_launch.closure);
+    g_cur->st = DONE;
+    Thread* t = g_cur;
+#ifdef EMU_ASAN
+    __sanitizer_start_switch_fiber(nullptr, g_sched_bottom, g_sched_size);
+#endif
+    emu_swap(&t->sp, g_sched_sp);
+    die("a finished coroutine was resumed", t);
+}
+
+void resume(Thread& t) {
+    g_cur = &t;
+#ifdef EMU_ASAN
+    __sanitizer_start_switch_fiber(&g_sched_fake, t.stack, STACK_BYTES);
+#endif
+    emu_swap(&g_sched_sp, t.sp);
+#ifdef EMU_ASAN
+    __sanitizer_finish_switch_fiber(g_sched_fake, &g_sched_bottom, &g_sched_size);
+#endif
+    g_cur = nullptr;
+}
+
+void init_thread(Thread& t, int i) {
+    t.stack = stack_of(i);
+    // initial frame: six callee-saved registers, then the return address
+    // emu_swap's `ret` takes (entry), then a dummy slot so that entry starts
+    // with the stack aligned as after a call
+    uint64_t* top = (uint64_t*)(t.stack + STACK_BYTES);
+    uint64_t* sp = top - 8;
+    for (int k = 0; k < 6; ++k) sp[k] = 0;
+    sp[6] = (uint64_t)(void*)&entry;
+    sp[7] = 0;
+    t.sp = sp;
+    t.st = RUN;
+    t.op = 0;
+}
+
+uint64_t dpp_src(int ctrl, int lane) {
+    if (ctrl <= 0xFF) {  // quad_perm
+        const int q = lane & ~3, k = lane & 3;
+        return (uint64_t)(q + ((ctrl >> (2 * k)) & 3));
+    }
+    if (ctrl == 0x140) return (uint64_t)((lane & ~15) + (15 - (lane & 15)));  // row_mirror
+    if (ctrl == 0x141) return (uint64_t)((lane & ~7) + (7 - (lane & 7)));     // row_half_mirror
+    die("unsupported DPP control", nullptr);
+}
+
+// resolves one wave whose live lanes all wait at the same builtin
+void resolve(int w0, int n) {
+    Thread* L = &g_th[w0];
+    int first = -1, op = 0;
+    for (int l = 0; l < n; ++l) {
+        if (L[l].st == DONE) continue;
+        if (first < 0) {
+            first = l;
+            op = L[l].op;
+        } else if (L[l].op != op) {
+            die("lanes of one wave wait at different wave builtins", &L[l]);
+        }
+    }
+    auto live = [&](int l) { return l >= 0 && l < n && L[l].st != DONE; };
+    uint64_t ballot = 0;
+    if (op == W_BALLOT)
+        for (int l = 0; l < n; ++l)
+            if (live(l) && L[l].val) ballot |= 1ull << l;
+    for (int l = 0; l < n; ++l) {
+        Thread& t = L[l];
+        if (t.st == DONE) continue;
+        const int width = (int)t.width;
+        const int base = l & ~(width - 1), off = l & (width - 1);
+        int src = l;
+        switch (op) {
+            case W_READFIRST: src = first; break;
+            case W_READLANE: src = (int)t.arg; break;
+            case W_BALLOT: break;
+            case W_SHFL: src = base + (int)(t.arg & (width - 1)); break;
+            case W_SHFL_UP: src = off >= t.arg ? l - (int)t.arg : l; break;
+            case W_SHFL_DOWN: src = off + t.arg < width ? l + (int)t.arg : l; break;
+            case W_SHFL_XOR: src = base + ((off ^ (int)t.arg) & (width - 1)); break;
+            case W_DPP: src = (int)dpp_src((int)t.arg, l); break;
+            default: die("unknown wave builtin", &t);
+        }
+        if (op == W_BALLOT) t.res = ballot;
+        else t.res = live(src) ? L[src].val : t.val;
+        t.st = RUN;
+    }
+}
+
+void run_block(dim3 bid, dim3 grid, dim3 block) {
+    const int n = g_launch.nthreads;
+    for (int i = 0; i < n; ++i) {
+        Thread& t = g_th[i];
+        init_thread(t, i);
+        t.v.tid = Idx{(uint32_t)(i % block.x), (uint32_t)((i / block.x) % block.y), (uint32_t)(i / (block.x * block.y))};
+        t.v.bid = Idx{bid.x, bid.y, bid.z};
+        t.v.bdim = Idx{block.x, block.y, block.z};
+        t.v.gdim = Idx{grid.x, grid.y, grid.z};
+        t.v.lane = i & 63;
+    }
+    for (;;) {
+        for (int i = 0; i < n; ++i)
+            if (g_th[i].st == RUN) resume(g_th[i]);
+        bool moved = false;
+        for (int w0 = 0; w0 < n; w0 += 64) {
+            const int wn = std::min(64, n - w0);
+            int live = 0, wop = 0;
+            for (int l = 0; l < wn; ++l) {
+                const State s = g_th[w0 + l].st;
+                live += s != DONE;
+                wop += s == WOP;
+            }
+            if (wop == 0) continue;
+            if (wop != live) {
+                for (int l = 0; l < wn; ++l)
+                    if (g_th[w0 + l].st == BAR) die("a wave waits at a barrier and at a wave builtin", &g_th[w0 + l]);
+                die("divergent wave", nullptr);
+            }
+            resolve(w0, wn);
+            moved = true;
+        }
+        if (moved) continue;
+        int live = 0, bar = 0;
+        for (int i = 0; i < n; ++i) {
+            live += g_th[i].st != DONE;
+            bar += g_th[i].st == BAR;
+        }
+        if (live == 0) break;
+        if (bar != live) die("deadlock: no thread can run", nullptr);
+        for (int i = 0; i < n; ++i)
+            if (g_th[i].st == BAR) g_th[i].st = RUN;
+    }
+}
+
+}  // namespace
+
+const ThreadView& view() {
+    if (!g_cur) die("thread index read outside a kernel", nullptr);
+    return g_cur->v;
+}
+
+char* lds_base() {
+    if (!g_cur) die("LDS used outside a kernel", nullptr);
+    return g_launch.lds;
+}
+
+void barrier() {
+    if (!g_cur) die("__syncthreads outside a kernel", nullptr);
+    g_cur->st = BAR;
+    to_scheduler();
+}
+
+uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width) {
+    if (!g_cur) die("wave builtin outside a kernel", nullptr);
+    Thread* t = g_cur;
+    t->op = op;
+    t->val = v;
+    t->arg = arg;
+    t->width = width;
+    t->st = WOP;
+    to_scheduler();
+    return t->res;
+}
+
+void launch_raw(const void*, dim3 grid, dim3 block, size_t lds, hipStream_t, Body body, void* closure) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const uint64_t nt = (uint64_t)block.x * block.y * block.z;
+    if (nt == 0 || nt > MAX_THREADS || grid.x == 0 || grid.y == 0 || grid.z == 0) {
+        g_last = hipErrorInvalidValue;
+        return;
+    }
+    if (lds > 160 * 1024) {
+        g_last = hipErrorInvalidValue;
+        return;
+    }
+    g_launch.body = body;
+    g_launch.closure = closure;
+    g_launch.nthreads = (int)nt;
+    g_launch.lds_bytes = lds;
+    for (uint32_t z = 0; z < grid.z; ++z)
+        for (uint32_t y = 0; y < grid.y; ++y)
+            for (uint32_t x = 0; x < grid.x; ++x) {
+                // exactly the launch's dynamic LDS (at least one byte), filled
+                // with a pattern so that reads of uncleared LDS show
+                g_launch.lds = (char*)malloc(lds ? lds : 1);
+                memset(g_launch.lds, 0xCD, lds ? lds : 1);
+                run_block(dim3(x, y, z), grid, block);
+                free(g_launch.lds);
+                g_launch.lds = nullptr;
+            }
+}
+
+}  // namespace emu
+
+// ---- runtime API -----------------------------------------------------------
+struct emu_stream {
+    int id;
+};
+struct emu_event {
+    double t;
+};
+
+static double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+hipError_t hipMalloc(void** p, size_t n) {
+    if (!p) return hipErrorInvalidValue;
+    *p = malloc(n ? n : 1);
+    if (!*p) return emu::g_last = hipErrorOutOfMemory;
+    memset(*p, 0xAB, n ? n : 1);  // device memory starts with garbage
+    return hipSuccess;
+}
+hipError_t hipFree(void* p) {
+    free(p);
+    return hipSuccess;
+}
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) {
+    if (n) memmove(d, s, n);
+    return hipSuccess;
+}
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t) { return hipMemcpy(d, s, n, k); }
+hipError_t hipMemset(void* d, int v, size_t n) {
+    if (n) memset(d, v, n);
+    return hipSuccess;
+}
+hipError_t hipMemsetAsync(void* d, int v, size_t n, hipStream_t) { return hipMemset(d, v, n); }
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) {
+    *s = new emu_stream{1};
+    return hipSuccess;
+}
+hipError_t hipStreamCreate(hipStream_t* s) { return hipStreamCreateWithFlags(s, 0); }
+hipError_t hipStreamDestroy(hipStream_t s) {
+    delete s;
+    return hipSuccess;
+}
+hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipDeviceSynchronize() { return hipSuccess; }
+hipError_t hipEventCreate(hipEvent_t* e) {
+    *e = new emu_event{0.0};
+    return hipSuccess;
+}
+hipError_t hipEventDestroy(hipEvent_t e) {
+    delete e;
+    return hipSuccess;
+}
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t) {
+    e->t = now_ms();
+    return hipSuccess;
+}
+hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
+    *ms = (float)(b->t - a->t);
+    return hipSuccess;
+}
+hipError_t hipSetDevice(int d) { return d == 0 ? hipSuccess : hipErrorInvalidDevice; }
+hipError_t hipGetDevice(int* d) {
+    *d = 0;
+    return hipSuccess;
+}
+hipError_t hipGetDeviceCount(int* n) {
+    *n = 1;
+    return hipSuccess;
+}
+hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int) {
+    switch (a) {
+        case hipDeviceAttributeMaxSharedMemoryPerBlock: *v = 160 * 1024; return hipSuccess;  // gfx950
+        case hipDeviceAttributeMultiprocessorCount: *v = 256; return hipSuccess;
+    }
+    return hipErrorInvalidValue;
+}
+hipError_t hipPointerGetAttributes(hipPointerAttribute_t* a, const void* p) {
+    // every pointer is "device" memory in the emulation
+    memset(a, 0, sizeof(*a));
+    a->type = hipMemoryTypeDevice;
+    a->devicePointer = (void*)p;
+    return hipSuccess;
+}
+hipError_t hipFuncSetAttribute(const void*, hipFuncAttribute, int v) {
+    return v <= 160 * 1024 ? hipSuccess : hipErrorInvalidValue;
+}
+hipError_t hipGetLastError() {
+    hipError_t e = emu::g_last;
+    emu::g_last = hipSuccess;
+    return e;
+}
+hipError_t hipPeekAtLastError() { return emu::g_last; }
+const char* hipGetErrorString(hipError_t e) {
+    switch (e) {
+        case hipSuccess: return "hipSuccess";
+        case hipErrorInvalidValue: return "hipErrorInvalidValue";
+        case hipErrorOutOfMemory: return "hipErrorOutOfMemory";
+        default: return "hipError (emulation)";
+    }
+}
+hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+    *p = (void*)sym;
+    return hipSuccess;
+}

@@ -1,0 +1,134 @@
+"""The library's own HIP kernels run on the CPU by the emulator in tests/emu
+(every GPU thread a coroutine, wave builtins resolved per 64-lane wave,
+device memory and each workgroup's LDS from malloc, AddressSanitizer on),
+through the C ABI, against the oracle.  These runs check index arithmetic,
+buffer sizes and bounds on every packing path and format without a GPU: an
+access outside an allocation or outside a workgroup's LDS aborts the run
+with the sanitizer's report.  They do not replace the GPU parity tests; the
+emulation knows nothing of timing, occupancy or the hardware's memory
+model."""
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+EMU = os.path.join(HERE, "emu")
+DRIVER = os.path.join(EMU, "_build", "emu_driver")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+pytestmark = pytest.mark.skipif(not os.path.exists(CLANG), reason="host clang++ of ROCm not present")
+
+
+@pytest.fixture(scope="module")
+def driver():
+    r = subprocess.run(["make", "-C", EMU, "-j8"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
+    return DRIVER
+
+
+def pack_words(oob):
+    t, n = oob.shape
+    w = (n + 31) // 32
+    pad = np.zeros((t, w * 32), np.uint64)
+    pad[:, :n] = oob
+    return (pad.reshape(t, w, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
+
+
+def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, zp=0.0, r0=0, r1=None,
+            nout=None, layout="tree"):
+    t, n = leaf.shape
+    r1 = n if r1 is None else r1
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        f.write(struct.pack("<iqiiiffqqii", mode, n, t, nleaf, fmt, np.float32(scale), np.float32(zp), r0, r1,
+                            int(nout is not None), int(layout == "sample")))
+        np.ascontiguousarray(leaf if layout == "tree" else leaf.T, dtype=np.int32).tofile(f)
+        pack_words(oob).tofile(f)
+        if nout is not None:
+            np.asarray(nout, np.int32).tofile(f)
+    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+    r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
+                       text=True, env=env)
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]
+    raw = outp.read_bytes()
+    status = struct.unpack_from("<i", raw, 0)[0]
+    assert status == 0, (status, r.stderr[-2000:])
+    if mode == 2:
+        return struct.unpack_from("<ff", raw, 4)
+    nb = struct.unpack_from("<q", raw, 4)[0]
+    out = np.frombuffer(raw, np.uint8, nb, 12)
+    guard_ok, recounts = struct.unpack_from("<iq", raw, 12 + nb)
+    assert guard_ok == 1, "write past the output"
+    return out.view(O.FMT_DTYPE[fmt]), recounts
+
+
+def forest(seed, n, t, nleaf, p_oob=0.368, p_invalid=0.0):
+    rng = np.random.default_rng(seed)
+    leaf = rng.integers(0, nleaf, size=(t, n)).astype(np.int32)
+    if p_invalid:
+        bad = rng.random((t, n)) < p_invalid
+        leaf[bad] = rng.choice(np.array([-1, nleaf, nleaf + 7], np.int32), size=int(bad.sum()))
+    oob = (rng.random((t, n)) < p_oob).astype(np.uint8)
+    return leaf, oob
+
+
+@pytest.mark.parametrize("fmt,scale,zp", [(O.FMT_U16, 1.0, 0.0), (O.FMT_F32, 1.0, 0.0), (O.FMT_F16, 1.0, 0.0),
+                                          (O.FMT_NF4, 1.0, 0.0), (O.FMT_U8, 1 / 255.0, 0.0),
+                                          (O.FMT_U8, 1 / 4000.0, 3.0), (O.FMT_I8, 1 / 2000.0, -100.0)])
+def test_whole_tree_path_every_format(driver, tmp_path, fmt, scale, zp):
+    leaf, oob = forest(3, 700, 40, 23, p_invalid=0.02)
+    got, _ = emulate(driver, tmp_path, 1, leaf, oob, 23, fmt, scale, zp)
+    want = O.upper_rows(leaf, oob, 23, fmt, scale=np.float32(scale), zp=np.float32(zp))
+    assert np.array_equal(got, want)
+
+
+def test_byte_sum_check_and_recount(driver, tmp_path):
+    # T = 700 turns on the 8-bit wrap check; samples 0..59 share a leaf in
+    # every tree, so their counts (~350) wrap and their items are recounted
+    leaf, oob = forest(4, 600, 700, 30, p_oob=0.5)
+    leaf[:, :60] = leaf[:, :1]
+    for fmt, scale in ((O.FMT_U16, 1.0), (O.FMT_U8, 1 / 255.0)):
+        got, rec = emulate(driver, tmp_path, 1, leaf, oob, 30, fmt, scale)
+        assert np.array_equal(got, O.upper_rows(leaf, oob, 30, fmt, scale=np.float32(scale)))
+        assert rec > 0
+
+
+@pytest.mark.parametrize("n,t,nleaf,bands", [
+    (40_000, 10, 400, [(0, 2), (19_999, 20_002), (39_995, 40_000)]),   # per-part path, keys in registers
+    (90_000, 4, 150, [(0, 2), (8_527, 8_530), (89_998, 90_000)]),      # rows split into two items
+    (40_000, 6, 1, [(0, 2), (25_000, 25_002)]),                        # buckets of 16,383+ members
+])
+def test_per_part_path_row_bands(driver, tmp_path, n, t, nleaf, bands):
+    leaf, oob = forest(5 + n + nleaf, n, t, nleaf, p_invalid=0.01)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for r0, r1 in bands:
+        for fmt, scale in ((O.FMT_U16, 1.0), (O.FMT_U8, 1 / 255.0)):
+            got, _ = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, r0=r0, r1=r1)
+            assert np.array_equal(got, idx.rows(fmt, r0, r1, np.float32(scale), np.float32(0.0))), (r0, fmt)
+    idx.close()
+
+
+def test_sample_major_layout_and_caller_nout(driver, tmp_path):
+    leaf, oob = forest(6, 500, 33, 5, p_invalid=0.05)
+    nout = np.random.default_rng(7).integers(0, 4, size=500).astype(np.int32)
+    got, _ = emulate(driver, tmp_path, 1, leaf, oob, 5, O.FMT_F32, nout=nout, layout="sample")
+    want = O.upper_rows(leaf, oob, 5, O.FMT_F32, nout_arr=nout)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_minmax_and_noalloc(driver, tmp_path):
+    leaf, oob = forest(8, 400, 60, 2)
+    nout = np.random.default_rng(9).integers(0, 3, size=400).astype(np.int32)
+    mn, mx = emulate(driver, tmp_path, 2, leaf, oob, 2, nout=nout)
+    tri = O.upper_rows(leaf, oob, 2, O.FMT_F32, nout_arr=nout)
+    assert (mn, mx) == (float(tri.min()), float(tri.max())) and mx > 1
+    band = tri[O.tri_idx(400, 350, 350):]
+    assert emulate(driver, tmp_path, 2, leaf, oob, 2, r0=350, r1=400, nout=nout) == (float(band.min()),
+                                                                                      float(band.max()))
+    got, _ = emulate(driver, tmp_path, 3, leaf, oob, 2, O.FMT_U8, 1 / 255.0, r0=17, r1=333)
+    assert np.array_equal(got, O.upper_rows(leaf, oob, 2, O.FMT_U8, scale=np.float32(1 / 255.0), r0=17, r1=333))
