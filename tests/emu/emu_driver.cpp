@@ -4,14 +4,16 @@
 // with the oracle.
 //
 // usage: emu_driver in.bin out.bin
-// in:  int32 mode (1 rfxp_upper, 2 rfxp_upper_minmax, 3 rfxp_upper_noalloc),
+// in:  int32 mode (1 rfxp_upper, 2 rfxp_upper_minmax, 3 rfxp_upper_noalloc,
+//      4 rfxp_lowrank_oob_pv: fmt is r, and N x r float32 V follows),
 //      int64 N, int32 T, int32 nleaf, int32 fmt, float scale, float zp,
 //      int64 r0, int64 r1, int32 has_nout, int32 layout (0 tree-major, 1
 //      sample-major), then the int32 leaf matrix, the T x ceil(N/32) OOB
 //      words and, with has_nout, N int32 nout
 // out: int32 status, then for modes 1 and 3: int64 nbytes, the bytes, int32
 //      1 when the 64 guard bytes after the output are untouched, int64 the
-//      recount counter (mode 1); for mode 2: float min, float max
+//      recount counter (mode 1); for mode 2: float min, float max; for mode
+//      4: N x r float32 Y
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -53,6 +55,8 @@ int main(int argc, char** argv) {
     rd(f, leaf.data(), leaf.size());
     rd(f, oob.data(), oob.size());
     rd(f, nout.data(), nout.size());
+    std::vector<float> V(mode == 4 ? (size_t)N * fmt : 0);
+    rd(f, V.data(), V.size());
     fclose(f);
     const int64_t si = layout ? T : 1, st = layout ? 1 : N;
     FILE* o = fopen(argv[2], "wb");
@@ -95,6 +99,13 @@ int main(int argc, char** argv) {
         if ((rc = rfxp_upper_minmax(ctx, r0, r1, mm))) return fail(rc);
         fwrite(&rc, 4, 1, o);
         fwrite(mm, 4, 2, o);
+    } else if (mode == 4) {
+        if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
+        std::vector<float> Y(V.size(), -7.0f);
+        if ((rc = rfxp_lowrank_oob_pv(ctx, V.data(), fmt, Y.data()))) return fail(rc);
+        rfxp_sync(ctx);
+        fwrite(&rc, 4, 1, o);
+        fwrite(Y.data(), 4, Y.size(), o);
     } else {
         return fail(-1);
     }

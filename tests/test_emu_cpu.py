@@ -40,7 +40,7 @@ def pack_words(oob):
 
 
 def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, zp=0.0, r0=0, r1=None,
-            nout=None, layout="tree"):
+            nout=None, layout="tree", V=None):
     t, n = leaf.shape
     r1 = n if r1 is None else r1
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
@@ -51,6 +51,8 @@ def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, 
         pack_words(oob).tofile(f)
         if nout is not None:
             np.asarray(nout, np.int32).tofile(f)
+        if V is not None:
+            np.ascontiguousarray(V, np.float32).tofile(f)
     env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
     r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
                        text=True, env=env)
@@ -60,6 +62,8 @@ def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, 
     assert status == 0, (status, r.stderr[-2000:])
     if mode == 2:
         return struct.unpack_from("<ff", raw, 4)
+    if mode == 4:
+        return np.frombuffer(raw, np.float32, n * fmt, 4).reshape(n, fmt)
     nb = struct.unpack_from("<q", raw, 4)[0]
     out = np.frombuffer(raw, np.uint8, nb, 12)
     guard_ok, recounts = struct.unpack_from("<iq", raw, 12 + nb)
@@ -132,3 +136,53 @@ def test_minmax_and_noalloc(driver, tmp_path):
                                                                                       float(band.max()))
     got, _ = emulate(driver, tmp_path, 3, leaf, oob, 2, O.FMT_U8, 1 / 255.0, r0=17, r1=333)
     assert np.array_equal(got, O.upper_rows(leaf, oob, 2, O.FMT_U8, scale=np.float32(1 / 255.0), r0=17, r1=333))
+
+
+@pytest.mark.parametrize("n,t,nleaf,plan", [
+    (600_000, 3, 16, "direct"),     # parts of 75,000 > 65,535 samples
+    (200_000, 4, 256, "sorted2"),   # 2-byte staging keeps two workgroups per CU
+    (200_000, 3, 2048, "sorted4"),  # parts of 25,000: keys read twice
+    (140_000, 3, 4096, "sorted4"),  # 8,192 buckets
+])
+def test_member_scatter_variants_row_bands(driver, tmp_path, n, t, nleaf, plan):
+    import rfxprox as R
+
+    assert R.pack_plan(n, t, nleaf) == {"direct": R.PACK_PARTS_DIRECT, "sorted2": R.PACK_PARTS_SORTED2,
+                                        "sorted4": R.PACK_PARTS_SORTED4}[plan]
+    leaf, oob = forest(11 + nleaf, n, t, nleaf, p_invalid=0.02)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for r0 in (0, n // 2 - 1, n - 3):
+        got, _ = emulate(driver, tmp_path, 1, leaf, oob, nleaf, O.FMT_U16, r0=r0, r1=r0 + 3)
+        assert np.array_equal(got, idx.rows(O.FMT_U16, r0, r0 + 3, 1.0, 0.0)), r0
+    idx.close()
+
+
+def oob_pv_reference(leaf, oob, nleaf, V):
+    """P V for the cpu_finishprox matrix P = 1/4 (D^-1 U + U D^-1) + I in
+    double, U applied per tree through bucket sums: (U X)_i is the sum of X
+    over the samples of i's leaf with the other OOB bit."""
+    t, n = leaf.shape
+    X2 = np.concatenate([V, V], axis=1).astype(np.float64)
+    nout = oob.sum(axis=0)
+    r = np.where(nout > 0, 1.0 / np.maximum(nout, 1), 1.0)
+    X2[:, V.shape[1]:] *= r[:, None]
+    Z = np.zeros_like(X2)
+    for k in range(t):
+        lv = leaf[k].astype(np.int64)
+        ok = (lv >= 0) & (lv < nleaf)
+        key = np.where(ok, 2 * lv + oob[k], 0)
+        S = np.zeros((2 * nleaf, X2.shape[1]))
+        np.add.at(S, key[ok], X2[ok])
+        Z[ok] += S[key[ok] ^ 1]
+    c = V.shape[1]
+    return 0.25 * (r[:, None] * Z[:, :c] + Z[:, c:]) + V.astype(np.float64)
+
+
+@pytest.mark.parametrize("n,t,nleaf", [(900, 20, 7),       # whole-tree path: buckets end where the next starts
+                                       (40_000, 5, 300)])  # per-part path: bucket ends from their own table
+def test_oob_normalised_pv(driver, tmp_path, n, t, nleaf):
+    leaf, oob = forest(21 + n, n, t, nleaf, p_invalid=0.01)
+    V = np.random.default_rng(22).standard_normal((n, 8)).astype(np.float32)
+    Y = emulate(driver, tmp_path, 4, leaf, oob, nleaf, fmt=8, V=V)
+    want = oob_pv_reference(leaf, oob, nleaf, V)
+    assert np.linalg.norm(Y - want) / np.linalg.norm(want) < 1e-6
