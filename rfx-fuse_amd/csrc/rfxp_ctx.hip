@@ -139,6 +139,7 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     }
     for (hipEvent_t ev : ctx->event_pool) (void)hipEventDestroy(ev);
     ctx->bkt_off.release();
+    ctx->bkt_end.release();
     ctx->bkt_mem.release();
     ctx->roffT.release();
     ctx->rlenT.release();

@@ -3,13 +3,22 @@
 // Built once per forest by rfxp_set_forest (rfxp_pack.hip) from the N x T
 // leaf matrix and OOB bitmask, then read by the triangle, top-K and
 // low-rank kernels.  Layout in HBM:
-//   mem  [T][N]   uint32  sample ids + 1 grouped, per tree, by bucket
+//   mem  [T][ms]  uint32  sample ids + 1 grouped, per tree, by bucket
 //                         b = 2*leaf + oob (buckets hold the samples of one
 //                         leaf with one OOB bit); the +1 keeps 0 free as "no
-//                         member" for masked loads
-//   off  [T][2L+1] int32  per-tree bucket offsets into mem[t]
+//                         member" for masked loads.  The tree stride ms is N
+//                         on the whole-tree packing path, where buckets lie
+//                         back to back.  The per-part path places them in
+//                         the line-fit layout (fit_start below): a bucket of
+//                         at most 32 members never straddles a 128-byte line
+//                         and a larger one ends on a line, so ms exceeds N by
+//                         the padding bound fit_stride
+//   off  [T][2L+1] int32  per-tree bucket starts in mem[t] (off[2L]: the
+//                         length used)
+//   bend [T][2L]  int32   bucket ends (per-part path; on the whole-tree path
+//                         a bucket ends where the next begins, off[b+1])
 //   roff [N][ldr] uint32  for sample i and tree t, the byte offset in mem
-//                         (4*(t*N + start)) of the run of i: the bucket of
+//                         (4*(t*ms + start)) of the run of i: the bucket of
 //                         i's leaf with the other OOB bit holds exactly the
 //                         samples that pair with i in tree t
 //                         (src/rf_proximity.cpp:179-230).  On the per-part
@@ -46,6 +55,38 @@ constexpr uint32_t REC_LONG = 16383u;  // 4*REC_LONG fits the uint16 length
 constexpr int64_t MAX_FOREST_N = 0x7ffffffe;
 constexpr int REC_PAD = 64;
 constexpr int MEM_PAD = 64;                   // readable slack after mem
+
+// Line-fit placement of a tree's buckets (per-part packing path).  A run is
+// a suffix of a bucket (from the first member of some part on) and costs one
+// 128-byte line of mem per line it touches.  Buckets placed back to back
+// straddle line boundaries at random: at N = 100,000 with 2,048 leaves a run
+// of ~12 ids touches 1.37 lines on average.  Here buckets are placed in
+// groups of FIT_GROUP, each group starting on a line.  Inside a group a
+// bucket of at most LINE_IDS members that does not fit in the rest of the
+// current line starts on the next one, and a larger bucket is placed so that
+// it ends on a line boundary (then every suffix of at most LINE_IDS ids lies
+// in its last line).  The same shape then needs 1.03 lines per run.  Each
+// non-empty bucket and each group wastes fewer than LINE_IDS ids.
+constexpr uint32_t LINE_IDS = 32;  // 128 bytes of 4-byte ids
+constexpr int FIT_GROUP = 16;
+
+// Start of a bucket of s members placed at or after pos (ids from a
+// line-aligned group start).
+__host__ __device__ inline uint32_t fit_start(uint32_t pos, uint32_t s) {
+    if (s == 0) return pos;
+    const uint32_t r = (0u - pos) & (LINE_IDS - 1u);  // ids left in the current line
+    if (s <= LINE_IDS) return s > r ? pos + r : pos;
+    return pos + ((0u - (pos + s)) & (LINE_IDS - 1u));
+}
+
+// Upper bound of a tree's mem length in the line-fit layout (a multiple of
+// LINE_IDS): N members, fewer than LINE_IDS ids of padding per non-empty
+// bucket and per group.
+__host__ __device__ inline int64_t fit_stride(int64_t N, int32_t nb) {
+    const int64_t ng = (nb + FIT_GROUP - 1) / FIT_GROUP;
+    const int64_t nonempty = N < nb ? N : nb;
+    return (N + (int64_t)(LINE_IDS - 1) * (nonempty + ng) + LINE_IDS - 1) / LINE_IDS * LINE_IDS;
+}
 
 struct LeafView {
     const int32_t* leaf;
@@ -100,7 +141,7 @@ __host__ __device__ inline int32_t view_buckets(const LeafView& v) {
 // builds buckets, records, the long-bucket table and nout / rinv / rrange;
 // reference mode (top-K, low rank) builds the buckets only.
 enum ForestBuf {
-    FB_OFF, FB_MEM, FB_ROFF, FB_RLEN, FB_ROFFT, FB_RLENT, FB_SCRATCH, FB_SCRATCH2, FB_KEY16, FB_NOUT, FB_RINV,
+    FB_OFF, FB_BEND, FB_MEM, FB_ROFF, FB_RLEN, FB_ROFFT, FB_RLENT, FB_SCRATCH, FB_SCRATCH2, FB_KEY16, FB_NOUT, FB_RINV,
     FB_RRANGE, FB_LNG, FB_LNGN, FB_FLAGS, FB_COUNT
 };
 
@@ -109,6 +150,8 @@ struct ForestSizes {
     size_t n[FB_COUNT] = {};
     int64_t ldr = 0;
     int32_t lmax = 0;
+    int64_t ms = 0;          // mem stride per tree (ids)
+    bool fit = false;        // line-fit bucket layout (per-part path, while T * ms + MEM_PAD < 2^30)
     bool part_path = false;  // per-part packing (forest mode, 2L <= 8192)
     bool seg_path = false;   // per-segment packing (reference mode, L <= 16384)
     bool lds_path = false;   // whole-tree histogram in LDS

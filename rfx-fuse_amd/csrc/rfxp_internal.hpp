@@ -40,8 +40,9 @@ struct DevBuf {
 // Every buffer of a forest index (rfxp_forest.hpp, ForestBuf), as pointers
 // into device memory: the context's own buffers, or a static workspace.
 struct ForestBufs {
-    int32_t* off = nullptr;        // [T][nb+1] bucket offsets
-    uint32_t* mem = nullptr;       // [T][N] + MEM_PAD members
+    int32_t* off = nullptr;        // [T][nb+1] bucket starts (off[nb]: the tree's used length)
+    int32_t* bend = nullptr;       // [T][nb] bucket ends (line-fit layout), or NULL: end = off[b+1]
+    uint32_t* mem = nullptr;       // [T][ms] + MEM_PAD members
     uint32_t* roff = nullptr;      // [N][ldr] + REC_PAD records (forest mode)
     uint16_t* rlen = nullptr;
     uint32_t* roffT = nullptr;     // [T][N] tree-major records (per-part packing)
@@ -57,6 +58,7 @@ struct ForestBufs {
     int32_t* flags = nullptr;      // [16] device status words
     int64_t ldr = 0;
     int32_t lmax = 0;
+    int64_t ms = 0;                // mem stride per tree (ids): N, or more for the line-fit layout
 };
 
 struct KernelTiming {
@@ -79,6 +81,7 @@ struct rfxp_ctx {
     int32_t T = 0;
     int32_t L = 0;
     DevBuf<int32_t> bkt_off;   // T x (2L+1): bucket b = 2*leaf + oob
+    DevBuf<int32_t> bkt_end;   // T x 2L: bucket ends of the line-fit layout
     DevBuf<uint32_t> bkt_mem;  // T x N (+ padding): sample ids grouped by bucket
     int64_t ldr = 0;           // record row stride: T rounded up to 16
     DevBuf<uint32_t> roff;     // N x ldr (+pad): offset of the opposite-OOB bucket of (i, t)

@@ -423,16 +423,19 @@ extern "C" int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, 
 
 namespace rfxp {
 
-// W[(t*nb + b)*c2 + c] = sum over bucket b of tree t of X[j*c2 + c]
-__global__ __launch_bounds__(256) void k_oob_w(const int32_t* off, const uint32_t* mem, int64_t N, int32_t T,
-                                               int32_t nb, const float* X, int32_t c2, float* W) {
+// W[(t*nb + b)*c2 + c] = sum over bucket b of tree t of X[j*c2 + c].  The
+// bucket's members are mem[t][off[b] .. end), end = bend[b] (line-fit
+// layout, tree stride ms) or off[b + 1].
+__global__ __launch_bounds__(256) void k_oob_w(const int32_t* off, const int32_t* bend, const uint32_t* mem,
+                                               int64_t ms, int32_t T, int32_t nb, const float* X, int32_t c2,
+                                               float* W) {
     const int64_t wb = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (wb >= (int64_t)T * nb) return;
     const int32_t t = (int32_t)(wb / nb), b = (int32_t)(wb % nb);
     const int32_t c = threadIdx.x & 63;
     const int32_t* ot = off + (int64_t)t * (nb + 1);
-    const uint32_t* m = mem + (int64_t)t * N;
-    const int32_t s = ot[b], e = ot[b + 1];
+    const uint32_t* m = mem + (int64_t)t * ms;
+    const int32_t s = ot[b], e = bend ? bend[(int64_t)t * nb + b] : ot[b + 1];
     double acc = 0.0;
     if (c < c2)
         for (int32_t k = s; k < e; ++k) acc += (double)X[(int64_t)((m[k] & MEM_ID) - 1u) * c2 + c];
@@ -491,8 +494,8 @@ extern "C" int rfxp_lowrank_oob_pv(rfxp_ctx* ctx, const float* V, int32_t r, flo
     const int64_t nw = (int64_t)T * nb;
     {
         LaunchTimer tm(ctx, "lr_oob_w");
-        hipLaunchKernelGGL(k_oob_w, dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, ctx->stream, ctx->fb.off, ctx->fb.mem,
-                           N, T, nb, ctx->lr_tmp.p, 2 * r, ctx->lr_w.p);
+        hipLaunchKernelGGL(k_oob_w, dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, ctx->stream, ctx->fb.off, ctx->fb.bend,
+                           ctx->fb.mem, ctx->fb.ms, T, nb, ctx->lr_tmp.p, 2 * r, ctx->lr_w.p);
     }
     {
         LaunchTimer tm(ctx, "lr_oob_y");

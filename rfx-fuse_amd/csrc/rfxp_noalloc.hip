@@ -66,6 +66,7 @@ static size_t noalloc_layout(const ForestSizes& z, unsigned char* base, ForestBu
     }
     fb = ForestBufs();
     fb.off = (int32_t*)at[FB_OFF];
+    fb.bend = (int32_t*)at[FB_BEND];
     fb.mem = (uint32_t*)at[FB_MEM];
     fb.roff = (uint32_t*)at[FB_ROFF];
     fb.rlen = (uint16_t*)at[FB_RLEN];
@@ -82,6 +83,7 @@ static size_t noalloc_layout(const ForestSizes& z, unsigned char* base, ForestBu
     fb.flags = (int32_t*)at[FB_FLAGS];
     fb.ldr = z.ldr;
     fb.lmax = z.lmax;
+    fb.ms = z.ms;
     return off;
 }
 

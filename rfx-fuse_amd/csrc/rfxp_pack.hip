@@ -664,33 +664,49 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) out[b] = sh[b];
 }
 
-// One workgroup per tree.  Buckets are taken 1024 at a time, one per
-// thread, so that every load and store of the part table is coalesced; a
-// workgroup-wide exclusive scan per chunk and a running carry give the
-// bucket starts, and each part's start in each bucket replaces its count.
-// It also lists the tree's buckets of REC_LONG or more members (start and
-// end byte offsets in mem, in lng[t][0 .. lngn[t]), lngn zeroed before).
-__global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, int64_t N, uint32_t* ph,
-                                                            int32_t* goff_all, uint2* lng, int32_t* lngn,
-                                                            int32_t lmax) {
+// One workgroup per tree.  Thread tid places the FIT_GROUP consecutive
+// buckets of group tid from a line-aligned group start (fit_start, the
+// line-fit layout), or back to back when fit is 0; a workgroup-wide
+// exclusive scan of the group lengths gives each group's start, so every
+// bucket gets its start (off) and end (bend) in mem[t], and each part's start
+// in each bucket replaces its count in the part table.  off[nb] is the
+// tree's used length (at most ms).  The kernel also lists the tree's buckets
+// of REC_LONG or more members (start and end byte offsets in mem, in
+// lng[t][0 .. lngn[t]), lngn zeroed before).
+__global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t T, int64_t ms, int32_t fit,
+                                                            uint32_t* ph, int32_t* goff_all, int32_t* gend_all,
+                                                            uint2* lng, int32_t* lngn, int32_t lmax) {
     __shared__ uint32_t wsum[PACK_THREADS / 64];
     const int32_t t = blockIdx.x;
     if (t >= T) return;
     uint32_t* pt = ph + (int64_t)t * PACK_PARTS * nb;
     int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    int32_t* gend = gend_all + (int64_t)t * nb;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tbase = (uint32_t)((int64_t)t * ms);  // T * ms < 2^30 (forest_sizes)
     uint32_t carry = 0;
-    for (int32_t c0 = 0; c0 < nb; c0 += PACK_THREADS) {
-        const int32_t b = c0 + tid;
-        uint32_t v[PACK_PARTS];
-        uint32_t s = 0;
+    for (int32_t c0 = 0; c0 < nb; c0 += PACK_THREADS * FIT_GROUP) {
+        const int32_t b0 = c0 + tid * FIT_GROUP;
+        // the group's bucket sizes (parts outer, so that the loads of one
+        // part's 16 counts are in flight together)
+        uint32_t sz[FIT_GROUP];
 #pragma unroll
+        for (int k = 0; k < FIT_GROUP; ++k) sz[k] = 0u;
         for (int q = 0; q < PACK_PARTS; ++q) {
-            v[q] = b < nb ? pt[(int64_t)q * nb + b] : 0u;
-            s += v[q];
+            const uint32_t* row = pt + (int64_t)q * nb;
+#pragma unroll
+            for (int k = 0; k < FIT_GROUP; ++k) sz[k] += b0 + k < nb ? row[b0 + k] : 0u;
         }
-        // inclusive scan within the wave, then across the waves
-        uint32_t incl = s;
+        uint32_t st[FIT_GROUP];
+        uint32_t pos = 0;
+#pragma unroll
+        for (int k = 0; k < FIT_GROUP; ++k) {
+            st[k] = fit ? fit_start(pos, sz[k]) : pos;
+            pos = st[k] + sz[k];
+        }
+        const uint32_t len = fit ? (pos + LINE_IDS - 1u) & ~(LINE_IDS - 1u) : pos;
+        // exclusive scan of the group lengths: within the wave, then across
+        uint32_t incl = len;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
             const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
@@ -706,18 +722,26 @@ __global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t 
             total += x;
         }
         __syncthreads();
-        uint32_t run = carry + before + incl - s;
-        if (b < nb && s >= REC_LONG) {
-            const int32_t slot = atomicAdd(&lngn[t], 1);
-            const uint32_t base = (uint32_t)t * (uint32_t)N;
-            if (slot < lmax) lng[(int64_t)t * lmax + slot] = make_uint2(4u * (base + run), 4u * (base + run + s));
-        }
-        if (b < nb) {
-            goff[b] = (int32_t)run;
+        const uint32_t gbase = carry + before + incl - len;
 #pragma unroll
-            for (int q = 0; q < PACK_PARTS; ++q) {
-                pt[(int64_t)q * nb + b] = run;
-                run += v[q];
+        for (int k = 0; k < FIT_GROUP; ++k) {
+            const int32_t b = b0 + k;
+            if (b < nb) {
+                const uint32_t start = gbase + st[k], n = sz[k];
+                goff[b] = (int32_t)start;
+                gend[b] = (int32_t)(start + n);
+                if (n >= REC_LONG) {
+                    const int32_t slot = atomicAdd(&lngn[t], 1);
+                    if (slot < lmax)
+                        lng[(int64_t)t * lmax + slot] = make_uint2(4u * (tbase + start), 4u * (tbase + start + n));
+                }
+                uint32_t run = start;
+                for (int q = 0; q < PACK_PARTS; ++q) {
+                    uint32_t* e = pt + (int64_t)q * nb + b;
+                    const uint32_t c = *e;
+                    *e = run;
+                    run += c;
+                }
             }
         }
         carry += total;
@@ -726,8 +750,8 @@ __global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t 
 }
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter(
-    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
-    uint32_t* roffT, uint16_t* rlenT) {
+    LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
+    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
@@ -735,25 +759,23 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     if (t >= v.T) return;
     const int32_t nb = view_buckets(v);
     uint32_t* cur = sh;            // nb cursors
-    uint32_t* off = sh + nb;       // nb + 1 bucket starts
-    uint32_t* ps0 = off + nb + 1;  // nb: where this part's members start in each bucket
+    uint32_t* end = sh + nb;       // nb bucket ends
+    uint32_t* ps0 = end + nb;      // nb: where this part's members start in each bucket
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
-    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
-    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
-        if (b < nb) {
-            const uint32_t x = pp[b];
-            cur[b] = x;
-            ps0[b] = x;
-        }
-        off[b] = (uint32_t)goff[b];
+    const int32_t* gend = gend_all + (int64_t)t * nb;
+    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) {
+        const uint32_t x = pp[b];
+        cur[b] = x;
+        ps0[b] = x;
+        end[b] = (uint32_t)gend[b];
     }
     __syncthreads();
     const int64_t N = v.N;
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
-    uint32_t* memt = mem + (int64_t)t * N;
+    uint32_t* memt = mem + (int64_t)t * ms;
     uint32_t* ro = roffT + (int64_t)t * N;
     uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     for (int64_t base = i0; base < i1; base += round) {
@@ -771,12 +793,12 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             uint32_t o = 0u, len = 0u;
             if (b != 0xffffu) {
                 const uint32_t pos = atomicAdd(&cur[b], 1u);
-                memt[pos] = (uint32_t)(i + 1);
+                if (pos < end[b]) memt[pos] = (uint32_t)(i + 1);
                 // the run of (i, t): members of the opposite bucket placed
                 // by this part and the later ones, i.e. every member j with
                 // j >= the part's first sample, and some j < i of the part
                 const uint32_t ob = b ^ 1u;
-                const uint32_t rs = ps0[ob], rem = off[ob + 1] - rs;
+                const uint32_t rs = ps0[ob], rem = end[ob] - rs;
                 o = (tbase + rs) * 4u;
                 len = min(rem, REC_LONG) * 4u;
             }
@@ -807,8 +829,8 @@ static size_t part_sorted_lds(int32_t nb, int64_t part) {
 }
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted(
-    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
-    uint32_t* roffT, uint16_t* rlenT) {
+    LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
+    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
@@ -816,22 +838,20 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     if (t >= v.T) return;
     const int32_t nb = view_buckets(v);
     uint32_t* lcur = sh;
-    uint32_t* off = sh + nb;
-    uint32_t* ps0 = off + nb + 1;
+    uint32_t* end = sh + nb;
+    uint32_t* ps0 = end + nb + 1;
     uint32_t* wsum = ps0 + nb;
     uint16_t* stg = (uint16_t*)(wsum + 16);
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
-    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    const int32_t* gend = gend_all + (int64_t)t * nb;
     // the part's count in bucket b runs up to the next part's start there
     // (the bucket's end for the last part)
-    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)goff + 1 : pp + nb;
-    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
-        off[b] = (uint32_t)goff[b];
-        if (b < nb) {
-            const uint32_t s = pp[b];
-            ps0[b] = s;
-            lcur[b] = pn[b] - s;
-        }
+    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)gend : pp + nb;
+    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) {
+        end[b] = (uint32_t)gend[b];
+        const uint32_t s = pp[b];
+        ps0[b] = s;
+        lcur[b] = pn[b] - s;
     }
     __syncthreads();
     // exclusive scan of the counts: thread tid takes buckets [tid*E, tid*E + E)
@@ -862,7 +882,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
     uint32_t* ro = roffT + (int64_t)t * N;
     uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     for (int64_t base = i0; base < i1; base += round) {
@@ -882,7 +902,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                 stg[atomicAdd(&lcur[b], 1u)] = (uint16_t)(i - i0);
                 // the run of (i, t), as in k_part_scatter
                 const uint32_t ob = b ^ 1u;
-                const uint32_t rs = ps0[ob], rem = off[ob + 1] - rs;
+                const uint32_t rs = ps0[ob], rem = end[ob] - rs;
                 o = (tbase + rs) * 4u;
                 len = min(rem, REC_LONG) * 4u;
             }
@@ -893,7 +913,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     __syncthreads();
     // staged member k belongs to the first bucket b with lcur[b] > k
     const uint32_t total = nb > 0 ? lcur[nb - 1] : 0u;
-    uint32_t* memt = mem + (int64_t)t * N;
+    uint32_t* memt = mem + (int64_t)t * ms;
     const uint32_t id0 = (uint32_t)i0 + 1u;
     for (uint32_t k = threadIdx.x; k < total; k += PACK_THREADS) {
         int32_t lo = 0, hi = nb - 1;
@@ -903,7 +923,8 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             else lo = mid + 1;
         }
         const uint32_t first = lo > 0 ? lcur[lo - 1] : 0u;
-        memt[ps0[lo] + (k - first)] = id0 + (uint32_t)stg[k];
+        const uint32_t pos = ps0[lo] + (k - first);
+        if (pos < end[lo]) memt[pos] = id0 + (uint32_t)stg[k];
     }
 }
 
@@ -917,8 +938,8 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 //   - the records are written in a pass of their own over the part's keys,
 //     after which the staging area reuses the bucket-offset table's LDS
 //     (the second pass reads the keys again, from L2).
-// LDS: ps0[nb], wsum[16], lc[nb] (uint16, padded to a word), then off[nb + 1]
-// (records pass) overlaid by stg[part] (staging and writes).
+// LDS: ps0[nb], wsum[16], lc[nb] (uint16, padded to a word), then end[nb]
+// (bucket ends, records pass) overlaid by stg[part] (staging and writes).
 constexpr int64_t PART_SORT4_MAX = 65535;
 
 static size_t part_sorted4_lds(int32_t nb, int64_t part) {
@@ -928,8 +949,8 @@ static size_t part_sorted4_lds(int32_t nb, int64_t part) {
 
 template <bool KEEP>
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted4(
-    LeafView v, const uint32_t* ph, const int32_t* goff_all, const uint16_t* key16, int64_t ldk, uint32_t* mem,
-    uint32_t* roffT, uint16_t* rlenT) {
+    LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
+    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
@@ -940,20 +961,18 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     uint32_t* wsum = ps0 + nb;
     uint16_t* lc = (uint16_t*)(wsum + 16);
     uint32_t* lc32 = wsum + 16;
-    uint32_t* off = wsum + 16 + (nb + 1) / 2;
-    uint32_t* stg = off;
+    uint32_t* end = wsum + 16 + (nb + 1) / 2;
+    uint32_t* stg = end;
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
-    const int32_t* goff = goff_all + (int64_t)t * (nb + 1);
+    const int32_t* gend = gend_all + (int64_t)t * nb;
     // the part's count in bucket b runs up to the next part's start there
     // (the bucket's end for the last part)
-    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)goff + 1 : pp + nb;
-    for (int32_t b = threadIdx.x; b <= nb; b += PACK_THREADS) {
-        off[b] = (uint32_t)goff[b];
-        if (b < nb) {
-            const uint32_t s = pp[b];
-            ps0[b] = s;
-            lc[b] = (uint16_t)(pn[b] - s);
-        }
+    const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)gend : pp + nb;
+    for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) {
+        end[b] = (uint32_t)gend[b];
+        const uint32_t s = pp[b];
+        ps0[b] = s;
+        lc[b] = (uint16_t)(pn[b] - s);
     }
     __syncthreads();
     // inclusive scan of the counts: thread tid takes buckets [tid*E, tid*E + E)
@@ -984,13 +1003,13 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     uint32_t* ro = roffT + (int64_t)t * N;
     uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)t * (uint32_t)N;
+    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
     // the record of sample i with key b (the run of (i, t), as in
     // k_part_scatter), and its staging
     auto record = [&](int64_t i, uint32_t b) {
         const uint32_t ob = (b ^ 1u) & 0xffffu;
         const uint32_t rs = ps0[ob < (uint32_t)nb ? ob : 0u];
-        const uint32_t rem = off[ob < (uint32_t)nb ? ob + 1u : 0u] - rs;
+        const uint32_t rem = end[ob < (uint32_t)nb ? ob : 0u] - rs;
         const bool ok = b != 0xffffu;
         ro[i] = ok ? (tbase + rs) * 4u : 0u;
         rl[i] = ok ? (uint16_t)(min(rem, REC_LONG) * 4u) : (uint16_t)0;
@@ -1017,7 +1036,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                 const int64_t i = i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x;
                 if (i < i1) record(i, key[r][k]);
             }
-        __syncthreads();  // off is dead from here on: stg overlays it
+        __syncthreads();  // end is dead from here on: stg overlays it
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -1038,7 +1057,7 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                 if (i < i1) record(i, key[k]);
             }
         }
-        __syncthreads();  // off is dead from here on: stg overlays it
+        __syncthreads();  // end is dead from here on: stg overlays it
         for (int64_t base = i0; base < i1; base += round) {
             uint32_t key[PACK_KR];
 #pragma unroll
@@ -1055,12 +1074,15 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     // lc[b] is now the start of bucket b's staged run
     uint32_t nval = 0;
     for (int w = 0; w < PACK_THREADS / 64; ++w) nval += wsum[w];
-    uint32_t* memt = mem + (int64_t)t * N;
+    uint32_t* memt = mem + (int64_t)t * ms;
     const uint32_t id0 = (uint32_t)i0 + 1u;
+    // a member's slot lies below its bucket's end, which is at most ms
+    const uint32_t lim = (uint32_t)ms;
     for (uint32_t k = threadIdx.x; k < nval; k += PACK_THREADS) {
         const uint32_t e = stg[k];
         const uint32_t b = e >> 16;
-        memt[ps0[b] + (k - (uint32_t)lc[b])] = id0 + (e & 0xffffu);
+        const uint32_t pos = ps0[b] + (k - (uint32_t)lc[b]);
+        if (pos < lim) memt[pos] = id0 + (e & 0xffffu);
     }
 }
 
@@ -1241,9 +1263,15 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     z.seg_path = !forest && v.L <= SEG_MAX_L;
     const size_t lds_bytes = (size_t)2 * (nb + 1) * 4;
     z.lds_path = (int64_t)lds_bytes + PACK_THREADS * 4 + 1024 <= max_lds;
+    // the line-fit layout keeps every byte offset of mem within 32 bits
+    // (mem_bytes of the triangle's buffer loads); past that the per-part
+    // path places its buckets back to back
+    z.fit = z.part_path && (int64_t)T * fit_stride(N, nb) + MEM_PAD < (1LL << 30);
+    z.ms = z.fit ? fit_stride(N, nb) : n1;
     z.n[FB_OFF] = (size_t)T * (nb + 1);
-    z.n[FB_MEM] = (size_t)T * n1 + MEM_PAD;
+    z.n[FB_MEM] = (size_t)T * z.ms + MEM_PAD;
     if (z.part_path) {
+        z.n[FB_BEND] = (size_t)T * nb;
         z.n[FB_KEY16] = (size_t)T * ldk;
         z.n[FB_SCRATCH] = (size_t)T * PACK_PARTS * nb;
         z.n[FB_ROFFT] = (size_t)T * N;
@@ -1279,12 +1307,14 @@ int ctx_forest_bufs(rfxp_ctx* ctx, const ForestSizes& z, DevBuf<int32_t>& off, D
     fb = ForestBufs();
     fb.ldr = z.ldr;
     fb.lmax = z.lmax;
+    fb.ms = z.ms;
 #define RFXP_FB(K, buf, field)                                  \
     if (z.n[K]) {                                               \
         RFXP_HIP(ctx, (buf).ensure(z.n[K]));                    \
         fb.field = (buf).p;                                     \
     }
     RFXP_FB(FB_OFF, off, off)
+    RFXP_FB(FB_BEND, ctx->bkt_end, bend)
     RFXP_FB(FB_MEM, mem, mem)
     RFXP_FB(FB_ROFF, ctx->roff, roff)
     RFXP_FB(FB_RLEN, ctx->rlen, rlen)
@@ -1305,7 +1335,7 @@ int ctx_forest_bufs(rfxp_ctx* ctx, const ForestSizes& z, DevBuf<int32_t>& off, D
 
 size_t forest_elem_bytes(int k) {
     switch (k) {
-        case FB_OFF: case FB_NOUT: case FB_LNGN: case FB_FLAGS: return 4;
+        case FB_OFF: case FB_BEND: case FB_NOUT: case FB_LNGN: case FB_FLAGS: return 4;
         case FB_MEM: case FB_ROFF: case FB_ROFFT: case FB_SCRATCH: case FB_SCRATCH2: return 4;
         case FB_RLEN: case FB_RLENT: case FB_KEY16: return 2;
         case FB_RINV: case FB_RRANGE: case FB_LNG: return 8;
@@ -1485,6 +1515,10 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
     const int64_t N = v.N;
     const int32_t T = v.T;
     const int32_t nb = view_buckets(v);
+    // every buffer these kernels write must have been sized by forest_sizes
+    if (!fb.off || !fb.bend || !fb.mem || !fb.roff || !fb.rlen || !fb.roffT || !fb.rlenT || !fb.scratch ||
+        !fb.key16 || !fb.lng || !fb.lngn || (!nout_in && !fb.scratch2))
+        return set_error(ctx, RFXP_ERR_STATE, "per-part packing: a forest index buffer was not allocated");
     const int64_t ldk = cdiv(N, 8) * 8;
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
     const unsigned grid = (unsigned)(8 * cdiv(T, 8) * PACK_PARTS);
@@ -1511,28 +1545,28 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
     if (int rc = check_launch(ctx, "k_part_hist")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scan");
-        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, N, fb.scratch, fb.off,
-                           fb.lng, fb.lngn, fb.lmax);
+        hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.ms,
+                           (int32_t)(fb.ms != N), fb.scratch, fb.off, fb.bend, fb.lng, fb.lngn, fb.lmax);
     }
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
         if (sorted4 && part <= 2 * PACK_THREADS * PACK_KR)
             hipLaunchKernelGGL(k_part_scatter_sorted4<true>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
-                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
-                               fb.mem, fb.roffT, fb.rlenT);
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
+                               ldk, fb.mem, fb.roffT, fb.rlenT);
         else if (sorted4)
             hipLaunchKernelGGL(k_part_scatter_sorted4<false>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
-                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
-                               fb.mem, fb.roffT, fb.rlenT);
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
+                               ldk, fb.mem, fb.roffT, fb.rlenT);
         else if (sorted)
             hipLaunchKernelGGL(k_part_scatter_sorted, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
-                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
-                               fb.mem, fb.roffT, fb.rlenT);
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
+                               ldk, fb.mem, fb.roffT, fb.rlenT);
         else
             hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
-                               (const uint32_t*)fb.scratch, (const int32_t*)fb.off, (const uint16_t*)fb.key16, ldk,
-                               fb.mem, fb.roffT, fb.rlenT);
+                               (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
+                               ldk, fb.mem, fb.roffT, fb.rlenT);
     }
     if (int rc = check_launch(ctx, "k_part_scatter")) return rc;
     {

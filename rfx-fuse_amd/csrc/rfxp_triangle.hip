@@ -265,7 +265,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mem_rsrc(const uint32_t* mem, 
 }
 
 // The 16 bucket loads of one record group (ro, rl point at its records).
-__device__ __forceinline__ void load_group(const uint32_t* mem, const uint32_t* __restrict__ ro,
+// Each load's range ends at its run's end, and never past mem_bytes, the
+// readable bytes of mem.
+__device__ __forceinline__ void load_group(const uint32_t* mem, uint32_t mem_bytes, const uint32_t* __restrict__ ro,
                                            const uint16_t* __restrict__ rl, uint32_t lane4, Group& G) {
     uint32_t off[16];
     uint32_t lw[8];
@@ -281,7 +283,8 @@ __device__ __forceinline__ void load_group(const uint32_t* mem, const uint32_t* 
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const uint32_t len4 = (lw[u >> 1] >> (16 * (u & 1))) & 0xffffu;
-        G.m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(mem_rsrc(mem, off[u] + len4), lane4, off[u], 0);
+        G.m[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(mem_rsrc(mem, min(off[u] + len4, mem_bytes)), lane4,
+                                                                off[u], 0);
     }
 }
 
@@ -351,7 +354,8 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
             const uint32_t len4 = __builtin_amdgcn_readfirstlane((uint32_t)rl[t0 + u]);
             if (len4 <= 256u) continue;
             const uint32_t off = __builtin_amdgcn_readfirstlane(ro[t0 + u]);
-            const uint32_t end = len4 == 4u * REC_LONG ? long_run_end(a, t0 + u, off, off + len4) : off + len4;
+            const uint32_t end = min(len4 == 4u * REC_LONG ? long_run_end(a, t0 + u, off, off + len4) : off + len4,
+                                     a.mem_bytes);
             const __amdgpu_buffer_rsrc_t rs = mem_rsrc(a.mem, end);
             for (uint32_t p4 = 256u; off + p4 < end; p4 += 8u * 256u) {
                 uint32_t m[8];
@@ -367,22 +371,22 @@ __device__ __forceinline__ uint32_t hit_phase(const TriArgs& a, int64_t i, int64
     // A and B in ping-pong: one group is counted while the other's loads
     // are in flight (no register copies between them)
     Group A, B;
-    load_group(a.mem, ro + 16 * g0, rl + 16 * g0, lane4, A);
-    if (g0 + 1 < g1) load_group(a.mem, ro + 16 * (g0 + 1), rl + 16 * (g0 + 1), lane4, B);
+    load_group(a.mem, a.mem_bytes, ro + 16 * g0, rl + 16 * g0, lane4, A);
+    if (g0 + 1 < g1) load_group(a.mem, a.mem_bytes, ro + 16 * (g0 + 1), rl + 16 * (g0 + 1), lane4, B);
     for (int32_t g = g0;; g += 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 16; ++u) count_hits<BITS, EMPTY_FIX>(A.m[u], base1, xlim);
         steps += 16;
         if (A.has_long) long_tail(16 * g);
-        if (g + 2 < g1) load_group(a.mem, ro + 16 * (g + 2), rl + 16 * (g + 2), lane4, A);
+        if (g + 2 < g1) load_group(a.mem, a.mem_bytes, ro + 16 * (g + 2), rl + 16 * (g + 2), lane4, A);
         if (g + 1 >= g1) break;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < 16; ++u) count_hits<BITS, EMPTY_FIX>(B.m[u], base1, xlim);
         steps += 16;
         if (B.has_long) long_tail(16 * (g + 1));
-        if (g + 3 < g1) load_group(a.mem, ro + 16 * (g + 3), rl + 16 * (g + 3), lane4, B);
+        if (g + 3 < g1) load_group(a.mem, a.mem_bytes, ro + 16 * (g + 3), rl + 16 * (g + 3), lane4, B);
         if (g + 2 >= g1) break;
     }
     return steps;
@@ -986,7 +990,7 @@ int upper_launch(rfxp_ctx* ctx, const ForestBufs& fb, int64_t N, int32_t T, int 
     a.lngn = fb.lngn;
     a.lmax = fb.lmax;
     a.mem = fb.mem;
-    a.mem_bytes = (uint32_t)(((uint64_t)T * (uint64_t)N + MEM_PAD) * 4u);
+    a.mem_bytes = (uint32_t)(((uint64_t)T * (uint64_t)fb.ms + MEM_PAD) * 4u);
     a.rinv = fb.rinv;
     a.rr = fb.rrange;
     a.N = N;
