@@ -592,18 +592,19 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // PACK_PARTS contiguous parts.
 //   k_part_hist    (tree, part): LDS histogram of the part's buckets -> ph,
 //                  and the part's 16-bit keys;
-//   k_part_scan    (tree): bucket starts (off) and, per part, the start of
-//                  its members in each bucket (ph, in place);
+//   k_part_scan    (tree): bucket starts (off) and ends (bend) in the
+//                  line-fit layout and, per part, the start of its members in
+//                  each bucket (ph, in place);
 //   k_part_scatter (tree, part): LDS cursors from ph; each member goes
-//                  straight to its slot in mem[t], and each sample's record
-//                  to the tree-major arrays.  The parts of a tree run at
-//                  once on one XCD, eight trees per XCD: the 4-byte member
+//                  straight to its slot in mem[t].  The parts of a tree run
+//                  at once on one XCD, eight trees per XCD: the 4-byte member
 //                  writes of those trees (8 x 4N bytes) merge in that XCD's
 //                  L2 before they reach HBM while that region fits the L2;
-//   k_part_scatter_sorted: the same, with the part's members sorted by
-//                  bucket in LDS first and written in bucket order (larger
-//                  forests, where the direct writes no longer merge);
-//   k_rec_transpose: tree-major records -> sample-major.
+//   k_part_scatter_sorted / _sorted4: the same, with the part's members
+//                  sorted by bucket in LDS first and written in bucket order
+//                  (larger forests, where the direct writes no longer merge);
+//   k_part_records (sample block, tree block): the sample-major run records
+//                  from the keys and the part table.
 // ---------------------------------------------------------------------------
 constexpr int PACK_PARTS = 8;
 constexpr int PART_MAX_NB = 8192;
@@ -751,31 +752,25 @@ __global__ __launch_bounds__(PACK_THREADS) void k_part_scan(int32_t nb, int32_t 
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter(
     LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
-    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
+    uint32_t* mem) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
     part_of_block(blockIdx.x, t, p);
     if (t >= v.T) return;
     const int32_t nb = view_buckets(v);
-    uint32_t* cur = sh;            // nb cursors
-    uint32_t* end = sh + nb;       // nb bucket ends
-    uint32_t* ps0 = end + nb;      // nb: where this part's members start in each bucket
+    uint32_t* cur = sh;       // nb cursors
+    uint32_t* end = sh + nb;  // nb bucket ends
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
     const int32_t* gend = gend_all + (int64_t)t * nb;
     for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) {
-        const uint32_t x = pp[b];
-        cur[b] = x;
-        ps0[b] = x;
+        cur[b] = pp[b];
         end[b] = (uint32_t)gend[b];
     }
     __syncthreads();
     const int64_t N = v.N;
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
     uint32_t* memt = mem + (int64_t)t * ms;
-    uint32_t* ro = roffT + (int64_t)t * N;
-    uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     for (int64_t base = i0; base < i1; base += round) {
@@ -783,27 +778,14 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
             const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < i1 ? (uint32_t)kt[i] : 0x10000u;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
         }
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
-            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
             const uint32_t b = key[k];
-            if (b == 0x10000u) continue;
-            uint32_t o = 0u, len = 0u;
-            if (b != 0xffffu) {
-                const uint32_t pos = atomicAdd(&cur[b], 1u);
-                if (pos < end[b]) memt[pos] = (uint32_t)(i + 1);
-                // the run of (i, t): members of the opposite bucket placed
-                // by this part and the later ones, i.e. every member j with
-                // j >= the part's first sample, and some j < i of the part
-                const uint32_t ob = b ^ 1u;
-                const uint32_t rs = ps0[ob], rem = end[ob] - rs;
-                o = (tbase + rs) * 4u;
-                len = min(rem, REC_LONG) * 4u;
-            }
-            ro[i] = o;
-            rl[i] = (uint16_t)len;
+            if (b == 0xffffu) continue;
+            const uint32_t pos = atomicAdd(&cur[b], 1u);
+            if (pos < end[b]) memt[pos] = (uint32_t)(base + (int64_t)k * PACK_THREADS + threadIdx.x + 1);
         }
     }
 }
@@ -815,10 +797,10 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // and the parts of a tree, which run at once on one XCD, sweep mem[t] in the
 // same bucket order, so the lines they share fill up in L2 before they are
 // written back (random 4-byte stores leave most lines partial).  Parts of at
-// most PART_SORT_MAX samples.  The records are written as in k_part_scatter.
+// most PART_SORT_MAX samples.
 //
 // LDS: lcur[nb] (the exclusive prefix of the part's bucket counts, used as
-// cursors, which leaves each bucket's inclusive end), off[nb + 1], ps0[nb],
+// cursors, which leaves each bucket's inclusive end), end[nb + 1], ps0[nb],
 // wsum[16], stg[part size] (uint16).
 constexpr int64_t PART_SORT_MAX = 65536;
 constexpr int64_t PART_SORT_MIN_N = 32768;
@@ -830,7 +812,7 @@ static size_t part_sorted_lds(int32_t nb, int64_t part) {
 
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted(
     LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
-    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
+    uint32_t* mem) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
@@ -880,9 +862,6 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     __syncthreads();
     const int64_t N = v.N;
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
-    uint32_t* ro = roffT + (int64_t)t * N;
-    uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
     for (int64_t base = i0; base < i1; base += round) {
@@ -890,24 +869,13 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
             const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-            key[k] = i < i1 ? (uint32_t)kt[i] : 0x10000u;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
         }
 #pragma unroll
         for (int k = 0; k < PACK_KR; ++k) {
             const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
             const uint32_t b = key[k];
-            if (b == 0x10000u) continue;
-            uint32_t o = 0u, len = 0u;
-            if (b != 0xffffu) {
-                stg[atomicAdd(&lcur[b], 1u)] = (uint16_t)(i - i0);
-                // the run of (i, t), as in k_part_scatter
-                const uint32_t ob = b ^ 1u;
-                const uint32_t rs = ps0[ob], rem = end[ob] - rs;
-                o = (tbase + rs) * 4u;
-                len = min(rem, REC_LONG) * 4u;
-            }
-            ro[i] = o;
-            rl[i] = (uint16_t)len;
+            if (b != 0xffffu) stg[atomicAdd(&lcur[b], 1u)] = (uint16_t)(i - i0);
         }
     }
     __syncthreads();
@@ -931,15 +899,11 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
 // k_part_scatter_sorted with 4-byte staging entries (bucket << 16 | offset
 // in the part), so that staged member k finds its slot without a search:
 // slot = ps0[b] + (k - start of b's staged run).  To keep the LDS at two
-// workgroups per CU at part sizes like 12,500 with 4,096 buckets:
-//   - the local cursors are 16-bit halves of 32-bit words counting down from
-//     each bucket's end, so that they end at its start (counts stay below
-//     2^16: parts of at most PART_SORT4_MAX samples);
-//   - the records are written in a pass of their own over the part's keys,
-//     after which the staging area reuses the bucket-offset table's LDS
-//     (the second pass reads the keys again, from L2).
-// LDS: ps0[nb], wsum[16], lc[nb] (uint16, padded to a word), then end[nb]
-// (bucket ends, records pass) overlaid by stg[part] (staging and writes).
+// workgroups per CU at part sizes like 12,500 with 4,096 buckets, the local
+// cursors are 16-bit halves of 32-bit words counting down from each bucket's
+// end, so that they end at its start (counts stay below 2^16: parts of at
+// most PART_SORT4_MAX samples).
+// LDS: ps0[nb], wsum[16], lc[nb] (uint16, padded to a word), stg[part].
 constexpr int64_t PART_SORT4_MAX = 65535;
 
 static size_t part_sorted4_lds(int32_t nb, int64_t part) {
@@ -947,10 +911,9 @@ static size_t part_sorted4_lds(int32_t nb, int64_t part) {
     return (size_t)(nb + 16 + (nb + 1) / 2 + un) * 4;
 }
 
-template <bool KEEP>
 __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_part_scatter_sorted4(
     LeafView v, const uint32_t* ph, const int32_t* gend_all, int64_t ms, const uint16_t* key16, int64_t ldk,
-    uint32_t* mem, uint32_t* roffT, uint16_t* rlenT) {
+    uint32_t* mem) {
     extern __shared__ uint32_t sh[];
     int32_t t;
     int p;
@@ -961,15 +924,13 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
     uint32_t* wsum = ps0 + nb;
     uint16_t* lc = (uint16_t*)(wsum + 16);
     uint32_t* lc32 = wsum + 16;
-    uint32_t* end = wsum + 16 + (nb + 1) / 2;
-    uint32_t* stg = end;
+    uint32_t* stg = wsum + 16 + (nb + 1) / 2;
     const uint32_t* pp = ph + ((int64_t)t * PACK_PARTS + p) * nb;
     const int32_t* gend = gend_all + (int64_t)t * nb;
     // the part's count in bucket b runs up to the next part's start there
     // (the bucket's end for the last part)
     const uint32_t* pn = p + 1 == PACK_PARTS ? (const uint32_t*)gend : pp + nb;
     for (int32_t b = threadIdx.x; b < nb; b += PACK_THREADS) {
-        end[b] = (uint32_t)gend[b];
         const uint32_t s = pp[b];
         ps0[b] = s;
         lc[b] = (uint16_t)(pn[b] - s);
@@ -997,77 +958,25 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             lc[b] = (uint16_t)run;
         }
     }
+    __syncthreads();  // every bucket's count-down cursor is in place
     const int64_t N = v.N;
     const int64_t i0 = part_begin(N, p), i1 = part_begin(N, p + 1);
     const uint16_t* kt = key16 + (int64_t)t * ldk;
     const int64_t round = (int64_t)PACK_THREADS * PACK_KR;
-    uint32_t* ro = roffT + (int64_t)t * N;
-    uint16_t* rl = rlenT + (int64_t)t * N;
-    const uint32_t tbase = (uint32_t)((int64_t)t * ms);
-    // the record of sample i with key b (the run of (i, t), as in
-    // k_part_scatter), and its staging
-    auto record = [&](int64_t i, uint32_t b) {
-        const uint32_t ob = (b ^ 1u) & 0xffffu;
-        const uint32_t rs = ps0[ob < (uint32_t)nb ? ob : 0u];
-        const uint32_t rem = end[ob < (uint32_t)nb ? ob : 0u] - rs;
-        const bool ok = b != 0xffffu;
-        ro[i] = ok ? (tbase + rs) * 4u : 0u;
-        rl[i] = ok ? (uint16_t)(min(rem, REC_LONG) * 4u) : (uint16_t)0;
-    };
-    auto stage = [&](int64_t i, uint32_t b) {
-        const uint32_t sh16 = (b & 1u) * 16u;
-        const uint32_t old = atomicSub(&lc32[b >> 1], 1u << sh16);
-        stg[((old >> sh16) & 0xffffu) - 1u] = (b << 16) | (uint32_t)(i - i0);
-    };
-    if constexpr (KEEP) {
-        // the part (at most 2 rounds) in registers: its keys are read once
-        uint32_t key[2][PACK_KR];
+    for (int64_t base = i0; base < i1; base += round) {
+        uint32_t key[PACK_KR];
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k) {
-                const int64_t i = i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x;
-                key[r][k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
-            }
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k) {
-                const int64_t i = i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x;
-                if (i < i1) record(i, key[r][k]);
-            }
-        __syncthreads();  // end is dead from here on: stg overlays it
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k)
-                if (key[r][k] != 0xffffu) stage(i0 + r * round + (int64_t)k * PACK_THREADS + threadIdx.x, key[r][k]);
-    } else {
-        // records pass, then the staging pass reading the keys again
-        for (int64_t base = i0; base < i1; base += round) {
-            uint32_t key[PACK_KR];
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k) {
-                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-                key[k] = (uint32_t)kt[i < i1 ? i : i0];
-            }
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k) {
-                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-                if (i < i1) record(i, key[k]);
-            }
+        for (int k = 0; k < PACK_KR; ++k) {
+            const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
+            key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
         }
-        __syncthreads();  // end is dead from here on: stg overlays it
-        for (int64_t base = i0; base < i1; base += round) {
-            uint32_t key[PACK_KR];
 #pragma unroll
-            for (int k = 0; k < PACK_KR; ++k) {
-                const int64_t i = base + (int64_t)k * PACK_THREADS + threadIdx.x;
-                key[k] = i < i1 ? (uint32_t)kt[i] : 0xffffu;
-            }
-#pragma unroll
-            for (int k = 0; k < PACK_KR; ++k)
-                if (key[k] != 0xffffu) stage(base + (int64_t)k * PACK_THREADS + threadIdx.x, key[k]);
+        for (int k = 0; k < PACK_KR; ++k) {
+            const uint32_t b = key[k];
+            if (b == 0xffffu) continue;
+            const uint32_t sh16 = (b & 1u) * 16u;
+            const uint32_t old = atomicSub(&lc32[b >> 1], 1u << sh16);
+            stg[((old >> sh16) & 0xffffu) - 1u] = (b << 16) | (uint32_t)(base + (int64_t)k * PACK_THREADS + threadIdx.x - i0);
         }
     }
     __syncthreads();
@@ -1084,6 +993,91 @@ __global__ __launch_bounds__(PACK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
         const uint32_t pos = ps0[b] + (k - (uint32_t)lc[b]);
         if (pos < lim) memt[pos] = id0 + (e & 0xffffu);
     }
+}
+
+// Sample-major run records of the per-part path, from the keys: workgroup
+// (block x of PREC_S samples, block y of PREC_T trees) looks up, for every
+// (sample i, tree t) of its tile, the start of i's own part in i's opposite
+// bucket (the part table after k_part_scan) and that bucket's end, and
+// writes the tile's rows of roff / rlen through LDS (one 128-byte row piece
+// per sample).  Consecutive workgroups take consecutive sample blocks of one
+// tree block, so the table slices they read (PREC_T trees of one part) stay
+// in L2.  Padding trees T..ldr-1 get empty records.  With acc (nout counted
+// here), each tile adds its trees' OOB bits of its samples to acc[i], one
+// atomic per sample and tile: nout_i = sum over trees of the OOB bits
+// (src/rf_bootstrap.cpp:67-70).
+constexpr int PREC_S = 128, PREC_T = 32;
+
+__global__ __launch_bounds__(256) void k_part_records(const uint16_t* key16, int64_t ldk, const uint32_t* ph,
+                                                     const int32_t* gend_all, int32_t nb, int64_t N, int32_t T,
+                                                     int64_t ms, int64_t ldr, uint32_t* roff, uint16_t* rlen,
+                                                     const uint32_t* oob, int64_t old, uint32_t* acc) {
+    __shared__ uint32_t so[PREC_S][PREC_T + 1];
+    __shared__ uint16_t sl[PREC_S][PREC_T + 2];
+    __shared__ uint32_t part[2][PREC_S];
+    const int64_t i0 = (int64_t)blockIdx.x * PREC_S;
+    const int32_t t0 = (int32_t)blockIdx.y * PREC_T;
+    const int64_t chunk = (N + PACK_PARTS - 1) / PACK_PARTS;
+    const int c = threadIdx.x & 63;
+    // keys of sample pair (i0 + 2c, i0 + 2c + 1) in trees t0 + r, r = w + 4q
+    // (w = threadIdx.x >> 6): all loads first
+    uint32_t kw[PREC_T / 4];
+#pragma unroll
+    for (int q = 0; q < PREC_T / 4; ++q) {
+        const int32_t t = t0 + (int32_t)(threadIdx.x >> 6) + 4 * q;
+        const int64_t i = i0 + 2 * c;
+        kw[q] = (t < T && i < N) ? *(const uint32_t*)(key16 + (int64_t)t * ldk + i) : 0xffffffffu;
+    }
+#pragma unroll
+    for (int q = 0; q < PREC_T / 4; ++q) {
+        const int r = (int)(threadIdx.x >> 6) + 4 * q;
+        const int32_t t = t0 + r;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t i = i0 + 2 * c + h;
+            const uint32_t b = (kw[q] >> (16 * h)) & 0xffffu;
+            uint32_t o = 0u, len = 0u;
+            if (b != 0xffffu && i < N) {
+                // the run of (i, t): members of the opposite bucket placed by
+                // i's part and the later ones, i.e. every member j from the
+                // part's first sample on
+                const uint32_t ob = b ^ 1u;
+                const int64_t p = i / chunk;
+                const uint32_t rs = ph[((int64_t)t * PACK_PARTS + p) * nb + ob];
+                const uint32_t e = (uint32_t)gend_all[(int64_t)t * nb + ob];
+                o = (uint32_t)((int64_t)t * ms + rs) * 4u;
+                len = min(e - rs, REC_LONG) * 4u;
+            }
+            so[2 * c + h][r] = o;
+            sl[2 * c + h][r] = (uint16_t)len;
+        }
+    }
+    if (acc) {
+        // thread (sample s, half g of the tile's trees): its OOB bits
+        const int s = threadIdx.x & (PREC_S - 1), g = threadIdx.x >> 7;
+        const int64_t i = i0 + s;
+        const int64_t ic = i < N ? i : 0;
+        uint32_t n = 0;
+#pragma unroll
+        for (int k = 0; k < PREC_T / 2; ++k) {
+            const int32_t t = t0 + g * (PREC_T / 2) + k;
+            const uint32_t w = t < T ? oob[(int64_t)t * old + (ic >> 5)] : 0u;
+            n += (w >> (ic & 31)) & 1u;
+        }
+        part[g][s] = n;
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < PREC_S * PREC_T; k += 256) {
+        const int s = k / PREC_T, r = k % PREC_T;
+        const int64_t i = i0 + s;
+        const int64_t t = t0 + r;
+        if (i < N && t < ldr) {
+            roff[i * ldr + t] = so[s][r];
+            rlen[i * ldr + t] = sl[s][r];
+        }
+    }
+    if (acc && threadIdx.x < PREC_S && i0 + threadIdx.x < N)
+        atomicAdd(&acc[i0 + threadIdx.x], part[0][threadIdx.x] + part[1][threadIdx.x]);
 }
 
 // [T][N] -> [N][ldr] for both record arrays, 64 x 64 tiles through LDS.
@@ -1274,8 +1268,6 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
         z.n[FB_BEND] = (size_t)T * nb;
         z.n[FB_KEY16] = (size_t)T * ldk;
         z.n[FB_SCRATCH] = (size_t)T * PACK_PARTS * nb;
-        z.n[FB_ROFFT] = (size_t)T * N;
-        z.n[FB_RLENT] = (size_t)T * N;
     } else if (z.seg_path) {
         z.n[FB_SCRATCH] = (size_t)T * (nb + 1);
     } else {
@@ -1516,8 +1508,8 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
     const int32_t T = v.T;
     const int32_t nb = view_buckets(v);
     // every buffer these kernels write must have been sized by forest_sizes
-    if (!fb.off || !fb.bend || !fb.mem || !fb.roff || !fb.rlen || !fb.roffT || !fb.rlenT || !fb.scratch ||
-        !fb.key16 || !fb.lng || !fb.lngn || (!nout_in && !fb.scratch2))
+    if (!fb.off || !fb.bend || !fb.mem || !fb.roff || !fb.rlen || !fb.scratch || !fb.key16 || !fb.lng ||
+        !fb.lngn || (!nout_in && !fb.scratch2))
         return set_error(ctx, RFXP_ERR_STATE, "per-part packing: a forest index buffer was not allocated");
     const int64_t ldk = cdiv(N, 8) * 8;
     // (tree, part) blocks: 8 XCDs x ceil(T/8) trees x PACK_PARTS parts
@@ -1526,13 +1518,12 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
     const int64_t part = cdiv(N, PACK_PARTS);
     const int kind = part_scatter_kind(N, nb, ctx->max_lds);
     const bool sorted4 = kind == RFXP_PACK_PARTS_SORTED4, sorted = kind == RFXP_PACK_PARTS_SORTED2;
-    const void* scatter = sorted4  ? (part <= 2 * PACK_THREADS * PACK_KR ? (const void*)k_part_scatter_sorted4<true>
-                                                                         : (const void*)k_part_scatter_sorted4<false>)
+    const void* scatter = sorted4  ? (const void*)k_part_scatter_sorted4
                           : sorted ? (const void*)k_part_scatter_sorted
                                    : (const void*)k_part_scatter;
     const size_t lds_s = sorted4  ? part_sorted4_lds(nb, part)
                          : sorted ? part_sorted_lds(nb, part)
-                                  : (size_t)(3 * nb + 1) * 4;
+                                  : (size_t)(2 * nb) * 4;
     if (lds_h > 32768)
         RFXP_HIP(ctx, hipFuncSetAttribute((const void*)k_part_hist, hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)lds_h));
@@ -1545,37 +1536,35 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
     if (int rc = check_launch(ctx, "k_part_hist")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scan");
+        // fit: the line-fit layout (the tree stride exceeds N exactly then)
         hipLaunchKernelGGL(k_part_scan, dim3((unsigned)T), dim3(PACK_THREADS), 0, s, nb, T, fb.ms,
                            (int32_t)(fb.ms != N), fb.scratch, fb.off, fb.bend, fb.lng, fb.lngn, fb.lmax);
     }
     if (int rc = check_launch(ctx, "k_part_scan")) return rc;
     {
         LaunchTimer tm(ctx, "pack_scatter");
-        if (sorted4 && part <= 2 * PACK_THREADS * PACK_KR)
-            hipLaunchKernelGGL(k_part_scatter_sorted4<true>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
+        if (sorted4)
+            hipLaunchKernelGGL(k_part_scatter_sorted4, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
                                (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
-                               ldk, fb.mem, fb.roffT, fb.rlenT);
-        else if (sorted4)
-            hipLaunchKernelGGL(k_part_scatter_sorted4<false>, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
-                               (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
-                               ldk, fb.mem, fb.roffT, fb.rlenT);
+                               ldk, fb.mem);
         else if (sorted)
             hipLaunchKernelGGL(k_part_scatter_sorted, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
                                (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
-                               ldk, fb.mem, fb.roffT, fb.rlenT);
+                               ldk, fb.mem);
         else
             hipLaunchKernelGGL(k_part_scatter, dim3(grid), dim3(PACK_THREADS), lds_s, s, v,
                                (const uint32_t*)fb.scratch, (const int32_t*)fb.bend, fb.ms, (const uint16_t*)fb.key16,
-                               ldk, fb.mem, fb.roffT, fb.rlenT);
+                               ldk, fb.mem);
     }
     if (int rc = check_launch(ctx, "k_part_scatter")) return rc;
     {
         LaunchTimer tm(ctx, "records");
-        hipLaunchKernelGGL(k_rec_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)cdiv(fb.ldr, 64)), dim3(256), 0, s,
-                           fb.roffT, fb.rlenT, N, T, fb.ldr, fb.roff, fb.rlen, v.oob, v.old,
+        hipLaunchKernelGGL(k_part_records, dim3((unsigned)cdiv(N, PREC_S), (unsigned)cdiv(fb.ldr, PREC_T)), dim3(256),
+                           0, s, (const uint16_t*)fb.key16, ldk, (const uint32_t*)fb.scratch,
+                           (const int32_t*)fb.bend, nb, N, T, fb.ms, fb.ldr, fb.roff, fb.rlen, v.oob, v.old,
                            nout_in ? nullptr : fb.scratch2);
     }
-    return check_launch(ctx, "k_rec_transpose");
+    return check_launch(ctx, "k_part_records");
 }
 
 // nout, 1/nout and its range (forest mode).
