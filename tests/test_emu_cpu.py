@@ -186,3 +186,19 @@ def test_oob_normalised_pv(driver, tmp_path, n, t, nleaf):
     Y = emulate(driver, tmp_path, 4, leaf, oob, nleaf, fmt=8, V=V)
     want = oob_pv_reference(leaf, oob, nleaf, V)
     assert np.linalg.norm(Y - want) / np.linalg.norm(want) < 1e-6
+
+
+@pytest.mark.parametrize("shape", [("100000", "500", "2048"),           # C3: per-part path
+                                   ("140000", "6", "4096", "0.02", "7"),  # 8,192 buckets, invalid labels
+                                   ("60000", "20", "2", "0", "5"),        # buckets past 16,383 members
+                                   ("40000", "30", "1000", "0.01", "3")])
+def test_line_fit_layout_host_check(driver, shape):
+    """The line-fit placement at full size, computed on the host with the
+    kernels' own rule and stride bound (tests/harness/layout_check.cpp):
+    buckets in order inside their tree's stride, small buckets in one line,
+    large ones ending on a line, every part's slots and every sample's run
+    inside its bucket, long-bucket entries inside mem."""
+    r = subprocess.run([os.path.join(EMU, "_build", "layout_check"), *shape], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
+    lines = float(r.stdout.split("lines_per_run=")[1].split()[0])
+    assert lines < 1.1 if shape[2] != "2" else True
