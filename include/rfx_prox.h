@@ -348,12 +348,25 @@ int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, int32_t ite
  * (include/rf_proximity_lowrank.hpp:27-433, rf_lowrank_helpers.hpp:13-34),
  * which is built on these calls in the same library.  The context holds one
  * accumulator: M = sum of the symmetric contributions added since
- * rfxp_symacc_reset, kept exactly as a sparse matrix in device memory. */
+ * rfxp_symacc_reset, kept in device memory as a list of the contributions'
+ * nonzero entries while that list and its symmetric CSR (28 bytes an entry)
+ * take less than the packed upper triangle of M in doubles, and as that
+ * triangle from then on.  Its memory is so at most
+ * 8 N(N+1)/2 + 24 (N+1) bytes plus one staging band of a host input (at
+ * most 256 MiB or one row), and up to 1.43 times the triangle while an add
+ * switches forms; the number of contributions does not enter. */
 
-/* Empties the accumulator and sets its order N (1 <= N < 2^31 - 1). */
+/* Empties the accumulator and sets its order N (1 <= N < 2^31 - 1);
+ * releases what a previous accumulation held beyond this N's list limit. */
 int rfxp_symacc_reset(rfxp_ctx* ctx, int64_t N);
-/* Number of stored entries (i <= j) so far; -1 for a NULL context. */
+/* Number of stored entries (i <= j) so far: the listed nonzeros, or
+ * N(N+1)/2 once the accumulator holds the dense triangle; -1 for a NULL
+ * context. */
 int64_t rfxp_symacc_nnz(rfxp_ctx* ctx);
+/* Bytes of device memory the accumulator holds now (list, CSR, triangle,
+ * staging; not the factor's work blocks); -1 for a NULL context.  No
+ * counterpart in the reference: it makes the memory bound above checkable. */
+int64_t rfxp_symacc_device_bytes(rfxp_ctx* ctx);
 /* Adds the symmetric matrix whose packed upper triangle (N(N+1)/2 entries,
  * host or device) is `tri`, read as the reference's low-rank path reads
  * per-tree triangles (cuda/rf_proximity_lowrank.cu:687-789):

@@ -180,7 +180,8 @@ int rfxp_ctx_destroy(rfxp_ctx* ctx) {
     ctx->sa_cnt.release();
     ctx->sa_rowptr.release();
     ctx->sa_deg.release();
-    for (auto* b : {&ctx->sa_stage, &ctx->sa_x, &ctx->sa_y, &ctx->sa_z, &ctx->sa_part, &ctx->sa_g, &ctx->sa_w, &ctx->sa_wv})
+    for (auto* b : {&ctx->sa_tri, &ctx->sa_stage, &ctx->sa_x, &ctx->sa_y, &ctx->sa_z, &ctx->sa_part, &ctx->sa_g,
+                    &ctx->sa_w, &ctx->sa_wv})
         b->release();
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();

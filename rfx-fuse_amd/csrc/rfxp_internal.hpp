@@ -134,10 +134,12 @@ struct rfxp_ctx {
     // symmetric accumulator of the low-rank class (rfxp_symacc_*)
     int64_t sa_N = 0, sa_nnz = 0;
     bool sa_csr_ok = false;
+    bool sa_dense = false;                       // entries in sa_tri instead of the COO list
     DevBuf<int32_t> sa_i, sa_j, sa_col, sa_sv;  // COO rows / cols, CSR columns, RF-GAP counts
     DevBuf<float> sa_v, sa_val;                  // COO / CSR values
     DevBuf<int64_t> sa_cnt, sa_rowptr;
     DevBuf<unsigned long long> sa_deg;
+    DevBuf<double> sa_tri;                       // packed upper triangle (dense form)
     DevBuf<double> sa_stage, sa_x, sa_y, sa_z, sa_part, sa_g, sa_w, sa_wv;
 
     // timing

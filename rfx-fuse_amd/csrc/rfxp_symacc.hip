@@ -8,12 +8,23 @@
 //     M = sum over contributions C of C   (C symmetric, given as its packed
 //                                         upper triangle or as a dense matrix)
 // and the factor is computed from M when it is asked for:
-//   * accumulation: per contribution, a row-count pass and an ordered emit
-//     pass append the nonzero entries (i <= j, value) to a device COO list;
-//     values are read the way the reference's low-rank path reads them (FP16
-//     as is, INT8 and NF4 dequantised and rounded to FP16,
-//     cuda/rf_proximity_lowrank.cu:199-240, 744-789; a dense matrix's upper
-//     triangle rounded to FP16, :654-685);
+//   * accumulation, sparse form: per contribution, a row-count pass and an
+//     ordered emit pass append the nonzero entries (i <= j, value) to a
+//     device COO list; values are read the way the reference's low-rank
+//     path reads them (FP16 as is, INT8 and NF4 dequantised and rounded to
+//     FP16, cuda/rf_proximity_lowrank.cu:199-240, 744-789; a dense matrix's
+//     upper triangle rounded to FP16, :654-685);
+//   * accumulation, dense form: once the list and its CSR (12 + 16 bytes an
+//     entry) would take more than the packed upper triangle of M in doubles
+//     (8 bytes an entry of N(N+1)/2), the list is summed into that triangle
+//     and every later contribution is added to it in place, one pass over
+//     the input.  The accumulator's memory is so bounded by the triangle,
+//     whatever the number of contributions.  Sums of FP16-valued entries
+//     (every format but F32) are exact in double up to 8192 contributions
+//     (multiples of 2^-24 below 2^16), so they do not depend on the order of
+//     the additions;
+//   * inputs in host memory are staged through the device in bands of rows
+//     of at most SA_STAGE_BYTES;
 //   * factor: the COO list becomes a symmetric CSR (both halves), then block
 //     subspace iteration with Rayleigh-Ritz: X_0 random normal, Q_k =
 //     orth(M Q_{k-1}), H = Q^T M Q = U diag(lambda) U^T, and
@@ -28,7 +39,8 @@
 // Dense blocks are N x b row-major doubles.  The host does the b x b linear
 // algebra (Cholesky, Jacobi eigenvalues).  The CSR is built with atomics,
 // so the order of the terms within a row -- and the last bits of the
-// double sums -- may change from run to run.
+// double sums -- may change from run to run; in the dense form the
+// products M X are summed in a fixed order.
 #include <math.h>
 #include <string.h>
 
@@ -145,12 +157,15 @@ static void host_triu_inv(int n, const std::vector<double>& R, std::vector<doubl
 
 // Source of a contribution: a packed upper triangle in one of the formats,
 // or a dense N x N matrix read row-major (element (i, j) at p[i*N + j]).
+// p may hold only a band of it: then p points at packed entry `base` (even
+// for NF4) or at row `base` of the dense matrix.
 enum SrcKind { SRC_F16 = 0, SRC_F32 = 1, SRC_I8 = 2, SRC_NF4 = 3, SRC_DENSE = 4 };
 struct SymSrc {
     const void* p;
     int kind;
     float scale, zp;  // INT8 dequantisation
     int64_t N;
+    int64_t base;
 };
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
@@ -158,20 +173,21 @@ __device__ __forceinline__ float round_half(float v) { return (float)(_Float16)v
 
 // Value of entry (i, j), i <= j, with packed index e.
 __device__ __forceinline__ float src_value(const SymSrc& s, int64_t i, int64_t j, int64_t e) {
+    const int64_t k = e - s.base;
     switch (s.kind) {
-        case SRC_F16: return half_bits_to_float(((const uint16_t*)s.p)[e]);
-        case SRC_F32: return ((const float*)s.p)[e];
+        case SRC_F16: return half_bits_to_float(((const uint16_t*)s.p)[k]);
+        case SRC_F32: return ((const float*)s.p)[k];
         case SRC_I8: {
             // int8_to_fp32 (include/rf_quantization_kernels.hpp:32-34), then FP16
-            const float v = ((float)((const int8_t*)s.p)[e] - s.zp) * s.scale;
+            const float v = ((float)((const int8_t*)s.p)[k] - s.zp) * s.scale;
             return round_half(v);
         }
         case SRC_NF4: {
-            const uint32_t q = (((const uint8_t*)s.p)[e >> 1] >> ((e & 1) * 4)) & 0xfu;
+            const uint32_t q = (((const uint8_t*)s.p)[k >> 1] >> ((k & 1) * 4)) & 0xfu;
             const float v = q <= 7u ? (float)q / 7.0f : -((float)(q - 8u)) / 7.0f;  // nf4_to_fp32
             return round_half(v);
         }
-        default: return round_half((float)((const double*)s.p)[i * s.N + j]);
+        default: return round_half((float)((const double*)s.p)[(i - s.base) * s.N + j]);
     }
 }
 
@@ -263,6 +279,82 @@ __global__ __launch_bounds__(256) void k_sa_spmm(const int64_t* rowptr, const in
             for (int64_t k = k0; k < k1; ++k) acc += (double)val[k] * X[(int64_t)col[k] * b + c];
         if (c < b) Y[i * b + c] = acc;
     }
+}
+
+// Dense form: the entries of rows row0 + blockIdx.x added to the packed
+// triangle tri, in place (each entry is written by one thread).
+__global__ __launch_bounds__(SA_THREADS) void k_sa_tri_add(SymSrc s, int64_t row0, double* tri) {
+    const int64_t i = row0 + blockIdx.x;
+    const int64_t e0 = tri_idx(s.N, i, i);
+    for (int64_t j = i + threadIdx.x; j < s.N; j += SA_THREADS) {
+        const int64_t e = e0 + (j - i);
+        tri[e] += (double)src_value(s, i, j, e);
+    }
+}
+
+// The COO list summed into the zeroed packed triangle (entries repeat
+// across contributions: atomic adds).
+__global__ void k_sa_list_to_tri(const int32_t* ci, const int32_t* cj, const float* cv, int64_t nnz, int64_t N,
+                                 double* tri) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nnz) return;
+    atomicAdd(&tri[tri_idx(N, ci[e], cj[e])], (double)cv[e]);
+}
+
+// Dense form of Y = M X: M symmetric from its packed upper triangle, X and Y
+// N x b row-major.  A workgroup computes the 64 x 64 tile of Y at rows
+// 64 blockIdx.x, columns 64 blockIdx.y, over slabs of 16 of the inner index
+// j with both operands in LDS, 4 x 4 outputs per thread.  A slab of M is
+// read along row i where it lies on or above the diagonal (j >= i) and
+// along row j, transposed, where it lies wholly below it, so that
+// neighbouring threads read neighbouring entries.
+constexpr int TS_T = 64, TS_K = 16;
+__global__ __launch_bounds__(256) void k_sa_tri_spmm(const double* tri, const double* X, int64_t N, int32_t b,
+                                                     double* Y) {
+    __shared__ double ms[TS_K][TS_T + 1];
+    __shared__ double xs[TS_K][TS_T];
+    const int64_t i0 = (int64_t)blockIdx.x * TS_T;
+    const int32_t c0 = blockIdx.y * TS_T;
+    const int32_t tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    double acc[4][4] = {};
+    for (int64_t j0 = 0; j0 < N; j0 += TS_K) {
+        const bool below = i0 >= j0 + TS_K;  // every i of the tile > every j of the slab
+        for (int32_t t = threadIdx.x; t < TS_K * TS_T; t += 256) {
+            const int32_t ii = below ? t % TS_T : t / TS_K, kk = below ? t / TS_T : t % TS_K;
+            const int64_t i = i0 + ii, j = j0 + kk;
+            double v = 0.0;
+            if (i < N && j < N) v = i <= j ? tri[tri_idx(N, i, j)] : tri[tri_idx(N, j, i)];
+            ms[kk][ii] = v;
+        }
+        for (int32_t t = threadIdx.x; t < TS_K * TS_T; t += 256) {
+            const int32_t kk = t / TS_T, cc = t % TS_T;
+            const int64_t j = j0 + kk;
+            xs[kk][cc] = j < N && c0 + cc < b ? X[j * b + c0 + cc] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int32_t kk = 0; kk < TS_K; ++kk) {
+            double ma[4], xc[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                ma[u] = ms[kk][ty * 4 + u];
+                xc[u] = xs[kk][tx * 4 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] += ma[u] * xc[v];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t i = i0 + ty * 4 + u;
+            const int32_t c = c0 + tx * 4 + v;
+            if (i < N && c < b) Y[i * b + c] = acc[u][v];
+        }
 }
 
 // Partial sums of G = X^T diag(w) Y over chunks of GR rows: X is N x bx,
@@ -542,44 +634,84 @@ extern "C" int rfxp_host_symeig(int32_t n, const double* a, double* w, double* v
     return RFXP_OK;
 }
 
-extern "C" int rfxp_symacc_reset(rfxp_ctx* ctx, int64_t N) {
-    if (!ctx) return RFXP_ERR_INVALID;
-    if (N < 1 || N > 0x7ffffffeLL) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_reset: need 1 <= N < 2^31 - 1");
-    ctx->sa_N = N;
-    ctx->sa_nnz = 0;
+namespace rfxp {
+
+#ifndef RFXP_SA_STAGE_BYTES
+#define RFXP_SA_STAGE_BYTES (256LL << 20)
+#endif
+// Largest band of a host input staged on the device at once.
+constexpr int64_t SA_STAGE_BYTES = RFXP_SA_STAGE_BYTES;
+
+static int64_t sa_entries(int64_t N) { return N * (N + 1) / 2; }
+
+// Largest COO list of the sparse form: beyond it, the list (12 bytes an
+// entry) and its symmetric CSR (up to 16 bytes an entry) would take more
+// than the triangle of doubles (8 bytes an entry).
+static int64_t sa_list_limit(int64_t N) { return sa_entries(N) / 7 * 2; }
+
+// Bytes of the source holding packed entries [e0, e1) (e0 even for NF4), or
+// dense rows [e0, e1).
+static int64_t src_bytes(int kind, int64_t N, int64_t e0, int64_t e1) {
+    switch (kind) {
+        case SRC_F16: return 2 * (e1 - e0);
+        case SRC_F32: return 4 * (e1 - e0);
+        case SRC_I8: return e1 - e0;
+        case SRC_NF4: return (e1 - e0 + 1) / 2;
+        default: return 8 * N * (e1 - e0);
+    }
+}
+
+// Switches the accumulator to the dense form: the CSR is dropped, the list
+// summed into a zeroed triangle and released.
+static int symacc_to_dense(rfxp_ctx* ctx) {
+    const int64_t N = ctx->sa_N, ne = sa_entries(N);
+    ctx->sa_col.release();
+    ctx->sa_val.release();
     ctx->sa_csr_ok = false;
+    if (ctx->sa_tri.ensure((size_t)ne) != hipSuccess)
+        return set_error(ctx, RFXP_ERR_NOMEM,
+                         "rfxp_symacc: cannot allocate the dense triangle (" + std::to_string(8 * ne) + " bytes)");
+    fill_u32(ctx, (uint32_t*)ctx->sa_tri.p, 2 * ne, 0u);
+    if (ctx->sa_nnz > 0)
+        hipLaunchKernelGGL(k_sa_list_to_tri, dim3(nblk(ctx->sa_nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p,
+                           ctx->sa_j.p, ctx->sa_v.p, ctx->sa_nnz, N, ctx->sa_tri.p);
+    if (int rc = check_launch(ctx, "k_sa_list_to_tri")) return rc;
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->sa_i.release();
+    ctx->sa_j.release();
+    ctx->sa_v.release();
+    ctx->sa_dense = true;
+    ctx->sa_nnz = ne;
     return RFXP_OK;
 }
 
-extern "C" int64_t rfxp_symacc_nnz(rfxp_ctx* ctx) { return ctx ? ctx->sa_nnz : -1; }
-
-static int symacc_add(rfxp_ctx* ctx, SymSrc s, size_t src_bytes) {
-    const int64_t N = ctx->sa_N;
-    RFXP_HIP(ctx, hipSetDevice(ctx->device));
-    if (!is_device_pointer(s.p)) {  // host input: staged on the device
-        RFXP_HIP(ctx, ctx->sa_stage.ensure((src_bytes + 7) / 8));
-        RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_stage.p, s.p, src_bytes, hipMemcpyHostToDevice, ctx->stream));
-        s.p = ctx->sa_stage.p;
-    }
-    RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
-    for (int64_t r0 = 0; r0 < N; r0 += 0x7fffffffLL) {
-        const unsigned nr = (unsigned)std::min<int64_t>(0x7fffffffLL, N - r0);
-        hipLaunchKernelGGL(k_sa_rowcount, dim3(nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p);
-    }
+// Appends the nonzero entries of rows [r0, r1) (source s, staged) to the
+// list, or, when the list would pass its limit, switches to the dense form
+// and adds them there.  cnt: host scratch of N counts.
+static int symacc_add_rows_sparse(rfxp_ctx* ctx, const SymSrc& s, int64_t r0, int64_t r1, std::vector<int64_t>& cnt) {
+    const int64_t nr = r1 - r0;
+    hipLaunchKernelGGL(k_sa_rowcount, dim3((unsigned)nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p);
     if (int rc = check_launch(ctx, "k_sa_rowcount")) return rc;
-    std::vector<int64_t> cnt((size_t)N);
-    RFXP_HIP(ctx, hipMemcpyAsync(cnt.data(), ctx->sa_cnt.p, sizeof(int64_t) * N, hipMemcpyDeviceToHost, ctx->stream));
+    RFXP_HIP(ctx, hipMemcpyAsync(cnt.data() + r0, ctx->sa_cnt.p + r0, sizeof(int64_t) * nr, hipMemcpyDeviceToHost,
+                                 ctx->stream));
     RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
     int64_t tot = 0;
-    for (int64_t i = 0; i < N; ++i) {
+    for (int64_t i = r0; i < r1; ++i) {
         const int64_t c = cnt[i];
         cnt[i] = ctx->sa_nnz + tot;
         tot += c;
     }
     if (tot == 0) return RFXP_OK;
-    const int64_t need = ctx->sa_nnz + tot;
-    if ((size_t)need > ctx->sa_i.n) {  // grow by half again, keeping the entries
-        const size_t cap = std::max<size_t>((size_t)need, ctx->sa_i.n + ctx->sa_i.n / 2);
+    const int64_t need = ctx->sa_nnz + tot, limit = sa_list_limit(ctx->sa_N);
+    if (need > limit) {
+        if (int rc = symacc_to_dense(ctx)) return rc;
+        hipLaunchKernelGGL(k_sa_tri_add, dim3((unsigned)nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_tri.p);
+        return check_launch(ctx, "k_sa_tri_add");
+    }
+    if ((size_t)need > ctx->sa_i.n) {  // grow by half again (up to the limit), keeping the entries
+        ctx->sa_col.release();          // the CSR is rebuilt after an add anyway
+        ctx->sa_val.release();
+        const size_t cap = std::min<size_t>((size_t)limit, std::max<size_t>((size_t)need, ctx->sa_i.n + ctx->sa_i.n / 2));
         DevBuf<int32_t> ni, nj;
         DevBuf<float> nv;
         if (ni.ensure(cap) != hipSuccess || nj.ensure(cap) != hipSuccess || nv.ensure(cap) != hipSuccess) {
@@ -601,54 +733,125 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s, size_t src_bytes) {
         nj.release();
         nv.release();
     }
-    RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_cnt.p, cnt.data(), sizeof(int64_t) * N, hipMemcpyHostToDevice, ctx->stream));
-    for (int64_t r0 = 0; r0 < N; r0 += 0x7fffffffLL) {
-        const unsigned nr = (unsigned)std::min<int64_t>(0x7fffffffLL, N - r0);
-        hipLaunchKernelGGL(k_sa_rowemit, dim3(nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p,
-                           ctx->sa_i.p, ctx->sa_j.p, ctx->sa_v.p);
-    }
+    RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_cnt.p + r0, cnt.data() + r0, sizeof(int64_t) * nr, hipMemcpyHostToDevice,
+                                 ctx->stream));
+    hipLaunchKernelGGL(k_sa_rowemit, dim3((unsigned)nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p,
+                       ctx->sa_i.p, ctx->sa_j.p, ctx->sa_v.p);
     if (int rc = check_launch(ctx, "k_sa_rowemit")) return rc;
-    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // host counts buffer goes out of scope
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // cnt is reused by the next band
     ctx->sa_nnz = need;
-    ctx->sa_csr_ok = false;
     return RFXP_OK;
+}
+
+static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
+    const int64_t N = ctx->sa_N;
+    RFXP_HIP(ctx, hipSetDevice(ctx->device));
+    const bool host = !is_device_pointer(s.p);
+    const bool packed = s.kind != SRC_DENSE;
+    std::vector<int64_t> cnt;
+    if (!ctx->sa_dense) {
+        RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
+        cnt.resize((size_t)N);
+    }
+    ctx->sa_csr_ok = false;
+    int64_t r0 = 0;
+    while (r0 < N) {
+        // band of rows [r0, r1): everything for a device input, else at most
+        // SA_STAGE_BYTES of the source (at least one row)
+        int64_t r1 = N;
+        SymSrc band = s;
+        if (host) {
+            const int64_t e0 = packed ? tri_idx(N, r0, r0) : r0;
+            const int64_t b0 = packed && s.kind == SRC_NF4 ? e0 & ~1LL : e0;
+            auto bytes_to = [&](int64_t r) { return src_bytes(s.kind, N, b0, packed ? tri_idx(N, r, r) : r); };
+            if (bytes_to(N) > SA_STAGE_BYTES) {  // the largest r1 whose band fits, at least r0 + 1
+                r1 = r0 + 1;
+                for (int64_t step = int64_t(1) << 40; step > 0; step >>= 1)
+                    if (r1 + step <= N && bytes_to(r1 + step) <= SA_STAGE_BYTES) r1 += step;
+            }
+            const int64_t nbytes = bytes_to(r1);
+            const int64_t off = src_bytes(s.kind, N, 0, b0);
+            RFXP_HIP(ctx, ctx->sa_stage.ensure((size_t)(nbytes + 7) / 8));
+            RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_stage.p, (const unsigned char*)s.p + off, (size_t)nbytes,
+                                         hipMemcpyHostToDevice, ctx->stream));
+            band.p = ctx->sa_stage.p;
+            band.base = b0;
+        }
+        if (ctx->sa_dense) {
+            hipLaunchKernelGGL(k_sa_tri_add, dim3((unsigned)(r1 - r0)), dim3(SA_THREADS), 0, ctx->stream, band, r0,
+                               ctx->sa_tri.p);
+            if (int rc = check_launch(ctx, "k_sa_tri_add")) return rc;
+        } else if (int rc = symacc_add_rows_sparse(ctx, band, r0, r1, cnt)) {
+            return rc;
+        }
+        r0 = r1;
+    }
+    // the input (and the staging band) may be reused once this returns
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return RFXP_OK;
+}
+
+}  // namespace rfxp
+
+extern "C" int rfxp_symacc_reset(rfxp_ctx* ctx, int64_t N) {
+    if (!ctx) return RFXP_ERR_INVALID;
+    if (N < 1 || N > 0x7ffffffeLL) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_reset: need 1 <= N < 2^31 - 1");
+    ctx->sa_N = N;
+    ctx->sa_nnz = 0;
+    ctx->sa_csr_ok = false;
+    ctx->sa_dense = false;
+    // nothing of a previous accumulation is kept beyond what this N allows
+    ctx->sa_tri.release();
+    ctx->sa_stage.release();
+    if (ctx->sa_i.n > (size_t)sa_list_limit(N)) {
+        ctx->sa_i.release();
+        ctx->sa_j.release();
+        ctx->sa_v.release();
+        ctx->sa_col.release();
+        ctx->sa_val.release();
+    }
+    return RFXP_OK;
+}
+
+extern "C" int64_t rfxp_symacc_nnz(rfxp_ctx* ctx) { return ctx ? ctx->sa_nnz : -1; }
+
+extern "C" int64_t rfxp_symacc_device_bytes(rfxp_ctx* ctx) {
+    if (!ctx) return -1;
+    return (int64_t)(4 * (ctx->sa_i.n + ctx->sa_j.n + ctx->sa_col.n) + 4 * (ctx->sa_v.n + ctx->sa_val.n) +
+                     8 * (ctx->sa_cnt.n + ctx->sa_rowptr.n + ctx->sa_deg.n + ctx->sa_tri.n + ctx->sa_stage.n));
 }
 
 extern "C" int rfxp_symacc_add_upper(rfxp_ctx* ctx, int fmt, const void* tri, float scale, float zp) {
     if (!ctx) return RFXP_ERR_INVALID;
     if (ctx->sa_N < 1) return set_error(ctx, RFXP_ERR_STATE, "rfxp_symacc_add_upper: no accumulator (rfxp_symacc_reset)");
     if (!tri) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_add_upper: tri is NULL");
-    const int64_t N = ctx->sa_N, ne = N * (N + 1) / 2;
-    SymSrc s{tri, 0, scale, zp, N};
-    size_t bytes;
+    SymSrc s{tri, 0, scale, zp, ctx->sa_N, 0};
     switch (fmt) {
-        case RFXP_FMT_F16: s.kind = SRC_F16; bytes = 2 * (size_t)ne; break;
-        case RFXP_FMT_F32: s.kind = SRC_F32; bytes = 4 * (size_t)ne; break;
+        case RFXP_FMT_F16: s.kind = SRC_F16; break;
+        case RFXP_FMT_F32: s.kind = SRC_F32; break;
         case RFXP_FMT_I8:
             if (!std::isfinite(scale) || !std::isfinite(zp))
                 return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_add_upper: scale / zp must be finite");
             s.kind = SRC_I8;
-            bytes = (size_t)ne;
             break;
-        case RFXP_FMT_NF4: s.kind = SRC_NF4; bytes = (size_t)(ne + 1) / 2; break;
+        case RFXP_FMT_NF4: s.kind = SRC_NF4; break;
         default: return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_add_upper: format must be F16, F32, I8 or NF4");
     }
-    return symacc_add(ctx, s, bytes);
+    return symacc_add(ctx, s);
 }
 
 extern "C" int rfxp_symacc_add_dense(rfxp_ctx* ctx, const double* full) {
     if (!ctx) return RFXP_ERR_INVALID;
     if (ctx->sa_N < 1) return set_error(ctx, RFXP_ERR_STATE, "rfxp_symacc_add_dense: no accumulator (rfxp_symacc_reset)");
     if (!full) return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc_add_dense: full is NULL");
-    const int64_t N = ctx->sa_N;
-    SymSrc s{full, SRC_DENSE, 1.0f, 0.0f, N};
-    return symacc_add(ctx, s, sizeof(double) * (size_t)N * N);
+    SymSrc s{full, SRC_DENSE, 1.0f, 0.0f, ctx->sa_N, 0};
+    return symacc_add(ctx, s);
 }
 
 namespace rfxp {
 
 static int symacc_csr(rfxp_ctx* ctx) {
-    if (ctx->sa_csr_ok) return RFXP_OK;
+    if (ctx->sa_csr_ok || ctx->sa_dense) return RFXP_OK;
     const int64_t N = ctx->sa_N, nnz = ctx->sa_nnz;
     RFXP_HIP(ctx, ctx->sa_deg.ensure((size_t)N + 1));
     RFXP_HIP(ctx, ctx->sa_rowptr.ensure((size_t)N + 1));
@@ -681,6 +884,11 @@ static int symacc_csr(rfxp_ctx* ctx) {
 
 static int symacc_spmm(rfxp_ctx* ctx, const double* X, int32_t b, double* Y) {
     const int64_t N = ctx->sa_N;
+    if (ctx->sa_dense) {
+        const dim3 grid((unsigned)((N + TS_T - 1) / TS_T), (unsigned)((b + TS_T - 1) / TS_T));
+        hipLaunchKernelGGL(k_sa_tri_spmm, grid, dim3(256), 0, ctx->stream, ctx->sa_tri.p, X, N, b, Y);
+        return check_launch(ctx, "k_sa_tri_spmm");
+    }
     hipLaunchKernelGGL(k_sa_spmm, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, ctx->stream, ctx->sa_rowptr.p,
                        ctx->sa_col.p, ctx->sa_val.p, X, N, b, Y);
     return check_launch(ctx, "k_sa_spmm");

@@ -95,6 +95,8 @@ def load(path: str = LIB_PATH):
     L.rfxp_symacc_reset.argtypes = [vp, i64]
     L.rfxp_symacc_nnz.argtypes = [vp]
     L.rfxp_symacc_nnz.restype = i64
+    L.rfxp_symacc_device_bytes.argtypes = [vp]
+    L.rfxp_symacc_device_bytes.restype = i64
     L.rfxp_symacc_add_upper.argtypes = [vp, C.c_int, vp, C.c_float, C.c_float]
     L.rfxp_symacc_add_dense.argtypes = [vp, vp]
     L.rfxp_symacc_apply.argtypes = [vp, vp, i32, vp]
@@ -400,6 +402,9 @@ class Context:
 
     def symacc_nnz(self) -> int:
         return self._L.rfxp_symacc_nnz(self.h)
+
+    def symacc_device_bytes(self) -> int:
+        return self._L.rfxp_symacc_device_bytes(self.h)
 
     def symacc_add_upper(self, fmt: int, tri, scale: float = 1.0, zp: float = 0.0):
         """tri: a device tensor or a host numpy array (packed triangle)."""

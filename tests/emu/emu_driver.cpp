@@ -14,11 +14,22 @@
 //      1 when the 64 guard bytes after the output are untouched, int64 the
 //      recount counter (mode 1); for mode 2: float min, float max; for mode
 //      4: N x r float32 Y
+//
+// mode 5 (the symmetric accumulator, rfxp_symacc_*) reads instead: int64 N,
+//      int32 contributions, int32 b, int32 rank, int32 iters, then per
+//      contribution int32 fmt (-1: dense N x N double), int32 on_device (0:
+//      passed as host memory), float scale, float zp, int64 nbytes, the
+//      bytes; then N x b double X.  It writes int32 status, then per
+//      contribution int64 nnz, int64 device bytes and the N x b double
+//      Y = M X after that add; then, with rank > 0, the N x rank
+//      column-major factor A and rank Ritz values.
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 #include <vector>
+
+#include <hip/hip_runtime.h>
 
 #include "rfx_prox.h"
 
@@ -30,6 +41,95 @@ static void rd(FILE* f, T* p, size_t n) {
     }
 }
 
+extern "C" void emu_track_host_memory(int on);
+
+static int run_symacc(FILE* f, FILE* o) {
+    int64_t N;
+    int32_t nc, b, rank, iters;
+    rd(f, &N, 1);
+    rd(f, &nc, 1);
+    rd(f, &b, 1);
+    rd(f, &rank, 1);
+    rd(f, &iters, 1);
+    struct Contrib {
+        int32_t fmt, on_device;
+        float scale, zp;
+        std::vector<unsigned char> bytes;
+    };
+    std::vector<Contrib> cs((size_t)nc);
+    for (auto& c : cs) {
+        int64_t nb;
+        rd(f, &c.fmt, 1);
+        rd(f, &c.on_device, 1);
+        rd(f, &c.scale, 1);
+        rd(f, &c.zp, 1);
+        rd(f, &nb, 1);
+        c.bytes.resize((size_t)nb);
+        rd(f, c.bytes.data(), c.bytes.size());
+    }
+    std::vector<double> X((size_t)N * b);
+    rd(f, X.data(), X.size());
+    fclose(f);
+    emu_track_host_memory(1);
+    rfxp_ctx* ctx = nullptr;
+    auto fail = [&](int code) {
+        char msg[512] = {0};
+        if (ctx) rfxp_last_error(ctx, msg, sizeof msg);
+        fprintf(stderr, "status %d: %s\n", code, msg);
+        fwrite(&code, 4, 1, o);
+        fclose(o);
+        return 0;
+    };
+    int rc = rfxp_ctx_create(0, &ctx);
+    if (rc) return fail(rc);
+    if ((rc = rfxp_symacc_reset(ctx, N))) return fail(rc);
+    double *Xd = nullptr, *Yd = nullptr;
+    hipMalloc((void**)&Xd, 8 * X.size());
+    hipMalloc((void**)&Yd, 8 * X.size());
+    hipMemcpy(Xd, X.data(), 8 * X.size(), hipMemcpyHostToDevice);
+    std::vector<unsigned char> out;
+    auto put = [&](const void* p, size_t n) {
+        out.insert(out.end(), (const unsigned char*)p, (const unsigned char*)p + n);
+    };
+    std::vector<double> Y(X.size());
+    for (auto& c : cs) {
+        void* src = c.bytes.data();
+        void* dsrc = nullptr;
+        if (c.on_device) {
+            hipMalloc(&dsrc, c.bytes.size());
+            hipMemcpy(dsrc, c.bytes.data(), c.bytes.size(), hipMemcpyHostToDevice);
+            src = dsrc;
+        }
+        rc = c.fmt < 0 ? rfxp_symacc_add_dense(ctx, (const double*)src)
+                       : rfxp_symacc_add_upper(ctx, c.fmt, src, c.scale, c.zp);
+        if (dsrc) hipFree(dsrc);
+        if (rc) return fail(rc);
+        const int64_t nnz = rfxp_symacc_nnz(ctx), bytes = rfxp_symacc_device_bytes(ctx);
+        if ((rc = rfxp_symacc_apply(ctx, Xd, b, Yd))) return fail(rc);
+        hipMemcpy(Y.data(), Yd, 8 * Y.size(), hipMemcpyDeviceToHost);
+        put(&nnz, 8);
+        put(&bytes, 8);
+        put(Y.data(), 8 * Y.size());
+    }
+    if (rank > 0) {
+        double* Ad = nullptr;
+        hipMalloc((void**)&Ad, 8 * (size_t)N * rank);
+        std::vector<double> A((size_t)N * rank), ev((size_t)rank);
+        if ((rc = rfxp_symacc_factor(ctx, rank, iters, 7, Ad, ev.data()))) return fail(rc);
+        hipMemcpy(A.data(), Ad, 8 * A.size(), hipMemcpyDeviceToHost);
+        hipFree(Ad);
+        put(A.data(), 8 * A.size());
+        put(ev.data(), 8 * ev.size());
+    }
+    hipFree(Xd);
+    hipFree(Yd);
+    fwrite(&rc, 4, 1, o);
+    fwrite(out.data(), 1, out.size(), o);
+    fclose(o);
+    rfxp_ctx_destroy(ctx);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc != 3) return 2;
     FILE* f = fopen(argv[1], "rb");
@@ -38,6 +138,10 @@ int main(int argc, char** argv) {
     int64_t N, r0, r1;
     float scale, zp;
     rd(f, &mode, 1);
+    if (mode == 5) {
+        FILE* o = fopen(argv[2], "wb");
+        return o ? run_symacc(f, o) : 2;
+    }
     rd(f, &N, 1);
     rd(f, &T, 1);
     rd(f, &nleaf, 1);

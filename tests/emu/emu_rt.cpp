@@ -21,6 +21,8 @@
 #include <time.h>
 
 #include <chrono>
+#include <iterator>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -316,14 +318,22 @@ static double now_ms() {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
 
+// Live hipMalloc allocations (base -> bytes), so that pointers outside them
+// can be reported as host memory when the driver asks for that.
+static std::map<uintptr_t, size_t> g_allocs;
+static bool g_track_host = false;
+extern "C" void emu_track_host_memory(int on) { g_track_host = on != 0; }
+
 hipError_t hipMalloc(void** p, size_t n) {
     if (!p) return hipErrorInvalidValue;
     *p = malloc(n ? n : 1);
     if (!*p) return emu::g_last = hipErrorOutOfMemory;
     memset(*p, 0xAB, n ? n : 1);  // device memory starts with garbage
+    g_allocs[(uintptr_t)*p] = n ? n : 1;
     return hipSuccess;
 }
 hipError_t hipFree(void* p) {
+    g_allocs.erase((uintptr_t)p);
     free(p);
     return hipSuccess;
 }
@@ -382,10 +392,20 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int) {
     return hipErrorInvalidValue;
 }
 hipError_t hipPointerGetAttributes(hipPointerAttribute_t* a, const void* p) {
-    // every pointer is "device" memory in the emulation
+    // every pointer is "device" memory in the emulation, unless host memory
+    // is tracked: then only pointers into hipMalloc allocations are
     memset(a, 0, sizeof(*a));
     a->type = hipMemoryTypeDevice;
     a->devicePointer = (void*)p;
+    if (g_track_host) {
+        auto it = g_allocs.upper_bound((uintptr_t)p);
+        const bool dev = it != g_allocs.begin() && (uintptr_t)p < std::prev(it)->first + std::prev(it)->second;
+        if (!dev) {
+            a->type = hipMemoryTypeHost;
+            a->devicePointer = nullptr;
+            a->hostPointer = (void*)p;
+        }
+    }
     return hipSuccess;
 }
 hipError_t hipFuncSetAttribute(const void*, hipFuncAttribute, int v) {

@@ -202,3 +202,157 @@ def test_line_fit_layout_host_check(driver, shape):
     assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
     lines = float(r.stdout.split("lines_per_run=")[1].split()[0])
     assert lines < 1.1 if shape[2] != "2" else True
+
+
+# ---- the symmetric accumulator behind the low-rank class (rfxp_symacc_*) ----
+
+def _sym(upper_vals, n):
+    d = np.zeros((n, n))
+    d[np.triu_indices(n)] = upper_vals
+    return d + np.triu(d, 1).T
+
+
+def _values(fmt, data, n, scale=1.0, zp=0.0):
+    """Entries i <= j of a contribution as the accumulator reads them
+    (cuda/rf_proximity_lowrank.cu:199-240, 654-685, 744-789): FP16 as is, F32
+    as is, INT8 and NF4 dequantised then rounded to FP16, a dense double
+    matrix's upper triangle rounded through float to FP16."""
+    ne = n * (n + 1) // 2
+    if fmt == O.FMT_F16:
+        return data.view(np.float16).astype(np.float64)
+    if fmt == O.FMT_F32:
+        return data.astype(np.float64)
+    if fmt == O.FMT_I8:
+        v = (data.astype(np.float32) - np.float32(zp)) * np.float32(scale)
+        return v.astype(np.float16).astype(np.float64)
+    if fmt == O.FMT_NF4:
+        nib = np.stack([data & 15, data >> 4], axis=1).ravel()[:ne].astype(np.int64)
+        v = np.where(nib <= 7, nib.astype(np.float32) / np.float32(7), -(nib - 8).astype(np.float32) / np.float32(7))
+        return v.astype(np.float16).astype(np.float64)
+    return data[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def emulate_symacc(driver, tmp_path, n, contribs, X, rank=0, iters=0):
+    """contribs: (fmt or -1 for dense, array, on_device, scale, zp).  Returns
+    per add (nnz, device bytes, M X) and, with rank, (A N x rank, Ritz values)."""
+    b = X.shape[1]
+    inp, outp = tmp_path / "sa_in.bin", tmp_path / "sa_out.bin"
+    with open(inp, "wb") as f:
+        f.write(struct.pack("<iqiiii", 5, n, len(contribs), b, rank, iters))
+        for fmt, arr, on_dev, scale, zp in contribs:
+            raw = np.ascontiguousarray(arr).tobytes()
+            f.write(struct.pack("<iiffq", fmt, int(on_dev), np.float32(scale), np.float32(zp), len(raw)))
+            f.write(raw)
+        np.ascontiguousarray(X, np.float64).tofile(f)
+    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+    r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
+                       text=True, env=env)
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]
+    raw = outp.read_bytes()
+    assert struct.unpack_from("<i", raw, 0)[0] == 0, r.stderr[-2000:]
+    off, steps = 4, []
+    for _ in contribs:
+        nnz, nbytes = struct.unpack_from("<qq", raw, off)
+        Y = np.frombuffer(raw, np.float64, n * b, off + 16).reshape(n, b)
+        steps.append((nnz, nbytes, Y))
+        off += 16 + 8 * n * b
+    if not rank:
+        return steps, None
+    A = np.frombuffer(raw, np.float64, n * rank, off).reshape(rank, n).T
+    ev = np.frombuffer(raw, np.float64, rank, off + 8 * n * rank)
+    return steps, (A, ev)
+
+
+def _check_steps(steps, contribs, n, X):
+    ne = n * (n + 1) // 2
+    limit = ne // 7 * 2                 # largest list of the sparse form
+    M = np.zeros((n, n))
+    listed, dense = 0, False
+    for (nnz, nbytes, Y), (fmt, arr, _, scale, zp) in zip(steps, contribs):
+        v = _values(fmt, arr, n, scale, zp)
+        M += _sym(v, n)
+        listed += int((v != 0).sum())
+        dense = dense or listed > limit
+        assert nnz == (ne if dense else listed)
+        # the bound: the triangle in doubles, three N + 1 count arrays, one
+        # staged band (at most 256 bytes in this build, or one row)
+        assert nbytes <= 8 * ne + 24 * (n + 1) + max(264, 8 * n), (nbytes, 8 * ne)
+        want = M @ X
+        assert np.abs(Y - want).max() <= 1e-12 * np.abs(M).sum(axis=1).max() * np.abs(X).max()
+    return M
+
+
+def test_symacc_sparse_then_dense(driver, tmp_path):
+    """Sparse contributions in host and device memory, then one whose early
+    rows are sparse and later rows dense, so that the list passes its limit
+    within a contribution and the accumulator changes form between two
+    staged bands; then dense-form adds from host (one row per band) and
+    device memory.  M X after every add against the dense sum; the
+    full-rank factor against numpy's eigendecomposition."""
+    rng = np.random.default_rng(51)
+    n = 45
+    ne = n * (n + 1) // 2
+    f16 = np.zeros(ne, np.float16)
+    hit = rng.random(ne) < 0.05
+    f16[hit] = rng.standard_normal(int(hit.sum())).astype(np.float16)
+    q8 = np.full(ne, 3, np.int8)
+    hit = rng.random(ne) < 0.08
+    q8[hit] = rng.integers(-128, 128, int(hit.sum()))
+    rows = np.repeat(np.arange(n), np.arange(n, 0, -1))
+    f32 = rng.standard_normal(ne).astype(np.float32)
+    f32[(rows < 25) & (rng.random(ne) < 0.9)] = 0      # sparse early rows, dense late rows
+    p4 = rng.integers(0, 256, (ne + 1) // 2).astype(np.uint8)
+    full = rng.standard_normal((n, n))
+    f16b = rng.standard_normal(ne).astype(np.float16)
+    contribs = [(O.FMT_F16, f16.view(np.uint16), False, 1.0, 0.0),
+                (O.FMT_I8, q8, True, 0.01, 3.0),
+                (O.FMT_F32, f32, False, 1.0, 0.0),
+                (O.FMT_NF4, p4, False, 1.0, 0.0),
+                (-1, full, False, 1.0, 0.0),
+                (O.FMT_F16, f16b.view(np.uint16), True, 1.0, 0.0)]
+    X = rng.standard_normal((n, 70))                  # two column tiles of the dense product
+    steps, (A, ev) = emulate_symacc(driver, tmp_path, n, contribs, X, rank=n, iters=3)
+    assert steps[1][0] < ne and steps[2][0] == ne     # the switch came within the F32 add
+    M = _check_steps(steps, contribs, n, X)
+    w, V = np.linalg.eigh(M)
+    w = np.maximum(w, 0.0)
+    want = (V * w) @ V.T
+    assert np.linalg.norm(A @ A.T - want) <= 1e-9 * np.linalg.norm(want)
+    assert np.allclose(np.sort(np.maximum(ev, 0))[::-1], np.sort(w)[::-1], atol=1e-9 * w.max())
+
+
+def test_symacc_stays_sparse(driver, tmp_path):
+    """Contributions that never reach the list's limit: the CSR product and
+    the factor of the sparse form."""
+    rng = np.random.default_rng(52)
+    n = 130
+    ne = n * (n + 1) // 2
+    contribs = []
+    for k in range(4):
+        f16 = np.zeros(ne, np.float16)
+        hit = rng.random(ne) < 0.04
+        f16[hit] = rng.standard_normal(int(hit.sum())).astype(np.float16)
+        contribs.append((O.FMT_F16, f16.view(np.uint16), bool(k % 2), 1.0, 0.0))
+    X = rng.standard_normal((n, 5))
+    steps, (A, ev) = emulate_symacc(driver, tmp_path, n, contribs, X, rank=n, iters=3)
+    assert steps[-1][0] < ne // 7 * 2
+    M = _check_steps(steps, contribs, n, X)
+    w, V = np.linalg.eigh(M)
+    w = np.maximum(w, 0.0)
+    want = (V * w) @ V.T
+    assert np.linalg.norm(A @ A.T - want) <= 1e-9 * np.linalg.norm(want)
+
+
+def test_symacc_dense_from_the_first_add(driver, tmp_path):
+    """A first contribution denser than the limit: the dense form from the
+    start (empty list), host NF4 bands that start at odd entries."""
+    rng = np.random.default_rng(53)
+    n = 77
+    ne = n * (n + 1) // 2
+    p4 = rng.integers(0, 256, (ne + 1) // 2).astype(np.uint8)
+    full = rng.standard_normal((n, n))
+    contribs = [(O.FMT_NF4, p4, False, 1.0, 0.0), (-1, full, True, 1.0, 0.0), (O.FMT_NF4, p4, True, 1.0, 0.0)]
+    X = rng.standard_normal((n, 3))
+    steps, _ = emulate_symacc(driver, tmp_path, n, contribs, X)
+    assert steps[0][0] == ne
+    _check_steps(steps, contribs, n, X)

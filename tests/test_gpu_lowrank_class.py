@@ -56,44 +56,48 @@ def random_forest_trees(rng, n, t, nnode=9):
 
 
 def test_symacc_apply_matches_dense_sum(gpu_ctx):
+    """M X against the dense sum of the same contributions after every add,
+    through the change from the entry list to the dense triangle (the three
+    trees list 3,867 entries, below the limit of 9,472; the INT8 add passes
+    it); the stored-entry count and the memory bound at each step."""
     rng = np.random.default_rng(41)
     n = 257
     ne = n * (n + 1) // 2
+    limit = ne // 7 * 2
+    X = rng.standard_normal((n, 70))
+    Xd = dev(X)
     gpu_ctx.symacc_reset(n)
     M = np.zeros((n, n))
-    nnz = 0
+    listed = 0
+
+    def added(v):
+        nonlocal M, listed
+        M += sym_from_upper(v, n)
+        listed += int((v != 0).sum())
+        assert gpu_ctx.symacc_nnz() == (ne if listed > limit else listed)
+        assert gpu_ctx.symacc_device_bytes() <= 8 * ne + 24 * (n + 1) + 8 * n * n
+        got = gpu_ctx.symacc_apply(Xd).cpu().numpy()
+        assert np.abs(got - M @ X).max() <= 1e-12 * np.abs(M).sum(axis=1).max() * np.abs(X).max()
+
     for k, (ns, nx, nin) in enumerate(random_forest_trees(rng, n, 3)):
         tri = O.tree_upper(O.FMT_F16, ns, nx, nin)
         gpu_ctx.symacc_add_upper(O.FMT_F16, tri if k % 2 else dev(tri))  # host and device inputs
-        v = tri.view(np.float16).astype(np.float64)
-        M += sym_from_upper(v, n)
-        nnz += int((v != 0).sum())
+        added(tri.view(np.float16).astype(np.float64))
     q8 = rng.integers(-128, 128, ne).astype(np.int8)
     q8[rng.random(ne) < 0.5] = 3                      # (3 - 3) * s = 0: not stored
     gpu_ctx.symacc_add_upper(O.FMT_I8, dev(q8), 0.01, 3.0)
-    v = i8_values(q8, 0.01, 3.0)
-    M += sym_from_upper(v, n)
-    nnz += int((v != 0).sum())
+    added(i8_values(q8, 0.01, 3.0))
     p4 = rng.integers(0, 256, (ne + 1) // 2).astype(np.uint8)
     gpu_ctx.symacc_add_upper(O.FMT_NF4, p4)
-    v = nf4_values(p4, ne)
-    M += sym_from_upper(v, n)
-    nnz += int((v != 0).sum())
+    added(nf4_values(p4, ne))
     f32 = rng.standard_normal(ne).astype(np.float32)
     f32[rng.random(ne) < 0.3] = 0
     gpu_ctx.symacc_add_upper(O.FMT_F32, dev(f32))
-    M += sym_from_upper(f32.astype(np.float64), n)
-    nnz += int((f32 != 0).sum())
+    added(f32.astype(np.float64))
     full = rng.standard_normal((n, n))                 # not symmetric: only i <= j is read
     gpu_ctx.symacc_add_dense(full)
-    v = full[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64)
-    M += sym_from_upper(v, n)
-    nnz += int((v != 0).sum())
-    assert gpu_ctx.symacc_nnz() == nnz
-    X = rng.standard_normal((n, 70))
-    got = gpu_ctx.symacc_apply(dev(X)).cpu().numpy()
-    want = M @ X
-    assert np.abs(got - want).max() <= 1e-12 * np.abs(M).sum(axis=1).max() * np.abs(X).max()
+    added(full[np.triu_indices(n)].astype(np.float32).astype(np.float16).astype(np.float64))
+    assert listed > limit                              # the dense form was reached
 
 
 def test_symacc_factor_full_rank_is_positive_part(gpu_ctx):
