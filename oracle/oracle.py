@@ -78,9 +78,9 @@ def lib():
         L.orc_index_free.argtypes = [C.c_void_p]
         L.orc_upper_from_counts.argtypes = [_u16, _i32, C.c_int64, C.c_int, C.c_float, C.c_float,
                                             C.c_void_p]
-        L.orc_topk_all.argtypes = [_i32, C.c_int64, C.c_int32, _i32, C.c_int64, C.c_int32,
+        L.orc_topk_all.argtypes = [_i32, C.c_int64, C.c_int32, C.c_int32, _i32, C.c_int64, C.c_int32,
                                    C.c_void_p, _i32, _u16, C.c_int]
-        L.orc_topk_oob.argtypes = [_i32, _u8, C.c_int64, C.c_int32, C.c_int64, C.c_int32, C.c_int,
+        L.orc_topk_oob.argtypes = [_i32, _u8, C.c_int64, C.c_int32, C.c_int32, C.c_int64, C.c_int32, C.c_int,
                                    _i32, _u16, _f32]
         L.orc_topk_oob.restype = C.c_int32
         L.orc_lowrank_pv.argtypes = [_i32, C.c_int64, C.c_int32, C.c_int32, _f64, C.c_int32, _f64]
@@ -284,24 +284,29 @@ def u8_scale_from_minmax(vmin, vmax):
 
 # ---- top-K ------------------------------------------------------------------
 
-def topk_all(ref_leaf_tn, qleaf_qt, K, exclude=None, threads=0):
+NO_NLEAF = 2**31 - 1   # without nleaf only negative labels are invalid
+
+
+def topk_all(ref_leaf_tn, qleaf_qt, K, exclude=None, threads=0, nleaf=None):
+    """Labels outside [0, nleaf) match nothing (negative ones when nleaf is None)."""
     t, n = ref_leaf_tn.shape
     q = qleaf_qt.shape[0]
     idx = np.empty((q, K), dtype=np.int32)
     cnt = np.empty((q, K), dtype=np.uint16)
     ex = None if exclude is None else _c(exclude, np.int32)
-    lib().orc_topk_all(_c(ref_leaf_tn, np.int32).ravel(), n, t, _c(qleaf_qt, np.int32).ravel(), q,
-                       K, ex.ctypes.data if ex is not None else None, idx, cnt, threads)
+    lib().orc_topk_all(_c(ref_leaf_tn, np.int32).ravel(), n, t, NO_NLEAF if nleaf is None else nleaf,
+                       _c(qleaf_qt, np.int32).ravel(), q, K, ex.ctypes.data if ex is not None else None, idx, cnt,
+                       threads)
     return idx, cnt
 
 
-def topk_oob(leaf_tn, oob_tn, q, K, exclude_self=True):
+def topk_oob(leaf_tn, oob_tn, q, K, exclude_self=True, nleaf=None):
     t, n = leaf_tn.shape
     idx = np.empty(K, dtype=np.int32)
     cnt = np.empty(K, dtype=np.uint16)
     sc = np.empty(K, dtype=np.float32)
-    m = lib().orc_topk_oob(_c(leaf_tn, np.int32).ravel(), _c(oob_tn, np.uint8).ravel(), n, t, q, K,
-                           int(exclude_self), idx, cnt, sc)
+    m = lib().orc_topk_oob(_c(leaf_tn, np.int32).ravel(), _c(oob_tn, np.uint8).ravel(), n, t,
+                           NO_NLEAF if nleaf is None else nleaf, q, K, int(exclude_self), idx, cnt, sc)
     return idx[:m], cnt[:m], sc[:m]
 
 

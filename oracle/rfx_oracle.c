@@ -462,7 +462,7 @@ static inline void topk_insert(int32_t K, int32_t* n_have, int32_t* bi, uint16_t
     *n_have = n + 1;
 }
 
-void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* qleaf, int64_t Q,
+void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, int32_t nleaf, const int32_t* qleaf, int64_t Q,
                   int32_t K, const int32_t* exclude, int32_t* idx_out, uint16_t* cnt_out,
                   int threads) {
 #ifdef _OPENMP
@@ -480,6 +480,7 @@ void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* 
             memset(cnt, 0, sizeof(uint16_t) * (size_t)N);
             for (int32_t t = 0; t < T; ++t) {
                 int32_t ql = qleaf[q * T + t];
+                if (ql < 0 || ql >= nleaf) continue;   /* an invalid label matches nothing */
                 const int32_t* rl = ref_leaf + (int64_t)t * N;
                 for (int64_t j = 0; j < N; ++j) cnt[j] += (rl[j] == ql);
             }
@@ -498,7 +499,7 @@ void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* 
     }
 }
 
-int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int64_t q,
+int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int64_t q,
                      int32_t K, int exclude_self, int32_t* idx_out, uint16_t* cnt_out,
                      float* score_out) {
     uint16_t* cnt = (uint16_t*)calloc((size_t)(N > 0 ? N : 1), sizeof(uint16_t));
@@ -507,6 +508,7 @@ int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t
         if (!oob[(int64_t)t * N + q]) continue;
         n_oob++;
         int32_t ql = leaf[(int64_t)t * N + q];
+        if (ql < 0 || ql >= nleaf) continue;   /* the tree counts in |OOB(q)|, its label matches nothing */
         const int32_t* rl = leaf + (int64_t)t * N;
         for (int64_t j = 0; j < N; ++j)
             if (rl[j] == ql && !(exclude_self && j == q)) cnt[j]++;

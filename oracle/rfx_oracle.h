@@ -116,16 +116,19 @@ void orc_upper_from_counts(const uint16_t* U, const int32_t* nout, int64_t N, in
 /* ---- top-K --------------------------------------------------------------- */
 
 /* All-trees semantics (python/randomforest_py.cpp:2496-2568, :624-672):
- * count(q,j) = #{t : qleaf[q*T+t] == ref_leaf[t*N+j]}; the K best j by
- * (count desc, j asc), zero counts included; exclude[q] >= 0 removes that j.
- * exclude may be NULL.  idx_out/cnt_out are Q x K. */
-void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, const int32_t* qleaf, int64_t Q,
+ * count(q,j) = #{t : qleaf[q*T+t] == ref_leaf[t*N+j], label in [0, nleaf)};
+ * the K best j by (count desc, j asc), zero counts included; exclude[q] >= 0
+ * removes that j.  exclude may be NULL.  idx_out/cnt_out are Q x K.  The
+ * reference compares its int16 labels as they are and never produces one
+ * outside [0, nleaf); here, as in the library, such a label matches nothing. */
+void orc_topk_all(const int32_t* ref_leaf, int64_t N, int32_t T, int32_t nleaf, const int32_t* qleaf, int64_t Q,
                   int32_t K, const int32_t* exclude, int32_t* idx_out, uint16_t* cnt_out, int threads);
 
 /* OOB-query semantics (src/rf_random_forest.cpp:4677-4782): trees where q is
- * OOB, j != q when exclude_self, counts > 0 only, ordered (count desc, j asc).
- * Returns the number of results (<= K). */
-int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int64_t q,
+ * OOB, j != q when exclude_self, counts > 0 only, ordered (count desc, j asc);
+ * a query label outside [0, nleaf) matches nothing (its tree still counts in
+ * |OOB(q)|).  Returns the number of results (<= K). */
+int32_t orc_topk_oob(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T, int32_t nleaf, int64_t q,
                      int32_t K, int exclude_self, int32_t* idx_out, uint16_t* cnt_out,
                      float* score_out);
 

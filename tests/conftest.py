@@ -29,3 +29,17 @@ def gpu_ctx():
     ctx.use_torch_stream()
     yield ctx
     ctx.close()
+
+
+@pytest.fixture(scope="session")
+def emu_driver():
+    """The CPU emulation build of the library (tests/emu/_build/emu_driver),
+    made once per session; skipped where ROCm's host clang++ is absent."""
+    import subprocess
+
+    if not os.path.exists("/opt/rocm/llvm/bin/clang++"):
+        pytest.skip("host clang++ of ROCm not present")
+    emu = os.path.join(REPO, "tests", "emu")
+    r = subprocess.run(["make", "-C", emu, "-j8"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
+    return os.path.join(emu, "_build", "emu_driver")

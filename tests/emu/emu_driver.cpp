@@ -23,10 +23,23 @@
 //      contribution int64 nnz, int64 device bytes and the N x b double
 //      Y = M X after that add; then, with rank > 0, the N x rank
 //      column-major factor A and rank Ritz values.
+//
+// mode 6 (a script of C ABI calls, for any function of include/rfx_prox.h)
+//      reads instead: int32 buffers, then per buffer int32 host (1: plain
+//      host memory, else hipMalloc), int32 want (written back), int64
+//      nbytes, int32 has_data, the bytes when has_data (else zero-filled);
+//      then int32 calls, per call int32 name length, the name, int32 args,
+//      per argument int32 tag (0 integer, 1 real, 2 buffer pointer, 3 NULL,
+//      4 the context), int64 value (the integer, the real's bits, or the
+//      buffer index), int64 byte offset into the buffer.  It writes int32 0,
+//      int32 calls, int64 each call's result (-999999 for an unknown name
+//      or a wrong argument count, and the script stops there), then the
+//      bytes of every buffer with want set.
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <string>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -130,6 +143,102 @@ static int run_symacc(FILE* f, FILE* o) {
     return 0;
 }
 
+struct Arg {
+    int64_t i;
+    double f;
+    void* p;
+};
+struct CallEntry {
+    const char* name;
+    int nargs;
+    int64_t (*fn)(const Arg*);
+};
+static const CallEntry CALLS[] = {
+#include "emu_calls.inc"
+};
+
+static int run_script(FILE* f, FILE* o) {
+    int32_t nb;
+    rd(f, &nb, 1);
+    std::vector<void*> bufs((size_t)nb, nullptr);
+    std::vector<int64_t> sizes((size_t)nb);
+    std::vector<int32_t> want((size_t)nb), host((size_t)nb);
+    emu_track_host_memory(1);
+    for (int32_t k = 0; k < nb; ++k) {
+        int32_t has;
+        rd(f, &host[k], 1);
+        rd(f, &want[k], 1);
+        rd(f, &sizes[k], 1);
+        rd(f, &has, 1);
+        const size_t n = (size_t)sizes[k];
+        if (host[k]) bufs[k] = malloc(n ? n : 1);
+        else hipMalloc(&bufs[k], n);
+        if (has) rd(f, (unsigned char*)bufs[k], n);
+        else memset(bufs[k], 0, n);
+    }
+    rfxp_ctx* ctx = nullptr;
+    int rc = rfxp_ctx_create(0, &ctx);
+    int32_t nc;
+    rd(f, &nc, 1);
+    std::vector<int64_t> results;
+    for (int32_t c = 0; c < nc && rc == 0; ++c) {
+        int32_t len, na;
+        rd(f, &len, 1);
+        std::string name((size_t)len, ' ');
+        rd(f, &name[0], (size_t)len);
+        rd(f, &na, 1);
+        std::vector<Arg> args((size_t)na);
+        for (auto& a : args) {
+            int32_t tag;
+            int64_t v, off;
+            rd(f, &tag, 1);
+            rd(f, &v, 1);
+            rd(f, &off, 1);
+            a = Arg{0, 0.0, nullptr};
+            if (tag == 0) {
+                a.i = v;
+                a.f = (double)v;
+            } else if (tag == 1) {
+                memcpy(&a.f, &v, 8);
+                a.i = (int64_t)a.f;
+            } else if (tag == 2) {
+                a.p = (unsigned char*)bufs.at((size_t)v) + off;
+            } else if (tag == 4) {
+                a.p = ctx;
+            }
+        }
+        const CallEntry* e = nullptr;
+        for (const auto& x : CALLS)
+            if (name == x.name) e = &x;
+        if (!e || e->nargs != na) {
+            fprintf(stderr, "script: unknown call or argument count: %s/%d\n", name.c_str(), na);
+            results.push_back(-999999);
+            break;
+        }
+        results.push_back(e->fn(args.data()));
+        rfxp_sync(ctx);
+    }
+    fclose(f);
+    if (rc) {
+        fwrite(&rc, 4, 1, o);
+        fclose(o);
+        return 0;
+    }
+    const int32_t zero = 0, nres = (int32_t)results.size();
+    fwrite(&zero, 4, 1, o);
+    fwrite(&nres, 4, 1, o);
+    fwrite(results.data(), 8, results.size(), o);
+    for (int32_t k = 0; k < nb; ++k)
+        if (want[k]) fwrite(bufs[k], 1, (size_t)sizes[k], o);
+    fclose(o);
+    rfxp_ctx_destroy(ctx);
+    for (int32_t k = 0; k < nb; ++k) {
+        if (host[k]) free(bufs[k]);
+        else hipFree(bufs[k]);
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc != 3) return 2;
     FILE* f = fopen(argv[1], "rb");
@@ -138,9 +247,10 @@ int main(int argc, char** argv) {
     int64_t N, r0, r1;
     float scale, zp;
     rd(f, &mode, 1);
-    if (mode == 5) {
+    if (mode == 5 || mode == 6) {
         FILE* o = fopen(argv[2], "wb");
-        return o ? run_symacc(f, o) : 2;
+        if (!o) return 2;
+        return mode == 5 ? run_symacc(f, o) : run_script(f, o);
     }
     rd(f, &N, 1);
     rd(f, &T, 1);

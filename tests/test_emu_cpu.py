@@ -18,17 +18,11 @@ import oracle as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 EMU = os.path.join(HERE, "emu")
-DRIVER = os.path.join(EMU, "_build", "emu_driver")
-CLANG = "/opt/rocm/llvm/bin/clang++"
-
-pytestmark = pytest.mark.skipif(not os.path.exists(CLANG), reason="host clang++ of ROCm not present")
 
 
 @pytest.fixture(scope="module")
-def driver():
-    r = subprocess.run(["make", "-C", EMU, "-j8"], capture_output=True, text=True)
-    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
-    return DRIVER
+def driver(emu_driver):
+    return emu_driver
 
 
 def pack_words(oob):

@@ -106,8 +106,9 @@ def test_invalid_labels_never_match(gpu_ctx):
     ref[rng.random((t, n)) < 0.1] = -1
     qs = rng.integers(0, nleaf, size=(q, t), dtype=np.int32)
     qs[rng.random((q, t)) < 0.2] = -2
+    qs[:, 0] = ref[0, :q]                        # equal invalid labels (-1 and -1) are no match either
     got_i, got_c = run_topk(gpu_ctx, ref, nleaf, qs, k)
-    want_i, want_c = O.topk_all(ref, qs, k)
+    want_i, want_c = O.topk_all(ref, qs, k, nleaf=nleaf)
     assert np.array_equal(got_c, want_c) and np.array_equal(got_i, want_i)
 
 

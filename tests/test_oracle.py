@@ -250,11 +250,12 @@ def test_u8_scale_rule_matches_reference_minmax_formula():
 
 # ---- top-K ----------------------------------------------------------------------
 
-def brute_topk(ref_leaf, qleaf, K, exclude=None):
+def brute_topk(ref_leaf, qleaf, K, exclude=None, nleaf=2**31 - 1):
     t, n = ref_leaf.shape
     out_i, out_c = [], []
     for q in range(qleaf.shape[0]):
-        cnt = (ref_leaf == qleaf[q][:, None]).sum(axis=0)
+        ok = (qleaf[q] >= 0) & (qleaf[q] < nleaf)
+        cnt = ((ref_leaf == qleaf[q][:, None]) & ok[:, None]).sum(axis=0)
         order = np.lexsort((np.arange(n), -cnt))
         if exclude is not None:
             order = order[order != exclude[q]]
@@ -275,6 +276,35 @@ def test_topk_all_trees_matches_brute_force_with_ties():
     idx, cnt = O.topk_all(ref, ql, K, exclude=ex)
     bi, bc = brute_topk(ref, ql, K, exclude=ex)
     assert np.array_equal(idx, bi) and np.array_equal(cnt, bc)
+
+
+def test_topk_invalid_labels_match_nothing():
+    """Labels outside [0, nleaf) on both sides: equal invalid labels (-1 and
+    -1, 5 and 5 with nleaf 4) are not matches, for new and OOB queries."""
+    rng = np.random.default_rng(3)
+    n, t, q, nleaf, K = 300, 25, 12, 4, 15
+    ref = rng.integers(0, nleaf, (t, n)).astype(np.int32)
+    ref[rng.random((t, n)) < 0.2] = -1
+    ref[rng.random((t, n)) < 0.1] = 5
+    ql = np.ascontiguousarray(ref[:, :q].T)            # the same invalid labels in the queries
+    idx, cnt = O.topk_all(ref, ql, K, nleaf=nleaf)
+    bi, bc = brute_topk(ref, ql, K, nleaf=nleaf)
+    assert np.array_equal(idx, bi) and np.array_equal(cnt, bc)
+    idx, cnt = O.topk_all(ref, ql, K)                    # without nleaf, 5 is a valid label
+    bi, bc = brute_topk(ref, ql, K)
+    assert np.array_equal(idx, bi) and np.array_equal(cnt, bc)
+    assert not np.array_equal(bc, brute_topk(ref, ql, K, nleaf=nleaf)[1])
+    oob = (rng.random((t, n)) < 0.4).astype(np.uint8)
+    for qq in (0, 5):
+        idx, cnt, sc = O.topk_oob(ref, oob, qq, K, nleaf=nleaf)
+        trees = np.nonzero(oob[:, qq])[0]
+        lab = ref[trees, qq]
+        c = ((ref[trees] == lab[:, None]) & ((lab >= 0) & (lab < nleaf))[:, None]).sum(axis=0)
+        c[qq] = 0
+        order = np.lexsort((np.arange(n), -c))
+        order = order[c[order] > 0][:K]
+        assert np.array_equal(idx, order) and np.array_equal(cnt, c[order])
+        assert np.array_equal(sc, c[order].astype(np.float32) * (np.float32(1) / np.float32(len(trees))))
 
 
 def test_topk_oob_semantics():
