@@ -319,9 +319,11 @@ static double now_ms() {
 }
 
 // Live hipMalloc allocations (base -> bytes), so that pointers outside them
-// can be reported as host memory when the driver asks for that.
+// can be reported as host memory when the driver asks for that (or the
+// environment sets EMU_TRACK_HOST, for programs that know nothing of the
+// emulation).
 static std::map<uintptr_t, size_t> g_allocs;
-static bool g_track_host = false;
+static bool g_track_host = getenv("EMU_TRACK_HOST") != nullptr;
 extern "C" void emu_track_host_memory(int on) { g_track_host = on != 0; }
 
 hipError_t hipMalloc(void** p, size_t n) {
