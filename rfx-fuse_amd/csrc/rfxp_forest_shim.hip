@@ -16,17 +16,39 @@
 
 #include "rfx_forest.hpp"
 #include "rfx_prox.h"
+#include "rfxp_device.hpp"
 #include "rfxp_internal.hpp"
 
 namespace rfxp {
 
-// N x N from the packed F32 triangle: out[i*N + j] = tri[idx(min, max)]
-__global__ void k_expand_sym(const float* tri, int64_t N, float* out) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= N * N) return;
-    const int64_t i = e / N, j = e % N;
-    const int64_t a = i < j ? i : j, b = i < j ? j : i;
-    out[e] = tri[a * N - a * (a + 1) / 2 + b];
+// N x N from the packed F32 triangle: out[i*N + j] = tri[idx(min, max)],
+// one 64 x 64 tile per workgroup (rows 64 blockIdx.y, columns 64
+// blockIdx.x).  A tile on or above the diagonal reads along the triangle's
+// rows; a tile below it (every j < i) reads rows j of the triangle into LDS
+// and writes them transposed, so that reads and writes stay coalesced.
+constexpr int EX_T = 64;
+__global__ __launch_bounds__(256) void k_expand_sym(const float* tri, int64_t N, float* out) {
+    __shared__ float tile[EX_T][EX_T + 1];
+    const int64_t i0 = (int64_t)blockIdx.y * EX_T, j0 = (int64_t)blockIdx.x * EX_T;
+    const int tx = threadIdx.x & (EX_T - 1), ty = threadIdx.x / EX_T;
+    if (j0 >= i0) {  // the diagonal tile mixes both sides: per entry
+        for (int r = ty; r < EX_T; r += 256 / EX_T) {
+            const int64_t i = i0 + r, j = j0 + tx;
+            if (i >= N || j >= N) continue;
+            const int64_t a = i < j ? i : j, b = i < j ? j : i;
+            out[i * N + j] = tri[tri_idx(N, a, b)];
+        }
+        return;
+    }
+    for (int r = ty; r < EX_T; r += 256 / EX_T) {
+        const int64_t j = j0 + r, i = i0 + tx;
+        if (i < N) tile[r][tx] = tri[tri_idx(N, j, i)];  // j < i0 <= N
+    }
+    __syncthreads();
+    for (int r = ty; r < EX_T; r += 256 / EX_T) {
+        const int64_t i = i0 + r, j = j0 + tx;
+        if (i < N) out[i * N + j] = tile[tx][r];
+    }
 }
 
 __global__ void k_i16_to_i32(const int16_t* in, int64_t n, int32_t* out) {
@@ -243,7 +265,8 @@ bool ForestProximity::get_proximity_matrix(float* out) const {
     }
     if (!s.check(fn, rfxp_upper(s.ctx, RFXP_FMT_F32, 1.0f, 0.0f, 0, N, tri.p))) return false;
     hipStream_t st = (hipStream_t)rfxp_ctx_stream(s.ctx);
-    hipLaunchKernelGGL(rfxp::k_expand_sym, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st, tri.p, N, full.p);
+    const unsigned nt = (unsigned)((N + rfxp::EX_T - 1) / rfxp::EX_T);
+    hipLaunchKernelGGL(rfxp::k_expand_sym, dim3(nt, nt), dim3(256), 0, st, tri.p, N, full.p);
     return hipGetLastError() == hipSuccess &&
            hipMemcpyAsync(out, full.p, sizeof(float) * nn, hipMemcpyDeviceToHost, st) == hipSuccess &&
            hipStreamSynchronize(st) == hipSuccess;
