@@ -96,6 +96,25 @@ def test_byte_sum_check_and_recount(driver, tmp_path):
         assert rec > 0
 
 
+@pytest.mark.parametrize("planted", [True, False])
+def test_thousand_trees_per_thread_dummy_words(driver, tmp_path, planted):
+    """T = 1,000 (769 to 3,072 trees: the byte-sum check with one dummy word
+    per thread) on row bands at both ends.  Planted: samples 0..99 share a
+    leaf in every tree, their counts (~465) wrap 8 bits and their items are
+    recounted; otherwise no item is."""
+    n, t = 1500, 1000
+    nleaf = 40 if planted else 200
+    leaf, oob = forest(97 + planted, n, t, nleaf, p_oob=0.368)
+    if planted:
+        leaf[:, :100] = leaf[:, :1]
+    runs = [(0, 12, O.FMT_U16, 1.0)] + ([(0, 12, O.FMT_U8, 1 / 255.0), (n - 9, n, O.FMT_U16, 1.0)] if planted else [])
+    for r0, r1, fmt, scale in runs:
+        got, rec = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, r0=r0, r1=r1)
+        want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(scale), r0=r0, r1=r1)
+        assert np.array_equal(got, want), (r0, fmt)
+        assert (rec > 0) == (planted and r0 == 0), (r0, rec)
+
+
 @pytest.mark.parametrize("n,t,nleaf,bands", [
     (40_000, 10, 400, [(0, 2), (19_999, 20_002), (39_995, 40_000)]),   # per-part path, keys in registers
     (90_000, 4, 150, [(0, 2), (8_527, 8_530), (89_998, 90_000)]),      # rows split into two items
