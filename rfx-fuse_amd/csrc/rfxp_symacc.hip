@@ -810,6 +810,9 @@ extern "C" int rfxp_symacc_reset(rfxp_ctx* ctx, int64_t N) {
         ctx->sa_col.release();
         ctx->sa_val.release();
     }
+    if (ctx->sa_cnt.n > (size_t)N + 1) ctx->sa_cnt.release();
+    if (ctx->sa_rowptr.n > (size_t)N + 1) ctx->sa_rowptr.release();
+    if (ctx->sa_deg.n > (size_t)N + 1) ctx->sa_deg.release();
     return RFXP_OK;
 }
 
