@@ -8,12 +8,13 @@
 //     M = sum over contributions C of C   (C symmetric, given as its packed
 //                                         upper triangle or as a dense matrix)
 // and the factor is computed from M when it is asked for:
-//   * accumulation, sparse form: per contribution, a row-count pass and an
-//     ordered emit pass append the nonzero entries (i <= j, value) to a
-//     device COO list; values are read the way the reference's low-rank
-//     path reads them (FP16 as is, INT8 and NF4 dequantised and rounded to
-//     FP16, cuda/rf_proximity_lowrank.cu:199-240, 744-789; a dense matrix's
-//     upper triangle rounded to FP16, :654-685);
+//   * accumulation, sparse form: per contribution, a row-count pass, a
+//     device prefix scan of the counts (the host reads back only their
+//     total, to size the list) and an ordered emit pass append the nonzero
+//     entries (i <= j, value) to a device COO list; values are read the way
+//     the reference's low-rank path reads them (FP16 as is, INT8 and NF4
+//     dequantised and rounded to FP16, cuda/rf_proximity_lowrank.cu:199-240,
+//     744-789; a dense matrix's upper triangle rounded to FP16, :654-685);
 //   * accumulation, dense form: once the list and its CSR (12 + 16 bytes an
 //     entry) would take more than the packed upper triangle of M in doubles
 //     (8 bytes an entry of N(N+1)/2), the list is summed into that triangle
@@ -238,6 +239,34 @@ __global__ __launch_bounds__(SA_THREADS) void k_sa_rowemit(SymSrc s, int64_t row
         pos += tot;
         __syncthreads();
     }
+}
+
+// cnt[r0 .. r0 + nr) replaced by its exclusive prefix sums plus base, the
+// total into *tot: one workgroup, each thread over a contiguous chunk, the
+// chunk sums scanned in LDS.
+constexpr int SCAN_T = 1024;
+__global__ __launch_bounds__(SCAN_T) void k_sa_scan(int64_t* cnt, int64_t r0, int64_t nr, int64_t base,
+                                                    int64_t* tot) {
+    __shared__ int64_t part[SCAN_T];
+    const int64_t per = (nr + SCAN_T - 1) / SCAN_T;
+    const int64_t b = r0 + min(nr, per * threadIdx.x), e = r0 + min(nr, per * (threadIdx.x + 1));
+    int64_t sum = 0;
+    for (int64_t i = b; i < e; ++i) sum += cnt[i];
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    for (int d = 1; d < SCAN_T; d <<= 1) {  // inclusive scan of the chunk sums
+        const int64_t v = threadIdx.x >= (unsigned)d ? part[threadIdx.x - d] : 0;
+        __syncthreads();
+        part[threadIdx.x] += v;
+        __syncthreads();
+    }
+    int64_t run = base + (threadIdx.x ? part[threadIdx.x - 1] : 0);
+    for (int64_t i = b; i < e; ++i) {
+        const int64_t c = cnt[i];
+        cnt[i] = run;
+        run += c;
+    }
+    if (threadIdx.x == SCAN_T - 1) *tot = part[SCAN_T - 1];
 }
 
 // Symmetric CSR from the COO list: degrees, then placement at cursors.
@@ -687,20 +716,17 @@ static int symacc_to_dense(rfxp_ctx* ctx) {
 
 // Appends the nonzero entries of rows [r0, r1) (source s, staged) to the
 // list, or, when the list would pass its limit, switches to the dense form
-// and adds them there.  cnt: host scratch of N counts.
-static int symacc_add_rows_sparse(rfxp_ctx* ctx, const SymSrc& s, int64_t r0, int64_t r1, std::vector<int64_t>& cnt) {
-    const int64_t nr = r1 - r0;
+// and adds them there.  Row counts and their prefix sums stay on the device
+// (sa_cnt[0 .. N)); only the total (sa_cnt[N]) is read back.
+static int symacc_add_rows_sparse(rfxp_ctx* ctx, const SymSrc& s, int64_t r0, int64_t r1) {
+    const int64_t nr = r1 - r0, N = ctx->sa_N;
     hipLaunchKernelGGL(k_sa_rowcount, dim3((unsigned)nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p);
-    if (int rc = check_launch(ctx, "k_sa_rowcount")) return rc;
-    RFXP_HIP(ctx, hipMemcpyAsync(cnt.data() + r0, ctx->sa_cnt.p + r0, sizeof(int64_t) * nr, hipMemcpyDeviceToHost,
-                                 ctx->stream));
-    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    hipLaunchKernelGGL(k_sa_scan, dim3(1), dim3(SCAN_T), 0, ctx->stream, ctx->sa_cnt.p, r0, nr, ctx->sa_nnz,
+                       ctx->sa_cnt.p + N);
+    if (int rc = check_launch(ctx, "k_sa_rowcount / k_sa_scan")) return rc;
     int64_t tot = 0;
-    for (int64_t i = r0; i < r1; ++i) {
-        const int64_t c = cnt[i];
-        cnt[i] = ctx->sa_nnz + tot;
-        tot += c;
-    }
+    RFXP_HIP(ctx, hipMemcpyAsync(&tot, ctx->sa_cnt.p + N, sizeof(int64_t), hipMemcpyDeviceToHost, ctx->stream));
+    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (tot == 0) return RFXP_OK;
     const int64_t need = ctx->sa_nnz + tot, limit = sa_list_limit(ctx->sa_N);
     if (need > limit) {
@@ -733,12 +759,9 @@ static int symacc_add_rows_sparse(rfxp_ctx* ctx, const SymSrc& s, int64_t r0, in
         nj.release();
         nv.release();
     }
-    RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_cnt.p + r0, cnt.data() + r0, sizeof(int64_t) * nr, hipMemcpyHostToDevice,
-                                 ctx->stream));
     hipLaunchKernelGGL(k_sa_rowemit, dim3((unsigned)nr), dim3(SA_THREADS), 0, ctx->stream, s, r0, ctx->sa_cnt.p,
                        ctx->sa_i.p, ctx->sa_j.p, ctx->sa_v.p);
     if (int rc = check_launch(ctx, "k_sa_rowemit")) return rc;
-    RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // cnt is reused by the next band
     ctx->sa_nnz = need;
     return RFXP_OK;
 }
@@ -748,11 +771,7 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     const bool host = !is_device_pointer(s.p);
     const bool packed = s.kind != SRC_DENSE;
-    std::vector<int64_t> cnt;
-    if (!ctx->sa_dense) {
-        RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
-        cnt.resize((size_t)N);
-    }
+    if (!ctx->sa_dense) RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
     ctx->sa_csr_ok = false;
     int64_t r0 = 0;
     while (r0 < N) {
@@ -781,7 +800,7 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
             hipLaunchKernelGGL(k_sa_tri_add, dim3((unsigned)(r1 - r0)), dim3(SA_THREADS), 0, ctx->stream, band, r0,
                                ctx->sa_tri.p);
             if (int rc = check_launch(ctx, "k_sa_tri_add")) return rc;
-        } else if (int rc = symacc_add_rows_sparse(ctx, band, r0, r1, cnt)) {
+        } else if (int rc = symacc_add_rows_sparse(ctx, band, r0, r1)) {
             return rc;
         }
         r0 = r1;

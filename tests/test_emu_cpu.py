@@ -369,3 +369,21 @@ def test_symacc_dense_from_the_first_add(driver, tmp_path):
     steps, _ = emulate_symacc(driver, tmp_path, n, contribs, X)
     assert steps[0][0] == ne
     _check_steps(steps, contribs, n, X)
+
+
+def test_symacc_list_scan_over_row_chunks(driver, tmp_path):
+    """N = 2,500 rows in one band: the device scan of the row counts gives
+    each of its 1,024 threads a chunk of three rows."""
+    rng = np.random.default_rng(54)
+    n = 2500
+    ne = n * (n + 1) // 2
+    contribs = []
+    for k in range(2):
+        f16 = np.zeros(ne, np.float16)
+        hit = rng.random(ne) < 0.002
+        f16[hit] = rng.standard_normal(int(hit.sum())).astype(np.float16)
+        contribs.append((O.FMT_F16, f16.view(np.uint16), True, 1.0, 0.0))
+    X = rng.standard_normal((n, 3))
+    steps, _ = emulate_symacc(driver, tmp_path, n, contribs, X)
+    assert 0 < steps[-1][0] < ne // 7 * 2
+    _check_steps(steps, contribs, n, X)
