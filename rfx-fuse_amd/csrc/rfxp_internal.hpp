@@ -45,7 +45,7 @@ struct ForestBufs {
     uint32_t* mem = nullptr;       // [T][ms] + MEM_PAD members
     uint32_t* roff = nullptr;      // [N][ldr] + REC_PAD records (forest mode)
     uint16_t* rlen = nullptr;
-    uint32_t* roffT = nullptr;     // [T][N] tree-major records (per-part packing)
+    uint32_t* roffT = nullptr;     // [T][N] tree-major records (whole-tree packing, before k_rec_transpose)
     uint16_t* rlenT = nullptr;
     uint32_t* scratch = nullptr;   // part histograms, or whole-tree counters / cursors
     uint32_t* scratch2 = nullptr;  // [N] OOB counts (nout not given)
@@ -82,14 +82,14 @@ struct rfxp_ctx {
     int32_t L = 0;
     DevBuf<int32_t> bkt_off;   // T x (2L+1): bucket b = 2*leaf + oob
     DevBuf<int32_t> bkt_end;   // T x 2L: bucket ends of the line-fit layout
-    DevBuf<uint32_t> bkt_mem;  // T x N (+ padding): sample ids grouped by bucket
+    DevBuf<uint32_t> bkt_mem;  // T x ms (+ padding): sample ids grouped by bucket
     int64_t ldr = 0;           // record row stride: T rounded up to 16
     DevBuf<uint32_t> roff;     // N x ldr (+pad): offset of the opposite-OOB bucket of (i, t)
     DevBuf<uint16_t> rlen;     // N x ldr (+pad): its length in bytes (see rfxp_forest.hpp)
     DevBuf<uint2> lng;         // T x lmax: start, end byte offsets of buckets of REC_LONG+ members
     DevBuf<int32_t> lngn;      // T: entries of lng per tree
     int32_t lmax = 0;
-    DevBuf<uint32_t> roffT;    // T x N: records, tree-major (packing)
+    DevBuf<uint32_t> roffT;    // T x N: records, tree-major (whole-tree packing)
     DevBuf<uint16_t> rlenT;
     DevBuf<uint32_t> scratch;  // packing scratch (part histograms, large leaf counts)
     DevBuf<uint32_t> scratch2; // per-sample OOB counts

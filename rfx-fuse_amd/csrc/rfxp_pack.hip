@@ -11,9 +11,10 @@
 // one XCD, where the later workgroups of a tree read its data from L2.
 //
 // nout_i = sum over trees of the OOB bits (src/rf_bootstrap.cpp:67-70) is
-// summed by k_rec_transpose; k_nout_final takes its reciprocal and the
-// reciprocal's range.  Reference sets (top-K, low rank) take the per-segment
-// path (k_seg_*).
+// summed by the kernel that writes the sample-major records (k_part_records
+// on the per-part path, k_rec_transpose on the whole-tree path) into a zeroed
+// array; k_nout_final takes its reciprocal and the reciprocal's range.
+// Reference sets (top-K, low rank) take the per-segment path (k_seg_*).
 #include <algorithm>
 
 #include "rfxp_device.hpp"
@@ -1571,7 +1572,8 @@ static int pack_forest_parts(rfxp_ctx* ctx, const LeafView& v, const int32_t* no
 static int pack_nout(rfxp_ctx* ctx, const LeafView& v, const int32_t* nout_in, const ForestBufs& fb) {
     hipStream_t s = ctx->stream;
     const int64_t N = v.N;
-    // without nout_in, k_rec_transpose has summed the OOB bits into fb.scratch2
+    // without nout_in, the records kernel (k_part_records or k_rec_transpose)
+    // has summed the OOB bits into fb.scratch2
     {
         LaunchTimer tm(ctx, "nout_final");
         hipLaunchKernelGGL(k_nout_final, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, s, N, nout_in,
