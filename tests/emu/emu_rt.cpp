@@ -57,6 +57,8 @@ struct Thread {
     int64_t arg = 0, width = 64;
     uint64_t res = 0;
     void* fake = nullptr;
+    const char* file = nullptr;  // source location of the barrier or wave builtin it waits at
+    int line = 0;
 };
 
 struct Launch {
@@ -80,8 +82,9 @@ std::mutex g_mu;  // one launch at a time
 
 [[noreturn]] void die(const char* what, const Thread* t) {
     if (t)
-        fprintf(stderr, "[emu] %s (thread %u,%u,%u of block %u,%u,%u, lane %d, op %d)\n", what, t->v.tid.x,
-                t->v.tid.y, t->v.tid.z, t->v.bid.x, t->v.bid.y, t->v.bid.z, t->v.lane, t->op);
+        fprintf(stderr, "[emu] %s (thread %u,%u,%u of block %u,%u,%u, lane %d, op %d, at %s:%d)\n", what, t->v.tid.x,
+                t->v.tid.y, t->v.tid.z, t->v.bid.x, t->v.bid.y, t->v.bid.z, t->v.lane, t->op,
+                t->file ? t->file : "?", t->line);
     else
         fprintf(stderr, "[emu] %s\n", what);
     fflush(stderr);
@@ -160,27 +163,38 @@ uint64_t dpp_src(int ctrl, int lane) {
     die("unsupported DPP control", nullptr);
 }
 
-// resolves one wave whose live lanes all wait at the same builtin
+// Resolves one wave's builtin over its active lanes: the lanes waiting at it
+// (all live lanes, or a subset whose other lanes wait further on at a
+// barrier, as the hardware runs a builtin inside a branch with the other
+// lanes masked off).  The active lanes must wait at one builtin at one
+// source location; a ballot counts only active lanes, readfirstlane reads
+// the first one, and a lane-to-lane read (shuffle, readlane, DPP) from an
+// inactive lane stops the run.
 void resolve(int w0, int n) {
     Thread* L = &g_th[w0];
     int first = -1, op = 0;
     for (int l = 0; l < n; ++l) {
-        if (L[l].st == DONE) continue;
+        if (L[l].st != WOP) continue;
         if (first < 0) {
             first = l;
             op = L[l].op;
-        } else if (L[l].op != op) {
+        } else if (L[l].op != op || L[l].line != L[first].line || L[l].file != L[first].file) {
+            fprintf(stderr, "[emu]   lane %d waits at %s:%d, lane %d at %s:%d\n", first,
+                    L[first].file ? L[first].file : "?", L[first].line, l, L[l].file ? L[l].file : "?", L[l].line);
             die("lanes of one wave wait at different wave builtins", &L[l]);
         }
     }
-    auto live = [&](int l) { return l >= 0 && l < n && L[l].st != DONE; };
+    uint64_t act = 0;  // the active set, taken before any lane is released
+    for (int l = 0; l < n; ++l)
+        if (L[l].st == WOP) act |= 1ull << l;
+    auto active = [&](int l) { return l >= 0 && l < n && ((act >> l) & 1u); };
     uint64_t ballot = 0;
     if (op == W_BALLOT)
         for (int l = 0; l < n; ++l)
-            if (live(l) && L[l].val) ballot |= 1ull << l;
+            if (active(l) && L[l].val) ballot |= 1ull << l;
     for (int l = 0; l < n; ++l) {
         Thread& t = L[l];
-        if (t.st == DONE) continue;
+        if (!active(l)) continue;
         const int width = (int)t.width;
         const int base = l & ~(width - 1), off = l & (width - 1);
         int src = l;
@@ -195,8 +209,10 @@ void resolve(int w0, int n) {
             case W_DPP: src = (int)dpp_src((int)t.arg, l); break;
             default: die("unknown wave builtin", &t);
         }
+        if (op != W_BALLOT && src >= 0 && src < n && L[src].st != DONE && !active(src))
+            die("a wave builtin reads a lane that does not take part in it", &t);
         if (op == W_BALLOT) t.res = ballot;
-        else t.res = live(src) ? L[src].val : t.val;
+        else t.res = active(src) ? L[src].val : t.val;
         t.st = RUN;
     }
 }
@@ -225,11 +241,8 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
                 wop += s == WOP;
             }
             if (wop == 0) continue;
-            if (wop != live) {
-                for (int l = 0; l < wn; ++l)
-                    if (g_th[w0 + l].st == BAR) die("a wave waits at a barrier and at a wave builtin", &g_th[w0 + l]);
-                die("divergent wave", nullptr);
-            }
+            // every live lane now waits at a builtin or a barrier; those at
+            // a barrier are the lanes a branch left out of the builtin
             resolve(w0, wn);
             moved = true;
         }
@@ -241,6 +254,20 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
         }
         if (live == 0) break;
         if (bar != live) die("deadlock: no thread can run", nullptr);
+        // one barrier releases the workgroup: every waiting thread must be
+        // at the same __syncthreads
+        const Thread* b0 = nullptr;
+        for (int i = 0; i < n; ++i) {
+            const Thread& t = g_th[i];
+            if (t.st != BAR) continue;
+            if (!b0) {
+                b0 = &t;
+            } else if (t.line != b0->line || t.file != b0->file) {
+                fprintf(stderr, "[emu]   a thread waits at %s:%d, another at %s:%d\n", b0->file ? b0->file : "?",
+                        b0->line, t.file ? t.file : "?", t.line);
+                die("threads of a workgroup wait at different barriers", &t);
+            }
+        }
         for (int i = 0; i < n; ++i)
             if (g_th[i].st == BAR) g_th[i].st = RUN;
     }
@@ -258,15 +285,19 @@ char* lds_base() {
     return g_launch.lds;
 }
 
-void barrier() {
+void barrier(const char* file, int line) {
     if (!g_cur) die("__syncthreads outside a kernel", nullptr);
+    g_cur->file = file;
+    g_cur->line = line;
     g_cur->st = BAR;
     to_scheduler();
 }
 
-uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width) {
+uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, int line) {
     if (!g_cur) die("wave builtin outside a kernel", nullptr);
     Thread* t = g_cur;
+    t->file = file;
+    t->line = line;
     t->op = op;
     t->val = v;
     t->arg = arg;

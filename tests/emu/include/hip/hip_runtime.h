@@ -112,11 +112,11 @@ struct ThreadView {
 };
 const ThreadView& view();
 char* lds_base();
-void barrier();
+void barrier(const char* file, int line);
 enum WaveOp {
     W_READFIRST = 1, W_READLANE, W_BALLOT, W_SHFL, W_SHFL_UP, W_SHFL_DOWN, W_SHFL_XOR, W_DPP
 };
-uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width);
+uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, int line);
 
 typedef void (*Body)(void* closure);
 void launch_raw(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Body body, void* closure);
@@ -158,36 +158,50 @@ inline void launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipS
 #define hipLaunchKernelGGL(kernel, grid, block, lds, stream, ...) \
     ::emu::launch(kernel, dim3(grid), dim3(block), (size_t)(lds), stream, ##__VA_ARGS__)
 
-inline void __syncthreads() { ::emu::barrier(); }
+// the call site of each barrier and wave builtin is recorded for the scheduler's checks
+#define EMU_AT const char* emu_file = __builtin_FILE(), int emu_line = __builtin_LINE()
+inline void __syncthreads(EMU_AT) { ::emu::barrier(emu_file, emu_line); }
 inline void __threadfence() {}
 inline void __threadfence_block() {}
 
 // ---- wave-wide operations ------------------------------------------------
 template <class T>
-inline T __shfl(T v, int src, int width = 64) {
-    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL, ::emu::to_bits(v), src, width));
+inline T __shfl(T v, int src, int width = 64, EMU_AT) {
+    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL, ::emu::to_bits(v), src, width,
+                                                emu_file, emu_line));
 }
 template <class T>
-inline T __shfl_up(T v, unsigned d, int width = 64) {
-    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_UP, ::emu::to_bits(v), (int64_t)d, width));
+inline T __shfl_up(T v, unsigned d, int width = 64, EMU_AT) {
+    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_UP, ::emu::to_bits(v), (int64_t)d, width,
+                                                emu_file, emu_line));
 }
 template <class T>
-inline T __shfl_down(T v, unsigned d, int width = 64) {
-    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_DOWN, ::emu::to_bits(v), (int64_t)d, width));
+inline T __shfl_down(T v, unsigned d, int width = 64, EMU_AT) {
+    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_DOWN, ::emu::to_bits(v), (int64_t)d, width,
+                                                emu_file, emu_line));
 }
 template <class T>
-inline T __shfl_xor(T v, int m, int width = 64) {
-    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_XOR, ::emu::to_bits(v), m, width));
+inline T __shfl_xor(T v, int m, int width = 64, EMU_AT) {
+    return ::emu::from_bits<T>(::emu::wave(::emu::W_SHFL_XOR, ::emu::to_bits(v), m, width,
+                                                emu_file, emu_line));
 }
-inline unsigned long long __ballot(int pred) { return ::emu::wave(::emu::W_BALLOT, pred != 0, 0, 64); }
-inline uint32_t emu_readfirstlane(uint32_t v) { return (uint32_t)::emu::wave(::emu::W_READFIRST, v, 0, 64); }
-inline int32_t emu_readfirstlane(int32_t v) { return (int32_t)::emu::wave(::emu::W_READFIRST, (uint32_t)v, 0, 64); }
-inline uint32_t emu_readlane(uint32_t v, int lane) { return (uint32_t)::emu::wave(::emu::W_READLANE, v, lane, 64); }
-inline int32_t emu_readlane(int32_t v, int lane) {
-    return (int32_t)::emu::wave(::emu::W_READLANE, (uint32_t)v, lane, 64);
+inline unsigned long long __ballot(int pred, EMU_AT) {
+    return ::emu::wave(::emu::W_BALLOT, pred != 0, 0, 64, emu_file, emu_line);
 }
-inline int emu_mov_dpp(int v, int ctrl, int, int, bool) {
-    return (int)::emu::wave(::emu::W_DPP, (uint32_t)v, ctrl, 64);
+inline uint32_t emu_readfirstlane(uint32_t v, EMU_AT) {
+    return (uint32_t)::emu::wave(::emu::W_READFIRST, v, 0, 64, emu_file, emu_line);
+}
+inline int32_t emu_readfirstlane(int32_t v, EMU_AT) {
+    return (int32_t)::emu::wave(::emu::W_READFIRST, (uint32_t)v, 0, 64, emu_file, emu_line);
+}
+inline uint32_t emu_readlane(uint32_t v, int lane, EMU_AT) {
+    return (uint32_t)::emu::wave(::emu::W_READLANE, v, lane, 64, emu_file, emu_line);
+}
+inline int32_t emu_readlane(int32_t v, int lane, EMU_AT) {
+    return (int32_t)::emu::wave(::emu::W_READLANE, (uint32_t)v, lane, 64, emu_file, emu_line);
+}
+inline int emu_mov_dpp(int v, int ctrl, int, int, bool, EMU_AT) {
+    return (int)::emu::wave(::emu::W_DPP, (uint32_t)v, ctrl, 64, emu_file, emu_line);
 }
 inline uint32_t emu_mbcnt_lo(uint32_t m, uint32_t acc) {
     const int l = ::emu::view().lane;

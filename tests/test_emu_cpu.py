@@ -1,6 +1,7 @@
 """The library's own HIP kernels run on the CPU by the emulator in tests/emu
-(every GPU thread a coroutine, wave builtins resolved per 64-lane wave,
-device memory and each workgroup's LDS from malloc, AddressSanitizer on),
+(every GPU thread a coroutine, wave builtins resolved per 64-lane wave over
+the lanes that reach them, device memory and each workgroup's LDS from
+malloc, AddressSanitizer on),
 through the C ABI, against the oracle.  These runs check index arithmetic,
 buffer sizes and bounds on every packing path and format without a GPU: an
 access outside an allocation or outside a workgroup's LDS aborts the run
@@ -387,3 +388,56 @@ def test_symacc_list_scan_over_row_chunks(driver, tmp_path):
     steps, _ = emulate_symacc(driver, tmp_path, n, contribs, X)
     assert 0 < steps[-1][0] < ne // 7 * 2
     _check_steps(steps, contribs, n, X)
+
+
+SWEEP_FMTS = [(O.FMT_U16, 1.0, 0.0), (O.FMT_F32, 1.0, 0.0), (O.FMT_F16, 1.0, 0.0), (O.FMT_U8, 1 / 255.0, 0.0),
+              (O.FMT_U8, 1 / 4000.0, 3.0), (O.FMT_I8, 1 / 127.0, 0.0), (O.FMT_I8, 1 / 2000.0, -100.0),
+              (O.FMT_NF4, 1.0, 0.0)]
+
+
+def random_case(seed):
+    """One random forest shape of the triangle sweep: N up to 130,000 (row
+    bands for large N), T up to 1,200, leaves from 1 to 20,000 (both packing
+    paths), any OOB rate, invalid labels, blocks of samples sharing leaves,
+    either layout, caller nout or not, every format."""
+    rng = np.random.default_rng(seed)
+    big = rng.random() < 0.15
+    n = int(rng.integers(40000, 130000)) if big else int(rng.integers(1, 3000))
+    t = int(rng.integers(1, 8)) if big else int(rng.choice([1, 2, 3, 17, 64, 255, 256, 300, 700, 1000,
+                                                             int(rng.integers(1, 1200))]))
+    nleaf = int(rng.choice([1, 2, 3, 50, 400, 2048, 4096, 4097, 9000, int(rng.integers(1, 20000))]))
+    p_oob = float(rng.choice([0.0, 0.37, 1.0, float(rng.random())]))
+    p_inv = float(rng.choice([0.0, 0.0, 0.02, 0.3]))
+    leaf, oob = forest(seed, n, t, nleaf, p_oob=p_oob, p_invalid=p_inv)
+    if rng.random() < 0.3 and n > 10:
+        k = int(rng.integers(2, min(n, 300)))
+        leaf[:, :k] = leaf[:, :1]
+    fmt, scale, zp = SWEEP_FMTS[int(rng.integers(len(SWEEP_FMTS)))]
+    if big or rng.random() < 0.4:
+        r0 = int(rng.integers(0, n))
+        r1 = int(min(n, r0 + rng.integers(1, 6)))
+    else:
+        r0, r1 = 0, n
+    layout = "sample" if rng.random() < 0.3 else "tree"
+    nout = rng.integers(0, t + 3, n).astype(np.int32) if rng.random() < 0.25 else None
+    return leaf, oob, nleaf, fmt, scale, zp, r0, r1, layout, nout
+
+
+# chosen from a sweep of ~470 such cases (all bit-exact) to cover both packing
+# paths, row bands of large N, both layouts, caller nout and every format
+@pytest.mark.parametrize("seed", [100000, 100002, 100005, 100011, 100021, 100033, 100035, 100039, 100055, 100079])
+def test_random_shapes(driver, tmp_path, seed):
+    leaf, oob, nleaf, fmt, scale, zp, r0, r1, layout, nout = random_case(seed)
+    n = leaf.shape[1]
+    got, _ = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, zp, r0=r0, r1=r1, nout=nout, layout=layout)
+    want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(scale), zp=np.float32(zp), r0=r0, r1=r1,
+                        nout_arr=nout)
+    g, w = got.view(np.uint8).copy(), want.view(np.uint8).copy()
+    if fmt == O.FMT_NF4 and len(g):   # nibbles of entries outside the rows are the caller's
+        if O.tri_idx(n, r0, r0) & 1:
+            g[0] &= 0xF0
+            w[0] &= 0xF0
+        if O.tri_idx(n, r1, r1) & 1:
+            g[-1] &= 0x0F
+            w[-1] &= 0x0F
+    assert np.array_equal(g, w)

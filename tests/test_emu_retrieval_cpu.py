@@ -34,7 +34,10 @@ def topk_script(s, ref, nleaf, qs, k, exclude_base=-1, oob_words=None, positive_
                                            (1000, 40, 7, 9, 20),
                                            (2100, 16, 300, 5, 64),
                                            (40000, 24, 50, 3, 20),   # 16-bit segments
-                                           (70001, 12, 9, 3, 1)])    # 8-bit segments
+                                           (70001, 12, 9, 3, 1),     # 8-bit segments
+                                           # K > 32 on 8-bit segments: candidates gathered with the
+                                           # lanes that hold none masked off (a ballot prefix in a branch)
+                                           (79353, 17, 64, 1, 42), (60434, 17, 1000, 4, 56)])
 def test_topk_all_trees(emu_driver, tmp_path, n, t, nleaf, q, k):
     rng = np.random.default_rng(n + t + q)
     ref = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
