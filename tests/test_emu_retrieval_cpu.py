@@ -176,24 +176,24 @@ def test_pair_proximity(emu_driver, tmp_path):
 
 def test_outlier_full_and_anchor_modes(emu_driver, tmp_path):
     rng = np.random.default_rng(33)
-    n, t, nleaf = 1200, 60, 25
+    n, t, nleaf = 800, 60, 25
     leaf = rng.integers(0, nleaf, size=(t, n), dtype=np.int32)
     s = EmuScript(emu_driver)
     lb = s.dev(leaf)
     raw = s.out(4 * n)
     s.call("rfxp_set_reference", CTX, lb, 1, n, n, t, nleaf)
     s.call("rfxp_outlier_raw", CTX, lb, 1, n, n, 0, None, float(n - 1), float(n) * 1e10, raw)
-    anchors = np.sort(rng.choice(n, 150, replace=False)).astype(np.int64)
+    anchors = np.sort(rng.choice(n, 100, replace=False)).astype(np.int64)
     ex = np.full(n, -1, np.int32)
     ex[anchors] = np.arange(len(anchors))
     aleaf = np.ascontiguousarray(leaf[:, anchors])
     raw2 = s.out(4 * n)
     s.call("rfxp_set_reference", CTX, s.dev(aleaf), 1, len(anchors), len(anchors), t, nleaf)
-    s.call("rfxp_outlier_raw", CTX, lb, 1, n, n, -1, s.dev(ex), 150.0, 150.0 * 1e10, raw2)
+    s.call("rfxp_outlier_raw", CTX, lb, 1, n, n, -1, s.dev(ex), 100.0, 100.0 * 1e10, raw2)
     assert s.run(tmp_path) == [0] * 4
     want = O.outlier_raw(leaf, nleaf, np.ascontiguousarray(leaf.T), exclude=np.arange(n, dtype=np.int32),
                          numerator=float(n - 1), isolated=float(n) * 1e10)
     assert np.allclose(raw.array(np.float32), want, rtol=1e-6, atol=0)
-    want = O.outlier_raw(aleaf, nleaf, np.ascontiguousarray(leaf.T), exclude=ex, numerator=150.0,
-                         isolated=150.0 * 1e10)
+    want = O.outlier_raw(aleaf, nleaf, np.ascontiguousarray(leaf.T), exclude=ex, numerator=100.0,
+                         isolated=100.0 * 1e10)
     assert np.allclose(raw2.array(np.float32), want, rtol=1e-6, atol=0)
