@@ -5,15 +5,18 @@
 // workgroup is a coroutine with its own stack; the scheduler runs every
 // runnable thread until it blocks:
 //   - at __syncthreads (a workgroup barrier: released when every thread
-//     that has not returned is waiting there);
+//     that has not returned is waiting there, all at the same call site);
 //   - at a wave-wide builtin (released when every live lane of its 64-lane
-//     wave waits at the same builtin; the results are computed from all the
-//     lanes' inputs at once, as the SIMD does).
-// A wave whose live lanes wait at different builtins, or at a builtin and a
-// barrier, is a divergence the kernel language does not define: the
-// emulator aborts with the call site.  Dynamic LDS is a malloc'd block of
-// exactly the launch's size, so an AddressSanitizer build reports LDS
-// accesses past it; device memory is malloc'd too.
+//     wave waits either there or at a barrier: the builtin runs over the
+//     lanes that reached it, as the SIMD runs it inside a branch with the
+//     other lanes masked off; the results are computed from those lanes'
+//     inputs at once).
+// Lanes of one wave at different builtins, a lane-to-lane read from a
+// masked lane, or threads at different barriers stop the run with the call
+// sites.  Dynamic LDS is a malloc'd block of exactly the launch's size, so
+// an AddressSanitizer build reports LDS accesses past it; device memory is
+// malloc'd too.  With EMU_STATS set, each launch prints its barrier
+// releases, wave builtin rounds and coroutine resumes.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -217,6 +220,14 @@ void resolve(int w0, int n) {
     }
 }
 
+// Counts of one launch for EMU_STATS: barrier releases and wave builtin
+// resolutions (per workgroup / per wave), and coroutine resumes.
+struct Stats {
+    uint64_t blocks = 0, barriers = 0, wave_ops = 0, resumes = 0;
+};
+Stats g_stats;
+const bool g_print_stats = getenv("EMU_STATS") != nullptr;
+
 void run_block(dim3 bid, dim3 grid, dim3 block) {
     const int n = g_launch.nthreads;
     for (int i = 0; i < n; ++i) {
@@ -228,9 +239,13 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
         t.v.gdim = Idx{grid.x, grid.y, grid.z};
         t.v.lane = i & 63;
     }
+    ++g_stats.blocks;
     for (;;) {
         for (int i = 0; i < n; ++i)
-            if (g_th[i].st == RUN) resume(g_th[i]);
+            if (g_th[i].st == RUN) {
+                resume(g_th[i]);
+                ++g_stats.resumes;
+            }
         bool moved = false;
         for (int w0 = 0; w0 < n; w0 += 64) {
             const int wn = std::min(64, n - w0);
@@ -244,6 +259,7 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
             // every live lane now waits at a builtin or a barrier; those at
             // a barrier are the lanes a branch left out of the builtin
             resolve(w0, wn);
+            ++g_stats.wave_ops;
             moved = true;
         }
         if (moved) continue;
@@ -270,6 +286,7 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
         }
         for (int i = 0; i < n; ++i)
             if (g_th[i].st == BAR) g_th[i].st = RUN;
+        ++g_stats.barriers;
     }
 }
 
@@ -307,7 +324,8 @@ uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, 
     return t->res;
 }
 
-void launch_raw(const void*, dim3 grid, dim3 block, size_t lds, hipStream_t, Body body, void* closure) {
+void launch_raw(const void*, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t, Body body,
+                void* closure) {
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t nt = (uint64_t)block.x * block.y * block.z;
     if (nt == 0 || nt > MAX_THREADS || grid.x == 0 || grid.y == 0 || grid.z == 0) {
@@ -333,6 +351,12 @@ void launch_raw(const void*, dim3 grid, dim3 block, size_t lds, hipStream_t, Bod
                 free(g_launch.lds);
                 g_launch.lds = nullptr;
             }
+    if (g_print_stats) {
+        fprintf(stderr, "[emu-stats] %s grid %ux%ux%u block %llu: %llu barriers, %llu wave-op rounds, %llu resumes\n",
+                name, grid.x, grid.y, grid.z, (unsigned long long)nt, (unsigned long long)g_stats.barriers,
+                (unsigned long long)g_stats.wave_ops, (unsigned long long)g_stats.resumes);
+    }
+    g_stats = Stats();
 }
 
 }  // namespace emu

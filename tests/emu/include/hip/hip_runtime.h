@@ -119,7 +119,8 @@ enum WaveOp {
 uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, int line);
 
 typedef void (*Body)(void* closure);
-void launch_raw(const void* kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Body body, void* closure);
+void launch_raw(const void* kernel, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, Body body,
+                void* closure);
 
 template <class T>
 inline uint64_t to_bits(T v) {
@@ -136,13 +137,14 @@ inline T from_bits(uint64_t b) {
 }
 
 template <class... P, class... A>
-inline void launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s, A&&... args) {
+inline void launch(void (*kernel)(P...), const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                   A&&... args) {
     std::tuple<std::decay_t<P>...> t(static_cast<std::decay_t<P>>(std::forward<A>(args))...);
     struct C {
         void (*k)(P...);
         std::tuple<std::decay_t<P>...>* t;
     } c{kernel, &t};
-    launch_raw((const void*)kernel, grid, block, lds, s,
+    launch_raw((const void*)kernel, name, grid, block, lds, s,
                [](void* p) {
                    C* cc = (C*)p;
                    std::apply(cc->k, *cc->t);
@@ -156,7 +158,7 @@ inline void launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipS
 #define blockDim (::emu::view().bdim)
 #define gridDim (::emu::view().gdim)
 #define hipLaunchKernelGGL(kernel, grid, block, lds, stream, ...) \
-    ::emu::launch(kernel, dim3(grid), dim3(block), (size_t)(lds), stream, ##__VA_ARGS__)
+    ::emu::launch(kernel, #kernel, dim3(grid), dim3(block), (size_t)(lds), stream, ##__VA_ARGS__)
 
 // the call site of each barrier and wave builtin is recorded for the scheduler's checks
 #define EMU_AT const char* emu_file = __builtin_FILE(), int emu_line = __builtin_LINE()
