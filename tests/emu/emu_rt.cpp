@@ -16,13 +16,17 @@
 // sites.  Dynamic LDS is a malloc'd block of exactly the launch's size, so
 // an AddressSanitizer build reports LDS accesses past it; device memory is
 // malloc'd too.  With EMU_STATS set, each launch prints its barrier
-// releases, wave builtin rounds and coroutine resumes.
+// releases, wave builtin rounds and coroutine resumes; EMU_ORDER and
+// EMU_LANES change the order in which waves and lanes run between
+// synchronization points (see below).
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 #include <sys/mman.h>
 #include <time.h>
 
+#include <algorithm>
 #include <chrono>
 #include <iterator>
 #include <map>
@@ -228,6 +232,37 @@ struct Stats {
 Stats g_stats;
 const bool g_print_stats = getenv("EMU_STATS") != nullptr;
 
+// Order in which the waves of a workgroup run between synchronization
+// points (EMU_ORDER): "forward" (default), "reverse", or "shuffle" (a new
+// random order every round, seeded by EMU_SEED).  Lanes of a wave keep their
+// order.  Kernels whose waves communicate only across barriers give the
+// same results in every order; a missing barrier shows as a difference.
+enum Order { FORWARD, REVERSE, SHUFFLE };
+const Order g_order = [] {
+    const char* e = getenv("EMU_ORDER");
+    if (!e || !strcmp(e, "forward")) return FORWARD;
+    if (!strcmp(e, "reverse")) return REVERSE;
+    if (!strcmp(e, "shuffle")) return SHUFFLE;
+    fprintf(stderr, "[emu] EMU_ORDER must be forward, reverse or shuffle\n");
+    abort();
+}();
+// EMU_LANES=reverse runs the lanes of each wave from the last to the first
+// between synchronization points.
+const bool g_lanes_reversed = [] {
+    const char* e = getenv("EMU_LANES");
+    return e && !strcmp(e, "reverse");
+}();
+uint64_t g_rng = [] {
+    const char* e = getenv("EMU_SEED");
+    return e ? strtoull(e, nullptr, 10) * 0x9e3779b97f4a7c15ull + 1 : 0x2545F4914F6CDD1Dull;
+}();
+uint32_t next_rand() {  // xorshift64*
+    g_rng ^= g_rng >> 12;
+    g_rng ^= g_rng << 25;
+    g_rng ^= g_rng >> 27;
+    return (uint32_t)((g_rng * 0x2545F4914F6CDD1Dull) >> 32);
+}
+
 void run_block(dim3 bid, dim3 grid, dim3 block) {
     const int n = g_launch.nthreads;
     for (int i = 0; i < n; ++i) {
@@ -240,12 +275,22 @@ void run_block(dim3 bid, dim3 grid, dim3 block) {
         t.v.lane = i & 63;
     }
     ++g_stats.blocks;
+    const int nw = (n + 63) / 64;
+    int worder[MAX_THREADS / 64];
+    for (int w = 0; w < nw; ++w) worder[w] = g_order == REVERSE ? nw - 1 - w : w;
     for (;;) {
-        for (int i = 0; i < n; ++i)
-            if (g_th[i].st == RUN) {
-                resume(g_th[i]);
-                ++g_stats.resumes;
+        if (g_order == SHUFFLE)
+            for (int w = nw - 1; w > 0; --w) std::swap(worder[w], worder[next_rand() % (uint32_t)(w + 1)]);
+        for (int wi = 0; wi < nw; ++wi) {
+            const int b = worder[wi] * 64, e = std::min(n, b + 64);
+            for (int k = 0; k < e - b; ++k) {
+                const int i = g_lanes_reversed ? e - 1 - k : b + k;
+                if (g_th[i].st == RUN) {
+                    resume(g_th[i]);
+                    ++g_stats.resumes;
+                }
             }
+        }
         bool moved = false;
         for (int w0 = 0; w0 < n; w0 += 64) {
             const int wn = std::min(64, n - w0);

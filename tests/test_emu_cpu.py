@@ -441,3 +441,22 @@ def test_random_shapes(driver, tmp_path, seed):
             g[-1] &= 0x0F
             w[-1] &= 0x0F
     assert np.array_equal(g, w)
+
+
+@pytest.mark.parametrize("order,lanes", [("reverse", "forward"), ("shuffle", "reverse")])
+def test_results_do_not_depend_on_wave_order(driver, tmp_path, monkeypatch, order, lanes):
+    """The emulator runs the waves of a workgroup in reverse or shuffled
+    order between synchronization points (and the lanes of a wave in reverse
+    order): a kernel whose waves exchange data without a barrier would give
+    a different result.  The whole-tree and per-part packing paths with the
+    triangle."""
+    monkeypatch.setenv("EMU_ORDER", order)
+    monkeypatch.setenv("EMU_LANES", lanes)
+    monkeypatch.setenv("EMU_SEED", "11")
+    leaf, oob = forest(12, 400, 260, 9, p_invalid=0.01)    # T > 255: the byte-sum check runs
+    leaf[:, :40] = leaf[:, :1]
+    got, _ = emulate(driver, tmp_path, 1, leaf, oob, 9, O.FMT_U8, 1 / 255.0)
+    assert np.array_equal(got, O.upper_rows(leaf, oob, 9, O.FMT_U8, scale=np.float32(1 / 255.0)))
+    leaf, oob = forest(13, 40_000, 6, 300)
+    got, _ = emulate(driver, tmp_path, 1, leaf, oob, 300, O.FMT_U16, r0=19_998, r1=20_001)
+    assert np.array_equal(got, O.upper_rows(leaf, oob, 300, O.FMT_U16, r0=19_998, r1=20_001))
