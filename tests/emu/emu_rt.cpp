@@ -16,9 +16,9 @@
 // sites.  Dynamic LDS is a malloc'd block of exactly the launch's size, so
 // an AddressSanitizer build reports LDS accesses past it; device memory is
 // malloc'd too.  With EMU_STATS set, each launch prints its barrier
-// releases, wave builtin rounds and coroutine resumes; EMU_ORDER and
-// EMU_LANES change the order in which waves and lanes run between
-// synchronization points (see below).
+// releases, wave builtin rounds and coroutine resumes; EMU_ORDER, EMU_LANES
+// and EMU_BLOCKS change the order in which waves and lanes run between
+// synchronization points and the order of a launch's workgroups (see below).
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -246,6 +246,16 @@ const Order g_order = [] {
     fprintf(stderr, "[emu] EMU_ORDER must be forward, reverse or shuffle\n");
     abort();
 }();
+// EMU_BLOCKS: the order of a launch's workgroups, as EMU_ORDER ("forward",
+// "reverse", "shuffle").
+const Order g_blocks = [] {
+    const char* e = getenv("EMU_BLOCKS");
+    if (!e || !strcmp(e, "forward")) return FORWARD;
+    if (!strcmp(e, "reverse")) return REVERSE;
+    if (!strcmp(e, "shuffle")) return SHUFFLE;
+    fprintf(stderr, "[emu] EMU_BLOCKS must be forward, reverse or shuffle\n");
+    abort();
+}();
 // EMU_LANES=reverse runs the lanes of each wave from the last to the first
 // between synchronization points.
 const bool g_lanes_reversed = [] {
@@ -385,17 +395,28 @@ void launch_raw(const void*, const char* name, dim3 grid, dim3 block, size_t lds
     g_launch.closure = closure;
     g_launch.nthreads = (int)nt;
     g_launch.lds_bytes = lds;
-    for (uint32_t z = 0; z < grid.z; ++z)
-        for (uint32_t y = 0; y < grid.y; ++y)
-            for (uint32_t x = 0; x < grid.x; ++x) {
-                // exactly the launch's dynamic LDS (at least one byte), filled
-                // with a pattern so that reads of uncleared LDS show
-                g_launch.lds = (char*)malloc(lds ? lds : 1);
-                memset(g_launch.lds, 0xCD, lds ? lds : 1);
-                run_block(dim3(x, y, z), grid, block);
-                free(g_launch.lds);
-                g_launch.lds = nullptr;
-            }
+    // workgroups in grid order, or reversed / shuffled (EMU_BLOCKS)
+    const uint64_t nb = (uint64_t)grid.x * grid.y * grid.z;
+    std::vector<uint64_t> bo;
+    if (g_blocks != FORWARD) {
+        bo.resize(nb);
+        for (uint64_t b = 0; b < nb; ++b) bo[b] = g_blocks == REVERSE ? nb - 1 - b : b;
+        if (g_blocks == SHUFFLE)
+            for (uint64_t b = nb - 1; b > 0; --b)
+                std::swap(bo[b], bo[((uint64_t)next_rand() << 32 | next_rand()) % (b + 1)]);
+    }
+    for (uint64_t k = 0; k < nb; ++k) {
+        const uint64_t b = bo.empty() ? k : bo[k];
+        const uint32_t x = (uint32_t)(b % grid.x), y = (uint32_t)(b / grid.x % grid.y),
+                       z = (uint32_t)(b / ((uint64_t)grid.x * grid.y));
+        // exactly the launch's dynamic LDS (at least one byte), filled with a
+        // pattern so that reads of uncleared LDS show
+        g_launch.lds = (char*)malloc(lds ? lds : 1);
+        memset(g_launch.lds, 0xCD, lds ? lds : 1);
+        run_block(dim3(x, y, z), grid, block);
+        free(g_launch.lds);
+        g_launch.lds = nullptr;
+    }
     if (g_print_stats) {
         fprintf(stderr, "[emu-stats] %s grid %ux%ux%u block %llu: %llu barriers, %llu wave-op rounds, %llu resumes\n",
                 name, grid.x, grid.y, grid.z, (unsigned long long)nt, (unsigned long long)g_stats.barriers,
