@@ -246,6 +246,14 @@ const Order g_order = [] {
     fprintf(stderr, "[emu] EMU_ORDER must be forward, reverse or shuffle\n");
     abort();
 }();
+// EMU_FILL: the byte that fresh LDS and fresh device allocations hold
+// (default 0xCD for LDS, 0xAB for device memory).  A kernel that reads
+// memory it never wrote gives results that change with it.
+const int g_fill = [] {
+    const char* e = getenv("EMU_FILL");
+    return e ? (int)(strtol(e, nullptr, 0) & 0xff) : -1;
+}();
+
 // EMU_BLOCKS: the order of a launch's workgroups, as EMU_ORDER ("forward",
 // "reverse", "shuffle").
 const Order g_blocks = [] {
@@ -412,7 +420,7 @@ void launch_raw(const void*, const char* name, dim3 grid, dim3 block, size_t lds
         // exactly the launch's dynamic LDS (at least one byte), filled with a
         // pattern so that reads of uncleared LDS show
         g_launch.lds = (char*)malloc(lds ? lds : 1);
-        memset(g_launch.lds, 0xCD, lds ? lds : 1);
+        memset(g_launch.lds, g_fill >= 0 ? g_fill : 0xCD, lds ? lds : 1);
         run_block(dim3(x, y, z), grid, block);
         free(g_launch.lds);
         g_launch.lds = nullptr;
@@ -451,7 +459,7 @@ hipError_t hipMalloc(void** p, size_t n) {
     if (!p) return hipErrorInvalidValue;
     *p = malloc(n ? n : 1);
     if (!*p) return emu::g_last = hipErrorOutOfMemory;
-    memset(*p, 0xAB, n ? n : 1);  // device memory starts with garbage
+    memset(*p, emu::g_fill >= 0 ? emu::g_fill : 0xAB, n ? n : 1);  // device memory starts with garbage
     g_allocs[(uintptr_t)*p] = n ? n : 1;
     return hipSuccess;
 }

@@ -443,17 +443,20 @@ def test_random_shapes(driver, tmp_path, seed):
     assert np.array_equal(g, w)
 
 
-@pytest.mark.parametrize("order,lanes,blocks", [("reverse", "forward", "reverse"), ("shuffle", "reverse", "shuffle")])
-def test_results_do_not_depend_on_wave_order(driver, tmp_path, monkeypatch, order, lanes, blocks):
+@pytest.mark.parametrize("order,lanes,blocks,fill", [("reverse", "forward", "reverse", "0x00"),
+                                                     ("shuffle", "reverse", "shuffle", "0xff")])
+def test_results_do_not_depend_on_wave_order(driver, tmp_path, monkeypatch, order, lanes, blocks, fill):
     """The emulator runs the waves of a workgroup in reverse or shuffled
     order between synchronization points, the lanes of a wave in reverse
-    order and a launch's workgroups in reverse or shuffled order: a kernel
-    whose waves exchange data without a barrier, or whose workgroups depend
-    on their order, would give a different result.  The whole-tree and
-    per-part packing paths with the triangle."""
+    order and a launch's workgroups in reverse or shuffled order, with fresh
+    LDS and device memory holding another byte: a kernel whose waves
+    exchange data without a barrier, whose workgroups depend on their order,
+    or that reads memory it never wrote would give a different result.  The
+    whole-tree and per-part packing paths with the triangle."""
     monkeypatch.setenv("EMU_ORDER", order)
     monkeypatch.setenv("EMU_LANES", lanes)
     monkeypatch.setenv("EMU_BLOCKS", blocks)
+    monkeypatch.setenv("EMU_FILL", fill)
     monkeypatch.setenv("EMU_SEED", "11")
     leaf, oob = forest(12, 400, 260, 9, p_invalid=0.01)    # T > 255: the byte-sum check runs
     leaf[:, :40] = leaf[:, :1]
