@@ -6,10 +6,11 @@
 // oob_trees_ (per sample, the trees where it is out-of-bag).  A
 // ForestProximity built from them answers the same questions as the methods
 // named below, with their argument meaning and results; RandomForest and the
-// Python binding forward to it without changing their signatures (the
-// forwarding lines are in INTEGRATION.md).  Leaf labels are compared as
-// node indices; a negative label never matches (the reference's labels are
-// node indices >= 0).  Top-K ties are broken by the lower index.
+// Python binding forward to it without changing their signatures (each
+// method's body becomes one call on a ForestProximity member).  Leaf labels
+// are compared as node indices; a negative label never matches (the
+// reference's labels are node indices >= 0).  Top-K ties are broken by the
+// lower index.
 // Failures print one line to stderr and are readable with
 // rfx_compat_last_error(); results are then empty / false.
 #ifndef RFX_FOREST_HPP

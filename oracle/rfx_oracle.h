@@ -89,8 +89,9 @@ int orc_upper_rows(const int32_t* leaf, const uint8_t* oob, int64_t N, int32_t T
                    const int32_t* nout, int fmt, float scale, float zp, int64_t r0, int64_t r1,
                    void* out, int threads);
 
-/* The "both OOB" proximity (R randomForest's oob.prox; BASELINE config 1's
- * prose), which the reference does not implement: for i != j
+/* The "both OOB" proximity (R randomForest's oob.prox, named by the
+ * benchmark's first configuration), which the reference does not
+ * implement: for i != j
  *   num_ij = #{t : oob_i(t), oob_j(t), leaf_i(t) == leaf_j(t), label valid}
  *   den_ij = #{t : oob_i(t), oob_j(t)}
  *   P_ij   = den_ij > 0 ? (float)num_ij / (float)den_ij : 0,   P_ii = 1.

@@ -317,7 +317,7 @@ def test_rejects_bad_arguments(gpu_ctx):
 
 
 def test_c1_forest_matches_reference_digests(gpu_ctx):
-    """BASELINE config 1 leaf matrix (CART forest, N=2000, T=100): the GPU
+    """The first benchmark configuration's leaf matrix (CART forest, N=2000, T=100): the GPU
     triangle hashes to the digests of the reference's own cpu_proximity +
     cpu_finishprox output (tests/golden/make_golden.py)."""
     import hashlib
@@ -441,7 +441,7 @@ def test_whole_triangle_invariants(gpu_ctx, n, t, nleaf):
 
 
 def test_c2_shape_full_triangle_f32(gpu_ctx):
-    """BASELINE config 2 shape: N=20,000, T=500, 1,000-4,096 leaves per tree
+    """The second benchmark configuration's shape: N=20,000, T=500, 1,000-4,096 leaves per tree
     (the per-part packing path), fp32 output.  The whole triangle (2e8
     entries) equals the oracle's bit for bit, and so do the raw counts."""
     import torch
@@ -474,7 +474,7 @@ def test_c2_shape_full_triangle_f32(gpu_ctx):
 
 
 def test_c2_data_grown_regression_forest(gpu_ctx):
-    """BASELINE config 2's data (N = 20,000, p = 50, y = sin(x0) + x1 x2 +
+    """The second benchmark configuration's data (N = 20,000, p = 50, y = sin(x0) + x1 x2 +
     N(0, 0.1)) through a forest grown on it (sklearn CART, mtry 17, leaves of
     at least 5 samples, seeded bootstrap; 100 of the config's 500 trees to
     keep the growing short): ~2,000 leaves per tree of skewed sizes, labels

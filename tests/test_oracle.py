@@ -48,7 +48,7 @@ def test_rfgap_matches_reference_fixture():
 
 
 def test_c1_forest_triangle_matches_reference_digests():
-    """BASELINE config 1 (N=2000, T=100 CART forest): the oracle's packed
+    """The first benchmark configuration (N=2000, T=100 CART forest): the oracle's packed
     counts, (float)P and uint8 codes hash to the reference's."""
     g = np.load(os.path.join(GOLD, "c1_forest.npz"))
     lab = g["label"].astype(np.int32)
