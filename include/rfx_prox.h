@@ -351,10 +351,10 @@ int rfxp_lowrank_subspace(rfxp_ctx* ctx, const float* V0, int32_t r, int32_t ite
  * rfxp_symacc_reset, kept in device memory as a list of the contributions'
  * nonzero entries while that list and its symmetric CSR (28 bytes an entry)
  * take less than the packed upper triangle of M in doubles, and as that
- * triangle from then on.  Its memory is so at most
- * 8 N(N+1)/2 + 24 (N+1) bytes plus one staging band of a host input (at
- * most 256 MiB or one row), and up to 1.43 times the triangle while an add
- * switches forms; the number of contributions does not enter. */
+ * triangle from then on.  Its memory is so at most 8 N(N+1)/2 + 24 (N+1)
+ * bytes plus one staging buffer for host inputs (at most 256 MiB, or one row
+ * and a byte), and up to 1.43 times the triangle while an add switches
+ * forms; the number of contributions does not enter. */
 
 /* Empties the accumulator and sets its order N (1 <= N < 2^31 - 1);
  * releases what a previous accumulation held beyond this N's list limit. */

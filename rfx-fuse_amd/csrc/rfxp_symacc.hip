@@ -737,7 +737,8 @@ static int symacc_add_rows_sparse(rfxp_ctx* ctx, const SymSrc& s, int64_t r0, in
     if ((size_t)need > ctx->sa_i.n) {  // grow by half again (up to the limit), keeping the entries
         ctx->sa_col.release();          // the CSR is rebuilt after an add anyway
         ctx->sa_val.release();
-        const size_t cap = std::min<size_t>((size_t)limit, std::max<size_t>((size_t)need, ctx->sa_i.n + ctx->sa_i.n / 2));
+        const size_t cap =
+            std::min<size_t>((size_t)limit, std::max<size_t>((size_t)need, ctx->sa_i.n + ctx->sa_i.n / 2));
         DevBuf<int32_t> ni, nj;
         DevBuf<float> nv;
         if (ni.ensure(cap) != hipSuccess || nj.ensure(cap) != hipSuccess || nv.ensure(cap) != hipSuccess) {
@@ -773,6 +774,17 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
     const bool packed = s.kind != SRC_DENSE;
     if (!ctx->sa_dense) RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
     ctx->sa_csr_ok = false;
+    if (host) {
+        // one staging buffer for every band, sized before the first: growing
+        // it between bands would free memory that the previous band's kernels
+        // may still read.  A band is at most SA_STAGE_BYTES or one row (the
+        // first row is the longest; NF4 adds a byte for a band that starts
+        // at an odd entry).
+        const int64_t total = src_bytes(s.kind, N, 0, packed ? sa_entries(N) : N);
+        const int64_t row0 = src_bytes(s.kind, N, 0, packed ? N : 1) + 1;
+        const int64_t cap = std::min(total, std::max(SA_STAGE_BYTES, row0));
+        RFXP_HIP(ctx, ctx->sa_stage.ensure((size_t)(cap + 7) / 8));
+    }
     int64_t r0 = 0;
     while (r0 < N) {
         // band of rows [r0, r1): everything for a device input, else at most
@@ -790,7 +802,8 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
             }
             const int64_t nbytes = bytes_to(r1);
             const int64_t off = src_bytes(s.kind, N, 0, b0);
-            RFXP_HIP(ctx, ctx->sa_stage.ensure((size_t)(nbytes + 7) / 8));
+            if ((size_t)nbytes > 8 * ctx->sa_stage.n)
+                return set_error(ctx, RFXP_ERR_INVALID, "rfxp_symacc: staging band larger than its buffer");
             RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_stage.p, (const unsigned char*)s.p + off, (size_t)nbytes,
                                          hipMemcpyHostToDevice, ctx->stream));
             band.p = ctx->sa_stage.p;

@@ -289,8 +289,10 @@ def _check_steps(steps, contribs, n, X):
         dense = dense or listed > limit
         assert nnz == (ne if dense else listed)
         # the bound: the triangle in doubles, three N + 1 count arrays, one
-        # staged band (at most 256 bytes in this build, or one row)
-        assert nbytes <= 8 * ne + 24 * (n + 1) + max(264, 8 * n), (nbytes, 8 * ne)
+        # staging buffer (at most 256 bytes in this build, or one row of a
+        # dense input and a byte, in 8-byte words)
+        stage = -(-max(256, 8 * n + 1) // 8) * 8
+        assert nbytes <= 8 * ne + 24 * (n + 1) + stage, (nbytes, 8 * ne)
         want = M @ X
         assert np.abs(Y - want).max() <= 1e-12 * np.abs(M).sum(axis=1).max() * np.abs(X).max()
     return M
