@@ -775,11 +775,11 @@ static int symacc_add(rfxp_ctx* ctx, SymSrc s) {
     if (!ctx->sa_dense) RFXP_HIP(ctx, ctx->sa_cnt.ensure((size_t)N + 1));
     ctx->sa_csr_ok = false;
     if (host) {
-        // one staging buffer for every band, sized before the first: growing
-        // it between bands would free memory that the previous band's kernels
-        // may still read.  A band is at most SA_STAGE_BYTES or one row (the
-        // first row is the longest; NF4 adds a byte for a band that starts
-        // at an odd entry).
+        // one staging buffer for every band, sized before the first, so that
+        // an add never frees and reallocates it (hipFree synchronises the
+        // whole device) between bands.  A band is at most SA_STAGE_BYTES or
+        // one row (the first row is the longest; NF4 adds a byte for a band
+        // that starts at an odd entry).
         const int64_t total = src_bytes(s.kind, N, 0, packed ? sa_entries(N) : N);
         const int64_t row0 = src_bytes(s.kind, N, 0, packed ? N : 1) + 1;
         const int64_t cap = std::min(total, std::max(SA_STAGE_BYTES, row0));
