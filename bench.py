@@ -40,6 +40,12 @@ CONFIGS = {
     # low-rank SpMM: measurement case
     "c4": dict(workload="C4 low-rank P V and rank-32 subspace iteration", n=1_000_000, t=500, nleaf=4096,
                r=32, iters=5, zipf=1.1, seed=20261201 + 4),
+    # the reference's live GPU low-rank sequence (growtree: per tree an FP16
+    # triangle + the class's incremental add, then finalize), at the size of
+    # the reference README's largest GPU run (59,047 samples), 100 of its
+    # 1,000 trees; opt-in (--config cs2), not part of the default run
+    "cs2": dict(workload="CS2 growtree low-rank class sequence", n=59_047, t=100, nleaf=2000, level=1,
+                seed=20261201 + 6),
 }
 
 # Kernel sources whose rocprofv3 traffic summary (profiles/k_tri_<cfg>_traffic.md)
@@ -689,7 +695,118 @@ def run_c4(args, name="c4"):
     return rec
 
 
-RUNNERS = {"c3": run_triangle, "c2": run_triangle, "c5": run_c5, "c4": run_c4}
+# the C++ program that calls the class through the reference's signatures
+LRDRIVER = os.path.join(REPO, "tests", "compat", "lowrank_driver")
+
+
+def run_cs2(args, name="cs2"):
+    """The class sequence of cuda/rf_growtree.cu:5219-5410 through the
+    reference's own C++ signatures (tests/compat/lowrank_driver, mode
+    "measure", a separate process linked against librfxprox.so): per tree
+    cudaMalloc + memset of the N(N+1)/2 FP16 triangle,
+    gpu_proximity_upper_triangle_fp16 from host nodestatus / nodextr / nin,
+    add_tree_contribution_incremental_upper_triangle_fp16, free; then
+    finalize_accumulation(T, true), get_lowrank_factors_host and
+    compute_mds_from_factors_host.  One step = one tree.  The forest is
+    synthetic: nleaf terminal nodes per tree with skewed sizes, bootstrap
+    multiplicities for nin.  Returns the record."""
+    import statistics
+    import subprocess
+    import tempfile
+
+    import numpy as np
+
+    cfg = CONFIGS["cs2"]
+    n = args.n or cfg["n"]
+    t, nleaf, level = cfg["t"], cfg["nleaf"], cfg["level"]
+    drv = LRDRIVER
+    if not os.path.exists(drv):
+        raise RuntimeError("tests/compat/lowrank_driver is not built (make -C rfx-fuse_amd driver)")
+    rng = np.random.default_rng(cfg["seed"])
+    nnode = 2 * nleaf - 1
+    w = 1.0 / np.arange(1, nleaf + 1) ** 0.8
+    w /= w.sum()
+    with tempfile.TemporaryDirectory() as tmp:
+        inp, outp = os.path.join(tmp, "in.bin"), os.path.join(tmp, "out.bin")
+        nout = np.zeros(n, np.int32)
+        with open(inp, "wb") as f:
+            np.array([n, t, 0], np.int32).tofile(f)
+            for _ in range(t):
+                ns = np.ones(nnode, np.int32)
+                term = rng.choice(nnode, nleaf, replace=False)
+                ns[term] = -1
+                nx = term[rng.permutation(nleaf)[rng.choice(nleaf, n, p=w)]].astype(np.int32)
+                nin = np.bincount(rng.integers(0, n, n), minlength=n).astype(np.int32)
+                nout += nin == 0
+                np.array([nnode], np.int32).tofile(f)
+                ns.tofile(f)
+                nx.tofile(f)
+                nin.tofile(f)
+            nout.tofile(f)
+        wall0 = time.perf_counter()
+        r = subprocess.run(["timeout", "-k", "10", "900", drv, inp, outp, "measure", str(level)],
+                           capture_output=True, text=True)
+        wall = time.perf_counter() - wall0
+        if r.returncode != 0:
+            raise RuntimeError(f"lowrank_driver exited {r.returncode}: {(r.stdout + r.stderr)[-400:]}")
+        raw = np.fromfile(outp, np.uint8)
+    rank = int(raw[:4].view(np.int32)[0])
+    # skip the sections before the measurements (layout in the driver's header)
+    off = 12 + 2 * 8 * n * rank
+    nc = int(raw[off:off + 8].view(np.int64)[0])
+    off += 8 + 8 * nc
+    rec_flag = int(raw[off:off + 4].view(np.int32)[0])
+    off += 4 + (8 * n * n if rec_flag else 0)
+    mem = raw[off:off + 32].view(np.uint64)
+    off += 32 + 8 + 16 + 8
+    tt = int(raw[off:off + 4].view(np.int32)[0])
+    off += 4
+    times = raw[off:off + 24 * tt].view(np.float64).reshape((tt, 3))
+    off += 24 * tt
+    used = raw[off:off + 8 * tt].view(np.uint64).astype(np.int64)
+    off += 8 * tt
+    used0 = int(raw[off:off + 8].view(np.uint64)[0])
+    fin_ms, fac_ms, mds_ms = (float(x) for x in raw[off + 8:off + 32].view(np.float64))
+    step_ms = float(statistics.median(times[:, 2]))
+    ne = n * (n + 1) // 2
+    # compulsory HBM bytes of one tree: the caller's memset of the FP16
+    # triangle and one read of it by the add
+    compulsory = 2 * ne * 2
+    return {
+        "metric": "trees/s of the growtree low-rank sequence (CS2)",
+        "value": 1e3 / step_ms,
+        "unit": "trees/s",
+        "n_gpus": 1,
+        "steps": tt,
+        "warmup": 0,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": (f"synthetic ({nleaf} terminal nodes per tree, sizes ~ 1/k^0.8, bootstrap nin, seeded); "
+                 "one step = one tree, median over the trees"),
+        "config": {"workload": cfg["workload"], "N": n, "T": t, "leaves_per_tree": nleaf, "level": level,
+                   "rank": rank},
+        "kernels_ms": {"triangle_median": float(np.median(times[:, 0])),
+                       "add_median": float(np.median(times[:, 1])),
+                       "step_first": float(times[0, 2]), "step_max": float(times[:, 2].max())},
+        "finalize_ms": fin_ms,
+        "factors_copy_ms": fac_ms,
+        "mds_ms": mds_ms,
+        "device_bytes_after_add": {"first": int(used[0] - used0), "last": int(used[-1] - used0),
+                                   "max": int(used.max() - used0)},
+        "get_memory_usage": [int(x) for x in mem],
+        "driver_wall_s": wall,
+        "roofline": {"bound": "hbm", "achieved": compulsory / (step_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": compulsory / (step_ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+                     "compulsory_bytes": compulsory, "traffic": None},
+        # the reference has no CPU form of this class; nothing to time beside it
+        "cpu_baseline": None,
+    }
+
+
+RUNNERS = {"c3": run_triangle, "c2": run_triangle, "c5": run_c5, "c4": run_c4, "cs2": run_cs2}
 
 
 if __name__ == "__main__":

@@ -12,6 +12,11 @@
 //             (cpu_proximity_rfgap) through add_tree_contribution into
 //             new LowRankProximityMatrix(N, 8, level, 16, 30), then
 //             set_oob_counts_for_rfgap(nout), no finalize call.
+//   measure   the growtree sequence, timed: per tree the wall time of the
+//             caller's steps (device synchronised after each), the device
+//             memory in use after the add (hipMemGetInfo, the tree's FP16
+//             triangle still allocated), then finalize, the factor copy and
+//             MDS; no reconstruction (N x N doubles).
 // Input: the forest dump of tests/test_gpu_compat.py.  Output (binary):
 // int32 rank, is_quantized, level; A, B (N*rank f64 each, column-major);
 // int64 n_coords, coords (f64, N x 3 row-major); int32 reconstructed
@@ -19,17 +24,32 @@
 // (4 x u64); should_use_incremental(N, 0) and (N, 2^40) (2 x i32);
 // estimate_optimal_rank at (N,1000), (N,5), (0,7), (-3,0) (4 x i32);
 // get_factors' rank and pointer state before any contribution (2 x i32).
+// measure appends: int32 T; per tree f64 triangle_ms, add_ms, step_ms
+// (allocation, clearing, triangle, add and free); per tree u64 device
+// bytes in use after the add; u64 bytes in use before the object existed;
+// f64 finalize_ms, factors_ms, mds_ms.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <chrono>
 #include <vector>
 
 #include "rfx_compat.hpp"
 
 using rf::cuda::LowRankProximityMatrix;
 using rf::cuda::QuantizationLevel;
+
+static double now_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+static uint64_t device_used() {
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) != hipSuccess) return 0;
+    return (uint64_t)(tot - fr);
+}
 
 static void rd(FILE* f, void* p, size_t n) {
     if (fread(p, 1, n, f) != n) {
@@ -40,10 +60,11 @@ static void rd(FILE* f, void* p, size_t n) {
 
 int main(int argc, char** argv) {
     if (argc != 5) {
-        fprintf(stderr, "usage: lowrank_driver in.bin out.bin growtree|rfgap level\n");
+        fprintf(stderr, "usage: lowrank_driver in.bin out.bin growtree|rfgap|measure level\n");
         return 2;
     }
     const bool rfgap = strcmp(argv[3], "rfgap") == 0;
+    const bool measure = strcmp(argv[3], "measure") == 0;
     const int level = atoi(argv[4]);
     FILE* f = fopen(argv[1], "rb");
     if (!f) return 2;
@@ -77,22 +98,44 @@ int main(int argc, char** argv) {
 
     LowRankProximityMatrix* lr = nullptr;
     const QuantizationLevel q = (QuantizationLevel)level;
+    std::vector<double> tri_ms(T), add_ms(T), step_ms(T);
+    std::vector<uint64_t> used(T);
+    double fin_ms = 0.0, fac_ms = 0.0, mds_ms = 0.0;
+    (void)hipDeviceSynchronize();
+    const uint64_t used0 = device_used();
     if (!rfgap) {
         lr = new LowRankProximityMatrix(N, 0, q, 1000, 30);
         if (!lr->initialize()) return 3;
         const size_t ne = (size_t)N * (N + 1) / 2;
         for (int32_t t = 0; t < T; ++t) {
+            const double t0 = now_ms();
             __half* d16 = nullptr;
             if (hipMalloc((void**)&d16, ne * sizeof(__half)) != hipSuccess) return 3;
             (void)hipMemset(d16, 0, ne * sizeof(__half));
+            if (measure) (void)hipDeviceSynchronize();
+            const double t1 = now_ms();
             rf::cuda::gpu_proximity_upper_triangle_fp16(status[t].data(), nodextr[t].data(), nin[t].data(), N,
                                                         nnode[t], d16, nullptr, nullptr, nullptr, nullptr, nullptr,
                                                         nullptr);
+            if (measure) (void)hipDeviceSynchronize();
+            const double t2 = now_ms();
             lr->add_tree_contribution_incremental_upper_triangle_fp16(d16, N);
+            if (measure) {
+                (void)hipDeviceSynchronize();
+                used[t] = device_used();
+            }
+            const double t3 = now_ms();
             (void)hipFree(d16);
+            if (measure) (void)hipDeviceSynchronize();
+            tri_ms[t] = t2 - t1;
+            add_ms[t] = t3 - t2;
+            step_ms[t] = now_ms() - t0;
         }
         (void)hipDeviceSynchronize();
+        const double t0 = now_ms();
         lr->finalize_accumulation(T, /*final_call=*/true);
+        (void)hipDeviceSynchronize();
+        fin_ms = now_ms() - t0;
     } else {
         std::vector<double> rg((size_t)N * N, 0.0);
         rf::cpu_proximity_rfgap(T, N, nin, nodextr, rg.data());
@@ -104,13 +147,17 @@ int main(int argc, char** argv) {
 
     double *A = nullptr, *B = nullptr;
     rf::integer_t r = 0;
+    double tm = now_ms();
     if (!rf::cuda::get_lowrank_factors_host(lr, &A, &B, &r, N)) {
         fprintf(stderr, "no factors: %s\n", rfx_compat_last_error());
         return 4;
     }
+    fac_ms = now_ms() - tm;
+    tm = now_ms();
     std::vector<double> coords = rf::cuda::compute_mds_from_factors_host(lr, 3);
+    mds_ms = now_ms() - tm;
     double* P = nullptr;
-    const int32_t rec = rf::cuda::reconstruct_proximity_matrix_host(lr, &P, N) ? 1 : 0;
+    const int32_t rec = !measure && rf::cuda::reconstruct_proximity_matrix_host(lr, &P, N) ? 1 : 0;
     uint64_t mem[4];
     for (int l = 0; l < 4; ++l) mem[l] = lr->get_memory_usage((QuantizationLevel)l);
     int32_t inc[2] = {LowRankProximityMatrix::should_use_incremental(N, 0) ? 1 : 0,
@@ -137,6 +184,17 @@ int main(int argc, char** argv) {
     fwrite(inc, 4, 2, o);
     fwrite(est, 4, 4, o);
     fwrite(empty_state, 4, 2, o);
+    if (measure) {
+        fwrite(&T, 4, 1, o);
+        for (int32_t t = 0; t < T; ++t) {
+            const double x[3] = {tri_ms[t], add_ms[t], step_ms[t]};
+            fwrite(x, 8, 3, o);
+        }
+        fwrite(used.data(), 8, (size_t)T, o);
+        fwrite(&used0, 8, 1, o);
+        const double y[3] = {fin_ms, fac_ms, mds_ms};
+        fwrite(y, 8, 3, o);
+    }
     fclose(o);
     delete[] A;
     delete[] B;

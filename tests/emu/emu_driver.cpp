@@ -285,19 +285,30 @@ int main(int argc, char** argv) {
         return 0;
     };
     if (rc) return fail(rc);
-    const int32_t* np = has_nout ? nout.data() : nullptr;
+    // the inputs and outputs in device memory, as the C ABI requires of them
+    auto to_dev = [](const void* h, size_t n) {
+        void* d = nullptr;
+        hipMalloc(&d, n ? n : 1);
+        if (n) hipMemcpy(d, h, n, hipMemcpyHostToDevice);
+        return d;
+    };
+    const int32_t* leaf_d = (const int32_t*)to_dev(leaf.data(), 4 * leaf.size());
+    const uint32_t* oob_d = (const uint32_t*)to_dev(oob.data(), 4 * oob.size());
+    const int32_t* np = has_nout ? (const int32_t*)to_dev(nout.data(), 4 * nout.size()) : nullptr;
     if (mode == 1 || mode == 3) {
         const int64_t nb = rfxp_upper_nbytes(fmt, N, r0, r1);
         std::vector<unsigned char> out((size_t)nb + 64, 0xA5);
+        unsigned char* out_d = (unsigned char*)to_dev(out.data(), out.size());
         if (mode == 1) {
-            if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
-            if ((rc = rfxp_upper(ctx, fmt, scale, zp, r0, r1, out.data()))) return fail(rc);
+            if ((rc = rfxp_set_forest(ctx, leaf_d, si, st, oob_d, ld, N, T, nleaf, np))) return fail(rc);
+            if ((rc = rfxp_upper(ctx, fmt, scale, zp, r0, r1, out_d))) return fail(rc);
         } else {
-            if ((rc = rfxp_upper_noalloc(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np, fmt, scale, zp, r0,
-                                         r1, out.data())))
+            if ((rc = rfxp_upper_noalloc(ctx, leaf_d, si, st, oob_d, ld, N, T, nleaf, np, fmt, scale, zp, r0, r1,
+                                         out_d)))
                 return fail(rc);
         }
         rfxp_sync(ctx);
+        hipMemcpy(out.data(), out_d, out.size(), hipMemcpyDeviceToHost);
         int32_t ok = 1;
         for (int k = 0; k < 64; ++k) ok &= out[(size_t)nb + k] == 0xA5;
         int64_t rec = -1;
@@ -308,16 +319,19 @@ int main(int argc, char** argv) {
         fwrite(&ok, 4, 1, o);
         fwrite(&rec, 8, 1, o);
     } else if (mode == 2) {
-        if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
+        if ((rc = rfxp_set_forest(ctx, leaf_d, si, st, oob_d, ld, N, T, nleaf, np))) return fail(rc);
         float mm[2] = {0, 0};
         if ((rc = rfxp_upper_minmax(ctx, r0, r1, mm))) return fail(rc);
         fwrite(&rc, 4, 1, o);
         fwrite(mm, 4, 2, o);
     } else if (mode == 4) {
-        if ((rc = rfxp_set_forest(ctx, leaf.data(), si, st, oob.data(), ld, N, T, nleaf, np))) return fail(rc);
+        if ((rc = rfxp_set_forest(ctx, leaf_d, si, st, oob_d, ld, N, T, nleaf, np))) return fail(rc);
         std::vector<float> Y(V.size(), -7.0f);
-        if ((rc = rfxp_lowrank_oob_pv(ctx, V.data(), fmt, Y.data()))) return fail(rc);
+        const float* V_d = (const float*)to_dev(V.data(), 4 * V.size());
+        float* Y_d = (float*)to_dev(Y.data(), 4 * Y.size());
+        if ((rc = rfxp_lowrank_oob_pv(ctx, V_d, fmt, Y_d))) return fail(rc);
         rfxp_sync(ctx);
+        hipMemcpy(Y.data(), Y_d, 4 * Y.size(), hipMemcpyDeviceToHost);
         fwrite(&rc, 4, 1, o);
         fwrite(Y.data(), 4, Y.size(), o);
     } else {

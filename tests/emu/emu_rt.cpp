@@ -15,7 +15,11 @@
 // masked lane, or threads at different barriers stop the run with the call
 // sites.  Dynamic LDS is a malloc'd block of exactly the launch's size, so
 // an AddressSanitizer build reports LDS accesses past it; device memory is
-// malloc'd too.  With EMU_STATS set, each launch prints its barrier
+// malloc'd too.  Every 8-byte word of a launch's arguments that points into
+// host memory -- the host thread's stack, or (AddressSanitizer build) a
+// heap block that is not a hipMalloc allocation -- stops the run: on the GPU
+// the kernel's access through it would be a memory fault (the library uses
+// no pinned or managed host memory).  With EMU_STATS set, each launch prints its barrier
 // releases, wave builtin rounds and coroutine resumes; EMU_ORDER, EMU_LANES
 // and EMU_BLOCKS change the order in which waves and lanes run between
 // synchronization points and the order of a launch's workgroups (see below).
@@ -38,7 +42,9 @@
 #define EMU_ASAN 1
 #endif
 #endif
+#include <pthread.h>
 #ifdef EMU_ASAN
+extern "C" const void* __sanitizer_get_allocated_begin(const void* p);
 extern "C" void __sanitizer_start_switch_fiber(void** fake_stack_save, const void* bottom, size_t size);
 extern "C" void __sanitizer_finish_switch_fiber(void* fake_stack_save, const void** bottom_old, size_t* size_old);
 #endif
@@ -387,8 +393,11 @@ uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, 
     return t->res;
 }
 
+void check_kernel_args(const char* name, const void* args, size_t bytes);
+
 void launch_raw(const void*, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t, Body body,
-                void* closure) {
+                void* closure, const void* args, size_t args_bytes) {
+    check_kernel_args(name, args, args_bytes);
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t nt = (uint64_t)block.x * block.y * block.z;
     if (nt == 0 || nt > MAX_THREADS || grid.x == 0 || grid.y == 0 || grid.z == 0) {
@@ -466,6 +475,62 @@ hipError_t hipMalloc(void** p, size_t n) {
 hipError_t hipFree(void* p) {
     g_allocs.erase((uintptr_t)p);
     free(p);
+    return hipSuccess;
+}
+namespace emu {
+
+// True when p lies in a live hipMalloc allocation or one past its end.
+static bool in_device_alloc(uintptr_t p) {
+    auto it = g_allocs.upper_bound(p);
+    if (it == g_allocs.begin()) return false;
+    --it;
+    return p <= it->first + it->second;
+}
+
+// The launch's arguments as stored for the kernel (8-byte words at 8-byte
+// offsets): a word pointing into the host thread's stack, or into a host
+// heap block (AddressSanitizer build), stops the run.
+void check_kernel_args(const char* name, const void* args, size_t bytes) {
+    static uintptr_t stack_lo = 0, stack_hi = 0;
+    if (!stack_hi) {
+        pthread_attr_t at;
+        void* base = nullptr;
+        size_t size = 0;
+        if (pthread_getattr_np(pthread_self(), &at) == 0) {
+            pthread_attr_getstack(&at, &base, &size);
+            pthread_attr_destroy(&at);
+        }
+        stack_lo = (uintptr_t)base;
+        stack_hi = stack_lo + size;
+    }
+    for (size_t o = 0; o + 8 <= bytes; o += 8) {
+        uintptr_t w;
+        memcpy(&w, (const char*)args + o, 8);
+        if (w < 4096 || in_device_alloc(w)) continue;
+        const char* what = nullptr;
+        if (w >= stack_lo && w < stack_hi) what = "the host stack";
+#ifdef EMU_ASAN
+        else if (const void* b = __sanitizer_get_allocated_begin((const void*)w))
+            if (!in_device_alloc((uintptr_t)b)) what = "host heap memory";
+#endif
+        if (what) {
+            fprintf(stderr, "emu: kernel %s: argument bytes %zu..%zu point into %s (%p), not device memory\n",
+                    name ? name : "?", o, o + 7, what, (void*)w);
+            abort();
+        }
+    }
+}
+
+}  // namespace emu
+
+// A device of MI355X's 288 GiB whose free memory is that less the live
+// hipMalloc allocations.
+hipError_t hipMemGetInfo(size_t* free_b, size_t* total_b) {
+    const size_t total = (size_t)288 << 30;
+    size_t used = 0;
+    for (const auto& a : g_allocs) used += a.second;
+    if (free_b) *free_b = used < total ? total - used : 0;
+    if (total_b) *total_b = total;
     return hipSuccess;
 }
 hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) {

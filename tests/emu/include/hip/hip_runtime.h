@@ -120,7 +120,7 @@ uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, 
 
 typedef void (*Body)(void* closure);
 void launch_raw(const void* kernel, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, Body body,
-                void* closure);
+                void* closure, const void* args, size_t args_bytes);
 
 template <class T>
 inline uint64_t to_bits(T v) {
@@ -149,7 +149,7 @@ inline void launch(void (*kernel)(P...), const char* name, dim3 grid, dim3 block
                    C* cc = (C*)p;
                    std::apply(cc->k, *cc->t);
                },
-               &c);
+               &c, (const void*)&t, sizeof(t));
 }
 }  // namespace emu
 
@@ -367,6 +367,7 @@ hipError_t hipMalloc(void** p, size_t n);
 template <class T>
 inline hipError_t hipMalloc(T** p, size_t n) { return hipMalloc((void**)p, n); }
 hipError_t hipFree(void* p);
+hipError_t hipMemGetInfo(size_t* free_b, size_t* total_b);
 hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind k);
 hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t st = nullptr);
 hipError_t hipMemset(void* d, int v, size_t n);

@@ -105,6 +105,7 @@ def cpu_bench(monkeypatch):
         "c2": dict(bench.CONFIGS["c2"], n=2000, t=40, nleaf=64, leaves=(20, 64)),
         "c5": dict(bench.CONFIGS["c5"], n=4000, q=64, t=24, nleaf=32),
         "c4": dict(bench.CONFIGS["c4"], n=3000, t=20, nleaf=64, r=8),
+        "cs2": dict(bench.CONFIGS["cs2"], n=300, t=6, nleaf=12),
     }
     monkeypatch.setattr(bench, "CONFIGS", small)
     _FakeContext.fail_on = None
@@ -177,3 +178,18 @@ def test_more_than_one_gpu_exits(cpu_bench):
         sys.argv = old
     assert e.value.code == 2
     assert "one GPU" in json.loads(buf.getvalue())["error"]
+
+
+def test_cs2_record_from_the_emulated_driver(cpu_bench, emu_driver, monkeypatch):
+    """--config cs2 runs the class driver in its measure mode and turns its
+    output into the record: here the driver is the one linked against the
+    CPU emulation of the library (tests/emu), on a small forest."""
+    monkeypatch.setattr(cpu_bench, "LRDRIVER", os.path.join(os.path.dirname(emu_driver), "lowrank_driver"))
+    monkeypatch.setenv("ASAN_OPTIONS", "detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+    monkeypatch.setenv("EMU_TRACK_HOST", "1")
+    rec = _run(cpu_bench, ["--config", "cs2"])
+    assert rec["config"]["N"] == 300 and rec["config"]["rank"] == 17 and rec["steps"] == 6
+    assert rec["ms_per_step"] > 0 and rec["value"] > 0 and rec["finalize_ms"] > 0
+    assert rec["roofline"]["compulsory_bytes"] == 2 * 2 * (300 * 301 // 2)
+    assert rec["device_bytes_after_add"]["max"] > 0
+    assert rec["get_memory_usage"][1] == 2 * 300 * 17 * 2    # FP16 factors A and B

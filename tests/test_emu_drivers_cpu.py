@@ -40,3 +40,14 @@ def test_lowrank_class_rfgap_sequence(emu_build, monkeypatch, tmp_path):
 def test_forest_proximity_object(emu_build, monkeypatch, tmp_path):
     monkeypatch.setattr(GF, "FDRIVER", os.path.join(emu_build, "forest_driver"))
     GF.test_forest_proximity_object(tmp_path, 400, 37, 9, 23, 24)   # pairs past N = 400 read as out of range
+
+
+def test_lowrank_class_growtree_sequence_through_the_dense_form(emu_build, monkeypatch, tmp_path):
+    """The growtree sequence at N = 1,200 with 30 trees of 12 leaves, whose
+    nonzeros pass the entry-list limit, so the accumulator changes to the
+    dense triangle on the way; the GPU suite runs the same check at
+    N = 5,000."""
+    monkeypatch.setattr(GL, "LRDRIVER", os.path.join(emu_build, "lowrank_driver"))
+    d = GL.check_growtree_at_scale(tmp_path, 1200, 30, 12, 1200, timeout=600)
+    used = d["stats"]["used"]
+    assert used[-1] == used[-2]   # the dense form holds no per-add memory
