@@ -402,10 +402,13 @@ def check_growtree_at_scale(tmp_path, n, t, nleaf, seed, timeout):
     rank-r positive-part error of the exact sum of the per-tree FP16
     triangles.  The trees' nonzeros pass the accumulator's entry-list limit
     (N(N+1)/2 / 7 * 2 entries), so the sequence goes through its change to
-    the dense triangle.  The device memory in use after every add stays below
-    the packed double triangle + one FP16 triangle + the list at its limit
-    (8 bytes an entry of N(N+1)/2 bounds list and CSR) and 256 MiB for the
-    rest of the context.  Returns the driver's output."""
+    the dense triangle.  Device memory: after every add, what is in use
+    beyond the start stays below the packed double triangle + one FP16
+    triangle + the list at its limit (8 bytes an entry of N(N+1)/2 bounds
+    list and CSR) + 1 GiB for the rest of the context and the HIP runtime's
+    own allocations; over the last 10 trees (dense form) it grows by at most
+    16 MiB (the list form would add 12 bytes per nonzero, about 3.5 MB a
+    tree at N = 5,000).  Returns the driver's output."""
     forest = grown_like_forest(seed, n, t, nleaf)
     d = run_lowrank_driver(tmp_path, "measure", 0, forest=forest, timeout=timeout)
     r, A = d["rank"], d["A"]
@@ -418,8 +421,10 @@ def check_growtree_at_scale(tmp_path, n, t, nleaf, seed, timeout):
     err = np.linalg.norm(A @ A.T - M)
     assert err <= 1.01 * top_positive_part_error(M, r)
     st = d["stats"]
-    bound = ne * 8 + ne * 2 + ne * 8 + (256 << 20)
-    assert (st["used"] - st["used0"] <= bound).all(), (st["used"].max() - st["used0"], bound)
+    used = st["used"].astype(np.int64)
+    bound = ne * 8 + ne * 2 + ne * 8 + (1 << 30)
+    assert (used - st["used0"] <= bound).all(), (used.max() - st["used0"], bound)
+    assert (used[-10:] - used[-10]).max() <= 16 << 20, used[-10:]
     assert (st["step_ms"] > 0).all() and st["finalize_ms"] > 0
     assert d["coords"].shape == (n, 3)
     return d
