@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X proximity hot path (one GPU).
 
-Workload (the north-star target): N=100,000
+Workload (the headline configuration, C3): N=100,000
 samples, T=500 trees, int32 leaf ids drawn uniformly from 2,048 leaves per
 tree, OOB bits Bernoulli(0.368) iid; output = the uint8-quantized normalised
 OOB proximity upper triangle (N(N+1)/2 = 5,000,050,000 bytes) with the
@@ -30,14 +30,14 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 CONFIGS = {
     "c3": dict(workload="C3 quantized uint8 upper triangle", n=100_000, t=500, nleaf=2048,
                leaves=(2048, 2048), p_oob=0.368, fmt="u8", seed=20261201 + 3),
-    # mid-size fp32 triangle: a measurement case
+    # mid-size fp32 triangle (C2): a measurement case
     "c2": dict(workload="C2 fp32 upper triangle", n=20_000, t=500, nleaf=4096,
                leaves=(1000, 4096), p_oob=0.368, fmt="f32", seed=20261201 + 2),
-    # top-K retrieval: a parity/measurement case,
+    # top-K retrieval of new queries over all trees (C5): a parity/measurement case,
     # not the driver's bench line
     "c5": dict(workload="C5 top-K retrieval", n=1_000_000, q=100_000, t=500, nleaf=2048, k=20,
                seed=20261201 + 5),
-    # low-rank SpMM: measurement case
+    # low-rank one-hot SpMM and subspace iteration (C4): measurement case
     "c4": dict(workload="C4 low-rank P V and rank-32 subspace iteration", n=1_000_000, t=500, nleaf=4096,
                r=32, iters=5, zipf=1.1, seed=20261201 + 4),
     # the reference's live GPU low-rank sequence (growtree: per tree an FP16

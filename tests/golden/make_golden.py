@@ -9,7 +9,7 @@ Fixtures
                       indices out of range, bootstrap multiplicities, rows
                       with nout = 0): rf::cpu_proximity accumulated over the
                       trees (casewise off and on) and rf::cpu_finishprox.
-  c1_forest.npz       BASELINE config 1 (N=2000, p=20, T=100, mtry=4,
+  c1_forest.npz       the first benchmark configuration (N=2000, p=20, T=100, mtry=4,
                       nodesize=1): leaf matrix of a CART forest grown here on
                       seeded bootstraps, plus SHA-256 digests of the
                       reference's packed count triangle, of (float)P of its
