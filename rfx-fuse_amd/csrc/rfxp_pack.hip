@@ -1237,6 +1237,13 @@ void fill_u32(rfxp_ctx* ctx, uint32_t* p, int64_t n, uint32_t val) {
                        p, n, val);
 }
 
+// Bound of T * ms + MEM_PAD (ids) for the line-fit layout: byte offsets of
+// mem below 2^32.  A build may lower it (the CPU emulation's tests do, to
+// run the per-part path's back-to-back placement on small forests).
+#ifndef RFXP_FIT_LIMIT
+#define RFXP_FIT_LIMIT (1LL << 30)
+#endif
+
 ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     ForestSizes z;
     const int64_t N = v.N, n1 = std::max<int64_t>(N, 1);
@@ -1261,7 +1268,7 @@ ForestSizes forest_sizes(const LeafView& v, bool count_nout, int max_lds) {
     // the line-fit layout keeps every byte offset of mem within 32 bits
     // (mem_bytes of the triangle's buffer loads); past that the per-part
     // path places its buckets back to back
-    z.fit = z.part_path && (int64_t)T * fit_stride(N, nb) + MEM_PAD < (1LL << 30);
+    z.fit = z.part_path && (int64_t)T * fit_stride(N, nb) + MEM_PAD < (int64_t)(RFXP_FIT_LIMIT);
     z.ms = z.fit ? fit_stride(N, nb) : n1;
     z.n[FB_OFF] = (size_t)T * (nb + 1);
     z.n[FB_MEM] = (size_t)T * z.ms + MEM_PAD;

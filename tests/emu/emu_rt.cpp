@@ -479,6 +479,11 @@ hipError_t hipFree(void* p) {
 }
 namespace emu {
 
+long long knob(const char* name, long long dflt) {
+    const char* e = getenv(name);
+    return e && *e ? strtoll(e, nullptr, 0) : dflt;
+}
+
 // True when p lies in a live hipMalloc allocation or one past its end.
 static bool in_device_alloc(uintptr_t p) {
     auto it = g_allocs.upper_bound(p);

@@ -118,6 +118,10 @@ enum WaveOp {
 };
 uint64_t wave(int op, uint64_t v, int64_t arg, int64_t width, const char* file, int line);
 
+// A build-time constant of the library that the emulation lets a test set:
+// the environment variable `name` as an integer, else dflt.
+long long knob(const char* name, long long dflt);
+
 typedef void (*Body)(void* closure);
 void launch_raw(const void* kernel, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, Body body,
                 void* closure, const void* args, size_t args_bytes);

@@ -68,7 +68,7 @@ class EmuScript:
     def call(self, name, *args):
         self.calls.append((name, args))
 
-    def run(self, tmp_path, timeout=900):
+    def run(self, tmp_path, timeout=900, env_extra=None):
         inp, outp = os.path.join(str(tmp_path), "script.bin"), os.path.join(str(tmp_path), "script.out")
         with open(inp, "wb") as f:
             f.write(struct.pack("<ii", 6, len(self.bufs)))
@@ -93,7 +93,8 @@ class EmuScript:
                         f.write(struct.pack("<idq", 1, float(a), 0))
                     else:
                         raise TypeError(f"argument {a!r} of {name}")
-        env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+        env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1",
+                   **(env_extra or {}))
         r = subprocess.run(["timeout", "-k", "10", str(timeout), self.driver, inp, outp], capture_output=True,
                            text=True, env=env)
         assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]

@@ -35,7 +35,7 @@ def pack_words(oob):
 
 
 def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, zp=0.0, r0=0, r1=None,
-            nout=None, layout="tree", V=None):
+            nout=None, layout="tree", V=None, env_extra=None):
     t, n = leaf.shape
     r1 = n if r1 is None else r1
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
@@ -48,7 +48,8 @@ def emulate(driver, tmp_path, mode, leaf, oob, nleaf, fmt=O.FMT_U16, scale=1.0, 
             np.asarray(nout, np.int32).tofile(f)
         if V is not None:
             np.ascontiguousarray(V, np.float32).tofile(f)
-    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1",
+               **(env_extra or {}))
     r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
                        text=True, env=env)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]
@@ -129,6 +130,41 @@ def test_per_part_path_row_bands(driver, tmp_path, n, t, nleaf, bands):
             got, _ = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, r0=r0, r1=r1)
             assert np.array_equal(got, idx.rows(fmt, r0, r1, np.float32(scale), np.float32(0.0))), (r0, fmt)
     idx.close()
+
+
+@pytest.mark.parametrize("n,t,nleaf,bands", [
+    (40_000, 10, 400, [(0, 2), (39_995, 40_000)]),
+    (90_000, 4, 150, [(8_527, 8_530), (89_998, 90_000)]),
+])
+def test_per_part_path_back_to_back_placement(driver, tmp_path, n, t, nleaf, bands):
+    """Per-part forests whose line-fit layout would pass 2^30 ids (T * the
+    padded tree stride) place their buckets back to back, tree stride N: at
+    C3's N that takes about 4,500 trees.  The emulation lowers the bound
+    (RFXP_FIT_LIMIT = 1) so that these small forests take that placement;
+    the counts, the split rows and the OOB-normalised P V through the bucket
+    ends stay exact."""
+    from emu_session import EmuScript
+
+    env = {"RFXP_FIT_LIMIT": "1"}
+    # the bound takes effect: the forest index (the noalloc workspace counts
+    # it) shrinks by the line-fit padding
+    ws = []
+    for extra in (None, env):
+        s = EmuScript(driver)
+        s.call("rfxp_upper_noalloc_workspace", n, t, nleaf, 0)
+        ws.append(s.run(tmp_path, env_extra=extra)[0])
+    assert 0 < ws[1] < ws[0], ws
+    leaf, oob = forest(15 + n + nleaf, n, t, nleaf, p_invalid=0.01)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for r0, r1 in bands:
+        for fmt, scale in ((O.FMT_U16, 1.0), (O.FMT_U8, 1 / 255.0)):
+            got, _ = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, r0=r0, r1=r1, env_extra=env)
+            assert np.array_equal(got, idx.rows(fmt, r0, r1, np.float32(scale), np.float32(0.0))), (r0, fmt)
+    idx.close()
+    V = np.random.default_rng(23).standard_normal((n, 4)).astype(np.float32)
+    Y = emulate(driver, tmp_path, 4, leaf, oob, nleaf, fmt=4, V=V, env_extra=env)
+    want = oob_pv_reference(leaf, oob, nleaf, V)
+    assert np.linalg.norm(Y - want) / np.linalg.norm(want) < 1e-6
 
 
 def test_sample_major_layout_and_caller_nout(driver, tmp_path):
@@ -258,7 +294,8 @@ def emulate_symacc(driver, tmp_path, n, contribs, X, rank=0, iters=0):
             f.write(struct.pack("<iiffq", fmt, int(on_dev), np.float32(scale), np.float32(zp), len(raw)))
             f.write(raw)
         np.ascontiguousarray(X, np.float64).tofile(f)
-    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
+    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1",
+               **(env_extra or {}))
     r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
                        text=True, env=env)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]
