@@ -294,8 +294,7 @@ def emulate_symacc(driver, tmp_path, n, contribs, X, rank=0, iters=0):
             f.write(struct.pack("<iiffq", fmt, int(on_dev), np.float32(scale), np.float32(zp), len(raw)))
             f.write(raw)
         np.ascontiguousarray(X, np.float64).tofile(f)
-    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1",
-               **(env_extra or {}))
+    env = dict(os.environ, ASAN_OPTIONS="detect_stack_use_after_return=0:detect_leaks=0:abort_on_error=1")
     r = subprocess.run(["timeout", "-k", "10", "600", driver, str(inp), str(outp)], capture_output=True,
                        text=True, env=env)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-6000:]
