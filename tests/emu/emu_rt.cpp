@@ -16,10 +16,12 @@
 // sites.  Dynamic LDS is a malloc'd block of exactly the launch's size, so
 // an AddressSanitizer build reports LDS accesses past it; device memory is
 // malloc'd too.  Every 8-byte word of a launch's arguments that points into
-// host memory -- the host thread's stack, or (AddressSanitizer build) a
-// heap block that is not a hipMalloc allocation -- stops the run: on the GPU
-// the kernel's access through it would be a memory fault (the library uses
-// no pinned or managed host memory).  With EMU_STATS set, each launch prints its barrier
+// host memory -- the live part of the host thread's stack, or
+// (AddressSanitizer build) a heap block that is not a hipMalloc allocation --
+// stops the run: on the GPU the kernel's access through it would be a
+// memory fault (the library uses no pinned or managed host memory).  The
+// build fills every local with a byte pattern before use, so padding bytes
+// between arguments hold that pattern, never a stale address.  With EMU_STATS set, each launch prints its barrier
 // releases, wave builtin rounds and coroutine resumes; EMU_ORDER, EMU_LANES
 // and EMU_BLOCKS change the order in which waves and lanes run between
 // synchronization points and the order of a launch's workgroups (see below).
@@ -508,12 +510,14 @@ void check_kernel_args(const char* name, const void* args, size_t bytes) {
         stack_lo = (uintptr_t)base;
         stack_hi = stack_lo + size;
     }
+    // the live part of the stack: from this frame up to the stack's top
+    const uintptr_t live_lo = (uintptr_t)__builtin_frame_address(0);
     for (size_t o = 0; o + 8 <= bytes; o += 8) {
         uintptr_t w;
         memcpy(&w, (const char*)args + o, 8);
         if (w < 4096 || in_device_alloc(w)) continue;
         const char* what = nullptr;
-        if (w >= stack_lo && w < stack_hi) what = "the host stack";
+        if (w >= live_lo && w < stack_hi && w >= stack_lo) what = "the host stack";
 #ifdef EMU_ASAN
         else if (const void* b = __sanitizer_get_allocated_begin((const void*)w))
             if (!in_device_alloc((uintptr_t)b)) what = "host heap memory";
