@@ -86,13 +86,15 @@ struct dim3 {
 };
 
 // ---- vector types --------------------------------------------------------
-struct uint2 { uint32_t x, y; };
-struct uint4 { uint32_t x, y, z, w; };
-struct int2 { int32_t x, y; };
-struct int4 { int32_t x, y, z, w; };
-struct float2 { float x, y; };
-struct float4 { float x, y, z, w; };
-struct double2 { double x, y; };
+// aligned as HIP aligns them (the size of the whole vector), so that layouts
+// match the device's and the alignment sanitizer sees misaligned accesses
+struct alignas(8) uint2 { uint32_t x, y; };
+struct alignas(16) uint4 { uint32_t x, y, z, w; };
+struct alignas(8) int2 { int32_t x, y; };
+struct alignas(16) int4 { int32_t x, y, z, w; };
+struct alignas(8) float2 { float x, y; };
+struct alignas(16) float4 { float x, y, z, w; };
+struct alignas(16) double2 { double x, y; };
 inline uint2 make_uint2(uint32_t a, uint32_t b) { return uint2{a, b}; }
 inline uint4 make_uint4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) { return uint4{a, b, c, d}; }
 inline int2 make_int2(int32_t a, int32_t b) { return int2{a, b}; }
