@@ -224,14 +224,21 @@ __device__ __forceinline__ uint32_t over_uc(uint32_t w, uint32_t kuc) { return (
 // Exact codes (I8 / U8 / NF4) for the counts >= uc of a chunk of NW words
 // of byte counters w, whose table codes are already in o: only those bytes
 // are recomputed from the closed form, each with its column's r_j (byte b
-// of the chunk is column j0 + b).  Inlined: the chunks that need it are
-// rare, and a call would make the kernel save registers around it.
+// of the chunk is column j0 + b).  Only the bytes of the item's own columns
+// count, bytes [b0, b1) of the chunk: a byte before or after them holds no
+// column (in a checked launch, the carry of a wrapped last column lands in
+// the byte after it, before the item is recounted), so its r_j would be
+// read outside rinv, and its code is never stored.  Inlined: the chunks
+// that need it are rare, and a call would make the kernel save registers
+// around it.
 template <int F, int NW>
 __device__ __forceinline__ void fix_codes(uint32_t (&o)[NW], const uint32_t (&w)[NW], uint32_t uc, double ri,
-                                          const double* rinv, int64_t j0, float scale, float zp) {
-    uint32_t m = 0;  // bit b: byte b holds a count >= uc
+                                          const double* rinv, int64_t j0, int32_t b0, int32_t b1, float scale,
+                                          float zp) {
+    uint32_t m = 0;  // bit b: byte b holds a count >= uc and a column of the item
 #pragma unroll
-    for (int b = 0; b < 4 * NW; ++b) m |= (byte_of(w[b >> 2], b & 3) >= uc ? 1u : 0u) << b;
+    for (int b = 0; b < 4 * NW; ++b)
+        m |= (byte_of(w[b >> 2], b & 3) >= uc && b >= b0 && b < b1 ? 1u : 0u) << b;
     while (m) {
         const int b = __builtin_ctz(m);
         m &= m - 1u;
@@ -651,7 +658,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             uint32_t o[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) o[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, wv[q]);
-            fix_codes<F>(o, wv, uc, ri, a.rinv, jb, a.scale, a.zp);
+            fix_codes<F>(o, wv, uc, ri, a.rinv, jb, shift - ck * 16, shift + width - ck * 16, a.scale, a.zp);
             store_chunk(ck, o);
         }
     } else {
@@ -668,6 +675,16 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
             if (check) {
                 bsum = __builtin_amdgcn_sad_u8(cw[0], 0u, bsum);
                 bsum = __builtin_amdgcn_sad_u8(cw[1], 0u, bsum);
+            }
+            const int32_t first = ck * epc, last = first + epc;
+            const bool whole = first >= shift && last <= shift + width;
+            if (!whole) {
+                // the item's first or last chunk: counters outside the item
+                // hold no column (a wrapped last column's carry can land in
+                // the byte after it); as zeros they read no r_j
+#pragma unroll
+                for (int b = 0; b < epc; ++b)
+                    if (first + b < shift || first + b >= shift + width) cw[b >> 2] &= ~(0xffu << (8 * (b & 3)));
             }
             const int64_t jb = lo + (int64_t)ck * epc - shift;
             uint32_t o[4];
@@ -688,8 +705,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
                 for (int b = 0; b < 4; ++b) o[b] = h[2 * b] | (h[2 * b + 1] << 16);
             }
             char* d = dst_al + (int64_t)ck * 16;
-            const int32_t first = ck * epc, last = first + epc;
-            if (first >= shift && last <= shift + width) {
+            if (whole) {
                 u32x4 v4 = {o[0], o[1], o[2], o[3]};
                 __builtin_nontemporal_store(v4, (u32x4*)d);
             } else {
@@ -816,7 +832,7 @@ __global__ __launch_bounds__(TRI_THREADS) __attribute__((amdgpu_waves_per_eu(8, 
         uint32_t codes[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) codes[q] = __builtin_amdgcn_perm(lut_hi, lut_lo, cw[q]);
-        fix_codes<NF4>(codes, cw, uc, ri, a.rinv, jb, 0.f, 0.f);
+        fix_codes<NF4>(codes, cw, uc, ri, a.rinv, jb, shift - ck * 32, shift + width - ck * 32, 0.f, 0.f);
         store_chunk(ck, codes);
     }
     if (check && !counts_exact(misc, bsum, cnt, (uint32_t)gm.nwords, a.dbytes / 4u)) redo_wide<NF4>(a, cnt, gm, ri);

@@ -98,6 +98,32 @@ def test_byte_sum_check_and_recount(driver, tmp_path):
         assert rec > 0
 
 
+@pytest.mark.parametrize("fmt,scale,zp", [(O.FMT_U8, 1 / 4000.0, 3.0), (O.FMT_I8, 1 / 2000.0, -100.0),
+                                          (O.FMT_NF4, 1.0, 0.0), (O.FMT_F32, 1.0, 0.0), (O.FMT_F16, 1.0, 0.0)])
+def test_wrapped_last_column_reads_no_entry_past_the_row(driver, tmp_path, fmt, scale, zp):
+    """Checked 8-bit counting (T = 700) where the last column of many rows
+    wraps: samples 0..299 and N - 1 share a leaf in every tree, so pairs
+    (i, N - 1) count about 325.  The wrap's carry lands in the first padding
+    byte after the row's last column; the epilogue must not code that byte
+    (whose column N does not exist: its 1/nout would be read past the end of
+    the array, which the sanitizer reports).  Column-dependent codes (every
+    nonzero count takes the exact per-column path) and a caller nout with
+    zeros for the integer formats; the float formats read r_j for every
+    nonzero count.  Rows 0..23 (items of different alignments) against the
+    oracle after the 16-bit recount."""
+    n, t, nleaf = 1003, 700, 3
+    leaf, oob = forest(31, n, t, nleaf, p_oob=0.45)
+    leaf[:, :300] = leaf[:, :1]
+    leaf[:, n - 1] = leaf[:, 0]
+    nout = np.random.default_rng(32).integers(0, t + 3, n).astype(np.int32)
+    nout[::11] = 0
+    got, rec = emulate(driver, tmp_path, 1, leaf, oob, nleaf, fmt, scale, zp, r0=0, r1=24, nout=nout)
+    want = O.upper_rows(leaf, oob, nleaf, fmt, scale=np.float32(scale), zp=np.float32(zp), r0=0, r1=24,
+                        nout_arr=nout)
+    assert np.array_equal(got, want)
+    assert rec > 0
+
+
 @pytest.mark.parametrize("planted", [True, False])
 def test_thousand_trees_per_thread_dummy_words(driver, tmp_path, planted):
     """T = 1,000 (769 to 3,072 trees: the byte-sum check with one dummy word
