@@ -603,3 +603,26 @@ def test_row_bands_back_to_back_on_the_context_stream():
                     f"band {r0}:{r1}")
         assert (host[nb:] == 0xA5).all()
     ctx.close()
+
+
+def test_per_part_back_to_back_placement_past_the_line_fit_bound(gpu_ctx):
+    """N = 33,000 with 1,031 leaves takes the per-part packing path; with
+    10,640 trees the line-fit layout would need T x 100,928 ids, past 2^30,
+    so the buckets are placed back to back (tree stride N) instead, and
+    10,640 trees count in the 16-bit mode.  Sampled rows at both ends and in
+    the middle, U16 and U8, against the oracle."""
+    n, t, nleaf = 33_000, 10_640, 1031
+    nb = 2 * nleaf
+    assert n >= 32_768 and n >= 16 * nb                       # per-part path
+    stride = (n + 31 * (nb + (nb + 15) // 16) + 31) // 32 * 32
+    assert t * stride + 64 >= 1 << 30 and n * t + 64 < (1 << 30) - 1
+    leaf, oob = make_forest(77, n, t, nleaf, p_oob=0.368)
+    keep = upload(gpu_ctx, leaf, oob, nleaf)
+    idx = O.RowIndex(leaf, oob, nleaf)
+    for fmt, scale, r0, r1 in [(O.FMT_U16, 1.0, 0, 3), (O.FMT_U8, 1 / 255.0, 16_500, 16_503),
+                               (O.FMT_U16, 1.0, n - 3, n)]:
+        got, guard = gpu_rows(gpu_ctx, fmt, r0, r1, scale=np.float32(scale))
+        check_equal(got, idx.rows(fmt, r0, r1, np.float32(scale), np.float32(0.0)), f"fmt {fmt} rows {r0}:{r1}")
+        assert (guard == 0xA5).all()
+    idx.close()
+    del keep
