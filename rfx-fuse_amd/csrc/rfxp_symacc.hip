@@ -271,26 +271,26 @@ __global__ __launch_bounds__(SCAN_T) void k_sa_scan(int64_t* cnt, int64_t r0, in
 
 // Symmetric CSR from the COO list: degrees, then placement at cursors.
 __global__ void k_sa_degree(const int32_t* ci, const int32_t* cj, int64_t nnz, unsigned long long* deg) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= nnz) return;
-    const int32_t i = ci[e], j = cj[e];
-    atomicAdd(&deg[i], 1ull);
-    if (j != i) atomicAdd(&deg[j], 1ull);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nnz; e += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t i = ci[e], j = cj[e];
+        atomicAdd(&deg[i], 1ull);
+        if (j != i) atomicAdd(&deg[j], 1ull);
+    }
 }
 
 __global__ void k_sa_place(const int32_t* ci, const int32_t* cj, const float* cv, int64_t nnz,
                            unsigned long long* cur, int32_t* col, float* val) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= nnz) return;
-    const int32_t i = ci[e], j = cj[e];
-    const float v = cv[e];
-    const unsigned long long p = atomicAdd(&cur[i], 1ull);
-    col[p] = j;
-    val[p] = v;
-    if (j != i) {
-        const unsigned long long q = atomicAdd(&cur[j], 1ull);
-        col[q] = i;
-        val[q] = v;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nnz; e += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t i = ci[e], j = cj[e];
+        const float v = cv[e];
+        const unsigned long long p = atomicAdd(&cur[i], 1ull);
+        col[p] = j;
+        val[p] = v;
+        if (j != i) {
+            const unsigned long long q = atomicAdd(&cur[j], 1ull);
+            col[q] = i;
+            val[q] = v;
+        }
     }
 }
 
@@ -325,9 +325,8 @@ __global__ __launch_bounds__(SA_THREADS) void k_sa_tri_add(SymSrc s, int64_t row
 // across contributions: atomic adds).
 __global__ void k_sa_list_to_tri(const int32_t* ci, const int32_t* cj, const float* cv, int64_t nnz, int64_t N,
                                  double* tri) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= nnz) return;
-    atomicAdd(&tri[tri_idx(N, ci[e], cj[e])], (double)cv[e]);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nnz; e += (int64_t)gridDim.x * blockDim.x)
+        atomicAdd(&tri[tri_idx(N, ci[e], cj[e])], (double)cv[e]);
 }
 
 // Dense form of Y = M X: M symmetric from its packed upper triangle, X and Y
@@ -474,12 +473,13 @@ __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
     return x ^ (x >> 31);
 }
 __global__ void k_randn(double* X, int64_t n, uint64_t seed) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= n) return;
-    const uint64_t h1 = splitmix(seed ^ splitmix((uint64_t)e * 2u)), h2 = splitmix(seed ^ splitmix((uint64_t)e * 2u + 1u));
-    const double u1 = ((double)(h1 >> 11) + 1.0) * (1.0 / 9007199254740993.0);  // (0, 1]
-    const double u2 = (double)(h2 >> 11) * (1.0 / 9007199254740992.0);         // [0, 1)
-    X[e] = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+        const uint64_t h1 = splitmix(seed ^ splitmix((uint64_t)e * 2u));
+        const uint64_t h2 = splitmix(seed ^ splitmix((uint64_t)e * 2u + 1u));
+        const double u1 = ((double)(h1 >> 11) + 1.0) * (1.0 / 9007199254740993.0);  // (0, 1]
+        const double u2 = (double)(h2 >> 11) * (1.0 / 9007199254740992.0);         // [0, 1)
+        X[e] = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    }
 }
 
 // Column-major N x r -> row-major N x r.
@@ -502,23 +502,24 @@ __global__ void k_to_rowmajor(const double* A, int64_t N, int32_t r, double* Ar)
 // step intends.
 __global__ void k_reconstruct(const double* A, const double* B, int64_t N, int32_t r, const double* winv,
                               const int32_t* s, double* out) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= N * N) return;
-    const int64_t row = e % N, cl = e / N;
-    double p = 0.0;
-    if (row == cl) {
-        p = 1.0;
-        if (s && s[row] > 0) p *= winv[row];
-    } else {
-        for (int32_t c = 0; c < r; ++c) p += A[row + (int64_t)c * N] * B[cl + (int64_t)c * N];
-        if (s) {
-            const int64_t lo = min(row, cl), hi = max(row, cl);
-            const double x = s[lo] > 0 ? p * winv[lo] : p;
-            const double y = s[hi] > 0 ? p * winv[hi] : p;
-            p = 0.5 * (x + y);
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < N * N;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = e % N, cl = e / N;
+        double p = 0.0;
+        if (row == cl) {
+            p = 1.0;
+            if (s && s[row] > 0) p *= winv[row];
+        } else {
+            for (int32_t c = 0; c < r; ++c) p += A[row + (int64_t)c * N] * B[cl + (int64_t)c * N];
+            if (s) {
+                const int64_t lo = min(row, cl), hi = max(row, cl);
+                const double x = s[lo] > 0 ? p * winv[lo] : p;
+                const double y = s[hi] > 0 ? p * winv[hi] : p;
+                p = 0.5 * (x + y);
+            }
         }
+        out[e] = p;
     }
-    out[e] = p;
 }
 
 // Per-row elementwise helpers of the MDS operator (row-major blocks).
@@ -571,6 +572,18 @@ __global__ void k_rownorm2(const double* A, int64_t N, int32_t r, double* d) {
 }
 
 static unsigned nblk(int64_t n, int t = 256) { return (unsigned)((n + t - 1) / t); }
+
+// Grid of a grid-stride kernel over n elements, 256 threads a workgroup:
+// enough workgroups to fill the device, and at most RFXP_GS_MAX_BLOCKS of
+// them, so that the launch's work-items per dimension stay within 32 bits
+// whatever n is.  (The CPU emulation's build lowers the bound, so that its
+// tests run every such kernel through several strides.)
+#ifndef RFXP_GS_MAX_BLOCKS
+#define RFXP_GS_MAX_BLOCKS (1 << 20)
+#endif
+static unsigned gsblk(int64_t n) {
+    return (unsigned)std::min<int64_t>(((n + 255) / 256), (int64_t)(RFXP_GS_MAX_BLOCKS));
+}
 
 // ---------------------------------------------------------------------------
 // dense block operations (host drivers)
@@ -702,7 +715,7 @@ static int symacc_to_dense(rfxp_ctx* ctx) {
                          "rfxp_symacc: cannot allocate the dense triangle (" + std::to_string(8 * ne) + " bytes)");
     fill_u32(ctx, (uint32_t*)ctx->sa_tri.p, 2 * ne, 0u);
     if (ctx->sa_nnz > 0)
-        hipLaunchKernelGGL(k_sa_list_to_tri, dim3(nblk(ctx->sa_nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p,
+        hipLaunchKernelGGL(k_sa_list_to_tri, dim3(gsblk(ctx->sa_nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p,
                            ctx->sa_j.p, ctx->sa_v.p, ctx->sa_nnz, N, ctx->sa_tri.p);
     if (int rc = check_launch(ctx, "k_sa_list_to_tri")) return rc;
     RFXP_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -892,7 +905,7 @@ static int symacc_csr(rfxp_ctx* ctx) {
     RFXP_HIP(ctx, ctx->sa_rowptr.ensure((size_t)N + 1));
     fill_u32(ctx, (uint32_t*)ctx->sa_deg.p, 2 * (N + 1), 0u);
     if (nnz > 0) {
-        hipLaunchKernelGGL(k_sa_degree, dim3(nblk(nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p, ctx->sa_j.p, nnz,
+        hipLaunchKernelGGL(k_sa_degree, dim3(gsblk(nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p, ctx->sa_j.p, nnz,
                            ctx->sa_deg.p);
         if (int rc = check_launch(ctx, "k_sa_degree")) return rc;
     }
@@ -908,7 +921,7 @@ static int symacc_csr(rfxp_ctx* ctx) {
     RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_rowptr.p, rp.data(), 8 * (N + 1), hipMemcpyHostToDevice, ctx->stream));
     RFXP_HIP(ctx, hipMemcpyAsync(ctx->sa_deg.p, rp.data(), 8 * N, hipMemcpyHostToDevice, ctx->stream));  // cursors
     if (nnz > 0) {
-        hipLaunchKernelGGL(k_sa_place, dim3(nblk(nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p, ctx->sa_j.p, ctx->sa_v.p,
+        hipLaunchKernelGGL(k_sa_place, dim3(gsblk(nnz)), dim3(256), 0, ctx->stream, ctx->sa_i.p, ctx->sa_j.p, ctx->sa_v.p,
                            nnz, ctx->sa_deg.p, ctx->sa_col.p, ctx->sa_val.p);
         if (int rc = check_launch(ctx, "k_sa_place")) return rc;
     }
@@ -954,7 +967,7 @@ extern "C" int rfxp_symacc_factor(rfxp_ctx* ctx, int32_t rank, int32_t iters, ui
     RFXP_HIP(ctx, ctx->sa_y.ensure((size_t)(N * b)));
     RFXP_HIP(ctx, ctx->sa_z.ensure((size_t)(N * b)));
     double *X = ctx->sa_x.p, *Y = ctx->sa_y.p, *Z = ctx->sa_z.p;
-    hipLaunchKernelGGL(k_randn, dim3(nblk(N * b)), dim3(256), 0, ctx->stream, X, N * b, seed);
+    hipLaunchKernelGGL(k_randn, dim3(gsblk(N * b)), dim3(256), 0, ctx->stream, X, N * b, seed);
     if (int rc = check_launch(ctx, "k_randn")) return rc;
     if (int rc = orth(ctx, ctx->sa_part, ctx->sa_g, ctx->sa_w, X, Y, Z, b, N)) return rc;  // Q in Y
     // Ritz values and vectors of M on the current basis Q (in Y); X = M Q
@@ -1012,7 +1025,7 @@ extern "C" int rfxp_factor_reconstruct(rfxp_ctx* ctx, const double* A, const dou
         wdev = ctx->sa_wv.p;
     }
     const int64_t nn = N * N;
-    hipLaunchKernelGGL(k_reconstruct, dim3(nblk(nn)), dim3(256), 0, ctx->stream, A, B, N, rank, wdev, sdev, out);
+    hipLaunchKernelGGL(k_reconstruct, dim3(gsblk(nn)), dim3(256), 0, ctx->stream, A, B, N, rank, wdev, sdev, out);
     return check_launch(ctx, "k_reconstruct");
 }
 

@@ -406,6 +406,14 @@ void launch_raw(const void*, const char* name, dim3 grid, dim3 block, size_t lds
         g_last = hipErrorInvalidValue;
         return;
     }
+    // the dispatch packet counts work-items per dimension in 32 bits, and
+    // HIP reports 65,536 as the largest y and z grid
+    if ((uint64_t)grid.x * block.x > 0xffffffffull || (uint64_t)grid.y * block.y > 0xffffffffull ||
+        (uint64_t)grid.z * block.z > 0xffffffffull || grid.y > 65536u || grid.z > 65536u) {
+        fprintf(stderr, "emu: kernel %s: grid %ux%ux%u of %ux%ux%u threads is past the dispatch limits\n",
+                name ? name : "?", grid.x, grid.y, grid.z, block.x, block.y, block.z);
+        abort();
+    }
     if (lds > 160 * 1024) {
         g_last = hipErrorInvalidValue;
         return;
