@@ -136,7 +136,8 @@ extern "C" int rfxp_both_oob(rfxp_ctx* ctx, const int32_t* leaf, int64_t stride_
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_both_oob: pointers must be device pointers");
     const int64_t nJ = (N + BO_TILE - 1) / BO_TILE;
     const int64_t t_r0 = row_begin / BO_TILE, t_r1 = (row_end + BO_TILE - 1) / BO_TILE;
-    if (nJ > 0x7fffffffLL || t_r1 - t_r0 > 65535)
+    // work-items per dimension within 32 bits, y within 65,535 workgroups
+    if (nJ * BO_THREADS > 0xffffffffLL || t_r1 - t_r0 > 65535)
         return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_both_oob: row band too large for one launch");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     BothOobArgs a{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf, row_begin, row_end, t_r0,

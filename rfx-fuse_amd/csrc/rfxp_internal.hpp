@@ -162,6 +162,19 @@ struct LaunchTimer {
     ~LaunchTimer();
 };
 int check_launch(rfxp_ctx* ctx, const char* what);
+
+// Workgroups of a grid-stride launch over n units, per units per workgroup:
+// enough to fill the device, and at most RFXP_GS_MAX_BLOCKS, so that the
+// launch's work-items per dimension stay within the dispatch packet's 32
+// bits whatever n is.  (The CPU emulation's build lowers the bound, so that
+// its tests run every such kernel through several strides.)
+#ifndef RFXP_GS_MAX_BLOCKS
+#define RFXP_GS_MAX_BLOCKS (1 << 20)
+#endif
+inline unsigned grid_stride_blocks(int64_t n, int64_t per_block) {
+    const int64_t b = (n + per_block - 1) / per_block;
+    return (unsigned)(b < (int64_t)(RFXP_GS_MAX_BLOCKS) ? b : (int64_t)(RFXP_GS_MAX_BLOCKS));
+}
 // Device address of rfxp_upper_noalloc's static workspace on `device`
 // (current), taken once per device (rfxp_noalloc.hip).
 void noalloc_setup(int device);

@@ -573,17 +573,8 @@ __global__ void k_rownorm2(const double* A, int64_t N, int32_t r, double* d) {
 
 static unsigned nblk(int64_t n, int t = 256) { return (unsigned)((n + t - 1) / t); }
 
-// Grid of a grid-stride kernel over n elements, 256 threads a workgroup:
-// enough workgroups to fill the device, and at most RFXP_GS_MAX_BLOCKS of
-// them, so that the launch's work-items per dimension stay within 32 bits
-// whatever n is.  (The CPU emulation's build lowers the bound, so that its
-// tests run every such kernel through several strides.)
-#ifndef RFXP_GS_MAX_BLOCKS
-#define RFXP_GS_MAX_BLOCKS (1 << 20)
-#endif
-static unsigned gsblk(int64_t n) {
-    return (unsigned)std::min<int64_t>(((n + 255) / 256), (int64_t)(RFXP_GS_MAX_BLOCKS));
-}
+// Grid of a grid-stride kernel over n elements, 256 threads a workgroup.
+static unsigned gsblk(int64_t n) { return grid_stride_blocks(n, 256); }
 
 // ---------------------------------------------------------------------------
 // dense block operations (host drivers)

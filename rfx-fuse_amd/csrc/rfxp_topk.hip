@@ -723,7 +723,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
             const uint32_t u0 = threadIdx.x * 2u * NW;
             uint32_t key[NW];
             if constexpr (NW >= 4) {
-    #pragma unroll
+#pragma unroll
                 for (int k = 0; k < NW; k += 4) {
                     const uint4 x = *(const uint4*)(kw + k);
                     key[k] = x.x;
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(8,
                     *(uint4*)(kw + k) = make_uint4(0u, 0u, 0u, 0u);
                 }
             } else {
-    #pragma unroll
+#pragma unroll
                 for (int k = 0; k < NW; ++k) {
                     key[k] = kw[k];
                     kw[k] = 0u;
@@ -825,13 +825,13 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
             uint4* pw[NB];
             uint32_t mh[NB];
             int32_t bal = 0;
-    #pragma unroll
+#pragma unroll
             for (int h = 0; h < NB; ++h) {
                 pw[h] = (uint4*)(sm + (uint32_t)h * (B / 4u) + 8u * threadIdx.x);
                 const uint4 x = pw[h][0], y = pw[h][1];
                 const uint32_t w8[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
                 uint32_t m2 = 0u;
-    #pragma unroll
+#pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     m2 = max_u16x2(m2, w8[k] & 0x00ff00ffu);
                     m2 = max_u16x2(m2, (w8[k] >> 8) & 0x00ff00ffu);
@@ -851,17 +851,17 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                 constexpr uint32_t SW = NB + 1;
                 uint32_t* const slot = L.red + 48 + SW * TOPK_WAVES * (uint32_t)(s & 1);
                 uint32_t wm[NB];
-    #pragma unroll
+#pragma unroll
                 for (int h = 0; h < NB; ++h) wm[h] = wave_max(mh[h]);
                 const uint32_t wb = CHECK ? wave_sum((uint32_t)bal) : 0u;
                 if (lane == 0) {
-    #pragma unroll
+#pragma unroll
                     for (int h = 0; h < NB; ++h) slot[SW * (threadIdx.x >> 6) + h] = wm[h];
                     slot[SW * (threadIdx.x >> 6) + NB] = wb;
                 }
                 __syncthreads();
                 const bool have = (uint32_t)lane < (uint32_t)TOPK_WAVES;
-    #pragma unroll
+#pragma unroll
                 for (int h = 0; h < NB; ++h) M[h] = wave_max(have ? slot[SW * lane + h] : 0u) + 1u;
                 if constexpr (CHECK) exact = wave_sum(have ? slot[SW * lane + NB] : 0u) == 0u;
             }
@@ -874,14 +874,14 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                     if ((uint32_t)h * B >= width) break;
                     const uint32_t lowest = max((uint32_t)a.floor_key, nrun == K ? kmin + 1u : 0u);
                     uint32_t Mh = M[0];
-    #pragma unroll
+#pragma unroll
                     for (int g = 1; g < NB; ++g) Mh = h == g ? M[g] : Mh;
                     if (Mh < lowest) continue;
                     const uint32_t loh = lo + (uint32_t)h * B;
                     // counts are read only in waves where some thread's largest
                     // count can enter
                     uint32_t mt = mh[0];
-    #pragma unroll
+#pragma unroll
                     for (int g = 1; g < NB; ++g) mt = h == g ? mh[g] : mt;
                     const bool wl = __ballot(mt + 1u >= lowest) != 0ull;
                     uint32_t w8[8];
@@ -891,7 +891,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                         w8[0] = x.x, w8[1] = x.y, w8[2] = x.z, w8[3] = x.w;
                         w8[4] = y.x, w8[5] = y.y, w8[6] = y.z, w8[7] = y.w;
                     } else {
-    #pragma unroll
+#pragma unroll
                         for (int k = 0; k < 8; ++k) w8[k] = 0u;
                     }
                     const int32_t rem = (int32_t)width - (int32_t)(h * B) - (int32_t)u0;
@@ -899,7 +899,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                     const int32_t exu = exd >= 0 && exd < 32 ? (int32_t)exd : -1;
                     select_bytes(a, w8, wl, rem, exu, Mh, lowest, loh, u0, L, nrun, kmin);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int h = 0; h < NB; ++h) {
                     pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
                     pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
@@ -908,7 +908,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
             } else {
                 // some count wrapped: recount the segment with 16-bit counters,
                 // block by block, zeroing each block's words as they are read
-    #pragma unroll
+#pragma unroll
                 for (int h = 0; h < NB; ++h) {
                     pw[h][0] = make_uint4(0u, 0u, 0u, 0u);
                     pw[h][1] = make_uint4(0u, 0u, 0u, 0u);
@@ -923,7 +923,7 @@ __global__ __launch_bounds__(TOPK_THREADS) __attribute__((amdgpu_waves_per_eu(16
                     count_query_segment<16>(a, q, s, soff, len4, tw0, tw1, lane, lane4, loh + 1u, dummy16);
                     __syncthreads();
                     uint32_t key[16];
-    #pragma unroll
+#pragma unroll
                     for (int k = 0; k < 16; k += 4) {
                         const uint4 x = *(const uint4*)(kw + k);
                         key[k] = x.x;
@@ -1210,27 +1210,28 @@ struct PairArgs {
 };
 
 __global__ __launch_bounds__(256) void k_pair_prox(PairArgs a) {
-    const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (p >= a.npairs) return;
-    const int64_t i = a.pi[p], j = a.pj[p];
-    const bool ok = i >= 0 && i < a.N && j >= 0 && j < a.N;
-    uint32_t match = 0, noob = 0;
-    if (ok) {
-        for (int32_t t = threadIdx.x & 63; t < a.T; t += 64) {
-            const uint32_t w = a.oob[(int64_t)t * a.old + (i >> 5)];
-            if (!((w >> (i & 31)) & 1u)) continue;
-            ++noob;
-            const int32_t li = a.leaf[i * a.si + (int64_t)t * a.st];
-            const int32_t lj = a.leaf[j * a.si + (int64_t)t * a.st];
-            match += (li == lj && li >= 0 && li < a.L) ? 1u : 0u;
+    // one wave per pair, grid-stride over the pairs (p is uniform in a wave)
+    for (int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); p < a.npairs; p += (int64_t)gridDim.x * 4) {
+        const int64_t i = a.pi[p], j = a.pj[p];
+        const bool ok = i >= 0 && i < a.N && j >= 0 && j < a.N;
+        uint32_t match = 0, noob = 0;
+        if (ok) {
+            for (int32_t t = threadIdx.x & 63; t < a.T; t += 64) {
+                const uint32_t w = a.oob[(int64_t)t * a.old + (i >> 5)];
+                if (!((w >> (i & 31)) & 1u)) continue;
+                ++noob;
+                const int32_t li = a.leaf[i * a.si + (int64_t)t * a.st];
+                const int32_t lj = a.leaf[j * a.si + (int64_t)t * a.st];
+                match += (li == lj && li >= 0 && li < a.L) ? 1u : 0u;
+            }
         }
-    }
 #pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-        match += (uint32_t)__shfl_xor((int)match, d, 64);
-        noob += (uint32_t)__shfl_xor((int)noob, d, 64);
+        for (int d = 32; d > 0; d >>= 1) {
+            match += (uint32_t)__shfl_xor((int)match, d, 64);
+            noob += (uint32_t)__shfl_xor((int)noob, d, 64);
+        }
+        if ((threadIdx.x & 63) == 0) a.out[p] = (ok && noob) ? (float)match / (float)noob : 0.0f;
     }
-    if ((threadIdx.x & 63) == 0) a.out[p] = (ok && noob) ? (float)match / (float)noob : 0.0f;
 }
 
 // Float scores of top-K results (src/rf_random_forest.cpp:4744, 4775-4778
@@ -1248,21 +1249,21 @@ struct ScoreArgs {
 };
 
 __global__ __launch_bounds__(256) void k_topk_scores(ScoreArgs a) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= a.Q * a.K) return;
-    const int64_t q = e / a.K;
-    float sc = 0.0f;
-    if (a.idx[e] >= 0) {
-        const float c = (float)a.cnt[e];
-        if (a.qoob) {
-            uint32_t n = 0;
-            for (int32_t t = 0; t < a.T; ++t) n += (a.qoob[(int64_t)t * a.qold + (q >> 5)] >> (q & 31)) & 1u;
-            sc = n ? c * (1.0f / (float)n) : 0.0f;
-        } else {
-            sc = c / (float)a.T;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < a.Q * a.K; e += (int64_t)gridDim.x * 256) {
+        const int64_t q = e / a.K;
+        float sc = 0.0f;
+        if (a.idx[e] >= 0) {
+            const float c = (float)a.cnt[e];
+            if (a.qoob) {
+                uint32_t n = 0;
+                for (int32_t t = 0; t < a.T; ++t) n += (a.qoob[(int64_t)t * a.qold + (q >> 5)] >> (q & 31)) & 1u;
+                sc = n ? c * (1.0f / (float)n) : 0.0f;
+            } else {
+                sc = c / (float)a.T;
+            }
         }
+        a.score[e] = sc;
     }
-    a.score[e] = sc;
 }
 
 // Queries per launch: gridDim.x * blockDim.x must stay below 2^32.
@@ -1443,9 +1444,7 @@ extern "C" int rfxp_topk_scores(rfxp_ctx* ctx, const uint32_t* q_oob_words, int6
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_topk_scores: q_oob_ld < ceil(Q/32)");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     ScoreArgs a{q_oob_words, q_oob_ld, Q, T, K, idx, cnt, score_out};
-    const int64_t nb = (Q * K + 255) / 256;
-    if (nb > 0x7fffffffLL) return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_topk_scores: Q * K too large");
-    hipLaunchKernelGGL(k_topk_scores, dim3((unsigned)nb), dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(k_topk_scores, dim3(grid_stride_blocks(Q * K, 256)), dim3(256), 0, ctx->stream, a);
     return check_launch(ctx, "k_topk_scores launch");
 }
 
@@ -1461,11 +1460,10 @@ extern "C" int rfxp_pair_proximity(rfxp_ctx* ctx, const int32_t* leaf, int64_t s
         !is_device_pointer(oob_words) || !is_device_pointer(pair_i) || !is_device_pointer(pair_j) ||
         !is_device_pointer(out))
         return set_error(ctx, RFXP_ERR_INVALID, "rfxp_pair_proximity: pointers must be device pointers");
-    if ((npairs + 3) / 4 > 0x7fffffffLL)
-        return set_error(ctx, RFXP_ERR_UNSUPPORTED, "rfxp_pair_proximity: too many pairs");
     RFXP_HIP(ctx, hipSetDevice(ctx->device));
     PairArgs a{leaf, stride_i, stride_t, oob_words, oob_ld, N, T, nleaf, pair_i, pair_j, npairs, out};
-    hipLaunchKernelGGL(k_pair_prox, dim3((unsigned)((npairs + 3) / 4)), dim3(256), 0, ctx->stream, a);
+    // four pairs per workgroup and stride
+    hipLaunchKernelGGL(k_pair_prox, dim3(grid_stride_blocks(npairs, 4)), dim3(256), 0, ctx->stream, a);
     return check_launch(ctx, "k_pair_prox launch");
 }
 
