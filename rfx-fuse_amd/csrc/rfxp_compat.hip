@@ -345,18 +345,53 @@ static __device__ __forceinline__ void add_half(__half* p, float v) {
     } while (old != assumed);
 }
 
+// The 32-bit word CAS of add_byte / add_half reads and writes back the whole
+// word that holds an entry.  When the N*N entries do not fill a whole number
+// of words, the last word runs past the buffer's end; the entries in it (at
+// most 3, all in column N-1) are left out of the CAS path and updated by the
+// thread of sample N-1 alone, with loads and stores of the entry's own width,
+// so no access leaves the buffer.  partial_word_start gives the first of
+// them (N*N when there are none).
+static __device__ __forceinline__ int64_t partial_word_start(integer_t nsample, int bytes) {
+    const int64_t ne = (int64_t)nsample * nsample, total = ne * bytes;
+    return (total & 3) ? (total & ~(int64_t)3) / bytes : ne;
+}
+
+// For each entry e >= e0: what the thread of its row r would add, as
+// add(e, nin[kk], nodesize), once per listing of kk among node k's members.
+template <class Add>
+static __device__ void partial_word_entries(const integer_t* nodexb, const integer_t* nin, integer_t nsample,
+                                            const integer_t* ndbegin, const integer_t* npcase, int64_t e0, Add add) {
+    const int64_t ne = (int64_t)nsample * nsample;
+    for (int64_t e = e0; e < ne; ++e) {
+        const int32_t r = (int32_t)(e % nsample), kk = (int32_t)(e / nsample);
+        const int32_t k = nodexb[r];
+        if (r > kk || k < 0 || nin[kk] <= 0) continue;
+        const int32_t nsz = node_size(nin, ndbegin, npcase, k);
+        if (nsz <= 0) continue;
+        for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j)
+            if (npcase[j] == kk) add(e, nin[kk], nsz);
+    }
+}
+
 __global__ void cuda_proximity_fp16_kernel(const integer_t* nodexb, const integer_t* nin, integer_t nsample,
                                            const integer_t* ndbegin, const integer_t* npcase, __half* prox_fp16) {
+    const int64_t e_tail = partial_word_start(nsample, 2);
     for (int32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < nsample; n += blockDim.x * gridDim.x) {
+        if (n == nsample - 1)
+            partial_word_entries(nodexb, nin, nsample, ndbegin, npcase, e_tail, [&](int64_t e, int32_t w, int32_t nsz) {
+                const float v = __half2float(__float2half((float)w / (float)nsz));
+                prox_fp16[e] = __float2half(__half2float(prox_fp16[e]) + v);
+            });
         const int32_t k = nodexb[n];
         if (k < 0) continue;
         const int32_t nsz = node_size(nin, ndbegin, npcase, k);
         if (nsz <= 0) continue;
         for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j) {
             const int32_t kk = npcase[j];
-            if (nin[kk] > 0 && n <= kk)
-                add_half(&prox_fp16[(int64_t)n + (int64_t)kk * nsample],
-                         __half2float(__float2half((float)nin[kk] / (float)nsz)));
+            const int64_t e = (int64_t)n + (int64_t)kk * nsample;
+            if (nin[kk] > 0 && n <= kk && e < e_tail)
+                add_half(&prox_fp16[e], __half2float(__float2half((float)nin[kk] / (float)nsz)));
         }
     }
 }
@@ -379,16 +414,24 @@ __global__ void cuda_proximity_kernel(const integer_t* nodexb, const integer_t* 
 __global__ void cuda_proximity_int8_kernel(const integer_t* nodexb, const integer_t* nin, integer_t nsample,
                                            const integer_t* ndbegin, const integer_t* npcase, int8_t* prox_int8,
                                            float scale, float zero_point) {
+    const int64_t e_tail = partial_word_start(nsample, 1);
+    uint8_t* const p = (uint8_t*)prox_int8;
     for (int32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < nsample; n += blockDim.x * gridDim.x) {
+        if (n == nsample - 1)
+            partial_word_entries(nodexb, nin, nsample, ndbegin, npcase, e_tail, [&](int64_t e, int32_t w, int32_t nsz) {
+                const int8_t q = QuantizationUtils::fp32_to_int8((float)w / (float)nsz, scale, zero_point);
+                p[e] = (uint8_t)(p[e] + (uint8_t)q);
+            });
         const int32_t k = nodexb[n];
         if (k < 0) continue;
         const int32_t nsz = node_size(nin, ndbegin, npcase, k);
         if (nsz <= 0) continue;
         for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j) {
             const int32_t kk = npcase[j];
-            if (nin[kk] > 0 && n <= kk) {
+            const int64_t e = (int64_t)n + (int64_t)kk * nsample;
+            if (nin[kk] > 0 && n <= kk && e < e_tail) {
                 const int8_t q = QuantizationUtils::fp32_to_int8((float)nin[kk] / (float)nsz, scale, zero_point);
-                add_byte((uint8_t*)&prox_int8[(int64_t)n + (int64_t)kk * nsample], (uint32_t)(uint8_t)q);
+                add_byte(&p[e], (uint32_t)(uint8_t)q);
             }
         }
     }
@@ -396,16 +439,21 @@ __global__ void cuda_proximity_int8_kernel(const integer_t* nodexb, const intege
 
 __global__ void cuda_proximity_nf4_kernel(const integer_t* nodexb, const integer_t* nin, integer_t nsample,
                                           const integer_t* ndbegin, const integer_t* npcase, uint8_t* prox_nf4) {
+    const int64_t e_tail = partial_word_start(nsample, 1);
     for (int32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < nsample; n += blockDim.x * gridDim.x) {
+        if (n == nsample - 1)
+            partial_word_entries(nodexb, nin, nsample, ndbegin, npcase, e_tail, [&](int64_t e, int32_t w, int32_t nsz) {
+                prox_nf4[e] = (uint8_t)(prox_nf4[e] + QuantizationUtils::fp32_to_nf4((float)w / (float)nsz));
+            });
         const int32_t k = nodexb[n];
         if (k < 0) continue;
         const int32_t nsz = node_size(nin, ndbegin, npcase, k);
         if (nsz <= 0) continue;
         for (int32_t j = ndbegin[k]; j < ndbegin[k + 1]; ++j) {
             const int32_t kk = npcase[j];
-            if (nin[kk] > 0 && n <= kk)
-                add_byte(&prox_nf4[(int64_t)n + (int64_t)kk * nsample],
-                         QuantizationUtils::fp32_to_nf4((float)nin[kk] / (float)nsz));
+            const int64_t e = (int64_t)n + (int64_t)kk * nsample;
+            if (nin[kk] > 0 && n <= kk && e < e_tail)
+                add_byte(&prox_nf4[e], QuantizationUtils::fp32_to_nf4((float)nin[kk] / (float)nsz));
         }
     }
 }
@@ -414,6 +462,13 @@ void QuantizationDispatcher::launch_proximity_kernel(QuantizationLevel level, co
                                                      const integer_t* nin, integer_t nsample,
                                                      const integer_t* ndbegin, const integer_t* npcase,
                                                      void* prox_data, int blocks, int threads) {
+    // the kernels' atomics act on whole aligned words (8 bytes for FP32's
+    // doubles, 4 for the narrower levels), so the output starts on one, as
+    // a device allocation does
+    if ((uintptr_t)prox_data & (level == QuantizationLevel::FP32 ? 7u : 3u)) {
+        ::rfxp::compat_report_msg("launch_proximity_kernel", "the output is not aligned to its word size");
+        return;
+    }
     switch (level) {
         case QuantizationLevel::FP32:
             hipLaunchKernelGGL(cuda_proximity_kernel, dim3(blocks), dim3(threads), 0, 0, nodexb, nin, nsample, ndbegin,

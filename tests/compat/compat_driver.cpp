@@ -123,7 +123,10 @@ int main(int argc, char** argv) {
     // inputs, a zeroed get_quantized_size(level, N*N) output, 256-thread
     // blocks over the samples.
     const std::vector<int32_t>& st0 = status[0];
-    std::vector<int32_t> nod(nnode[0] > 0 ? nnode[0] : 1, -1), ncount(N, 0), ncn(N, 0), nodexb(N, -1);
+    // ncount is indexed by terminal ordinal, and a tree can hold more
+    // terminal nodes than samples, so it is sized by the node count
+    std::vector<int32_t> nod(nnode[0] > 0 ? nnode[0] : 1, -1), ncount(nnode[0] > 0 ? nnode[0] : 1, 0), ncn(N, 0),
+        nodexb(N, -1);
     int32_t nterm = 0;
     for (int32_t k = 0; k < nnode[0]; ++k)
         if (st0[k] == -1) nod[k] = nterm++;

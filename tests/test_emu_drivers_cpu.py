@@ -26,6 +26,15 @@ def test_reference_signatures(emu_build, monkeypatch, tmp_path, cw):
     GC.test_reference_signatures_through_cpp_driver(tmp_path, cw)
 
 
+@pytest.mark.parametrize("n,nnode,t,cw,seed", GC.RANDOM_DRIVER_CASES)
+def test_reference_signatures_on_random_forests(emu_build, monkeypatch, tmp_path, n, nnode, t, cw, seed):
+    """Includes N*N odd, where the dense FP16 / INT8 / NF4 outputs of
+    launch_proximity_kernel end inside a 32-bit word: the sanitizer sees any
+    access past the output's last byte."""
+    monkeypatch.setattr(GC, "DRIVER", os.path.join(emu_build, "compat_driver"))
+    GC.check_random_forest_through_cpp_driver(tmp_path, n, nnode, t, cw, seed)
+
+
 @pytest.mark.parametrize("level", [0, 1, 2, 3])
 def test_lowrank_class_growtree_sequence(emu_build, monkeypatch, tmp_path, level):
     monkeypatch.setattr(GL, "LRDRIVER", os.path.join(emu_build, "lowrank_driver"))

@@ -175,16 +175,13 @@ def write_driver_input(path, ns, nx, nin, nout, casewise):
         nout.astype(np.int32).tofile(f)
 
 
-@pytest.mark.parametrize("cw", [0, 1])
-def test_reference_signatures_through_cpp_driver(tmp_path, cw):
-    """The rf:: functions, called with the reference's signatures from a C++
-    program linked against librfxprox.so, reproduce the reference fixture
-    and the oracle."""
+def run_cpp_driver(tmp_path, ns, nx, nin, nout, cw):
+    """Runs tests/compat/compat_driver on the forest and returns its outputs
+    by name (the order is the one its header comment gives)."""
     assert os.path.exists(DRIVER), "tests/compat/compat_driver not built (make -C rfx-fuse_amd driver)"
-    ns, nx, nin, g = fixture()
     t, n = nx.shape
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
-    write_driver_input(inp, ns, nx, nin, g["nout"], cw)
+    write_driver_input(inp, ns, nx, nin, nout, cw)
     r = subprocess.run(["timeout", "-k", "10", "120", DRIVER, str(inp), str(outp)], capture_output=True,
                        text=True)
     assert r.returncode == 0, r.stdout + r.stderr
@@ -200,43 +197,105 @@ def test_reference_signatures_through_cpp_driver(tmp_path, cw):
         return a
 
     F = lambda a: a.reshape((n, n), order="F")  # noqa: E731
-    prox, sym, prox2, rg, rg2 = (F(take(nn, np.float64)) for _ in range(5))
-    f16, i8, nf4 = take(ne, np.uint16), take(ne, np.int8), take((ne + 1) // 2, np.uint8)
-    i8u, gap16 = take(ne, np.int8), take(ne, np.uint16)
-    qs, sc = take(4, np.uint64), take(4, np.float32)
-    sym2 = F(take(nn, np.float64))
+    d = {}
+    for name in ("prox", "sym", "prox2", "rg", "rg2"):
+        d[name] = F(take(nn, np.float64))
+    d["f16"], d["i8"], d["nf4"] = take(ne, np.uint16), take(ne, np.int8), take((ne + 1) // 2, np.uint8)
+    d["i8u"], d["gap16"] = take(ne, np.int8), take(ne, np.uint16)
+    d["qs"], d["sc"] = take(4, np.uint64), take(4, np.float32)
+    d["sym2"] = F(take(nn, np.float64))
     nterm = int(take(1, np.int32)[0])
-    nodexb, ndbegin, npcase = take(n, np.int32), take(nterm + 1, np.int32), take(n, np.int32)
-    lev = [F(take(nn, dt)) for dt in (np.float64, np.uint16, np.int8, np.uint8)]
+    d["nodexb"], d["ndbegin"], d["npcase"] = take(n, np.int32), take(nterm + 1, np.int32), take(n, np.int32)
+    d["lev"] = [F(take(nn, dt)) for dt in (np.float64, np.uint16, np.int8, np.uint8)]
     assert off == raw.size
-    assert np.array_equal(prox, g[f"prox_cw{cw}"])
-    assert np.array_equal(prox2, g[f"prox_cw{cw}"])
-    assert np.array_equal(sym, g[f"proxsym_cw{cw}"])
+    return d
+
+
+def check_cpp_driver_outputs(d, ns, nx, nin, cw, prox, sym):
+    """Every output of the driver against the oracle, given the forest's
+    accumulated prox and proxsym (from the reference fixture or the
+    oracle)."""
+    assert np.array_equal(d["prox"], prox) and np.array_equal(d["prox2"], prox)
+    assert np.array_equal(d["sym"], sym)
     want_rg = O.rfgap(nin, nx)
-    assert np.array_equal(rg, want_rg) and np.array_equal(rg2, want_rg)
-    assert np.array_equal(f16, O.tree_upper(O.FMT_F16, ns[0], nx[0], nin[0], casewise=bool(cw)))
-    assert np.array_equal(i8, O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
-                                           scale=np.float32(1.0 / 60.0), zp=0.5))
-    assert np.array_equal(nf4, O.tree_upper(O.FMT_NF4, ns[0], nx[0], nin[0], casewise=bool(cw)))
-    assert np.array_equal(i8u, O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
-                                            scale=np.float32(1.0) / np.float32(127.0), zp=0.0))
-    assert np.array_equal(gap16, O.rfgap_tree_upper(nin[0], nx[0]))
+    assert np.array_equal(d["rg"], want_rg) and np.array_equal(d["rg2"], want_rg)
+    assert np.array_equal(d["f16"], O.tree_upper(O.FMT_F16, ns[0], nx[0], nin[0], casewise=bool(cw)))
+    assert np.array_equal(d["i8"], O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
+                                                scale=np.float32(1.0 / 60.0), zp=0.5))
+    assert np.array_equal(d["nf4"], O.tree_upper(O.FMT_NF4, ns[0], nx[0], nin[0], casewise=bool(cw)))
+    assert np.array_equal(d["i8u"], O.tree_upper(O.FMT_I8, ns[0], nx[0], nin[0], casewise=bool(cw),
+                                                 scale=np.float32(1.0) / np.float32(127.0), zp=0.0))
+    assert np.array_equal(d["gap16"], O.rfgap_tree_upper(nin[0], nx[0]))
+    qs, sc = d["qs"], d["sc"]
     # cuda/rf_quantization_kernels.cu:393-406: FP32 counts sizeof(dp_t), NF4 one byte per entry
     assert list(qs) == [8000, 2000, 1000, 1000]
-    col = g[f"proxsym_cw{cw}"][:, 0].astype(np.float32)
+    # compute_int8_scaling of the first column (host rule: a constant column
+    # gives scale 0 and zero point -min/0, as the reference's division does)
+    # and compute_int8_scaling_gpu of the whole matrix (scale 1/127 below 1e-10)
+    col = sym[:, 0].astype(np.float32)
     mn, mx = col.min(), col.max()
     s = (mx - mn) / np.float32(255.0)
-    assert sc[0] == s and sc[1] == np.float32(-mn / s)
-    full = g[f"proxsym_cw{cw}"].astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        want = np.array([s, -mn / s], np.float32)
+    assert np.array_equal(sc[:2], want, equal_nan=True), (sc[:2], want)
+    full = sym.astype(np.float32)
     s2 = (full.max() - full.min()) / np.float32(255.0)
+    if s2 < np.float32(1e-10):
+        s2 = np.float32(1.0) / np.float32(127.0)
     assert sc[2] == s2 and sc[3] == np.float32(-full.min() / s2)
-    # rf::gpu_finishprox = the fixture's proxsym (src/rf_finishprox.cpp:12-74)
-    assert np.array_equal(sym2, g[f"proxsym_cw{cw}"])
+    # rf::gpu_finishprox = proxsym (src/rf_finishprox.cpp:12-74)
+    assert np.array_equal(d["sym2"], sym)
     # the driver's terminal CSR is the reference's (src/rf_proximity.cpp:110-171)
+    nodexb, ndbegin, npcase = d["nodexb"], d["ndbegin"], d["npcase"]
+    nterm = ndbegin.size - 1
     assert np.array_equal(nodexb, O.terminal_leaf(ns[0], nx[0]))
     assert ndbegin[0] == 0 and ndbegin[-1] == int((nodexb >= 0).sum())
     for k in range(nterm):
         assert np.array_equal(npcase[ndbegin[k]:ndbegin[k + 1]], np.flatnonzero(nodexb == k))
     # QuantizationDispatcher::launch_proximity_kernel at the four levels
     for level in range(4):
-        assert np.array_equal(lev[level], O.dispatch_prox(level, nodexb, nin[0], ndbegin, npcase)), level
+        assert np.array_equal(d["lev"][level], O.dispatch_prox(level, nodexb, nin[0], ndbegin, npcase)), level
+
+
+@pytest.mark.parametrize("cw", [0, 1])
+def test_reference_signatures_through_cpp_driver(tmp_path, cw):
+    """The rf:: functions, called with the reference's signatures from a C++
+    program linked against librfxprox.so, reproduce the reference fixture
+    and the oracle."""
+    ns, nx, nin, g = fixture()
+    d = run_cpp_driver(tmp_path, ns, nx, nin, g["nout"], cw)
+    check_cpp_driver_outputs(d, ns, nx, nin, cw, g[f"prox_cw{cw}"], g[f"proxsym_cw{cw}"])
+
+
+def random_forest(seed, n, nnode, t, p_term):
+    """t random trees over n samples: node statuses (-1 terminal), node
+    indices per sample that fall outside [0, nnode) now and then, bootstrap
+    counts with zeros; nout counts the trees a sample is out of bag in."""
+    rng = np.random.default_rng(seed)
+    ns = np.where(rng.random((t, nnode)) < p_term, -1, rng.integers(1, 3, (t, nnode))).astype(np.int32)
+    nx = rng.integers(-2, nnode + 2, (t, n)).astype(np.int32)
+    nin = np.stack([np.bincount(rng.integers(0, n, n), minlength=n) for _ in range(t)]).astype(np.int32)
+    nout = (nin == 0).sum(axis=0).astype(np.int32)
+    return ns, nx, nin, nout
+
+
+# (n, nnode, trees, casewise, seed): N*N odd, so the FP16, INT8 and NF4
+# dense outputs of launch_proximity_kernel end inside a 32-bit word; trees
+# with more terminal nodes than samples; a single node.
+RANDOM_DRIVER_CASES = [(3, 9, 5, 0, 1), (3, 46, 2, 1, 2), (17, 1, 5, 1, 3), (17, 47, 3, 0, 4), (129, 9, 2, 1, 5),
+                       (241, 8, 5, 0, 6), (64, 3, 3, 1, 7)]
+
+
+def check_random_forest_through_cpp_driver(tmp_path, n, nnode, t, cw, seed):
+    ns, nx, nin, nout = random_forest(seed, n, nnode, t, 0.8)
+    prox = np.zeros((n, n), order="F")
+    for k in range(t):
+        O.cpu_proximity(ns[k], nx[k], nin[k], nnode, prox, bool(cw))
+    d = run_cpp_driver(tmp_path, ns, nx, nin, nout, cw)
+    check_cpp_driver_outputs(d, ns, nx, nin, cw, prox, O.finishprox(nout, prox))
+
+
+@pytest.mark.parametrize("n,nnode,t,cw,seed", RANDOM_DRIVER_CASES)
+def test_reference_signatures_on_random_forests(tmp_path, n, nnode, t, cw, seed):
+    """The C++ driver on random forests, every output against the oracle."""
+    check_random_forest_through_cpp_driver(tmp_path, n, nnode, t, cw, seed)
